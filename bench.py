@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-linear hot path.
+
+Default workload (BASELINE.json metric): the W8A8 linear at M=4352, K=3072,
+N=12288 (config 1's up-projection) -- one step is one fused linear: the
+rotate+quantise prologue over the bf16 activations, then the int8 MFMA GEMM
+with the scale/bias epilogue to bf16.  Inputs are resident in HBM before the
+timed region.  Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--config c1_up|c1_down|c2|c3_attn|c3_mlp|c4|c0]
+                  [--no-cpu-baseline]
+
+Only one GPU is used: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "phi-agent_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "W8A8 linear TOPS & % int8 MFMA peak at M=4352,K=3072,N=12288"
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+CPU_SAMPLE_ROWS = 1024    # rows of the reference CPU linear timed for the baseline
+
+CONFIGS = {
+    "c0": dict(kind="w8a8", M=256, K=3072, N=3072),
+    "c1_up": dict(kind="w8a8", M=4352, K=3072, N=12288),
+    "c1_down": dict(kind="w8a8", M=4352, K=12288, N=3072),
+    "c2": dict(kind="w4a8", M=4352, K=3072, N=9216, group=128),
+    "c3_attn": dict(kind="w8a8", M=32760, K=5120, N=5120),
+    "c3_mlp": dict(kind="w8a8", M=32760, K=5120, N=13824),
+    "c4": dict(kind="gemv", M=1, K=3072, N=18432, items=60),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg) -> dict | None:
+    """The reference's CPU linear (convrot + quantise + naive gemm_int8,
+    core/host/quant.cpp) on a bounded row sample, single thread."""
+    import oracle
+
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    rows = min(M, CPU_SAMPLE_ROWS)
+    if oracle.ref_available():
+        secs = oracle.ref_bench_q8(M, N, K, rows)
+        kind = "reference"
+    else:
+        # The C restatement: same loops, timed the same way.
+        import numpy as np
+
+        from phi_qlinear import synth
+
+        x = synth.activations(rows, K, seed=0)
+        w = synth.int8_weight(N, K, seed=1).numpy()
+        xb = x.view(__import__("torch").int16).numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        q, s = oracle.quantize_rows(xb)
+        oracle.gemm_i8_i32(q, w)
+        secs = time.perf_counter() - t0
+        kind = "port"
+    tops = 2.0 * rows * N * K / secs / 1e12
+    return {"value": tops, "unit": "TOPS", "cores": 1, "kind": kind,
+            "sample": f"{rows} of {M} rows x N={N} x K={K} (naive loop is linear in M), {secs:.2f} s"}
+
+
+def bench_w8a8(cfg, steps, warmup):
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        Q.quant_rotate(x, q=q8, s=s8)
+        mid = torch.cuda.Event(enable_timing=True)
+        mid.record()
+        Q.i8_gemm(q8, W, s8, sW, b, C=y)
+        return mid
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    mids = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for a, z in ev:
+        a.record()
+        mids.append(step())
+        z.record()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gemm_ms = sum(m.elapsed_time(z) for m, (_, z) in zip(mids, ev)) / steps
+    pro_ms = sum(a.elapsed_time(m) for m, (a, _) in zip(mids, ev)) / steps
+    ops = 2.0 * M * N * K
+    return {
+        "value": ops / (ms * 1e-3) / 1e12, "ms": ms, "gemm_ms": gemm_ms, "prologue_ms": pro_ms,
+        "roofline": {"bound": "mfma", "achieved": ops / (gemm_ms * 1e-3) / 1e12,
+                     "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "traffic": None},
+        "dtype": "int8", "extra": {"prologue_us": pro_ms * 1e3, "gemm_us": gemm_ms * 1e3,
+                                   "fused_linear_tops": ops / (ms * 1e-3) / 1e12},
+    }
+
+
+def bench_w4a8(cfg, steps, warmup):
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K, N, group = cfg["M"], cfg["K"], cfg["N"], cfg["group"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=3, device=dev)
+    lut, sw = Q.w4a8_prepare(codes, s_rel, Q.F16, sch, k=K, group=group, correction=corr)
+    q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    for _ in range(warmup):
+        Q.w4a8_linear(x, codes, lut, sw, group=group, q8=q8, s8=s8, C=y)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        Q.w4a8_linear(x, codes, lut, sw, group=group, q8=q8, s8=s8, C=y)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    ops = 2.0 * M * N * K
+    return {"value": ops / (ms * 1e-3) / 1e12, "ms": ms, "dtype": "int8",
+            "roofline": {"bound": "mfma", "achieved": ops / (ms * 1e-3) / 1e12, "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                         "traffic": None}}
+
+
+def bench_gemv(cfg, steps, warmup):
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K, N, n = cfg["M"], cfg["K"], cfg["N"], cfg["items"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    q8, s8 = Q.quant_rotate(x)
+    Ws = [synth.int8_weight(N, K, seed=200 + i, device=dev) for i in range(n)]
+    sc = [synth.weight_scale(0.002, device=dev) for _ in range(n)]
+    outs = [torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _ in range(n)]
+    for _ in range(warmup):
+        Q.gemv_batched(q8, s8, Ws, sc, outs=outs)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        Q.gemv_batched(q8, s8, Ws, sc, outs=outs)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    wbytes = float(n) * N * K
+    gbs = wbytes / (ms * 1e-3) / 1e9
+    return {"value": gbs, "ms": ms, "dtype": "int8", "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None}}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c1_up", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU (one MI355X); multi-GPU runs are not part of it",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    cfg = CONFIGS[args.config]
+    log(f"bench: config {args.config} {cfg}, warmup {args.warmup}, steps {args.steps}")
+    if cfg["kind"] == "w8a8":
+        r = bench_w8a8(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "w4a8":
+        r = bench_w4a8(cfg, args.steps, args.warmup)
+    else:
+        r = bench_gemv(cfg, args.steps, args.warmup)
+    log(f"bench: {r['ms'] * 1e3:.1f} us per step")
+
+    cpu = None
+    if not args.no_cpu_baseline and cfg["kind"] == "w8a8":
+        log("bench: timing the reference CPU path on a row sample ...")
+        cpu = cpu_baseline(cfg)
+    unit = r.get("unit", "TOPS")
+    workload = {"c1_up": "W8A8 linear M=4352 K=3072 N=12288 (config 1 up-projection)"}.get(
+        args.config, f"{args.config} {cfg}")
+    line = {
+        "metric": METRIC if args.config == "c1_up" else f"{args.config} {unit}",
+        "value": r["value"], "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": r["ms"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": r["dtype"],
+        "data": "synthetic (seeded: bf16 N(0,1) activations with 0.1% x20 outlier channels, "
+                "int8 U[-127,127] weights, scale 0.002, bf16 N(0,0.02) bias)",
+        "config": {"workload": workload, **{k: v for k, v in cfg.items() if k != "kind"},
+                   "parallelism": "single GPU"},
+        "roofline": r["roofline"], "cpu_baseline": cpu,
+    }
+    if "extra" in r:
+        line["extra"] = r["extra"]
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

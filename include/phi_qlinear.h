@@ -1,0 +1,207 @@
+/*
+ * phi_qlinear.h -- C ABI of the MI355X (gfx950) quantized-linear library.
+ *
+ * The library is the device half of Phi's int8 linear: the 256-wide convrot
+ * rotation + per-token int8 quantiser, the int8 x int8 -> int32 GEMM with the
+ * scale/bias epilogue, the grouped 4/6-bit weight decode, and the M<=8 GEMV.
+ * Every entry point enqueues work on the caller's HIP stream and returns;
+ * nothing synchronises and nothing allocates device memory: the caller owns
+ * every buffer (the reference's GpuAlloc contract, core/runtime/sched.hpp:27-32,
+ * and its VRAM accountant, core/runtime/vram_budget.hpp:42-264).
+ *
+ * Pointers are plain device addresses (the reference passes GpuBuffer* plus a
+ * byte offset, core/runtime/compute.hpp:176-217: fold the offset in).
+ * Sizes are int64_t.  Errors come back as a phi_status plus a thread-local
+ * message from phi_hip_last_error(); the C++ shim turns them into MediaError
+ * the way the reference's dispatchers throw (core/runtime/compute.cpp:552,
+ * :665-668, core/kernels/w4a8_expand.cpp:264-281).
+ */
+#ifndef PHI_QLINEAR_H
+#define PHI_QLINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PHI_QLINEAR_ABI_VERSION 1
+
+/* A hipStream_t (NULL = the default stream). */
+typedef void* phi_stream_t;
+
+typedef enum phi_status {
+    PHI_OK = 0,
+    PHI_ERR_ARG = 1,         /* null pointer, bad enum, negative size */
+    PHI_ERR_SHAPE = 2,       /* shape contract violated (K % 256, K % group, ...) */
+    PHI_ERR_ALIGN = 3,       /* a pointer or leading dimension breaks the alignment rule */
+    PHI_ERR_WORKSPACE = 4,   /* workspace too small: see phi_hip_workspace_bytes */
+    PHI_ERR_HIP = 5,         /* a HIP runtime call failed */
+    PHI_ERR_DEVICE_LOST = 6, /* memory fault / illegal address: the device is unusable */
+    PHI_ERR_UNSUPPORTED = 7  /* combination the library does not implement */
+} phi_status;
+
+/* Element types. */
+typedef enum phi_dtype {
+    PHI_F32 = 0,
+    PHI_BF16 = 1,
+    PHI_F16 = 2,
+    PHI_I32 = 3,
+    PHI_I8 = 4,
+    PHI_F8_E4M3 = 5,
+    PHI_F8_E5M2 = 6,
+    PHI_U8_E4M3 = 7 /* an E4M3 table in a byte container (RelDType::U8_E4M3) */
+} phi_dtype;
+
+/* Rounding of v * (1/scale) onto the integer grid. */
+typedef enum phi_round {
+    PHI_ROUND_HALF_AWAY = 0, /* the reference's rule (core/host/quant.cpp:163-166) */
+    PHI_ROUND_HALF_EVEN = 1  /* documented alternative */
+} phi_round;
+
+/* Message for the last failing call on this thread ("" after success). */
+const char* phi_hip_last_error(void);
+int phi_hip_abi_version(void);
+
+/*
+ * Rotate + quantise activations, per row (token).
+ * Replaces dispatch_quant_convrot / QuantConvrotArgs
+ * (core/runtime/compute.hpp:200-217, core/runtime/compute.cpp:663-684;
+ * kernel core/kernels/int8_gemm.cpp:699-802; host maths core/host/quant.cpp:109-169).
+ *
+ *   x      [rows, ldx] of x_dtype (PHI_F32 or PHI_BF16); ldx >= K
+ *   q      [rows, ldq] int8 out; ldq >= K
+ *   s      [rows] fp32 out: scale = amax > 1e-30 ? amax / qmax : 1
+ *   rotate 1: 256-wide J-2R Hadamard per group first (K % 256 == 0 required)
+ *   qmax   127 for int8, 7 for the w4a4 tower (any integer value 1..127)
+ * rows == 0 is a no-op (as in the reference).  K <= 32768 when rotate == 1.
+ */
+phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
+                                float qmax, int round_mode, int rotate);
+
+/*
+ * int8 GEMM with the fused dequant epilogue:
+ *   C[m,n] = fma((float)acc[m,n] * sA[m], sB[n], bias[n])   (bias = 0 when NULL)
+ *   acc[m,n] = sum_k A[m,k] * B[n,k]   (int32, exact)
+ * Replaces dispatch_int8_gemm / Int8GemmArgs (core/runtime/compute.hpp:176-198,
+ * core/runtime/compute.cpp:551-661; kernel core/kernels/int8_gemm.cpp:466-621,
+ * epilogue :588-620).
+ *
+ *   A [M, lda] int8, B [N, ldb] int8 (K contiguous: the checkpoint's [N,K]).
+ *   sA [M] fp32; sB [N] fp32, or [1] when sb_scalar (per-tensor scale).
+ *   bias: NULL, or [N] of bias_dtype (PHI_F32 / PHI_BF16).
+ *   C [M, ldc] of c_dtype: PHI_F32 (reference), PHI_BF16 (RNE), or PHI_I32
+ *     (raw accumulators; scales and bias are then ignored and may be NULL).
+ *   A, B: 16-byte aligned; lda, ldb multiples of 16; K % 64 == 0.
+ *   workspace: may be NULL when phi_hip_workspace_bytes() returns 0.
+ */
+phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
+                           int64_t ldb, const float* sA, const float* sB, int sb_scalar,
+                           const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
+                           int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes);
+
+/* Workspace (bytes) phi_hip_i8_gemm / phi_hip_q8_linear need for this shape. */
+size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * The fused W8A8 linear: rotate+quantise x into the caller's q8/s8 scratch,
+ * then phi_hip_i8_gemm.  Replaces linear_gemm's int8 branch
+ * (core/models/model_common.cpp:1384-1411), including its "activation
+ * scratch" contract (q8 [M,K] int8, s8 [M] fp32 owned by the caller).
+ */
+phi_status phi_hip_q8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,
+                             int64_t M, int64_t K, const int8_t* W, int64_t ldw, const float* sW,
+                             int sw_scalar, const void* bias, int bias_dtype, int64_t N, void* C,
+                             int c_dtype, int64_t ldc, int8_t* q8, float* s8, int round_mode,
+                             void* workspace, size_t ws_bytes);
+
+/* A grouped low-bit weight as the checkpoint stores it
+ * (W4a8ExpandArgs, core/kernels/w4a8_expand.hpp:86-117). */
+typedef struct phi_w4a8_weight {
+    const uint8_t* codes;      /* [rows, codes_row_bytes] packed codes */
+    int64_t codes_row_bytes;   /* >= k/2 (nibble4) or k/2 + k/4 (packed6) */
+    const void* s_rel;         /* [rows, srel_row_bytes]: k/group relative scales */
+    int s_rel_dtype;           /* PHI_F32/F16/BF16/F8_E4M3/F8_E5M2/U8_E4M3 */
+    int64_t srel_row_bytes;
+    const float* s_channel;    /* NULL (1.0), [rows], or [1] when sch_scalar */
+    int sch_scalar;
+    const float* codebook;     /* NULL (level = code - 8), or 16 fp32 levels */
+    const float* correction;   /* NULL, or [k/group, rows] fp32 additive plane */
+    int64_t rows;              /* N */
+    int64_t k;                 /* K, a whole number of groups */
+    int64_t group;             /* columns per relative scale */
+    int layout;                /* 0: nibble4 (asym_w4a8_int8), 1: packed6 (w6a8_int8) */
+} phi_w4a8_weight;
+
+/*
+ * Decode to the int8 GEMM operand: q [rows, k] int8 and s [rows] fp32, the
+ * reference's device expand (core/kernels/w4a8_expand.cpp:151-258,
+ * dispatch :263-303) and host decode+requantise (core/host/quant.cpp:315-389
+ * then :134-169 without rotation).  A correction plane (host path only in the
+ * reference, core/host/st.cpp:447-491) is supported.
+ */
+phi_status phi_hip_w4a8_expand(phi_stream_t stream, const phi_w4a8_weight* w, int8_t* q,
+                               float* s);
+
+/*
+ * Load-time preparation for the in-register W4A8 GEMM: per (row, group) a
+ * 16-entry int8 table lut[row][group][code] equal to the expanded code the
+ * reference would produce for that nibble, and the per-row scale s [rows].
+ * Nibble4 layout only.  No reference counterpart as an entry point: it is the
+ * expand of phi_hip_w4a8_expand factored per (row, group), so the GEMM can
+ * unpack nibbles in registers.
+ */
+phi_status phi_hip_w4a8_prepare(phi_stream_t stream, const phi_w4a8_weight* w, int8_t* lut,
+                                float* s);
+
+/*
+ * W4A8 linear with nibbles unpacked in registers through the prepared table.
+ * Equal, bit for bit, to phi_hip_w4a8_expand followed by phi_hip_q8_linear.
+ *   codes [N, codes_row_bytes] nibble4; lut [N, K/group, 16]; s_w [N].
+ *   group % 64 == 0.
+ */
+phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,
+                               int64_t M, int64_t K, const uint8_t* codes,
+                               int64_t codes_row_bytes, const int8_t* lut, int64_t group,
+                               const float* s_w, const void* bias, int bias_dtype, int64_t N,
+                               void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8,
+                               int round_mode, void* workspace, size_t ws_bytes);
+
+/* One weight of a batched GEMV. */
+typedef struct phi_gemv_item {
+    const int8_t* W;   /* [N, K] int8, rows 16-byte aligned */
+    const float* sW;   /* [N] fp32, or [1] when sw_scalar */
+    int sw_scalar;
+    const void* bias;  /* NULL or [N] of the call's bias_dtype */
+    void* C;           /* [M, ldc] of the call's c_dtype */
+    int64_t ldc;
+} phi_gemv_item;
+
+/*
+ * Small-M (M <= 8) linear over many weights that share one quantised
+ * activation block: C_i = epilogue(q8 . W_i^T) for every item.  The
+ * activations are quantised by the caller (phi_hip_quant_rotate) into
+ * q8 [M, K] / s8 [M].  The adaLN modulation shape of the DiT blocks
+ * (reference: host fp32, core/models/image_dit.cpp:1047-1072); same
+ * arithmetic contract as phi_hip_i8_gemm.  items must be in host memory.
+ */
+phi_status phi_hip_i8_gemv_batched(phi_stream_t stream, const int8_t* q8, const float* s8,
+                                   int64_t M, int64_t K, int64_t N, const phi_gemv_item* items,
+                                   int n_items, int bias_dtype, int c_dtype, void* workspace,
+                                   size_t ws_bytes);
+
+/* Workspace for phi_hip_i8_gemv_batched (holds the item table on the device). */
+size_t phi_hip_gemv_workspace_bytes(int n_items);
+
+/* GELU-tanh over bf16 or fp32 [n] (core/kernels/ops.cpp:83-89), in place
+ * allowed; out_dtype PHI_BF16 rounds RNE. */
+phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, void* y,
+                             int y_dtype, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PHI_QLINEAR_H */

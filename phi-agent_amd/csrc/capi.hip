@@ -1,0 +1,377 @@
+// C ABI of the quantized-linear library: argument validation, dispatch to the
+// gfx950 kernels, and the error contract.
+//
+// The reference's dispatchers throw MediaError on a contract violation
+// (core/runtime/compute.cpp:552, :665-668; core/kernels/w4a8_expand.cpp:264-281)
+// and mark the device lost on a memory fault (compute.cpp:461-467).  Here every
+// entry point returns a phi_status and leaves a message for
+// phi_hip_last_error(); a memory fault or illegal-address status from HIP is
+// reported as PHI_ERR_DEVICE_LOST and stays sticky for the process.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/phi_qlinear.h"
+#include "gemv.hpp"
+#include "i8_gemm.hpp"
+#include "w4a8.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+std::atomic<bool> g_lost{false};
+
+phi_status fail(phi_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return st;
+}
+
+phi_status ok() {
+    g_err.clear();
+    return PHI_OK;
+}
+
+bool is_fatal(hipError_t e) {
+    return e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorECCNotCorrectable ||
+           e == hipErrorAssert;
+}
+
+phi_status check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return ok();
+    if (is_fatal(e)) {
+        g_lost = true;
+        return fail(PHI_ERR_DEVICE_LOST, "%s: device lost (%s)", what, hipGetErrorString(e));
+    }
+    return fail(PHI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int bias_kind_of(const void* bias, int bias_dtype, phi_status* st) {
+    *st = PHI_OK;
+    if (!bias) return phi_dev::BIAS_NONE;
+    if (bias_dtype == PHI_F32) return phi_dev::BIAS_F32;
+    if (bias_dtype == PHI_BF16) return phi_dev::BIAS_BF16;
+    *st = PHI_ERR_ARG;
+    return -1;
+}
+
+int c_kind_of(int c_dtype) {
+    if (c_dtype == PHI_F32) return phi_dev::C_F32;
+    if (c_dtype == PHI_BF16) return phi_dev::C_BF16;
+    if (c_dtype == PHI_I32) return phi_dev::C_I32;
+    return -1;
+}
+
+size_t c_elem_bytes(int c_dtype) { return c_dtype == PHI_BF16 ? 2 : 4; }
+
+constexpr int64_t kMaxRotK = 24576;  // rotated row held in LDS: 96 groups = 129 KB
+
+// Shared validation of the GEMM operands (A [M,lda], B [N,ldb]).
+phi_status check_gemm(const char* who, const int8_t* A, int64_t lda, const void* B, int64_t ldb,
+                      int64_t M, int64_t N, int64_t K, const float* sA, const float* sB,
+                      void* C, int c_dtype, int64_t ldc, bool w4) {
+    if (M <= 0 || N <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem (M=%lld N=%lld K=%lld)", who, (long long)M, (long long)N, (long long)K);
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: dimension exceeds 2^31", who);
+    if (!A || !B || !C) return fail(PHI_ERR_ARG, "%s: null operand", who);
+    if (c_kind_of(c_dtype) < 0) return fail(PHI_ERR_ARG, "%s: bad output dtype %d", who, c_dtype);
+    if (c_dtype != PHI_I32 && (!sA || !sB)) return fail(PHI_ERR_ARG, "%s: scales are required for a scaled output", who);
+    if (K % 64 != 0) return fail(PHI_ERR_SHAPE, "%s: K=%lld is not a multiple of 64", who, (long long)K);
+    if (lda < K || ldc < N) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than the row", who);
+    if (!aligned(A, 16) || lda % 16 != 0) return fail(PHI_ERR_ALIGN, "%s: A must be 16-byte aligned with lda %% 16 == 0", who);
+    if (w4) {
+        if (ldb < K / 2) return fail(PHI_ERR_SHAPE, "%s: a %lld-column nibble row needs %lld bytes, got %lld", who, (long long)K, (long long)(K / 2), (long long)ldb);
+        if (!aligned(B, 8) || ldb % 8 != 0) return fail(PHI_ERR_ALIGN, "%s: codes must be 8-byte aligned with row bytes %% 8 == 0", who);
+    } else {
+        if (ldb < K) return fail(PHI_ERR_SHAPE, "%s: ldb < K", who);
+        if (!aligned(B, 16) || ldb % 16 != 0) return fail(PHI_ERR_ALIGN, "%s: B must be 16-byte aligned with ldb %% 16 == 0", who);
+    }
+    if (!aligned(C, c_elem_bytes(c_dtype))) return fail(PHI_ERR_ALIGN, "%s: C is misaligned", who);
+    return PHI_OK;
+}
+
+int gemm_cfg_for(int64_t M, int64_t N) {
+    // 256x128 tiles unless that leaves most of the 256 CUs idle.
+    const int64_t big = ((M + 255) / 256) * ((N + 127) / 128);
+    return big >= 256 ? 0 : 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* phi_hip_last_error(void) { return g_err.c_str(); }
+
+int phi_hip_abi_version(void) { return PHI_QLINEAR_ABI_VERSION; }
+
+phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
+                                float qmax, int round_mode, int rotate) {
+    static const char* who = "quant_rotate";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0) return ok();
+    if (x_dtype != PHI_F32 && x_dtype != PHI_BF16) return fail(PHI_ERR_ARG, "%s: x dtype must be f32 or bf16", who);
+    if (round_mode != PHI_ROUND_HALF_AWAY && round_mode != PHI_ROUND_HALF_EVEN) return fail(PHI_ERR_ARG, "%s: bad round mode", who);
+    if (!x || !q || !s) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (K <= 0 || K % 256 != 0)
+        return fail(PHI_ERR_SHAPE, "quant_convrot: K=%lld is not a multiple of 256 (convrot group size)", (long long)K);
+    if (K > kMaxRotK) return fail(PHI_ERR_UNSUPPORTED, "%s: K=%lld exceeds %lld", who, (long long)K, (long long)kMaxRotK);
+    if (rows > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: rows exceeds 2^31", who);
+    if (!(qmax >= 1.0f && qmax <= 127.0f) || qmax != (float)(int)qmax) return fail(PHI_ERR_ARG, "%s: qmax must be an integer in [1,127]", who);
+    if (ldx < K || ldq < K) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than K", who);
+    const size_t esz = x_dtype == PHI_BF16 ? 2 : 4;
+    if (!aligned(x, 16) || (ldx * (int64_t)esz) % 16 != 0 || !aligned(q, 16) || ldq % 16 != 0 || !aligned(s, 4))
+        return fail(PHI_ERR_ALIGN, "%s: x and q rows must be 16-byte aligned", who);
+    return check_hip(phi_dev::launch_quant_rotate((hipStream_t)stream, x, x_dtype == PHI_BF16, rows, K, ldx, q, ldq, s,
+                                                  qmax, round_mode == PHI_ROUND_HALF_EVEN, rotate ? 1 : 0),
+                     who);
+}
+
+size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    (void)M;
+    (void)N;
+    (void)K;
+    return 0;
+}
+
+phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
+                           int64_t ldb, const float* sA, const float* sB, int sb_scalar,
+                           const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
+                           int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes) {
+    static const char* who = "int8_gemm";
+    (void)workspace;
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, C, c_dtype, ldc, false);
+    if (st != PHI_OK) return st;
+    if (ws_bytes < phi_hip_workspace_bytes(M, N, K)) return fail(PHI_ERR_WORKSPACE, "%s: workspace too small", who);
+    const int bk = bias_kind_of(bias, bias_dtype, &st);
+    if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    phi_dev::GemmParams p{};
+    p.A = A;
+    p.B = B;
+    p.sA = sA;
+    p.sB = sB;
+    p.bias = bias;
+    p.C = C;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.ldc = ldc;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.sb_scalar = sb_scalar ? 1 : 0;
+    p.bias_kind = bk;
+    p.c_kind = c_kind_of(c_dtype);
+    p.group_m = 4;
+    return check_hip(phi_dev::launch_i8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
+}
+
+phi_status phi_hip_q8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,
+                             int64_t M, int64_t K, const int8_t* W, int64_t ldw, const float* sW,
+                             int sw_scalar, const void* bias, int bias_dtype, int64_t N, void* C,
+                             int c_dtype, int64_t ldc, int8_t* q8, float* s8, int round_mode,
+                             void* workspace, size_t ws_bytes) {
+    static const char* who = "linear_gemm";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!q8 || !s8) return fail(PHI_ERR_ARG, "linear_gemm: the int8 path needs activation scratch");
+    if (M <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
+    phi_status st = check_gemm(who, q8, K, W, ldw, M, N, K, s8, sW, C, c_dtype, ldc, false);
+    if (st != PHI_OK) return st;
+    st = phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
+    if (st != PHI_OK) return st;
+    return phi_hip_i8_gemm(stream, q8, K, W, ldw, s8, sW, sw_scalar, bias, bias_dtype, C, c_dtype, ldc, M, N, K,
+                           workspace, ws_bytes);
+}
+
+static phi_status check_w4a8(const char* who, const phi_w4a8_weight* w, bool lut) {
+    if (!w) return fail(PHI_ERR_ARG, "%s: null weight descriptor", who);
+    if (w->rows < 0 || w->k < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (w->group <= 0 || w->k % w->group != 0)
+        return fail(PHI_ERR_SHAPE, "w4a8_expand: K=%lld is not a multiple of group=%lld", (long long)w->k, (long long)w->group);
+    if (w->layout != 0 && w->layout != 1) return fail(PHI_ERR_ARG, "%s: bad layout %d", who, w->layout);
+    if (w->group % (w->layout == 0 ? 2 : 4) != 0)
+        return fail(PHI_ERR_SHAPE, "w4a8_expand: group=%lld is not a whole number of code groups for this layout", (long long)w->group);
+    if (w->k % 16 != 0) return fail(PHI_ERR_SHAPE, "%s: K=%lld is not a multiple of 16", who, (long long)w->k);
+    const int64_t need = w->layout == 0 ? w->k / 2 : w->k / 2 + w->k / 4;
+    if (w->codes_row_bytes < need)
+        return fail(PHI_ERR_SHAPE, "w4a8_expand: a %lld-column row needs %lld packed bytes, got %lld", (long long)w->k, (long long)need, (long long)w->codes_row_bytes);
+    if (!w->codes) return fail(PHI_ERR_ARG, "w4a8_expand: missing binding");
+    if (w->codebook && w->layout != 0) return fail(PHI_ERR_ARG, "w4a8_expand: only the 4-bit family indexes a codebook");
+    const int d = w->s_rel_dtype;
+    if (w->s_rel && !(d == PHI_F32 || d == PHI_F16 || d == PHI_BF16 || d == PHI_F8_E4M3 || d == PHI_F8_E5M2 || d == PHI_U8_E4M3))
+        return fail(PHI_ERR_ARG, "%s: unreadable relative-scale dtype %d", who, d);
+    const int64_t rsz = d == PHI_F32 ? 4 : (d == PHI_F16 || d == PHI_BF16) ? 2 : 1;
+    if (w->s_rel && w->srel_row_bytes < (w->k / w->group) * rsz) return fail(PHI_ERR_SHAPE, "%s: relative-scale row too short", who);
+    if (lut && w->layout != 0) return fail(PHI_ERR_UNSUPPORTED, "%s: the in-register table is for the nibble layout only", who);
+    if (w->rows > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: rows exceeds 2^31", who);
+    return PHI_OK;
+}
+
+static phi_dev::W4a8Params w4a8_params(const phi_w4a8_weight* w) {
+    phi_dev::W4a8Params p{};
+    p.codes = w->codes;
+    p.codes_row_bytes = w->codes_row_bytes;
+    p.s_rel = w->s_rel;
+    p.s_rel_dtype = w->s_rel_dtype;
+    p.srel_row_bytes = w->srel_row_bytes;
+    p.s_channel = w->s_channel;
+    p.sch_scalar = w->sch_scalar;
+    p.codebook = w->codebook;
+    p.correction = w->correction;
+    p.rows = w->rows;
+    p.k = w->k;
+    p.group = w->group;
+    p.layout = w->layout;
+    return p;
+}
+
+phi_status phi_hip_w4a8_expand(phi_stream_t stream, const phi_w4a8_weight* w, int8_t* q, float* s) {
+    static const char* who = "w4a8_expand";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    phi_status st = check_w4a8(who, w, false);
+    if (st != PHI_OK) return st;
+    if (w->rows == 0 || w->k == 0) return ok();
+    if (!q || !s) return fail(PHI_ERR_ARG, "w4a8_expand: missing binding");
+    if (!aligned(q, 16)) return fail(PHI_ERR_ALIGN, "%s: q must be 16-byte aligned", who);
+    return check_hip(phi_dev::launch_w4a8_rows((hipStream_t)stream, w4a8_params(w), q, s, false), who);
+}
+
+phi_status phi_hip_w4a8_prepare(phi_stream_t stream, const phi_w4a8_weight* w, int8_t* lut, float* s) {
+    static const char* who = "w4a8_prepare";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    phi_status st = check_w4a8(who, w, true);
+    if (st != PHI_OK) return st;
+    if (w->rows == 0 || w->k == 0) return ok();
+    if (!lut || !s) return fail(PHI_ERR_ARG, "%s: missing binding", who);
+    if (!aligned(lut, 16)) return fail(PHI_ERR_ALIGN, "%s: lut must be 16-byte aligned", who);
+    return check_hip(phi_dev::launch_w4a8_rows((hipStream_t)stream, w4a8_params(w), lut, s, true), who);
+}
+
+phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,
+                               int64_t M, int64_t K, const uint8_t* codes,
+                               int64_t codes_row_bytes, const int8_t* lut, int64_t group,
+                               const float* s_w, const void* bias, int bias_dtype, int64_t N,
+                               void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8,
+                               int round_mode, void* workspace, size_t ws_bytes) {
+    static const char* who = "w4a8_linear";
+    (void)workspace;
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!q8 || !s8) return fail(PHI_ERR_ARG, "%s: the int8 path needs activation scratch", who);
+    if (!lut || !s_w) return fail(PHI_ERR_ARG, "%s: missing prepared table or row scales", who);
+    phi_status st = check_gemm(who, q8, K, codes, codes_row_bytes, M, N, K, s8, s_w, C, c_dtype, ldc, true);
+    if (st != PHI_OK) return st;
+    if (group <= 0 || group % 64 != 0 || K % group != 0 || (group & (group - 1)) != 0)
+        return fail(PHI_ERR_SHAPE, "%s: group=%lld must be a power of two, a multiple of 64 and divide K", who, (long long)group);
+    if (!aligned(lut, 16)) return fail(PHI_ERR_ALIGN, "%s: lut must be 16-byte aligned", who);
+    if (ws_bytes < phi_hip_workspace_bytes(M, N, K)) return fail(PHI_ERR_WORKSPACE, "%s: workspace too small", who);
+    const int bk = bias_kind_of(bias, bias_dtype, &st);
+    if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    st = phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
+    if (st != PHI_OK) return st;
+    phi_dev::GemmParams p{};
+    p.A = q8;
+    p.B = (const int8_t*)codes;
+    p.sA = s8;
+    p.sB = s_w;
+    p.bias = bias;
+    p.C = C;
+    p.lda = K;
+    p.ldb = codes_row_bytes;
+    p.ldc = ldc;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.sb_scalar = 0;
+    p.bias_kind = bk;
+    p.c_kind = c_kind_of(c_dtype);
+    p.group_m = 4;
+    p.lut = lut;
+    p.lut_groups = K / group;
+    int sh = 0;
+    while ((1ll << sh) < group) sh++;
+    p.group_shift = sh;
+    return check_hip(phi_dev::launch_w4a8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
+}
+
+size_t phi_hip_gemv_workspace_bytes(int n_items) {
+    (void)n_items;
+    return 0;
+}
+
+phi_status phi_hip_i8_gemv_batched(phi_stream_t stream, const int8_t* q8, const float* s8,
+                                   int64_t M, int64_t K, int64_t N, const phi_gemv_item* items,
+                                   int n_items, int bias_dtype, int c_dtype, void* workspace,
+                                   size_t ws_bytes) {
+    static const char* who = "i8_gemv_batched";
+    (void)workspace;
+    (void)ws_bytes;
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (n_items < 0 || M < 0 || N < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (n_items == 0 || M == 0 || N == 0) return ok();
+    if (M > 8) return fail(PHI_ERR_SHAPE, "%s: M=%lld exceeds 8 (use the GEMM)", who, (long long)M);
+    if (K <= 0 || K % 16 != 0) return fail(PHI_ERR_SHAPE, "%s: K=%lld is not a positive multiple of 16", who, (long long)K);
+    if (N > INT32_MAX || K > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: dimension exceeds 2^31", who);
+    if (!q8 || !s8 || !items) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (!aligned(q8, 16)) return fail(PHI_ERR_ALIGN, "%s: q8 must be 16-byte aligned", who);
+    const int ck = c_kind_of(c_dtype);
+    if (ck < 0) return fail(PHI_ERR_ARG, "%s: bad output dtype %d", who, c_dtype);
+    for (int i = 0; i < n_items; i++) {
+        const phi_gemv_item& it = items[i];
+        if (!it.W || !it.C || (ck != phi_dev::C_I32 && !it.sW)) return fail(PHI_ERR_ARG, "%s: item %d has a null pointer", who, i);
+        if (!aligned(it.W, 16)) return fail(PHI_ERR_ALIGN, "%s: item %d weight must be 16-byte aligned", who, i);
+        if (it.ldc < N) return fail(PHI_ERR_SHAPE, "%s: item %d ldc < N", who, i);
+        if (it.bias && bias_dtype != PHI_F32 && bias_dtype != PHI_BF16) return fail(PHI_ERR_ARG, "%s: bias dtype must be f32 or bf16", who);
+    }
+    for (int i0 = 0; i0 < n_items; i0 += phi_dev::GEMV_MAX_ITEMS) {
+        const int cnt = n_items - i0 < phi_dev::GEMV_MAX_ITEMS ? n_items - i0 : phi_dev::GEMV_MAX_ITEMS;
+        phi_dev::GemvBatch b{};
+        b.q8 = q8;
+        b.s8 = s8;
+        b.M = (int)M;
+        b.N = (int)N;
+        b.K = (int)K;
+        b.n_items = cnt;
+        b.c_kind = ck;
+        // All items share the call's bias dtype; an item without bias reads none.
+        b.bias_kind = phi_dev::BIAS_NONE;
+        bool any_bias = false, all_bias = true;
+        for (int j = 0; j < cnt; j++) {
+            const phi_gemv_item& it = items[i0 + j];
+            b.W[j] = it.W;
+            b.sW[j] = it.sW;
+            b.bias[j] = it.bias;
+            b.C[j] = it.C;
+            b.ldc[j] = it.ldc;
+            if (it.sw_scalar) b.sw_scalar_mask |= 1ull << j;
+            any_bias |= it.bias != nullptr;
+            all_bias &= it.bias != nullptr;
+        }
+        if (any_bias && !all_bias) return fail(PHI_ERR_UNSUPPORTED, "%s: mixed biased and bias-free items in one call", who);
+        if (any_bias) b.bias_kind = bias_dtype == PHI_BF16 ? phi_dev::BIAS_BF16 : phi_dev::BIAS_F32;
+        phi_status st = check_hip(phi_dev::launch_gemv((hipStream_t)stream, b), who);
+        if (st != PHI_OK) return st;
+    }
+    return ok();
+}
+
+phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, void* y, int y_dtype, int64_t n) {
+    static const char* who = "gelu_tanh";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (n < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (n == 0) return ok();
+    if (!x || !y) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if ((x_dtype != PHI_F32 && x_dtype != PHI_BF16) || (y_dtype != PHI_F32 && y_dtype != PHI_BF16))
+        return fail(PHI_ERR_ARG, "%s: dtypes must be f32 or bf16", who);
+    return check_hip(phi_dev::launch_gelu((hipStream_t)stream, x, x_dtype == PHI_BF16, y, y_dtype == PHI_BF16, n), who);
+}
+
+}  // extern "C"

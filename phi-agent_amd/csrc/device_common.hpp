@@ -1,0 +1,84 @@
+// Device helpers shared by the gfx950 kernels of the quantized linear.
+//
+// Everything here is exact integer / IEEE arithmetic: the kernels are built
+// with -ffp-contract=off, so a product is never fused into a following add
+// unless the code says fmaf().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace phi_dev {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// bf16 bits -> fp32, exact.
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits by the integer carry rule: add 0x7fff plus the kept lsb and
+// keep the top half.  This is round-to-nearest-even for every finite value and
+// is the reference's conversion bit for bit (core/util/media_common.cpp:187-193).
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t b = __float_as_uint(f);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return b >> 16;
+}
+
+// IEEE binary16 -> fp32 (exact).
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+}
+
+// E4M3FN: bias 7, no infinity, S.1111.111 is NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+    const uint32_t s = (b >> 7) & 1u, e = (b >> 3) & 15u, m = b & 7u;
+    float v;
+    if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);
+    else if (e == 0u) v = (float)m * 0x1p-9f;
+    else v = (float)(8u + m) * __uint_as_float((e - 10u + 127u) << 23);
+    return s ? -v : v;
+}
+
+// E5M2: bias 15, IEEE-shaped.
+__device__ __forceinline__ float e5m2_to_f32(uint32_t b) {
+    const uint32_t s = (b >> 7) & 1u, e = (b >> 2) & 31u, m = b & 3u;
+    float v;
+    if (e == 31u) v = m == 0u ? __uint_as_float(0x7f800000u) : __uint_as_float(0x7fc00000u);
+    else if (e == 0u) v = (float)m * 0x1p-16f;
+    else v = (float)(4u + m) * __uint_as_float((e - 17u + 127u) << 23);
+    return s ? -v : v;
+}
+
+// Nearest integer to d, ties away from zero, exactly: d - trunc(d) is exact in
+// fp32, so the tie test sees the true fraction.  Equal to the reference's
+// (long)((double)d +- 0.5) for every fp32 d (core/host/quant.cpp:163-166).
+__device__ __forceinline__ float round_half_away(float d) {
+    const float t = truncf(d);
+    const float frac = d - t;
+    return fabsf(frac) >= 0.5f ? t + copysignf(1.0f, d) : t;
+}
+
+// v * inv onto the integer grid, clamped to +-qmax (qmax integral).
+__device__ __forceinline__ int quant_code(float v, float inv, float qmax, int half_even) {
+    const float d = v * inv;
+    float r = half_even ? rintf(d) : round_half_away(d);
+    r = fminf(fmaxf(r, -qmax), qmax);
+    return (int)r;
+}
+
+// Four int codes -> one little-endian dword of int8.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return ((uint32_t)a & 0xffu) | (((uint32_t)b & 0xffu) << 8) | (((uint32_t)c & 0xffu) << 16) |
+           ((uint32_t)d << 24);
+}
+
+// Wave-wide max over 64 lanes.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace phi_dev

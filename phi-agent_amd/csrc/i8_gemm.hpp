@@ -1,0 +1,39 @@
+// Launch parameters shared by the int8 GEMM / GEMV kernels and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace phi_dev {
+
+enum CKind { C_F32 = 0, C_BF16 = 1, C_I32 = 2 };
+enum BiasKind { BIAS_NONE = 0, BIAS_F32 = 1, BIAS_BF16 = 2 };
+
+struct GemmParams {
+    const int8_t* A;
+    const int8_t* B;
+    const float* sA;
+    const float* sB;
+    const void* bias;
+    void* C;
+    int64_t lda, ldb, ldc;
+    int M, N, K;
+    int sb_scalar;
+    int bias_kind;
+    int c_kind;
+    int group_m;  // tile-rows walked together inside one XCD's range
+    // W4A8 operand (B = packed nibbles): per (row, group) 16-entry int8 table.
+    const int8_t* lut;
+    int64_t lut_groups;  // groups per row (K / group)
+    int group_shift;     // log2(group)
+};
+
+hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
+hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
+
+hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
+                               int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
+                               float qmax, int half_even, int rotate);
+size_t quant_rotate_lds_bytes(int64_t K);
+
+}  // namespace phi_dev

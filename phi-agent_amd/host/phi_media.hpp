@@ -1,0 +1,161 @@
+// C++ host layer over the C ABI, keeping the reference's quantized-linear call
+// surface so its callers (the DiT blocks' quant_gemm, the node graph) can drop
+// it in:
+//
+//   QuantLinear / linear_gemm          core/models/model_common.hpp:37-49, :172-173
+//   Int8GemmArgs / dispatch_int8_gemm  core/runtime/compute.hpp:176-198
+//   QuantConvrotArgs / dispatch_quant_convrot  core/runtime/compute.hpp:200-217
+//   W4a8ExpandArgs / dispatch_w4a8_expand      core/kernels/w4a8_expand.hpp:65-120
+//   GpuBuffer / GpuAlloc               core/runtime/cuda_device.hpp:28-33, sched.hpp:27-32
+//   MediaError                         core/util/media_common.hpp:28-30
+//
+// Buffers are caller-owned (base + byte offset), dispatches enqueue on the
+// context's one stream and nothing synchronises until submit(), as in the
+// reference (core/runtime/compute.cpp:434-490).  A failing call throws
+// MediaError with the library's message; a device fault marks the context lost.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace phi::media {
+
+using i64 = int64_t;
+using u8 = uint8_t;
+using u32 = uint32_t;
+using u64 = uint64_t;
+
+struct MediaError : std::runtime_error {
+    explicit MediaError(const std::string& what) : std::runtime_error(what) {}
+};
+
+enum class DType { Unknown, F32, F16, BF16, I8, U8, I4, F8_E4M3, F8_E5M2 };
+
+// A device allocation: a plain address and its size.
+struct GpuBuffer {
+    uintptr_t base = 0;
+    u64 bytes = 0;
+};
+
+struct GpuAlloc {
+    GpuBuffer* res = nullptr;
+    u64 off = 0;
+    u64 bytes = 0;
+    explicit operator bool() const { return res != nullptr; }
+};
+
+// One device, one stream.  begin()/submit() bracket a batch of dispatches;
+// submit() is the fence.
+class ComputeContext {
+public:
+    explicit ComputeContext(int device = 0);
+    ~ComputeContext();
+    ComputeContext(const ComputeContext&) = delete;
+    ComputeContext& operator=(const ComputeContext&) = delete;
+
+    void begin() {}
+    void submit();
+    bool lost() const { return lost_; }
+    hipStream_t stream() const { return stream_; }
+    int device() const { return device_; }
+
+    GpuBuffer* create_device_buffer(u64 bytes);
+    void release_buffer(GpuBuffer* b);
+    void upload(GpuBuffer* dst, const void* src, u64 bytes, u64 dst_off = 0);
+    void download(GpuBuffer* src, void* dst, u64 bytes, u64 src_off = 0);
+
+    // Converts a library status into MediaError (and device-lost state).
+    void check(int status, const char* what);
+
+private:
+    int device_ = 0;
+    hipStream_t stream_ = nullptr;
+    bool lost_ = false;
+};
+
+struct Int8GemmArgs {
+    GpuBuffer* a = nullptr;  // [M,K] int8
+    u64 a_offset = 0;
+    GpuBuffer* b = nullptr;  // [N,K] int8
+    u64 b_offset = 0;
+    GpuBuffer* sa = nullptr;  // [M] fp32
+    u64 sa_offset = 0;
+    GpuBuffer* sb = nullptr;  // [N] fp32 (or [1] with sb_scalar)
+    u64 sb_offset = 0;
+    GpuBuffer* c = nullptr;  // [M,N] of c_dtype
+    u64 c_offset = 0;
+    GpuBuffer* bias = nullptr;  // optional [N] of bias_dtype
+    u64 bias_offset = 0;
+    i64 M = 0, N = 0, K = 0;
+    // Extensions over the reference surface (defaults keep its behaviour).
+    DType c_dtype = DType::F32;
+    DType bias_dtype = DType::F32;
+    bool sb_scalar = false;
+};
+
+void dispatch_int8_gemm(ComputeContext& ctx, const Int8GemmArgs& args);
+
+struct QuantConvrotArgs {
+    GpuBuffer* x = nullptr;  // [rows,K] fp32 (or bf16 with x_dtype)
+    u64 x_offset = 0;
+    GpuBuffer* q = nullptr;  // [rows,K] int8 out
+    u64 q_offset = 0;
+    GpuBuffer* s = nullptr;  // [rows] fp32 out
+    u64 s_offset = 0;
+    i64 rows = 0, K = 0;
+    float qmax = 127.0f;
+    DType x_dtype = DType::F32;
+    bool round_half_even = false;
+};
+
+void dispatch_quant_convrot(ComputeContext& ctx, const QuantConvrotArgs& args);
+
+enum class RelDType : int { F32 = 0, F16 = 1, BF16 = 2, F8_E4M3 = 3, F8_E5M2 = 4, U8_E4M3 = 5 };
+enum class CodeLayout : int { Nibble4 = 0, Packed6 = 1 };
+
+struct W4a8ExpandArgs {
+    GpuBuffer* pool = nullptr;
+    u64 codes_off = 0;
+    u64 srel_off = 0;
+    u64 sch_off = 0;
+    u64 cb_off = 0;
+    GpuBuffer* q = nullptr;
+    u64 q_off = 0;
+    GpuBuffer* s = nullptr;
+    u64 s_off = 0;
+    i64 rows = 0;
+    i64 k = 0;
+    i64 group = 0;
+    i64 codes_row_bytes = 0;
+    i64 srel_row_bytes = 0;
+    RelDType rel_dtype = RelDType::F8_E4M3;
+    CodeLayout layout = CodeLayout::Nibble4;
+    bool has_channel_scale = false;
+    bool has_codebook = false;
+};
+
+void dispatch_w4a8_expand(ComputeContext& ctx, const W4a8ExpandArgs& args);
+
+// One linear weight in the int8 form the GEMM reads.
+struct QuantLinear {
+    GpuAlloc w;      // [n,k] int8
+    GpuAlloc scale;  // [n] fp32
+    GpuAlloc d;      // dense float storage (not served by this library)
+    DType dtype = DType::Unknown;
+    i64 n = 0, k = 0;
+    bool dense() const { return dtype == DType::F16 || dtype == DType::BF16 || dtype == DType::F32; }
+};
+
+struct GpuCtx {
+    ComputeContext* ctx = nullptr;
+    bool ok() const { return ctx != nullptr; }
+};
+
+// rotate+quantise x into q8/s8, then the int8 GEMM; out is [m, n] fp32.
+void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 k,
+                 const GpuAlloc& out, const GpuAlloc& q8, const GpuAlloc& s8);
+
+}  // namespace phi::media

@@ -1,0 +1,284 @@
+"""Python front end of the gfx950 quantized-linear library.
+
+Thin ctypes bindings over the C ABI in ``include/phi_qlinear.h``
+(``lib/libphi_qlinear.so``).  PyTorch provides device memory and the stream;
+every computation runs in the HIP kernels.  There is no fallback: if the
+library is missing or the device is absent the calls raise.
+
+Names and argument meaning follow the reference's dispatchers:
+``quant_rotate`` is ``dispatch_quant_convrot`` (core/runtime/compute.cpp:663-684),
+``i8_gemm`` is ``dispatch_int8_gemm`` (:551-661), ``q8_linear`` is
+``linear_gemm``'s int8 branch (core/models/model_common.cpp:1363-1412) and
+``w4a8_expand`` is ``dispatch_w4a8_expand`` (core/kernels/w4a8_expand.cpp:263-303).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(os.path.dirname(PKG_DIR), "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libphi_qlinear.so")
+MEDIA_LIB_PATH = os.path.join(LIB_DIR, "libphi_media.so")
+INCLUDE_DIR = os.path.join(os.path.dirname(os.path.dirname(PKG_DIR)), "include")
+
+# phi_dtype
+F32, BF16, F16, I32, I8, F8_E4M3, F8_E5M2, U8_E4M3 = range(8)
+# phi_round
+ROUND_HALF_AWAY, ROUND_HALF_EVEN = 0, 1
+# phi_status
+STATUS = {0: "PHI_OK", 1: "PHI_ERR_ARG", 2: "PHI_ERR_SHAPE", 3: "PHI_ERR_ALIGN",
+          4: "PHI_ERR_WORKSPACE", 5: "PHI_ERR_HIP", 6: "PHI_ERR_DEVICE_LOST",
+          7: "PHI_ERR_UNSUPPORTED"}
+
+
+class QLinearError(RuntimeError):
+    """A failing library call: ``status`` is the phi_status, the message is the
+    library's own (the reference raises MediaError with the same text)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+class W4a8Weight(ctypes.Structure):
+    _fields_ = [("codes", ctypes.c_void_p), ("codes_row_bytes", ctypes.c_int64),
+                ("s_rel", ctypes.c_void_p), ("s_rel_dtype", ctypes.c_int),
+                ("srel_row_bytes", ctypes.c_int64), ("s_channel", ctypes.c_void_p),
+                ("sch_scalar", ctypes.c_int), ("codebook", ctypes.c_void_p),
+                ("correction", ctypes.c_void_p), ("rows", ctypes.c_int64),
+                ("k", ctypes.c_int64), ("group", ctypes.c_int64), ("layout", ctypes.c_int)]
+
+
+class GemvItem(ctypes.Structure):
+    _fields_ = [("W", ctypes.c_void_p), ("sW", ctypes.c_void_p), ("sw_scalar", ctypes.c_int),
+                ("bias", ctypes.c_void_p), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64)]
+
+
+EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", "phi_hip_i8_gemm",
+           "phi_hip_workspace_bytes", "phi_hip_q8_linear", "phi_hip_w4a8_expand",
+           "phi_hip_w4a8_prepare", "phi_hip_w4a8_linear", "phi_hip_i8_gemv_batched",
+           "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh"]
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load lib/libphi_qlinear.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: run __graft_entry__.build() (make -C phi-agent_amd)")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I64, I, F, SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    L.phi_hip_last_error.restype = ctypes.c_char_p
+    L.phi_hip_abi_version.restype = I
+    L.phi_hip_quant_rotate.argtypes = [P, P, I, I64, I64, I64, P, I64, P, F, I, I]
+    L.phi_hip_i8_gemm.argtypes = [P, P, I64, P, I64, P, P, I, P, I, P, I, I64, I64, I64, I64, P, SZ]
+    L.phi_hip_workspace_bytes.argtypes = [I64, I64, I64]
+    L.phi_hip_workspace_bytes.restype = SZ
+    L.phi_hip_q8_linear.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, P, P,
+                                    I, P, SZ]
+    L.phi_hip_w4a8_expand.argtypes = [P, ctypes.POINTER(W4a8Weight), P, P]
+    L.phi_hip_w4a8_prepare.argtypes = [P, ctypes.POINTER(W4a8Weight), P, P]
+    L.phi_hip_w4a8_linear.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I64, P, P, I, I64, P, I,
+                                      I64, P, P, I, P, SZ]
+    L.phi_hip_i8_gemv_batched.argtypes = [P, P, P, I64, I64, I64, ctypes.POINTER(GemvItem), I, I,
+                                          I, P, SZ]
+    L.phi_hip_gemv_workspace_bytes.argtypes = [I]
+    L.phi_hip_gemv_workspace_bytes.restype = SZ
+    L.phi_hip_gelu_tanh.argtypes = [P, P, I, P, I, I64]
+    for name in EXPORTS:
+        f = getattr(L, name)
+        if f.restype is None:
+            f.restype = I
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return load().phi_hip_last_error().decode()
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise QLinearError(status, last_error())
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _dt(t: torch.Tensor) -> int:
+    return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32,
+            torch.int8: I8}[t.dtype]
+
+
+def _require_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("phi_qlinear operates on device tensors")
+
+
+# ---------------------------------------------------------------- A1-A3
+def quant_rotate(x: torch.Tensor, *, qmax: float = 127.0, round_mode: int = ROUND_HALF_AWAY,
+                 rotate: bool = True, q: torch.Tensor | None = None,
+                 s: torch.Tensor | None = None, stream=None):
+    """Rotate (256-wide convrot) and quantise rows of x [rows, K] (f32/bf16).
+
+    Returns (q int8 [rows, K], s f32 [rows])."""
+    _require_device(x)
+    rows, K = x.shape
+    if q is None:
+        q = torch.empty((rows, K), dtype=torch.int8, device=x.device)
+    if s is None:
+        s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    _check(load().phi_hip_quant_rotate(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0),
+                                       _ptr(q), q.stride(0), _ptr(s), float(qmax), round_mode,
+                                       1 if rotate else 0))
+    return q, s
+
+
+# ---------------------------------------------------------------- A4-A6
+def i8_gemm(A: torch.Tensor, B: torch.Tensor, sA: torch.Tensor | None, sB: torch.Tensor | None,
+            bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
+            C: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """C = fma((float)(A . B^T) * sA, sB, bias) in out_dtype (int32: raw acc)."""
+    _require_device(A, B, sA, sB, bias, C)
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=A.device)
+    sb_scalar = 1 if (sB is not None and sB.numel() == 1) else 0
+    _check(load().phi_hip_i8_gemm(_stream(stream), _ptr(A), A.stride(0), _ptr(B), B.stride(0),
+                                  _ptr(sA), _ptr(sB), sb_scalar, _ptr(bias),
+                                  _dt(bias) if bias is not None else F32, _ptr(C), _dt(C),
+                                  C.stride(0), M, N, K, None, 0))
+    return C
+
+
+def q8_linear(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
+              bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
+              q8: torch.Tensor | None = None, s8: torch.Tensor | None = None,
+              C: torch.Tensor | None = None, round_mode: int = ROUND_HALF_AWAY,
+              stream=None) -> torch.Tensor:
+    """The W8A8 linear: rotate+quantise x into q8/s8, int8 GEMM, epilogue."""
+    _require_device(x, W, sW, bias, q8, s8, C)
+    M, K = x.shape
+    N = W.shape[0]
+    if q8 is None:
+        q8 = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if s8 is None:
+        s8 = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    _check(load().phi_hip_q8_linear(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(W),
+                                    W.stride(0), _ptr(sW), 1 if sW.numel() == 1 else 0,
+                                    _ptr(bias), _dt(bias) if bias is not None else F32, N,
+                                    _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8), round_mode,
+                                    None, 0))
+    return C
+
+
+# ---------------------------------------------------------------- A7
+def _w4a8_desc(codes, s_rel, s_rel_dtype, s_channel, codebook, correction, k, group, layout):
+    _require_device(codes, s_rel, s_channel, codebook, correction)
+    w = W4a8Weight()
+    w.codes = codes.data_ptr()
+    w.codes_row_bytes = codes.stride(0)
+    w.s_rel = s_rel.data_ptr() if s_rel is not None else None
+    w.s_rel_dtype = s_rel_dtype
+    w.srel_row_bytes = (s_rel.stride(0) * s_rel.element_size()) if s_rel is not None else 0
+    w.s_channel = s_channel.data_ptr() if s_channel is not None else None
+    w.sch_scalar = 1 if (s_channel is not None and s_channel.numel() == 1) else 0
+    w.codebook = codebook.data_ptr() if codebook is not None else None
+    w.correction = correction.data_ptr() if correction is not None else None
+    w.rows = codes.shape[0]
+    w.k = k
+    w.group = group
+    w.layout = layout
+    return w
+
+
+def w4a8_expand(codes, s_rel, s_rel_dtype, s_channel=None, *, k, group, codebook=None,
+                correction=None, layout=0, stream=None):
+    """Decode a grouped 4-bit / 6-bit weight to (q int8 [N, k], s f32 [N])."""
+    w = _w4a8_desc(codes, s_rel, s_rel_dtype, s_channel, codebook, correction, k, group, layout)
+    q = torch.empty((w.rows, k), dtype=torch.int8, device=codes.device)
+    s = torch.empty((w.rows,), dtype=torch.float32, device=codes.device)
+    _check(load().phi_hip_w4a8_expand(_stream(stream), ctypes.byref(w), _ptr(q), _ptr(s)))
+    return q, s
+
+
+def w4a8_prepare(codes, s_rel, s_rel_dtype, s_channel=None, *, k, group, codebook=None,
+                 correction=None, stream=None):
+    """Per-(row, group) 16-entry int8 tables + row scales for the in-register GEMM."""
+    w = _w4a8_desc(codes, s_rel, s_rel_dtype, s_channel, codebook, correction, k, group, 0)
+    lut = torch.empty((w.rows, k // group, 16), dtype=torch.int8, device=codes.device)
+    s = torch.empty((w.rows,), dtype=torch.float32, device=codes.device)
+    _check(load().phi_hip_w4a8_prepare(_stream(stream), ctypes.byref(w), _ptr(lut), _ptr(s)))
+    return lut, s
+
+
+def w4a8_linear(x, codes, lut, s_w, *, group, bias=None, out_dtype=torch.bfloat16, q8=None,
+                s8=None, C=None, round_mode=ROUND_HALF_AWAY, stream=None):
+    _require_device(x, codes, lut, s_w, bias, q8, s8, C)
+    M, K = x.shape
+    N = codes.shape[0]
+    if q8 is None:
+        q8 = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if s8 is None:
+        s8 = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    _check(load().phi_hip_w4a8_linear(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K,
+                                      _ptr(codes), codes.stride(0), _ptr(lut), group, _ptr(s_w),
+                                      _ptr(bias), _dt(bias) if bias is not None else F32, N,
+                                      _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8),
+                                      round_mode, None, 0))
+    return C
+
+
+# ---------------------------------------------------------------- GEMV
+def gemv_batched(q8: torch.Tensor, s8: torch.Tensor, weights, scales, *, biases=None,
+                 outs=None, out_dtype=torch.bfloat16, stream=None):
+    """C_i = epilogue(q8 . W_i^T) for every weight (M = q8.shape[0] <= 8)."""
+    _require_device(q8, s8)
+    M, K = q8.shape
+    N = weights[0].shape[0]
+    n = len(weights)
+    if outs is None:
+        outs = [torch.empty((M, N), dtype=out_dtype, device=q8.device) for _ in range(n)]
+    items = (GemvItem * n)()
+    bias_dt = F32
+    for i in range(n):
+        items[i].W = weights[i].data_ptr()
+        items[i].sW = scales[i].data_ptr() if scales is not None else None
+        items[i].sw_scalar = 1 if (scales is not None and scales[i].numel() == 1) else 0
+        b = biases[i] if biases is not None else None
+        if b is not None:
+            bias_dt = _dt(b)
+        items[i].bias = b.data_ptr() if b is not None else None
+        items[i].C = outs[i].data_ptr()
+        items[i].ldc = outs[i].stride(0)
+    _check(load().phi_hip_i8_gemv_batched(_stream(stream), _ptr(q8), _ptr(s8), M, K, N, items, n,
+                                          bias_dt, _dt(outs[0]), None, 0))
+    return outs
+
+
+def gelu_tanh(x: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    _require_device(x, out)
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load().phi_hip_gelu_tanh(_stream(stream), _ptr(x), _dt(x), _ptr(out), _dt(out),
+                                    x.numel()))
+    return out

@@ -1,0 +1,188 @@
+// Test program for the C++ host layer (phi-agent_amd/host/phi_media.hpp), the
+// drop-in for the reference's dispatch surface.  It mirrors the reference's own
+// in-binary gates (core/bench/media_bench.cpp:110-279: upload, dispatch,
+// submit, download, compare with the host arithmetic), but every comparison
+// here is bit-exact against the oracle (oracle/oracle.h).  Exit code 0 = pass.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "oracle.h"
+#include "phi_media.hpp"
+
+using namespace phi::media;
+
+static int failures = 0;
+#define CHECK(cond, ...)                       \
+    do {                                       \
+        if (!(cond)) {                         \
+            printf("FAIL %s:%d ", __FILE__, __LINE__); \
+            printf(__VA_ARGS__);               \
+            printf("\n");                      \
+            failures++;                        \
+        }                                      \
+    } while (0)
+
+static void test_linear_gemm(ComputeContext& ctx) {
+    const i64 m = 67, k = 1024, n = 320;
+    std::mt19937 rng(7);
+    std::normal_distribution<float> nd(0.0f, 2.0f);
+    std::uniform_int_distribution<int> ud(-127, 127);
+    std::uniform_real_distribution<float> us(0.001f, 0.01f);
+    std::vector<float> x(m * k), sw(n);
+    std::vector<int8_t> w(n * k);
+    for (auto& v : x) v = nd(rng);
+    for (auto& v : w) v = (int8_t)ud(rng);
+    for (auto& v : sw) v = us(rng);
+
+    // One arena-like buffer carved into sub-allocations, as GpuArena hands out.
+    const u64 off_x = 0, off_w = off_x + m * k * 4, off_s = off_w + n * k, off_q8 = off_s + 4096,
+              off_s8 = off_q8 + m * k, off_y = off_s8 + 4096;
+    GpuBuffer* pool = ctx.create_device_buffer(off_y + m * n * 4);
+    ctx.upload(pool, x.data(), m * k * 4, off_x);
+    ctx.upload(pool, w.data(), n * k, off_w);
+    ctx.upload(pool, sw.data(), n * 4, off_s);
+
+    GpuCtx g;
+    g.ctx = &ctx;
+    QuantLinear ql;
+    ql.w = GpuAlloc{pool, off_w, (u64)(n * k)};
+    ql.scale = GpuAlloc{pool, off_s, (u64)(n * 4)};
+    ql.n = n;
+    ql.k = k;
+    ctx.begin();
+    linear_gemm(g, ql, GpuAlloc{pool, off_x, (u64)(m * k * 4)}, m, k, GpuAlloc{pool, off_y, (u64)(m * n * 4)},
+                GpuAlloc{pool, off_q8, (u64)(m * k)}, GpuAlloc{pool, off_s8, (u64)(m * 4)});
+    ctx.submit();
+
+    std::vector<float> y(m * n), s8(m);
+    std::vector<int8_t> q8(m * k);
+    ctx.download(pool, y.data(), m * n * 4, off_y);
+    ctx.download(pool, q8.data(), m * k, off_q8);
+    ctx.download(pool, s8.data(), m * 4, off_s8);
+
+    std::vector<float> yo(m * n), so(m);
+    std::vector<int8_t> qo(m * k);
+    orc_q8_linear(x.data(), ORC_F32, m, k, w.data(), sw.data(), 0, nullptr, -1, n, ORC_ROUND_HALF_AWAY,
+                  yo.data(), ORC_F32, qo.data(), so.data(), nullptr);
+    CHECK(memcmp(q8.data(), qo.data(), q8.size()) == 0, "linear_gemm: int8 activations differ");
+    CHECK(memcmp(s8.data(), so.data(), s8.size() * 4) == 0, "linear_gemm: activation scales differ");
+    CHECK(memcmp(y.data(), yo.data(), y.size() * 4) == 0, "linear_gemm: fp32 outputs differ");
+    ctx.release_buffer(pool);
+    printf("linear_gemm %lldx%lldx%lld: %s\n", (long long)m, (long long)n, (long long)k,
+           failures ? "mismatch" : "bit-exact");
+}
+
+static void test_w4a8_expand(ComputeContext& ctx) {
+    const i64 rows = 48, k = 512, group = 64, groups = k / group;
+    std::mt19937 rng(3);
+    std::uniform_int_distribution<int> ub(0, 255);
+    std::uniform_real_distribution<float> ur(0.5f, 20.0f), uc(0.001f, 0.01f);
+    std::vector<uint8_t> codes(rows * k / 2);
+    for (auto& v : codes) v = (uint8_t)ub(rng);
+    std::vector<uint16_t> srel(rows * groups);  // fp16 relative scales
+    for (auto& v : srel) {
+        const float f = ur(rng);
+        uint32_t b;
+        memcpy(&b, &f, 4);
+        const int e = (int)((b >> 23) & 255) - 127 + 15;
+        v = (uint16_t)((e << 10) | ((b >> 13) & 0x3ff));  // truncation onto fp16 (values are exact)
+    }
+    std::vector<float> sch(rows), cb(16);
+    for (auto& v : sch) v = uc(rng);
+    for (int i = 0; i < 16; i++) cb[i] = (float)(i - 8) * 0.75f + 0.125f;
+
+    const u64 o_codes = 0, o_srel = 256 * ((codes.size() + 255) / 256),
+              o_sch = o_srel + 256 * ((srel.size() * 2 + 255) / 256), o_cb = o_sch + 256 * ((rows * 4 + 255) / 256),
+              o_q = o_cb + 256, o_s = o_q + rows * k;
+    GpuBuffer* pool = ctx.create_device_buffer(o_s + rows * 4);
+    ctx.upload(pool, codes.data(), codes.size(), o_codes);
+    ctx.upload(pool, srel.data(), srel.size() * 2, o_srel);
+    ctx.upload(pool, sch.data(), rows * 4, o_sch);
+    ctx.upload(pool, cb.data(), 64, o_cb);
+    W4a8ExpandArgs a;
+    a.pool = pool;
+    a.codes_off = o_codes;
+    a.srel_off = o_srel;
+    a.sch_off = o_sch;
+    a.cb_off = o_cb;
+    a.q = pool;
+    a.q_off = o_q;
+    a.s = pool;
+    a.s_off = o_s;
+    a.rows = rows;
+    a.k = k;
+    a.group = group;
+    a.codes_row_bytes = k / 2;
+    a.srel_row_bytes = groups * 2;
+    a.rel_dtype = RelDType::F16;
+    a.layout = CodeLayout::Nibble4;
+    a.has_channel_scale = true;
+    a.has_codebook = true;
+    dispatch_w4a8_expand(ctx, a);
+    ctx.submit();
+    std::vector<int8_t> q(rows * k), qo(rows * k);
+    std::vector<float> s(rows), so(rows);
+    ctx.download(pool, q.data(), q.size(), o_q);
+    ctx.download(pool, s.data(), rows * 4, o_s);
+    orc_w4a8_expand(codes.data(), k / 2, srel.data(), ORC_F16, groups * 2, sch.data(), 0, cb.data(), nullptr, rows, k,
+                    group, 0, qo.data(), so.data(), nullptr);
+    const int before = failures;
+    CHECK(memcmp(q.data(), qo.data(), q.size()) == 0, "w4a8_expand: codes differ");
+    CHECK(memcmp(s.data(), so.data(), s.size() * 4) == 0, "w4a8_expand: row scales differ");
+    ctx.release_buffer(pool);
+    printf("w4a8_expand %lldx%lld (fp16 s_rel, codebook): %s\n", (long long)rows, (long long)k,
+           failures == before ? "bit-exact" : "mismatch");
+}
+
+static void test_errors(ComputeContext& ctx) {
+    bool threw = false;
+    try {
+        QuantConvrotArgs qa;
+        GpuBuffer dummy{0x1000, 0};
+        qa.x = qa.q = qa.s = &dummy;
+        qa.rows = 4;
+        qa.K = 300;
+        dispatch_quant_convrot(ctx, qa);
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "not a multiple of 256") != nullptr;
+    }
+    CHECK(threw, "quant_convrot K=300 must throw MediaError");
+    threw = false;
+    try {
+        Int8GemmArgs ga;
+        dispatch_int8_gemm(ctx, ga);
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "empty problem") != nullptr;
+    }
+    CHECK(threw, "int8_gemm M=0 must throw MediaError");
+    threw = false;
+    try {
+        GpuCtx g;
+        g.ctx = &ctx;
+        QuantLinear ql;
+        ql.k = 512;
+        GpuAlloc none;
+        linear_gemm(g, ql, none, 1, 256, none, none, none);
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "K mismatch") != nullptr;
+    }
+    CHECK(threw, "linear_gemm K mismatch must throw MediaError");
+    printf("error contract: %s\n", failures ? "mismatch" : "ok");
+}
+
+int main() {
+    try {
+        ComputeContext ctx(0);
+        test_errors(ctx);
+        test_linear_gemm(ctx);
+        test_w4a8_expand(ctx);
+    } catch (const std::exception& e) {
+        printf("FAIL exception: %s\n", e.what());
+        return 1;
+    }
+    printf("%s (%d failures)\n", failures ? "FAILED" : "PASSED", failures);
+    return failures ? 1 : 0;
+}

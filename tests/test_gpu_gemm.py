@@ -1,0 +1,138 @@
+"""GPU parity: int8 MFMA GEMM + epilogue (phi_hip_i8_gemm) vs the oracle.
+
+Bar: int32 accumulators bit-exact; fp32 / bf16 outputs bit-exact against the
+oracle's epilogue fma((float)acc*sa, sb, bias) (reference
+core/kernels/int8_gemm.cpp:588-620), and within 1 bf16 ulp of the separately
+rounded form (the tolerance stated for floating point, rel <= 8e-3).
+At full benchmark sizes the int32 product is checked by row/column checksums
+(sum_n C = A . sum_n B, sum_m C = (sum_m A) . B), exact in float64."""
+import numpy as np
+import pytest
+import torch
+
+import phi_qlinear as Q
+from phi_qlinear import synth
+
+pytestmark = pytest.mark.gpu
+
+BF16_REL_TOL = 8e-3  # 1 bf16 ulp (2^-7), as stated for the bf16 outputs
+
+
+def u16(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def rand_i8(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 64), (1, 37, 128), (5, 300, 192), (256, 256, 3072),
+                                   (257, 129, 640), (300, 1000, 256), (512, 384, 1024),
+                                   (33, 4100, 64), (1000, 70, 576)])
+def test_int32_accumulators_exact(dev, orc, M, N, K):
+    A, B = rand_i8((M, K), M + K), rand_i8((N, K), N + 7)
+    C = Q.i8_gemm(A.to(dev), B.to(dev), None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    want = orc.gemm_i8_i32_fast(A.numpy(), B.numpy())
+    assert np.array_equal(C.cpu().numpy(), want)
+
+
+def test_extreme_accumulators(dev, orc):
+    """All +-127 at K = 12288: |acc| = 1.98e8 > 2^24, so (float)acc rounds."""
+    M, N, K = 64, 128, 12288
+    A = torch.full((M, K), 127, dtype=torch.int8)
+    A[1::2] = -127
+    B = torch.full((N, K), 127, dtype=torch.int8)
+    B[:, ::3] = -127
+    sa = torch.rand(M) * 0.01 + 0.001
+    sb = torch.rand(N) * 0.01 + 0.001
+    C32 = Q.i8_gemm(A.to(dev), B.to(dev), None, None, out_dtype=torch.int32).cpu().numpy()
+    acc = orc.gemm_i8_i32_fast(A.numpy(), B.numpy())
+    assert np.array_equal(C32, acc)
+    Cf = Q.i8_gemm(A.to(dev), B.to(dev), sa.to(dev), sb.to(dev), out_dtype=torch.float32)
+    want = orc.epilogue(acc, sa.numpy(), sb.numpy(), out="f32")
+    assert np.array_equal(Cf.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("bias_kind", [None, "f32", "bf16"])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+@pytest.mark.parametrize("sb_scalar", [True, False])
+def test_epilogue_bit_exact(dev, orc, bias_kind, out, sb_scalar):
+    M, N, K = 130, 260, 384
+    A, B = rand_i8((M, K), 3), rand_i8((N, K), 4)
+    g = torch.Generator().manual_seed(9)
+    sa = torch.rand(M, generator=g) * 0.05 + 0.002
+    sb = torch.full((1,), 0.002) if sb_scalar else torch.rand(N, generator=g) * 0.05 + 0.002
+    bias = None
+    if bias_kind == "f32":
+        bias = torch.randn(N, generator=g) * 0.02
+    elif bias_kind == "bf16":
+        bias = (torch.randn(N, generator=g) * 0.02).to(torch.bfloat16)
+    C = Q.i8_gemm(A.to(dev), B.to(dev), sa.to(dev), sb.to(dev),
+                  None if bias is None else bias.to(dev),
+                  out_dtype=torch.bfloat16 if out == "bf16" else torch.float32)
+    acc = orc.gemm_i8_i32_fast(A.numpy(), B.numpy())
+    b_np = None if bias is None else (u16(bias) if bias.dtype == torch.bfloat16 else bias.numpy())
+    want = orc.epilogue(acc, sa.numpy(), sb.numpy(), b_np, out=out)
+    got = u16(C) if out == "bf16" else C.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, want if out == "bf16" else want.view(np.uint32))
+    if out == "bf16" and bias is not None:
+        # vs the separately rounded epilogue: within one bf16 ulp
+        alt = orc.bf16_to_f32(orc.epilogue(acc, sa.numpy(), sb.numpy(), b_np, out="bf16", fused=False))
+        g32 = orc.bf16_to_f32(got)
+        np.testing.assert_allclose(g32, alt, rtol=BF16_REL_TOL, atol=1e-30)
+
+
+def test_reference_gemm_int8_equality(dev, orc):
+    """No bias, fp32 out: the product equals the reference host gemm_int8's
+    (float)acc * sx[m] * sw[n] (core/host/quant.cpp:223-236) bit for bit."""
+    if not orc.ref_available():
+        pytest.skip("reference build (oracle/_ref) not present on this machine")
+    M, N, K = 64, 96, 512
+    A, B = rand_i8((M, K), 21), rand_i8((N, K), 22)
+    sa = torch.rand(M) * 0.01 + 0.001
+    sb = torch.rand(N) * 0.01 + 0.001
+    C = Q.i8_gemm(A.to(dev), B.to(dev), sa.to(dev), sb.to(dev), out_dtype=torch.float32)
+    want = orc.ref_gemm(A.numpy(), sa.numpy(), B.numpy(), sb.numpy())
+    assert np.array_equal(C.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def checksums_ok(A, B, C32):
+    """Exact ABFT identities in float64 on the device."""
+    Af, Bf, Cf = A.double(), B.double(), C32.double()
+    row_ok = torch.equal(Cf.sum(1), Af @ Bf.sum(0))
+    col_ok = torch.equal(Cf.sum(0), Bf @ Af.sum(0))
+    return row_ok and col_ok
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4352, 3072, 12288), (4352, 9216, 3072),
+                                   (32760, 5120, 5120)])
+def test_full_size_checksums(dev, M, N, K):
+    A = synth.int8_weight(M, K, seed=M, device=dev)
+    B = synth.int8_weight(N, K, seed=N, device=dev)
+    C32 = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert checksums_ok(A, B, C32)
+    # A sampled block against an independent exact product.
+    rs = torch.arange(0, M, 97, device=dev)[:64]
+    cs = torch.arange(0, N, 89, device=dev)[:64]
+    blk = (A[rs].double() @ B[cs].double().t()).to(torch.int64)
+    assert torch.equal(C32[rs][:, cs].to(torch.int64), blk)
+    # bf16 epilogue at full size: same accumulators through the scaled store.
+    sa = torch.rand(M, device=dev) * 0.01 + 1e-3
+    sb = torch.full((1,), 0.002, device=dev)
+    Cb = Q.i8_gemm(A, B, sa, sb, out_dtype=torch.bfloat16)
+    want = (C32.float() * sa[:, None] * sb).to(torch.bfloat16)
+    assert torch.equal(Cb.view(torch.int16), want.view(torch.int16))
+
+
+def test_contract_errors(dev):
+    A = torch.zeros((4, 100), dtype=torch.int8, device=dev)
+    B = torch.zeros((4, 100), dtype=torch.int8, device=dev)
+    with pytest.raises(Q.QLinearError, match="multiple of 64"):
+        Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
+    A = torch.zeros((0, 64), dtype=torch.int8, device=dev)
+    with pytest.raises(Q.QLinearError, match="empty problem"):
+        Q.i8_gemm(A, B[:, :64].contiguous(), None, None, out_dtype=torch.int32)

@@ -1,0 +1,106 @@
+"""GPU parity: rotate + per-token quantise (phi_hip_quant_rotate) vs the oracle.
+
+Bar: int8 codes and fp32 scales bit-exact (reference
+core/host/quant.cpp:109-169)."""
+import numpy as np
+import pytest
+import torch
+
+import phi_qlinear as Q
+from phi_qlinear import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits_u16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def run(dev, orc, x, **kw):
+    q, s = Q.quant_rotate(x.to(dev), **kw)
+    torch.cuda.synchronize()
+    xin = bits_u16(x) if x.dtype == torch.bfloat16 else x.numpy()
+    rot = kw.get("rotate", True)
+    qo, so = orc.quantize_rows(xin, rotate=rot, qmax=kw.get("qmax", 127.0),
+                               round_mode=kw.get("round_mode", 0))
+    return q.cpu().numpy(), s.cpu().numpy(), qo, so
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (3, 768), (256, 3072), (17, 5120), (8, 12288),
+                                 (2, 24576), (65, 1024)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rotate_quant_bit_exact(dev, orc, M, K, dtype):
+    x = synth.activations(M, K, seed=M * 131 + K, dtype=dtype)
+    q, s, qo, so = run(dev, orc, x)
+    assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+def test_c0_activation_block(dev, orc):
+    """config 0's activation: [256, 3072] bf16 with outlier channels, seed 0."""
+    x = synth.activations(256, 3072, seed=0)
+    q, s, qo, so = run(dev, orc, x)
+    assert np.array_equal(q, qo) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    assert np.abs(q).max() == 127
+
+
+@pytest.mark.parametrize("rotate", [True, False])
+@pytest.mark.parametrize("qmax", [127.0, 7.0])
+@pytest.mark.parametrize("round_mode", [Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN])
+def test_modes(dev, orc, rotate, qmax, round_mode):
+    x = synth.activations(33, 2048, seed=5, dtype=torch.float32) * 3
+    q, s, qo, so = run(dev, orc, x, rotate=rotate, qmax=qmax, round_mode=round_mode)
+    assert np.array_equal(q, qo)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+def test_exact_ties_and_the_half_boundary(dev, orc):
+    """Rows with amax 127 quantise with inv == 1, so the input is the value that
+    is rounded.  Exact .5 ties separate half-away from half-even, and
+    0.5 - 2^-25 is the fp32 value where a float d + 0.5f rounding gives 1 while
+    the reference's double rule gives 0."""
+    K = 256
+    vals = np.array([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -126.5,
+                     np.float32(0.5) - np.float32(2.0 ** -25), -(np.float32(0.5) - np.float32(2.0 ** -25)),
+                     0.49999997, 1.4999999, 127.0, -127.0, 0.0, -0.0], np.float32)
+    row = np.zeros(K, np.float32)
+    row[:vals.size] = vals
+    row[-1] = 127.0
+    x = torch.from_numpy(np.stack([row, row * 0.5]))
+    for mode in (Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN):
+        q, s, qo, so = run(dev, orc, x, rotate=False, round_mode=mode)
+        assert np.array_equal(q, qo)
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    q, _, _, _ = run(dev, orc, x, rotate=False)
+    assert list(q[0, :10]) == [1, -1, 2, -2, 3, -3, 127, -127, 0, 0]
+
+
+def test_zero_rows_and_tiny_rows(dev, orc):
+    x = torch.zeros((4, 512), dtype=torch.float32)
+    x[1, 7] = 1e-31  # amax below 1e-30 -> scale 1
+    x[2, 3] = 3e-30
+    q, s, qo, so = run(dev, orc, x)
+    assert np.array_equal(q, qo)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    assert s[0] == 1.0 and not q[0].any()
+
+
+def test_strided_rows_and_empty(dev, orc):
+    big = synth.activations(9, 1280, seed=11, dtype=torch.float32).to(dev)
+    x = big[:, :1024]
+    q = torch.empty((9, 1024 + 64), dtype=torch.int8, device=dev)
+    s = torch.empty((9,), dtype=torch.float32, device=dev)
+    Q.quant_rotate(x, q=q, s=s)
+    torch.cuda.synchronize()
+    qo, so = orc.quantize_rows(x.cpu().numpy())
+    assert np.array_equal(q[:, :1024].cpu().numpy(), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    e = torch.empty((0, 256), device=dev)
+    Q.quant_rotate(e)  # rows == 0 is a no-op
+
+
+def test_contract_errors(dev):
+    with pytest.raises(Q.QLinearError, match="multiple of 256"):
+        Q.quant_rotate(torch.zeros((2, 300), device=dev))
+    with pytest.raises(Q.QLinearError, match="exceeds"):
+        Q.quant_rotate(torch.zeros((1, 24576 + 256), device=dev))
