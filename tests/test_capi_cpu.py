@@ -1,0 +1,161 @@
+"""CPU checks of the C ABI boundary (no GPU needed).
+
+* libphi_qlinear.so loads and exports every function include/*.h declares;
+* libphi_media.so (the C++ host layer) loads and exports the reference-named
+  dispatch entry points;
+* contract violations are refused before any device work, with the status
+  codes and the messages the reference's dispatchers raise
+  (core/runtime/compute.cpp:552, :665-668; core/kernels/w4a8_expand.cpp:264-281).
+"""
+import ctypes
+import glob
+import os
+import re
+import subprocess
+
+import pytest
+
+import phi_qlinear as Q
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = ctypes.c_void_p(0x10000)  # a well-aligned address; never dereferenced on these paths
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(phi_hip_\w+)\s*\(", text))
+    return names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 12
+    out = subprocess.run(["nm", "-D", "--defined-only", Q.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (phi_hip_\w+)", out))
+    assert names <= exported, f"declared but not exported: {sorted(names - exported)}"
+    assert set(Q.EXPORTS) == names
+    for n in names:
+        getattr(lib, n)
+
+
+def test_abi_version(lib):
+    assert lib.phi_hip_abi_version() == 1
+
+
+def test_host_layer_library_exports_reference_names():
+    assert os.path.exists(Q.MEDIA_LIB_PATH)
+    ctypes.CDLL(Q.MEDIA_LIB_PATH)
+    out = subprocess.run(["nm", "-DC", "--defined-only", Q.MEDIA_LIB_PATH], capture_output=True,
+                         text=True).stdout
+    for name in ("phi::media::dispatch_int8_gemm", "phi::media::dispatch_quant_convrot",
+                 "phi::media::dispatch_w4a8_expand", "phi::media::linear_gemm",
+                 "phi::media::ComputeContext::submit"):
+        assert name in out, name
+
+
+def status_and_msg(lib, rc):
+    return rc, Q.last_error()
+
+
+def test_quant_rotate_contract(lib):
+    rc, msg = status_and_msg(lib, lib.phi_hip_quant_rotate(None, FAKE, Q.F32, 4, 300, 300, FAKE, 304,
+                                                           FAKE, 127.0, 0, 1))
+    assert rc == 2 and "K=300 is not a multiple of 256" in msg
+    rc, msg = status_and_msg(lib, lib.phi_hip_quant_rotate(None, FAKE, Q.F32, 4, 256, 256, FAKE, 256,
+                                                           FAKE, 127.5, 0, 1))
+    assert rc == 1 and "qmax" in msg
+    rc, msg = status_and_msg(lib, lib.phi_hip_quant_rotate(None, FAKE, Q.I8, 4, 256, 256, FAKE, 256,
+                                                           FAKE, 127.0, 0, 1))
+    assert rc == 1
+    rc, msg = status_and_msg(lib, lib.phi_hip_quant_rotate(None, ctypes.c_void_p(0x10004), Q.F32, 4,
+                                                           256, 256, FAKE, 256, FAKE, 127.0, 0, 1))
+    assert rc == 3
+    # rows == 0 is a no-op, as in dispatch_quant_convrot
+    assert lib.phi_hip_quant_rotate(None, None, Q.F32, 0, 300, 300, None, 300, None, 127.0, 0, 1) == 0
+    assert Q.last_error() == ""
+
+
+def test_gemm_contract(lib):
+    g = lib.phi_hip_i8_gemm
+    rc, msg = status_and_msg(lib, g(None, FAKE, 64, FAKE, 64, FAKE, FAKE, 0, None, 0, FAKE, Q.BF16, 64,
+                                    0, 64, 64, None, 0))
+    assert rc == 2 and "empty problem" in msg
+    rc, msg = status_and_msg(lib, g(None, FAKE, 100, FAKE, 100, FAKE, FAKE, 0, None, 0, FAKE, Q.BF16,
+                                    64, 8, 64, 100, None, 0))
+    assert rc == 2 and "multiple of 64" in msg
+    rc, msg = status_and_msg(lib, g(None, FAKE, 64, FAKE, 64, None, FAKE, 0, None, 0, FAKE, Q.BF16, 64,
+                                    8, 64, 64, None, 0))
+    assert rc == 1 and "scales" in msg
+    rc, msg = status_and_msg(lib, g(None, FAKE, 72, FAKE, 64, FAKE, FAKE, 0, None, 0, FAKE, Q.BF16, 64,
+                                    8, 64, 64, None, 0))
+    assert rc == 3
+    rc, msg = status_and_msg(lib, g(None, FAKE, 64, FAKE, 64, FAKE, FAKE, 0, FAKE, Q.I8, FAKE, Q.BF16,
+                                    64, 8, 64, 64, None, 0))
+    assert rc == 1 and "bias" in msg
+    rc, msg = status_and_msg(lib, g(None, FAKE, 64, FAKE, 64, FAKE, FAKE, 0, None, 0, FAKE, Q.F16, 64,
+                                    8, 64, 64, None, 0))
+    assert rc == 1 and "output dtype" in msg
+
+
+def test_linear_requires_activation_scratch(lib):
+    rc = lib.phi_hip_q8_linear(None, FAKE, Q.BF16, 256, 4, 256, FAKE, 256, FAKE, 1, None, 0, 64,
+                               FAKE, Q.BF16, 64, None, None, 0, None, 0)
+    assert rc == 1 and "activation scratch" in Q.last_error()
+
+
+def w4(rows=4, k=128, group=32, layout=0, crb=64, cb=None):
+    w = Q.W4a8Weight()
+    w.codes = 0x10000
+    w.codes_row_bytes = crb
+    w.s_rel = 0x20000
+    w.s_rel_dtype = Q.F32
+    w.srel_row_bytes = 4 * max(1, k // max(group, 1))
+    w.rows, w.k, w.group, w.layout = rows, k, group, layout
+    w.codebook = cb
+    return w
+
+
+def test_w4a8_contract(lib):
+    e = lib.phi_hip_w4a8_expand
+    rc = e(None, ctypes.byref(w4(k=200, group=64)), FAKE, FAKE)
+    assert rc == 2 and "K=200 is not a multiple of group=64" in Q.last_error()
+    rc = e(None, ctypes.byref(w4(k=128, group=32, crb=50)), FAKE, FAKE)
+    assert rc == 2 and "needs 64 packed bytes, got 50" in Q.last_error()
+    rc = e(None, ctypes.byref(w4(k=128, group=2, layout=1, crb=96)), FAKE, FAKE)
+    assert rc == 2 and "whole number of code groups" in Q.last_error()
+    rc = e(None, ctypes.byref(w4(k=128, group=32, layout=1, crb=96, cb=0x30000)), FAKE, FAKE)
+    assert rc == 1 and "codebook" in Q.last_error()
+    rc = lib.phi_hip_w4a8_prepare(None, ctypes.byref(w4(k=128, group=32, layout=1, crb=96)), FAKE, FAKE)
+    assert rc == 7
+    # group must be a power of two >= 64 for the in-register GEMM
+    rc = lib.phi_hip_w4a8_linear(None, FAKE, Q.BF16, 256, 4, 256, FAKE, 128, FAKE, 32, FAKE, None, 0,
+                                 64, FAKE, Q.BF16, 64, FAKE, FAKE, 0, None, 0)
+    assert rc == 2 and "group=32" in Q.last_error()
+
+
+def test_gemv_contract(lib):
+    items = (Q.GemvItem * 1)()
+    items[0].W, items[0].sW, items[0].C, items[0].ldc = 0x10000, 0x20000, 0x30000, 64
+    rc = lib.phi_hip_i8_gemv_batched(None, FAKE, FAKE, 9, 256, 64, items, 1, Q.F32, Q.BF16, None, 0)
+    assert rc == 2 and "M=9" in Q.last_error()
+    rc = lib.phi_hip_i8_gemv_batched(None, FAKE, FAKE, 1, 250, 64, items, 1, Q.F32, Q.BF16, None, 0)
+    assert rc == 2
+    items[0].ldc = 10
+    rc = lib.phi_hip_i8_gemv_batched(None, FAKE, FAKE, 1, 256, 64, items, 1, Q.F32, Q.BF16, None, 0)
+    assert rc == 2 and "ldc" in Q.last_error()
+    assert lib.phi_hip_i8_gemv_batched(None, FAKE, FAKE, 1, 256, 64, items, 0, Q.F32, Q.BF16, None, 0) == 0
+
+
+def test_workspace_queries(lib):
+    assert lib.phi_hip_workspace_bytes(4352, 12288, 3072) >= 0
+    assert lib.phi_hip_gemv_workspace_bytes(60) >= 0
+
+
+def test_binding_refuses_host_tensors():
+    import torch
+
+    with pytest.raises(ValueError):
+        Q.quant_rotate(torch.zeros((2, 256)))
