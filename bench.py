@@ -29,7 +29,7 @@ for _p in (ROOT, PKG):
 METRIC = "W8A8 linear TOPS & % int8 MFMA peak at M=4352,K=3072,N=12288"
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
-CPU_SAMPLE_ROWS = 1024    # rows of the reference CPU linear timed for the baseline
+CPU_SAMPLE_ROWS = 4352    # rows of the reference CPU linear timed for the baseline (all of c1)
 
 CONFIGS = {
     "c0": dict(kind="w8a8", M=256, K=3072, N=3072),

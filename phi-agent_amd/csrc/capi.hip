@@ -12,6 +12,8 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <string>
 
 #include "../../include/phi_qlinear.h"
@@ -104,6 +106,30 @@ int gemm_cfg_for(int64_t M, int64_t N) {
     return big >= 256 ? 0 : 1;
 }
 
+// Kernel choice for the W8A8 GEMM.  PHI_GEMM_KERNEL=tile256 / tile128 forces
+// one (an A/B switch for tests, like the reference's PHI_INT8_DP4A,
+// core/runtime/compute.cpp:566-571); otherwise the 256x256 kernel takes every
+// problem with enough tiles to occupy the GPU.
+enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1 };
+
+GemmKernel gemm_kernel_for(int64_t M, int64_t N) {
+    const char* e = getenv("PHI_GEMM_KERNEL");
+    if (e && strcmp(e, "tile256") == 0) return GK_TILE256;
+    if (e && strcmp(e, "tile128") == 0) return GK_TILE128;
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    return t256 >= 128 ? GK_TILE256 : GK_TILE128;
+}
+
+// Vector-store / vector-load eligibility of the epilogue operands.
+void set_vec_flags(phi_dev::GemmParams& p, int c_dtype, int64_t ldc) {
+    const size_t cal = c_dtype == PHI_BF16 ? 8 : 16;
+    p.c_vec = aligned(p.C, cal) && ldc % 4 == 0;
+    const bool sb_ok = p.sb_scalar || !p.sB || aligned(p.sB, 16);
+    const bool b_ok = p.bias_kind == phi_dev::BIAS_NONE ||
+                      aligned(p.bias, p.bias_kind == phi_dev::BIAS_BF16 ? 8 : 16);
+    p.s_vec = sb_ok && b_ok;
+}
+
 }  // namespace
 
 extern "C" {
@@ -172,6 +198,8 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.bias_kind = bk;
     p.c_kind = c_kind_of(c_dtype);
     p.group_m = 4;
+    set_vec_flags(p, c_dtype, ldc);
+    if (gemm_kernel_for(M, N) == GK_TILE256) return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);
     return check_hip(phi_dev::launch_i8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
 }
 

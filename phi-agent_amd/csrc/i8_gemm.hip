@@ -22,8 +22,9 @@
 //     current one is multiplied, then written to the idle stage: one barrier
 //     per K-tile.
 //   * LDS rows are 64 B (four 16-B chunks); chunk c of row r is stored at
-//     chunk c ^ ((r >> 1) & 3), so the 16-B operand reads of 8 consecutive
-//     rows hit 8 distinct bank windows.
+//     chunk c ^ (((r >> 1) ^ (r >> 2)) & 3), so the 16-B operand reads of 16
+//     consecutive rows (one LDS clock: 16 lanes x 16 B) hit 16 distinct bank
+//     windows.
 //   * Tile order: workgroup ids are dealt round-robin to the 8 XCDs; the id is
 //     first remapped so each XCD owns a contiguous run of tiles, then the run
 //     is walked GROUP_M tile-rows at a time so concurrently running tiles share
@@ -35,7 +36,7 @@ namespace phi_dev {
 
 constexpr int GEMM_BK = 64;
 
-__device__ __forceinline__ int swz(int row, int c) { return c ^ ((row >> 1) & 3); }
+__device__ __forceinline__ int swz(int row, int c) { return c ^ (((row >> 1) ^ (row >> 2)) & 3); }
 
 // Four nibbles (bits 0..15 of `nib`, column i in bits 4i..4i+3) -> four int8
 // through a 16-entry byte table held in `t` (entry c is byte c): v_perm_b32

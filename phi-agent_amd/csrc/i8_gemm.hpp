@@ -26,10 +26,13 @@ struct GemmParams {
     const int8_t* lut;
     int64_t lut_groups;  // groups per row (K / group)
     int group_shift;     // log2(group)
+    int c_vec;           // C rows allow 4-element vector stores (alignment and ldc % 4)
+    int s_vec;           // sB and bias allow 4-element vector loads (16-byte / 8-byte aligned)
 };
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
+hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
 
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,

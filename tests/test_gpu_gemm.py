@@ -27,10 +27,23 @@ def rand_i8(shape, seed):
     return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
 
 
+KERNELS = ["auto", "tile256", "tile128"]
+
+
+@pytest.fixture(params=KERNELS)
+def kernel(request, monkeypatch):
+    """The PHI_GEMM_KERNEL A/B switch: both GEMM kernels see every shape."""
+    if request.param == "auto":
+        monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("PHI_GEMM_KERNEL", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 1, 64), (1, 37, 128), (5, 300, 192), (256, 256, 3072),
                                    (257, 129, 640), (300, 1000, 256), (512, 384, 1024),
-                                   (33, 4100, 64), (1000, 70, 576)])
-def test_int32_accumulators_exact(dev, orc, M, N, K):
+                                   (33, 4100, 64), (1000, 70, 576), (513, 777, 320)])
+def test_int32_accumulators_exact(dev, orc, kernel, M, N, K):
     A, B = rand_i8((M, K), M + K), rand_i8((N, K), N + 7)
     C = Q.i8_gemm(A.to(dev), B.to(dev), None, None, out_dtype=torch.int32)
     torch.cuda.synchronize()
@@ -58,8 +71,8 @@ def test_extreme_accumulators(dev, orc):
 @pytest.mark.parametrize("bias_kind", [None, "f32", "bf16"])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 @pytest.mark.parametrize("sb_scalar", [True, False])
-def test_epilogue_bit_exact(dev, orc, bias_kind, out, sb_scalar):
-    M, N, K = 130, 260, 384
+def test_epilogue_bit_exact(dev, orc, kernel, bias_kind, out, sb_scalar):
+    M, N, K = 130, 262, 384
     A, B = rand_i8((M, K), 3), rand_i8((N, K), 4)
     g = torch.Generator().manual_seed(9)
     sa = torch.rand(M, generator=g) * 0.05 + 0.002
@@ -98,6 +111,34 @@ def test_reference_gemm_int8_equality(dev, orc):
     assert np.array_equal(C.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("out", [torch.int32, torch.float32, torch.bfloat16])
+def test_strided_and_unaligned_operands(dev, orc, kernel, out):
+    """lda > K, ldb > K, and an output row pitch that is not a multiple of 4
+    (the epilogue's scalar-store path), with a bias view at an odd offset."""
+    M, N, K = 300, 290, 448
+    Aw, Bw = rand_i8((M, K + 64), 31), rand_i8((N, K + 128), 32)
+    A, B = Aw[:, 16:16 + K], Bw[:, 32:32 + K]
+    g = torch.Generator().manual_seed(33)
+    sa = torch.rand(M, generator=g) * 0.05 + 0.002
+    sbw = torch.rand(N + 1, generator=g) * 0.05 + 0.002
+    biasw = torch.randn(N + 1, generator=g) * 0.02
+    Ad, Bd = Aw.to(dev)[:, 16:16 + K], Bw.to(dev)[:, 32:32 + K]
+    Cw = torch.zeros((M, N + 3), dtype=out, device=dev)
+    C = Cw[:, :N]
+    scaled = out != torch.int32
+    Q.i8_gemm(Ad, Bd, sa.to(dev) if scaled else None, sbw.to(dev)[1:] if scaled else None,
+              biasw.to(dev)[1:] if scaled else None, C=C)
+    acc = orc.gemm_i8_i32_fast(A.contiguous().numpy(), B.contiguous().numpy())
+    if not scaled:
+        assert np.array_equal(C.cpu().numpy(), acc)
+    else:
+        o = "bf16" if out == torch.bfloat16 else "f32"
+        want = orc.epilogue(acc, sa.numpy(), sbw[1:].numpy(), biasw[1:].numpy(), out=o)
+        got = u16(C.contiguous()) if o == "bf16" else C.cpu().contiguous().numpy().view(np.uint32)
+        assert np.array_equal(got, want if o == "bf16" else want.view(np.uint32))
+    assert torch.count_nonzero(Cw[:, N:]) == 0, "wrote past the row"
+
+
 def checksums_ok(A, B, C32):
     """Exact ABFT identities in float64 on the device."""
     Af, Bf, Cf = A.double(), B.double(), C32.double()
@@ -109,7 +150,7 @@ def checksums_ok(A, B, C32):
 @pytest.mark.slow
 @pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4352, 3072, 12288), (4352, 9216, 3072),
                                    (32760, 5120, 5120)])
-def test_full_size_checksums(dev, M, N, K):
+def test_full_size_checksums(dev, kernel, M, N, K):
     A = synth.int8_weight(M, K, seed=M, device=dev)
     B = synth.int8_weight(N, K, seed=N, device=dev)
     C32 = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
