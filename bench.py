@@ -8,7 +8,12 @@ with the scale/bias epilogue to bf16.  Inputs are resident in HBM before the
 timed region.  Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W] [--config c1_up|c1_down|c2|c3_attn|c3_mlp|c4|c0]
-                  [--no-cpu-baseline]
+                  [--no-cpu-baseline] [--calibrate-copy MIB]
+
+--calibrate-copy launches a plain device copy of MIB MiB (three times, after the
+timed region) so a rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run of this same
+command can scale the counters to bytes; the measured HBM bytes per launch of
+the dominant kernel are read back from profiles/traffic_<config>.json.
 
 Only one GPU is used: --gpus above 1 exits with a message.
 """
@@ -44,6 +49,28 @@ CONFIGS = {
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def traffic_for(config: str):
+    """HBM bytes per launch of the dominant kernel, measured by rocprofv3
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration) and
+    committed as profiles/traffic_<config>.json; None when not measured."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return float(json.load(f)["hbm_bytes_per_launch"])
+
+
+def calibrate_copy(mib: int) -> None:
+    import torch
+
+    n = mib * 1024 * 1024
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def cpu_baseline(cfg) -> dict | None:
@@ -194,6 +221,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c1_up", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU (one MI355X); multi-GPU runs are not part of it",
@@ -214,6 +242,9 @@ def main() -> int:
     else:
         r = bench_gemv(cfg, args.steps, args.warmup)
     log(f"bench: {r['ms'] * 1e3:.1f} us per step")
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+    r["roofline"]["traffic"] = traffic_for(args.config)
 
     cpu = None
     if not args.no_cpu_baseline and cfg["kind"] == "w8a8":
