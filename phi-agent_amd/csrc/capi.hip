@@ -106,24 +106,31 @@ int gemm_cfg_for(int64_t M, int64_t N) {
     return big >= 256 ? 0 : 1;
 }
 
-// Kernel choice for the W8A8 GEMM.  PHI_GEMM_KERNEL=tile256 / tile128 forces
-// one (an A/B switch for tests, like the reference's PHI_INT8_DP4A,
-// core/runtime/compute.cpp:566-571); otherwise the 256x256 kernel takes every
-// problem with enough tiles to occupy the GPU.
-enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1 };
+// Kernel choice for the W8A8 GEMM.  PHI_GEMM_KERNEL forces one (an A/B
+// switch for tests, like the reference's PHI_INT8_DP4A,
+// core/runtime/compute.cpp:566-571):
+//   tile128   the 256x128 / 128x128 register-staged kernel (small problems)
+//   tile256   256x256, eight 128x64 waves, 64-deep K-steps
+//   tile256w4 256x256, four 128x128 waves, 128-deep K-steps (needs K % 128 == 0)
+// Unset, problems with enough 256x256 tiles to occupy the GPU take the
+// four-wave kernel when K % 128 == 0 and the eight-wave one otherwise.
+enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1, GK_TILE256W4 = 2 };
 
-GemmKernel gemm_kernel_for(int64_t M, int64_t N) {
+GemmKernel gemm_kernel_for(int64_t M, int64_t N, int64_t K) {
     const char* e = getenv("PHI_GEMM_KERNEL");
+    if (e && strcmp(e, "tile256w4") == 0 && K % 128 == 0) return GK_TILE256W4;
     if (e && strcmp(e, "tile256") == 0) return GK_TILE256;
     if (e && strcmp(e, "tile128") == 0) return GK_TILE128;
     const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-    return t256 >= 128 ? GK_TILE256 : GK_TILE128;
+    if (t256 < 128) return GK_TILE128;
+    return K % 128 == 0 ? GK_TILE256W4 : GK_TILE256;
 }
 
 // Vector-store / vector-load eligibility of the epilogue operands.
 void set_vec_flags(phi_dev::GemmParams& p, int c_dtype, int64_t ldc) {
     const size_t cal = c_dtype == PHI_BF16 ? 8 : 16;
     p.c_vec = aligned(p.C, cal) && ldc % 4 == 0;
+    p.c_vec16 = aligned(p.C, 16) && (ldc * (int64_t)c_elem_bytes(c_dtype)) % 16 == 0;
     const bool sb_ok = p.sb_scalar || !p.sB || aligned(p.sB, 16);
     const bool b_ok = p.bias_kind == phi_dev::BIAS_NONE ||
                       aligned(p.bias, p.bias_kind == phi_dev::BIAS_BF16 ? 8 : 16);
@@ -199,7 +206,11 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.c_kind = c_kind_of(c_dtype);
     p.group_m = 4;
     set_vec_flags(p, c_dtype, ldc);
-    if (gemm_kernel_for(M, N) == GK_TILE256) return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);
+    const GemmKernel gk = gemm_kernel_for(M, N, K);
+    if (gk != GK_TILE128) {
+        p.schedule = gk == GK_TILE256W4 ? 1 : 0;
+        return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);
+    }
     return check_hip(phi_dev::launch_i8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
 }
 

@@ -17,13 +17,21 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // bf16 bits -> fp32, exact.
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// fp32 -> bf16 bits by the integer carry rule: add 0x7fff plus the kept lsb and
-// keep the top half.  This is round-to-nearest-even for every finite value and
-// is the reference's conversion bit for bit (core/util/media_common.cpp:187-193).
+// fp32 -> bf16 bits, round to nearest even.  The reference's conversion is the
+// integer carry rule (add 0x7fff plus the kept lsb, keep the top half;
+// core/util/media_common.cpp:187-193), which is exactly round-to-nearest-even
+// for every finite value; gfx950's v_cvt_pk_bf16_f32 (what a __bf16 cast
+// lowers to) rounds the same way in one instruction.  The two differ only in
+// NaN payloads, which the linear cannot produce from finite operands.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    uint32_t b = __float_as_uint(f);
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return b >> 16;
+    return __builtin_bit_cast(unsigned short, (__bf16)f);
+}
+
+// Two values in one v_cvt_pk_bf16_f32: lo in bits 0..15, hi in bits 16..31.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 // IEEE binary16 -> fp32 (exact).

@@ -27,7 +27,9 @@ struct GemmParams {
     int64_t lut_groups;  // groups per row (K / group)
     int group_shift;     // log2(group)
     int c_vec;           // C rows allow 4-element vector stores (alignment and ldc % 4)
+    int c_vec16;         // C rows allow 16-byte stores (16-byte aligned, row pitch a multiple of 16 bytes)
     int s_vec;           // sB and bias allow 4-element vector loads (16-byte / 8-byte aligned)
+    int schedule;        // 256x256 kernel: 0 = eight waves, 64-deep K; 1 = four waves, 128-deep K
 };
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);

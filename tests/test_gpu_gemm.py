@@ -27,7 +27,7 @@ def rand_i8(shape, seed):
     return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
 
 
-KERNELS = ["auto", "tile256", "tile128"]
+KERNELS = ["auto", "tile256", "tile256w4", "tile128"]
 
 
 @pytest.fixture(params=KERNELS)
