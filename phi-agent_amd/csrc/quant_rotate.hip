@@ -21,6 +21,8 @@
 // LDS: a group's 256 floats sit as 16 slots of 20 floats (16 values + 4 pad,
 // so the 16-B slot accesses of 8 lanes land on 8 distinct 4-bank windows), and
 // groups are 336 floats apart (a 16-bank shift between the teams of a wave).
+#include <cstdlib>
+
 #include "device_common.hpp"
 
 namespace phi_dev {
@@ -133,11 +135,285 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
     if (tid == 0) s[row] = scale;
 }
 
+// ---------------------------------------------------------------------------
+// Register-resident form, K <= 16384 (at most 64 groups).
+//
+// A wave works on 4R consecutive 256-groups of one row in R rounds of four,
+// one 16-lane team per group, and keeps its rotated values in registers (16
+// per lane per round) until the row amax is known.  WPR = ceil(G / 4R) waves
+// cover a row (threadIdx.x) and a block holds RPB rows (threadIdx.y); only the
+// amax crosses waves (one barrier, none when WPR is 1).  The two transposes
+// of a round go through a 16x16 tile private to the team: a wave's LDS
+// operations complete in issue order, so they need no barrier.
+//
+// Tile layout: row a holds group elements 16a..16a+15, and its 16-byte chunk c
+// sits in chunk slot c ^ (a >> 2).  Row accesses (16 lanes x 16 B) and column
+// accesses (one float per lane) are then free of bank conflicts; the four
+// tiles of a wave are 272 floats apart, so the teams' column accesses use
+// different banks.
+//
+// The kernel issues about fifteen VALU instructions per element against four
+// bytes of HBM traffic (bf16 in, int8 out), so VALU issue bounds it next to
+// HBM.  Hence: one fma per butterfly output (sum - 2x is exact as
+// fma(-2, x, sum), the product being exact), the final 1/16 folded into the
+// scale, the amax as v_max3 over |.|, and half-away rounding as add +
+// truncate (pre_half_away) with the truncation done by the int conversion.
+// R > 1 spreads the per-wave costs (addresses, scale division, reductions)
+// over more elements.
+constexpr int QT_TILE = 272;
+constexpr int QT_WAVE = 4 * QT_TILE;
+constexpr int QT_MAX_ROUNDS = 5;
+
+// Orders one wave's LDS accesses across lanes for the compiler: the hardware
+// already completes a wave's LDS operations in issue order, and a wavefront-
+// scope fence emits no instruction, but it keeps the compiler from moving a
+// load of another lane's slot above the store that fills it.
+__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
+
+// bfly16 with y = fma(-2, x[3-j], sum): bit-identical, one instruction fewer
+// per output.
+template <int ST>
+__device__ __forceinline__ void bfly16f(float (&v)[16]) {
+#pragma unroll
+    for (int o = 0; o < 4; o++) {
+        const int b = ST == 1 ? 4 * o : o;
+        const float x0 = v[b], x1 = v[b + ST], x2 = v[b + 2 * ST], x3 = v[b + 3 * ST];
+        const float sum = ((x0 + x1) + x2) + x3;
+        v[b] = fmaf(-2.0f, x3, sum);
+        v[b + ST] = fmaf(-2.0f, x2, sum);
+        v[b + 2 * ST] = fmaf(-2.0f, x1, sum);
+        v[b + 3 * ST] = fmaf(-2.0f, x0, sum);
+    }
+}
+
+// max(m, |a|, |b|) in one instruction (fmaxf would first canonicalise each
+// operand separately).
+__device__ __forceinline__ float max3_abs(float m, float a, float b) {
+    float r;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
+}
+
+// Wave-wide max of non-negative floats, as their bit patterns (same order):
+// four DPP steps leave each 16-lane row's max in all its lanes, then the four
+// row maxima are read out.  The result is wave-uniform.
+__device__ __forceinline__ uint32_t wave_max_bits(uint32_t u) {
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x140, 0xF, 0xF, false));  // row_mirror
+    const uint32_t a = __builtin_amdgcn_readlane(u, 0), b = __builtin_amdgcn_readlane(u, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(u, 32), d = __builtin_amdgcn_readlane(u, 48);
+    return max(max(a, b), max(c, d));
+}
+
+// For ties away from zero: min(|v| inv + (0.5 - 2^-25), qmax) with v's sign,
+// whose truncation toward zero is the code.  For every non-negative fp32 d,
+// floor(fl(d + (0.5 - 2^-25))) is d rounded half away from zero (checked over
+// all fp32 d < 2^25; above that d is an integer and the addition returns d),
+// and |v| * inv is |v * inv| exactly.  The clamp commutes with the truncation
+// because qmax is an integer.
+__device__ __forceinline__ float pre_half_away(float v, float inv, float qmax) {
+    return copysignf(fminf(fabsf(v) * inv + 0.49999997f, qmax), v);
+}
+
+__device__ __forceinline__ float pre_half_even(float v, float inv, float qmax) {
+    return fminf(fmaxf(rintf(v * inv), -qmax), qmax);
+}
+
+// Four fp32 values truncated to int and packed little-endian into one dword.
+// Callers pass values whose truncations fit int8.
+__device__ __forceinline__ uint32_t cvt_pack4(float a, float b, float c, float d) {
+    return pack4((int)a, (int)b, (int)c, (int)d);
+}
+
+template <bool BF16_IN, bool HALF_EVEN, int R>
+__global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
+                                                           int G, int8_t* __restrict__ q, int64_t ldq,
+                                                           float* __restrict__ s, float qmax, int rotate) {
+    extern __shared__ __align__(16) float lds[];
+    constexpr int NW = BF16_IN ? 8 : 16;  // input dwords per lane per round
+    const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
+    const int wave = threadIdx.y * wpr + wr;
+    const int row = blockIdx.x * blockDim.y + threadIdx.y;
+    const int team = lane >> 4, tl = lane & 15, sw = tl >> 2;
+    const int g0 = wr * 4 * R + team;  // round r works on group g0 + 4 r
+    float* T = lds + wave * QT_WAVE + team * QT_TILE;
+    float* trow = T + tl * 16;
+    uint32_t* red = (uint32_t*)(lds + blockDim.y * wpr * QT_WAVE);
+
+    // Every round's loads first.  Lanes past the row's last group, or in a
+    // row past the last, read valid data of another group and discard it.
+    const int64_t xrow = (int64_t)min(row, rows - 1) * ldx + tl * 16;
+    uint32_t raw[R][NW];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int64_t off = xrow + (int64_t)min(g0 + 4 * r, G - 1) * 256;
+        const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)x + off) : (const uint4*)((const float*)x + off);
+#pragma unroll
+        for (int i = 0; i < NW / 4; i++) {
+            const uint4 t = src[i];
+            raw[r][4 * i] = t.x;
+            raw[r][4 * i + 1] = t.y;
+            raw[r][4 * i + 2] = t.z;
+            raw[r][4 * i + 3] = t.w;
+        }
+    }
+
+    float rot[R][16];
+    uint32_t amax = 0;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            if (BF16_IN) v[i] = __uint_as_float(i & 1 ? raw[r][i >> 1] & 0xffff0000u : raw[r][i >> 1] << 16);
+            else v[i] = __uint_as_float(raw[r][i]);
+        }
+        if (rotate) {
+            bfly16f<1>(v);
+            bfly16f<4>(v);
+        }
+        // Row tl of the tile, then column tl: w[j] = element 16 j + tl.
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            *(float4*)(trow + 4 * (c ^ sw)) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+        wave_lds_fence();
+        float(&w)[16] = rot[r];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float* col = T + 64 * k + 4 * (sw ^ k) + (tl & 3);
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[4 * k + i] = col[16 * i];
+        }
+        wave_lds_fence();
+        if (rotate) {
+            bfly16f<1>(w);
+            bfly16f<4>(w);
+        }
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) m = max3_abs(m, w[j], w[j + 1]);
+        if (g0 + 4 * r < G) amax = max(amax, __float_as_uint(m));
+    }
+
+    amax = wave_max_bits(amax);
+    if (wpr > 1) {
+        if (lane == 0) red[wave] = amax;
+        __syncthreads();
+        for (int i = 0; i < wpr; i++) amax = max(amax, red[threadIdx.y * wpr + i]);
+    }
+    // The rotation's final 1/16 is applied to the amax and to inv instead of
+    // to every element.  max |w|/16 rounds to the max of the rounded |w|/16,
+    // so the amax and scale are exact.  When inv/16 is exact (inv >= 2^-122,
+    // i.e. amax below ~2^122 qmax), round(w * (inv/16)) = round((w/16) * inv)
+    // wherever w/16 is exact, and where it is not (|w| < 2^-122) the code is 0
+    // either way (|w| inv/16 < 1e-5).  Otherwise each element is scaled first.
+    const float sixteenth = rotate ? 1.0f / 16.0f : 1.0f;
+    const float rmax = __uint_as_float(amax) * sixteenth;
+    const float scale = rmax > 1e-30f ? rmax / qmax : 1.0f;
+    const float inv = 1.0f / scale;
+    const bool fold = !rotate || inv >= 0x1p-122f;
+    const float pre = fold ? 1.0f : sixteenth, post = fold ? inv * sixteenth : inv;
+
+    int8_t* qrow = q + (int64_t)row * ldq + tl * 16;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        // Column tl back into the tile, row tl out: 16 contiguous elements.
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float* col = T + 64 * k + 4 * (sw ^ k) + (tl & 3);
+#pragma unroll
+            for (int i = 0; i < 4; i++) col[16 * i] = rot[r][4 * k + i];
+        }
+        wave_lds_fence();
+        uint32_t packed[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 t = *(const float4*)(trow + 4 * (c ^ sw));
+            float4 u = t;
+            if (!fold) u = make_float4(t.x * pre, t.y * pre, t.z * pre, t.w * pre);  // wave-uniform, rare
+            if (HALF_EVEN)
+                packed[c] = cvt_pack4(pre_half_even(u.x, post, qmax), pre_half_even(u.y, post, qmax),
+                                      pre_half_even(u.z, post, qmax), pre_half_even(u.w, post, qmax));
+            else
+                packed[c] = cvt_pack4(pre_half_away(u.x, post, qmax), pre_half_away(u.y, post, qmax),
+                                      pre_half_away(u.z, post, qmax), pre_half_away(u.w, post, qmax));
+        }
+        wave_lds_fence();
+        if (row < rows && g0 + 4 * r < G)
+            *(uint4*)(qrow + (int64_t)(g0 + 4 * r) * 256) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    }
+    if (wr == 0 && lane == 0 && row < rows) s[row] = scale;
+}
+
+// Rounds per wave for G groups.  A large problem is bound by VALU issue, so R
+// minimises instructions per element: ~14.3 per element plus ~90 per wave and
+// round-set spread over the 16 R elements a lane holds, times the share of
+// lanes doing live work, with 10 % more for R >= 4 (at most five waves per
+// SIMD).  A small one (under 2^17 groups, about two waves of waves on the
+// chip) is bound by latency, and the most waves (R = 1) wins.
+static int tile_rounds(int64_t rows, int G) {
+    const char* env = getenv("PHI_QR_ROUNDS");  // A/B switch: force R where it fits
+    const int forced = env ? atoi(env) : 0;
+    if (forced >= 1 && forced <= QT_MAX_ROUNDS && (G + 4 * forced - 1) / (4 * forced) <= 16) return forced;
+    if (rows * G < (1 << 17) && G <= 64) return 1;
+    int best = 1;
+    double best_cost = 1e30;
+    for (int R = 1; R <= QT_MAX_ROUNDS; R++) {
+        const int wpr = (G + 4 * R - 1) / (4 * R);
+        if (wpr > 16) continue;
+        const double cost = (double)(4 * R * wpr) / G * (14.3 + 90.0 / (16 * R)) * (R >= 4 ? 1.1 : 1.0);
+        if (cost < best_cost - 1e-9) best = R, best_cost = cost;
+    }
+    return best;
+}
+
+template <bool BF16_IN, bool HALF_EVEN, int R>
+static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
+                                 int64_t ldq, float* s, float qmax, int rotate) {
+    const int wpr = (G + 4 * R - 1) / (4 * R);
+    const int rpb = wpr >= 8 ? 1 : 8 / wpr;
+    const size_t lds = ((size_t)rpb * wpr * QT_WAVE + 16) * sizeof(float);
+    static bool lds_set = false;  // one attribute call per instantiation and process
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)quant_rotate_tiles<BF16_IN, HALF_EVEN, R>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)((16 * QT_WAVE + 16) * sizeof(float)));
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
+    hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R>), grid, block, lds, stream, x, ldx, (int)rows, G, q,
+                       ldq, s, qmax, rotate);
+    return hipGetLastError();
+}
+
+template <bool BF16_IN, bool HALF_EVEN>
+static hipError_t launch_tiles(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
+                               int64_t ldq, float* s, float qmax, int rotate) {
+    switch (tile_rounds(rows, G)) {
+        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+    }
+}
+
 // Host-side launcher.  Validation is done by the C ABI layer.
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
                                float qmax, int half_even, int rotate) {
     const int G = (int)(K / 256);
+    if (rows == 0) return hipSuccess;
+    if (G <= 64) {
+        if (bf16_in)
+            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate)
+                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate)
+                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+    }
     int threads = ((16 * G + 63) / 64) * 64;
     if (threads > 1024) threads = 1024;
     const size_t lds_bytes = ((size_t)G * QR_GSTRIDE + 16) * sizeof(float);

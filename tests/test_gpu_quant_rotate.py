@@ -36,6 +36,37 @@ def test_rotate_quant_bit_exact(dev, orc, M, K, dtype):
     assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
 
 
+@pytest.mark.parametrize("G", list(range(1, 50)))
+def test_every_group_count(dev, orc, G):
+    """Each 256-group count up to 49 (the register-resident kernel's rounds of
+    four groups, its partial last round, and the first count past it), with a
+    row count that leaves a partial block of rows."""
+    M, K = 5, 256 * G
+    dtype = torch.float32 if G % 7 == 3 else torch.bfloat16
+    x = synth.activations(M, K, seed=G, dtype=dtype)
+    q, s, qo, so = run(dev, orc, x)
+    assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("rounds", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("G", [1, 7, 12, 20, 33, 48, 64])
+def test_forced_rounds(dev, orc, monkeypatch, rounds, G):
+    """Every rounds-per-wave instance of the register-resident kernel
+    (PHI_QR_ROUNDS), bf16 and fp32 input, with dead groups and rows."""
+    monkeypatch.setenv("PHI_QR_ROUNDS", str(rounds))
+    for dtype in (torch.bfloat16, torch.float32):
+        x = synth.activations(11, 256 * G, seed=100 * rounds + G, dtype=dtype)
+        q, s, qo, so = run(dev, orc, x)
+        assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"
+        assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    x = synth.activations(6, 256 * G, seed=7 + G, dtype=torch.bfloat16)
+    q, s, qo, so = run(dev, orc, x, round_mode=Q.ROUND_HALF_EVEN, qmax=7.0)
+    assert np.array_equal(q, qo) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    q, s, qo, so = run(dev, orc, x, rotate=False)
+    assert np.array_equal(q, qo) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+
+
 def test_c0_activation_block(dev, orc):
     """config 0's activation: [256, 3072] bf16 with outlier channels, seed 0."""
     x = synth.activations(256, 3072, seed=0)
@@ -73,6 +104,22 @@ def test_exact_ties_and_the_half_boundary(dev, orc):
         assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
     q, _, _, _ = run(dev, orc, x, rotate=False)
     assert list(q[0, :10]) == [1, -1, 2, -2, 3, -3, 127, -127, 0, 0]
+
+
+def test_huge_rows(dev, orc):
+    """Rows whose amax is so large that inv/16 would be subnormal (qmax 1,
+    amax 1e37): the kernel then scales each element by 1/16 before inv, as the
+    reference does.  A constant group rotates to 16 c before the 1/16."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((3, 1024)) * 1e35).astype(np.float32)
+    x[0, :256] = 1e37
+    x[1, 256:512] = -6e36
+    x = torch.from_numpy(x)
+    for qmax in (1.0, 7.0, 127.0):
+        for mode in (Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN):
+            q, s, qo, so = run(dev, orc, x, qmax=qmax, round_mode=mode)
+            assert np.array_equal(q, qo), (qmax, mode, (q != qo).sum())
+            assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
 
 
 def test_zero_rows_and_tiny_rows(dev, orc):
