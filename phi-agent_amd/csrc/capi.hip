@@ -112,18 +112,47 @@ int gemm_cfg_for(int64_t M, int64_t N) {
 //   tile128   the 256x128 / 128x128 register-staged kernel (small problems)
 //   tile256   256x256, eight 128x64 waves, 64-deep K-steps
 //   tile256w4 256x256, four 128x128 waves, 128-deep K-steps (needs K % 128 == 0)
-// Unset, problems with enough 256x256 tiles to occupy the GPU take the
-// four-wave kernel when K % 128 == 0 and the eight-wave one otherwise.
-enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1, GK_TILE256W4 = 2 };
+//   persist   persistent 256x256 tiles with cross-tile prefetch (persist_ok)
+// Unset, every problem the persistent kernel accepts takes it; otherwise
+// problems with enough 256x256 tiles to occupy the GPU take the four-wave
+// kernel when K % 128 == 0 and the eight-wave one otherwise.
+enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1, GK_TILE256W4 = 2, GK_PERSIST = 3 };
 
-GemmKernel gemm_kernel_for(int64_t M, int64_t N, int64_t K) {
+// The persistent kernel's contract: 128-deep K-steps in pairs and at least
+// two pairs, whole 16-byte output pieces (8 bf16 or 4 fp32/int32 columns)
+// on 16-byte aligned rows, and 32-bit byte offsets within a 256-row tile.
+bool persist_ok(const void* C, int c_dtype, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc) {
+    const int64_t esz = c_dtype == PHI_BF16 ? 2 : 4;
+    if (K % 256 != 0 || K < 512) return false;
+    if (N % (16 / esz) != 0) return false;
+    if (!aligned(C, 16) || (ldc * esz) % 16 != 0) return false;
+    const int64_t lim = (int64_t)1 << 23;  // 256 rows x pitch < 2^31
+    return lda < lim && ldb < lim && ldc * esz < lim;
+}
+
+GemmKernel gemm_kernel_for(int64_t M, int64_t N, int64_t K, bool pok) {
     const char* e = getenv("PHI_GEMM_KERNEL");
+    if (e && strcmp(e, "persist") == 0 && pok) return GK_PERSIST;
     if (e && strcmp(e, "tile256w4") == 0 && K % 128 == 0) return GK_TILE256W4;
     if (e && strcmp(e, "tile256") == 0) return GK_TILE256;
     if (e && strcmp(e, "tile128") == 0) return GK_TILE128;
+    if (pok) return GK_PERSIST;
     const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
     if (t256 < 128) return GK_TILE128;
     return K % 128 == 0 ? GK_TILE256W4 : GK_TILE256;
+}
+
+// Compute units of the current device (one persistent workgroup each).
+int num_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 // Vector-store / vector-load eligibility of the epilogue operands.
@@ -206,7 +235,8 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.c_kind = c_kind_of(c_dtype);
     p.group_m = 4;
     set_vec_flags(p, c_dtype, ldc);
-    const GemmKernel gk = gemm_kernel_for(M, N, K);
+    const GemmKernel gk = gemm_kernel_for(M, N, K, persist_ok(C, c_dtype, N, K, lda, ldb, ldc));
+    if (gk == GK_PERSIST) return check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, p, num_cus()), who);
     if (gk != GK_TILE128) {
         p.schedule = gk == GK_TILE256W4 ? 1 : 0;
         return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);

@@ -35,6 +35,8 @@ struct GemmParams {
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
+// Persistent 256x256-tile kernel (K % 256 == 0, K >= 512): min(tiles, num_cus) workgroups.
+hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus);
 
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,

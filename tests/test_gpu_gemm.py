@@ -27,7 +27,7 @@ def rand_i8(shape, seed):
     return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
 
 
-KERNELS = ["auto", "tile256", "tile256w4", "tile128"]
+KERNELS = ["auto", "persist", "tile256", "tile256w4", "tile128"]
 
 
 @pytest.fixture(params=KERNELS)
@@ -42,7 +42,12 @@ def kernel(request, monkeypatch):
 
 @pytest.mark.parametrize("M,N,K", [(1, 1, 64), (1, 37, 128), (5, 300, 192), (256, 256, 3072),
                                    (257, 129, 640), (300, 1000, 256), (512, 384, 1024),
-                                   (33, 4100, 64), (1000, 70, 576), (513, 777, 320)])
+                                   (33, 4100, 64), (1000, 70, 576), (513, 777, 320),
+                                   # shapes the persistent kernel takes (K % 256 == 0, K >= 512,
+                                   # N % 4 == 0): partial tiles in M and N, one to several tiles
+                                   # per workgroup, the shortest K it accepts
+                                   (1, 4, 512), (300, 1000, 512), (257, 264, 768), (777, 520, 1280),
+                                   (2049, 2052, 512), (4100, 4104, 1024)])
 def test_int32_accumulators_exact(dev, orc, kernel, M, N, K):
     A, B = rand_i8((M, K), M + K), rand_i8((N, K), N + 7)
     C = Q.i8_gemm(A.to(dev), B.to(dev), None, None, out_dtype=torch.int32)
@@ -71,8 +76,8 @@ def test_extreme_accumulators(dev, orc):
 @pytest.mark.parametrize("bias_kind", [None, "f32", "bf16"])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 @pytest.mark.parametrize("sb_scalar", [True, False])
-def test_epilogue_bit_exact(dev, orc, kernel, bias_kind, out, sb_scalar):
-    M, N, K = 130, 262, 384
+@pytest.mark.parametrize("M,N,K", [(130, 262, 384), (130, 264, 512), (600, 776, 1024)])
+def test_epilogue_bit_exact(dev, orc, kernel, bias_kind, out, sb_scalar, M, N, K):
     A, B = rand_i8((M, K), 3), rand_i8((N, K), 4)
     g = torch.Generator().manual_seed(9)
     sa = torch.rand(M, generator=g) * 0.05 + 0.002
@@ -112,10 +117,11 @@ def test_reference_gemm_int8_equality(dev, orc):
 
 
 @pytest.mark.parametrize("out", [torch.int32, torch.float32, torch.bfloat16])
-def test_strided_and_unaligned_operands(dev, orc, kernel, out):
+@pytest.mark.parametrize("M,N,K,pad", [(300, 290, 448, 3), (300, 296, 512, 8)])
+def test_strided_and_unaligned_operands(dev, orc, kernel, out, M, N, K, pad):
     """lda > K, ldb > K, and an output row pitch that is not a multiple of 4
-    (the epilogue's scalar-store path), with a bias view at an odd offset."""
-    M, N, K = 300, 290, 448
+    (the epilogue's scalar-store path) or padded by 8 (the persistent
+    kernel's whole-row stores), with a bias view at an odd offset."""
     Aw, Bw = rand_i8((M, K + 64), 31), rand_i8((N, K + 128), 32)
     A, B = Aw[:, 16:16 + K], Bw[:, 32:32 + K]
     g = torch.Generator().manual_seed(33)
@@ -123,7 +129,7 @@ def test_strided_and_unaligned_operands(dev, orc, kernel, out):
     sbw = torch.rand(N + 1, generator=g) * 0.05 + 0.002
     biasw = torch.randn(N + 1, generator=g) * 0.02
     Ad, Bd = Aw.to(dev)[:, 16:16 + K], Bw.to(dev)[:, 32:32 + K]
-    Cw = torch.zeros((M, N + 3), dtype=out, device=dev)
+    Cw = torch.zeros((M, N + pad), dtype=out, device=dev)
     C = Cw[:, :N]
     scaled = out != torch.int32
     Q.i8_gemm(Ad, Bd, sa.to(dev) if scaled else None, sbw.to(dev)[1:] if scaled else None,
