@@ -155,6 +155,39 @@ int num_cus() {
     return n;
 }
 
+// Split phase of the persistent kernel: when the 256 x 256 tiles leave a
+// partial last round, the last full round and the partial one (between one
+// and two tiles per CU) are cut into equal K-step ranges instead, so every
+// CU finishes at about the same time.  Opt-in (PHI_GEMM_SPLIT=1): measured at
+// 4352 x 12288 x 3072 and 4352 x 9216 x 3072 it balances the CUs but each
+// K-step of the split phase runs ~30 % slower, because the CUs of an XCD then
+// sit at different K offsets and no longer share their A and B chunks in L2,
+// which costs more than the idle CUs of the partial round.
+bool split_plan(int64_t M, int64_t N, int64_t K, int G, int* dp_tiles, int* sk_tiles) {
+    const char* e = getenv("PHI_GEMM_SPLIT");
+    if (!e || strcmp(e, "1") != 0) return false;
+    const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t rounds = tiles / G, rem = tiles % G;
+    if (rounds < 1 || rem == 0 || rem * 8 > (int64_t)G * 7) return false;
+    const int64_t units = (tiles - (rounds - 1) * G) * (K / 128);
+    if (units * G >= ((int64_t)1 << 31)) return false;
+    *dp_tiles = (int)((rounds - 1) * G);
+    *sk_tiles = (int)(tiles - (rounds - 1) * G);
+    return true;
+}
+
+// Polls of a ready word before a head share gives up (about a second).
+// PHI_GEMM_SPLIT_SPIN overrides it (0: never wait), so a test can force the
+// give-up path from the host.
+int split_spin() {
+    const char* e = getenv("PHI_GEMM_SPLIT_SPIN");
+    if (e && *e) {
+        const long v = strtol(e, nullptr, 10);
+        return v < 0 ? 0 : (v > (1 << 30) ? (1 << 30) : (int)v);
+    }
+    return 1 << 20;
+}
+
 // Vector-store / vector-load eligibility of the epilogue operands.
 void set_vec_flags(phi_dev::GemmParams& p, int c_dtype, int64_t ldc) {
     const size_t cal = c_dtype == PHI_BF16 ? 8 : 16;
@@ -199,10 +232,9 @@ phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype,
 }
 
 size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-    (void)M;
-    (void)N;
-    (void)K;
-    return 0;
+    int dp = 0, sk = 0;
+    if (M <= 0 || N <= 0 || K % 256 != 0 || K < 512 || !split_plan(M, N, K, num_cus(), &dp, &sk)) return 0;
+    return phi_dev::persist_workspace_bytes(num_cus());
 }
 
 phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
@@ -210,11 +242,10 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
                            const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
                            int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes) {
     static const char* who = "int8_gemm";
-    (void)workspace;
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, C, c_dtype, ldc, false);
     if (st != PHI_OK) return st;
-    if (ws_bytes < phi_hip_workspace_bytes(M, N, K)) return fail(PHI_ERR_WORKSPACE, "%s: workspace too small", who);
+    if (workspace && !aligned(workspace, 256)) return fail(PHI_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
     const int bk = bias_kind_of(bias, bias_dtype, &st);
     if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
     phi_dev::GemmParams p{};
@@ -236,7 +267,18 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.group_m = 4;
     set_vec_flags(p, c_dtype, ldc);
     const GemmKernel gk = gemm_kernel_for(M, N, K, persist_ok(C, c_dtype, N, K, lda, ldb, ldc));
-    if (gk == GK_PERSIST) return check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, p, num_cus()), who);
+    if (gk == GK_PERSIST) {
+        const int G = num_cus();
+        int dp = 0, sk = 0;
+        if (workspace && ws_bytes >= phi_dev::persist_workspace_bytes(G) && split_plan(M, N, K, G, &dp, &sk)) {
+            p.sk_dp_tiles = dp;
+            p.sk_tiles = sk;
+            p.sk_cnt = (int*)workspace;
+            p.sk_part = (int8_t*)workspace + phi_dev::kPersistCounterBytes;
+            p.sk_spin = split_spin();
+        }
+        return check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, p, G), who);
+    }
     if (gk != GK_TILE128) {
         p.schedule = gk == GK_TILE256W4 ? 1 : 0;
         return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);
@@ -341,7 +383,7 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     if (group <= 0 || group % 64 != 0 || K % group != 0 || (group & (group - 1)) != 0)
         return fail(PHI_ERR_SHAPE, "%s: group=%lld must be a power of two, a multiple of 64 and divide K", who, (long long)group);
     if (!aligned(lut, 16)) return fail(PHI_ERR_ALIGN, "%s: lut must be 16-byte aligned", who);
-    if (ws_bytes < phi_hip_workspace_bytes(M, N, K)) return fail(PHI_ERR_WORKSPACE, "%s: workspace too small", who);
+    (void)ws_bytes;  // the in-register W4A8 kernel needs no workspace
     const int bk = bias_kind_of(bias, bias_dtype, &st);
     if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
     st = phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);

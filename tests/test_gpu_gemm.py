@@ -183,3 +183,74 @@ def test_contract_errors(dev):
     A = torch.zeros((0, 64), dtype=torch.int8, device=dev)
     with pytest.raises(Q.QLinearError, match="empty problem"):
         Q.i8_gemm(A, B[:, :64].contiguous(), None, None, out_dtype=torch.int32)
+
+
+# ---------------------------------------------------------------- split schedule
+# Shapes whose 256 x 256 tiles leave a partial last round on 256 CUs: the
+# persistent kernel then cuts the last rounds into K-step ranges and a tile's
+# two shares meet through the workspace.
+SPLIT_SHAPES = [(4352, 4352, 512), (4352, 12288, 512), (2304, 8192, 1024), (4352, 9216, 768),
+                (4100, 4104, 1536)]
+
+
+def exact_product(A, B):
+    return (A.double() @ B.double().t()).to(torch.int64)
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_split_schedule_exact(dev, lib, monkeypatch, M, N, K):
+    monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
+    monkeypatch.setenv("PHI_GEMM_SPLIT", "1")
+    n = lib.phi_hip_workspace_bytes(M, N, K)
+    assert n > 0, "shape expected to take the split schedule"
+    A = rand_i8((M, K), M + 3).to(dev)
+    B = rand_i8((N, K), N + 5).to(dev)
+    ws = torch.zeros(n, dtype=torch.uint8, device=dev)
+    want = exact_product(A, B)
+    for call in range(2):  # the second call reuses the ready words the first left clear
+        C = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(C.to(torch.int64), want), f"call {call}"
+        assert torch.count_nonzero(ws[:4096]) == 0, "error or ready words left set"
+    C0 = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=None)  # whole tiles only
+    assert torch.equal(C0.to(torch.int64), want)
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_split_schedule_epilogue(dev, orc, monkeypatch, out):
+    """Head tiles run the scaled epilogue on the sum of both shares."""
+    monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
+    monkeypatch.setenv("PHI_GEMM_SPLIT", "1")
+    M, N, K = 4352, 4352, 512
+    A, B = rand_i8((M, K), 41), rand_i8((N, K), 42)
+    g = torch.Generator().manual_seed(43)
+    sa = torch.rand(M, generator=g) * 0.05 + 0.002
+    sb = torch.rand(N, generator=g) * 0.05 + 0.002
+    bias = (torch.randn(N, generator=g) * 0.02).to(torch.bfloat16)
+    C = Q.i8_gemm(A.to(dev), B.to(dev), sa.to(dev), sb.to(dev), bias.to(dev),
+                  out_dtype=torch.bfloat16 if out == "bf16" else torch.float32)
+    acc = exact_product(A.to(dev), B.to(dev)).cpu().numpy().astype(np.int32)
+    want = orc.epilogue(acc, sa.numpy(), sb.numpy(), u16(bias), out=out)
+    got = u16(C) if out == "bf16" else C.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, want if out == "bf16" else want.view(np.uint32))
+
+
+def test_split_schedule_gives_up_without_hanging(dev, lib, monkeypatch):
+    """A head share whose wait runs out (forced from the host: zero polls)
+    counts the failure in the workspace's error word instead of waiting; the
+    kernel still finishes, and the whole-tile schedule is unaffected."""
+    monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
+    monkeypatch.setenv("PHI_GEMM_SPLIT", "1")
+    M, N, K = 4352, 4352, 512
+    A, B = rand_i8((M, K), 51).to(dev), rand_i8((N, K), 52).to(dev)
+    n = lib.phi_hip_workspace_bytes(M, N, K)
+    assert n > 0
+    ws = torch.zeros(n, dtype=torch.uint8, device=dev)
+    monkeypatch.setenv("PHI_GEMM_SPLIT_SPIN", "0")
+    Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=ws)
+    torch.cuda.synchronize()
+    errors = int(ws[:4].view(torch.int32).item())
+    assert errors > 0
+    monkeypatch.delenv("PHI_GEMM_SPLIT_SPIN")
+    C = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=None)
+    assert torch.equal(C.to(torch.int64), exact_product(A, B))
