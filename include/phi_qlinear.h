@@ -95,22 +95,15 @@ phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype,
  *   C [M, ldc] of c_dtype: PHI_F32 (reference), PHI_BF16 (RNE), or PHI_I32
  *     (raw accumulators; scales and bias are then ignored and may be NULL).
  *   A, B: 16-byte aligned; lda, ldb multiples of 16; K % 64 == 0.
- *   workspace: optional.  phi_hip_workspace_bytes() gives the size that
- *     enables the split-K-range schedule for this shape (0: none applies);
- *     with NULL or less, whole tiles are used and the result is the same bit
- *     for bit.  256-byte aligned, zero-filled before its first use; every
- *     call leaves it zero-filled, except that its first int32 counts split
- *     shares whose wait for their partner ran out (nonzero: the output is
- *     wrong and the buffer must be cleared again).  One workspace per stream:
- *     calls sharing one concurrently race.
+ *   workspace: may be NULL when phi_hip_workspace_bytes() returns 0 (it
+ *     does for every shape: the kernels keep all scratch in LDS).
  */
 phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
                            int64_t ldb, const float* sA, const float* sB, int sb_scalar,
                            const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
                            int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes);
 
-/* Workspace (bytes) with which phi_hip_i8_gemm / phi_hip_q8_linear can use
- * the split schedule for this shape; 0 when it does not apply. */
+/* Workspace (bytes) phi_hip_i8_gemm / phi_hip_q8_linear need for this shape. */
 size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*

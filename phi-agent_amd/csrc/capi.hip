@@ -112,18 +112,20 @@ int gemm_cfg_for(int64_t M, int64_t N) {
 //   tile128   the 256x128 / 128x128 register-staged kernel (small problems)
 //   tile256   256x256, eight 128x64 waves, 64-deep K-steps
 //   tile256w4 256x256, four 128x128 waves, 128-deep K-steps (needs K % 128 == 0)
-//   persist   persistent 256x256 tiles with cross-tile prefetch (persist_ok)
+//   persist   persistent kernel: 256x256 tiles for whole rounds, 128x128 for
+//             the remaining rows (persist_ok)
+//   persist256 / persist128  the persistent kernel with one tile size only
 // Unset, every problem the persistent kernel accepts takes it; otherwise
 // problems with enough 256x256 tiles to occupy the GPU take the four-wave
 // kernel when K % 128 == 0 and the eight-wave one otherwise.
-enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1, GK_TILE256W4 = 2, GK_PERSIST = 3 };
+enum GemmKernel { GK_TILE128 = 0, GK_TILE256 = 1, GK_TILE256W4 = 2, GK_PERSIST = 3, GK_PERSIST256 = 4, GK_PERSIST128 = 5 };
 
-// The persistent kernel's contract: 128-deep K-steps in pairs and at least
-// two pairs, whole 16-byte output pieces (8 bf16 or 4 fp32/int32 columns)
-// on 16-byte aligned rows, and 32-bit byte offsets within a 256-row tile.
+// The persistent kernel's contract: 128-deep K-steps in pairs, whole 16-byte
+// output pieces (8 bf16 or 4 fp32/int32 columns) on 16-byte aligned rows, and
+// 32-bit byte offsets within a 256-row tile.
 bool persist_ok(const void* C, int c_dtype, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc) {
     const int64_t esz = c_dtype == PHI_BF16 ? 2 : 4;
-    if (K % 256 != 0 || K < 512) return false;
+    if (K % 256 != 0) return false;
     if (N % (16 / esz) != 0) return false;
     if (!aligned(C, 16) || (ldc * esz) % 16 != 0) return false;
     const int64_t lim = (int64_t)1 << 23;  // 256 rows x pitch < 2^31
@@ -133,6 +135,8 @@ bool persist_ok(const void* C, int c_dtype, int64_t N, int64_t K, int64_t lda, i
 GemmKernel gemm_kernel_for(int64_t M, int64_t N, int64_t K, bool pok) {
     const char* e = getenv("PHI_GEMM_KERNEL");
     if (e && strcmp(e, "persist") == 0 && pok) return GK_PERSIST;
+    if (e && strcmp(e, "persist256") == 0 && pok) return GK_PERSIST256;
+    if (e && strcmp(e, "persist128") == 0 && pok) return GK_PERSIST128;
     if (e && strcmp(e, "tile256w4") == 0 && K % 128 == 0) return GK_TILE256W4;
     if (e && strcmp(e, "tile256") == 0) return GK_TILE256;
     if (e && strcmp(e, "tile128") == 0) return GK_TILE128;
@@ -155,37 +159,30 @@ int num_cus() {
     return n;
 }
 
-// Split phase of the persistent kernel: when the 256 x 256 tiles leave a
-// partial last round, the last full round and the partial one (between one
-// and two tiles per CU) are cut into equal K-step ranges instead, so every
-// CU finishes at about the same time.  Opt-in (PHI_GEMM_SPLIT=1): measured at
-// 4352 x 12288 x 3072 and 4352 x 9216 x 3072 it balances the CUs but each
-// K-step of the split phase runs ~30 % slower, because the CUs of an XCD then
-// sit at different K offsets and no longer share their A and B chunks in L2,
-// which costs more than the idle CUs of the partial round.
-bool split_plan(int64_t M, int64_t N, int64_t K, int G, int* dp_tiles, int* sk_tiles) {
-    const char* e = getenv("PHI_GEMM_SPLIT");
-    if (!e || strcmp(e, "1") != 0) return false;
-    const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    const int64_t rounds = tiles / G, rem = tiles % G;
-    if (rounds < 1 || rem == 0 || rem * 8 > (int64_t)G * 7) return false;
-    const int64_t units = (tiles - (rounds - 1) * G) * (K / 128);
-    if (units * G >= ((int64_t)1 << 31)) return false;
-    *dp_tiles = (int)((rounds - 1) * G);
-    *sk_tiles = (int)(tiles - (rounds - 1) * G);
-    return true;
-}
+// Rows of the problem the persistent kernel covers with 256 x 256 tiles; the
+// rest (a multiple of 256 rows, from the bottom) get 128 x 128 tiles in a
+// second launch.  A 256-tile round that leaves most CUs idle costs almost a
+// full round (at 4352 x 12288 x 3072 the 48 tiles of the 17th tile-row took
+// 41 of 183 us on 256 CUs), while 128 x 128 tiles spread the same rows over
+// four times as many CUs.  The plan minimises
+//   ceil(big tiles / CUs) + kSmallRound * ceil(small tiles / CUs)
+// with kSmallRound the measured cost of a round of 128 x 128 tiles relative
+// to a round of 256 x 256 ones at the same K.
+constexpr double kSmallRound = 0.35;
 
-// Polls of a ready word before a head share gives up (about a second).
-// PHI_GEMM_SPLIT_SPIN overrides it (0: never wait), so a test can force the
-// give-up path from the host.
-int split_spin() {
-    const char* e = getenv("PHI_GEMM_SPLIT_SPIN");
-    if (e && *e) {
-        const long v = strtol(e, nullptr, 10);
-        return v < 0 ? 0 : (v > (1 << 30) ? (1 << 30) : (int)v);
+int64_t big_tile_rows(int64_t M, int64_t N, int G) {
+    const int64_t tm = (M + 255) / 256, tn = (N + 255) / 256, tn2 = (N + 127) / 128;
+    int64_t best_r = tm;
+    double best = (double)((tm * tn + G - 1) / G);
+    for (int64_t r = tm - 1; r >= 0; r--) {
+        const int64_t small = ((M - 256 * r + 127) / 128) * tn2;
+        const double cost = (double)((r * tn + G - 1) / G) + kSmallRound * (double)((small + G - 1) / G);
+        if (cost < best - 1e-9) {
+            best = cost;
+            best_r = r;
+        }
     }
-    return 1 << 20;
+    return best_r * 256 < M ? best_r * 256 : M;
 }
 
 // Vector-store / vector-load eligibility of the epilogue operands.
@@ -232,9 +229,10 @@ phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype,
 }
 
 size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-    int dp = 0, sk = 0;
-    if (M <= 0 || N <= 0 || K % 256 != 0 || K < 512 || !split_plan(M, N, K, num_cus(), &dp, &sk)) return 0;
-    return phi_dev::persist_workspace_bytes(num_cus());
+    (void)M;
+    (void)N;
+    (void)K;
+    return 0;
 }
 
 phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
@@ -245,7 +243,8 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, C, c_dtype, ldc, false);
     if (st != PHI_OK) return st;
-    if (workspace && !aligned(workspace, 256)) return fail(PHI_ERR_ALIGN, "%s: workspace must be 256-byte aligned", who);
+    (void)workspace;  // no kernel needs one (phi_hip_workspace_bytes is 0)
+    (void)ws_bytes;
     const int bk = bias_kind_of(bias, bias_dtype, &st);
     if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
     phi_dev::GemmParams p{};
@@ -267,17 +266,22 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.group_m = 4;
     set_vec_flags(p, c_dtype, ldc);
     const GemmKernel gk = gemm_kernel_for(M, N, K, persist_ok(C, c_dtype, N, K, lda, ldb, ldc));
-    if (gk == GK_PERSIST) {
+    if (gk == GK_PERSIST || gk == GK_PERSIST256 || gk == GK_PERSIST128) {
         const int G = num_cus();
-        int dp = 0, sk = 0;
-        if (workspace && ws_bytes >= phi_dev::persist_workspace_bytes(G) && split_plan(M, N, K, G, &dp, &sk)) {
-            p.sk_dp_tiles = dp;
-            p.sk_tiles = sk;
-            p.sk_cnt = (int*)workspace;
-            p.sk_part = (int8_t*)workspace + phi_dev::kPersistCounterBytes;
-            p.sk_spin = split_spin();
+        const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, N, G) : gk == GK_PERSIST256 ? M : 0;
+        if (rows > 0) {
+            phi_dev::GemmParams q = p;
+            q.M = (int)rows;
+            st = check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, q, G, 128), who);
+            if (st != PHI_OK || rows == M) return st;
         }
-        return check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, p, G), who);
+        // The remaining rows: A, sA and C start `rows` rows down.
+        phi_dev::GemmParams q = p;
+        q.M = (int)(M - rows);
+        q.A = A + rows * lda;
+        if (q.sA) q.sA = sA + rows;
+        q.C = (int8_t*)C + rows * ldc * (int64_t)c_elem_bytes(c_dtype);
+        return check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, q, G, 64), who);
     }
     if (gk != GK_TILE128) {
         p.schedule = gk == GK_TILE256W4 ? 1 : 0;

@@ -30,23 +30,14 @@ struct GemmParams {
     int c_vec16;         // C rows allow 16-byte stores (16-byte aligned, row pitch a multiple of 16 bytes)
     int s_vec;           // sB and bias allow 4-element vector loads (16-byte / 8-byte aligned)
     int schedule;        // 256x256 kernel: 0 = eight waves, 64-deep K; 1 = four waves, 128-deep K
-    // Persistent kernel's split phase (sk_tiles == 0: whole tiles only).
-    int sk_dp_tiles;     // tiles dealt whole first (a multiple of the grid)
-    int sk_tiles;        // tiles split by K-step ranges after them
-    int* sk_cnt;         // [0]: error count; then a ready word per split tile (zero between calls)
-    int8_t* sk_part;     // tail-share slots, one per workgroup
-    int sk_spin;         // polls of a ready word before a head gives up
 };
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
-// Persistent 256x256-tile kernel (K % 128 == 0, K >= 256): min(tiles, num_cus)
-// workgroups, or num_cus with a split phase.
-hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus);
-// Workspace of the split phase: error and ready words, then a 256 KB slot a workgroup.
-size_t persist_workspace_bytes(int num_cus);
-constexpr size_t kPersistCounterBytes = 4096;
+// Persistent kernel (K % 256 == 0): square tiles of 2 * wave_tile (128 -> 256 x 256,
+// 64 -> 128 x 128), min(tiles, num_cus) workgroups.
+hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile);
 
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,

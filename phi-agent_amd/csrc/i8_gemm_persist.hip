@@ -1,6 +1,7 @@
-// Persistent int8 GEMM for gfx950: one workgroup per CU walks 256 x 256
-// output tiles, and the next tile's first K-steps are loaded while the
-// current tile finishes, so no tile starts on an empty pipeline.
+// Persistent int8 GEMM for gfx950: one workgroup per CU walks square output
+// tiles (256 x 256, or 128 x 128 for the rows a whole number of 256-row
+// rounds does not cover), and the next tile's first K-steps are loaded while
+// the current tile finishes, so no tile starts on an empty pipeline.
 //
 //   acc[m,n] = sum_k A[m,k] * B[n,k]                  (exact int32)
 //   C[m,n]   = fma((float)acc * sA[m], sB[n], bias[n])  -> bf16 (RNE) / fp32 / raw int32
@@ -9,29 +10,29 @@
 // (core/kernels/int8_gemm.cpp:466-621, epilogue :588-620) and host gemm_int8
 // (core/host/quant.cpp:223-236).
 //
-// Design:
-//   * Four waves (one per SIMD), each 128 x 128 outputs as 4 x 4 blocks of
-//     v_mfma_i32_32x32x32_i8 with the 256 accumulators in AGPRs; 128-deep
-//     K-steps in two 64 KB LDS stages (A and B 256 rows x 128 bytes each).
+// Design (WT = wave tile, 128 or 64; the workgroup tile is 2WT x 2WT):
+//   * Four waves (one per SIMD), each WT x WT outputs as NB x NB blocks of
+//     v_mfma_i32_32x32x32_i8 (NB = WT/32) with the accumulators in AGPRs;
+//     128-deep K-steps in two LDS stages (A and B 2WT rows x 128 bytes each).
 //   * Operands go global -> LDS by buffer_load ... lds (no staging
 //     registers).  Each tile gets its own buffer resources, so rows past M or
-//     N read as zero and need no clamping; lane offsets stay in VGPRs and the
-//     per-load row offsets in SGPRs.  A load instruction moves eight whole
-//     128-byte rows; chunk c of row r sits in slot c ^ ((r >> 1) & 7), so the
-//     operand reads of 16 consecutive rows hit 16 distinct bank windows.
+//     N read as zero and need no clamping.  A load instruction moves eight
+//     whole 128-byte rows; chunk c of row r sits in slot c ^ ((r >> 1) & 7),
+//     so the operand reads of 16 consecutive rows hit 16 distinct bank
+//     windows.
 //   * One barrier per K-step, before its last quarter: every wave has then
 //     finished with the stage the last quarter's loads overwrite, and the
 //     next stage has landed.  Loads, LDS reads and MFMAs are interleaved
 //     with sched_group_barrier.
-//   * Cross-tile prefetch: the last two K-steps of a tile load the first two
-//     of the workgroup's next tile, together with that tile's row scales,
-//     column scales and bias (into one of two small LDS areas, by tile
-//     parity).  The first MFMA of a tile starts from a zero accumulator.
-//   * Epilogue: 32-row strips of the 128 x 128 wave tile are converted,
-//     written to a 4 KB per-wave LDS area (swizzled) and read back so every
-//     global store writes whole 128-byte rows (16 bytes a lane, 8 lanes a
-//     row); stores past row M or column N are dropped by the buffer range
-//     check or skipped.
+//   * Cross-tile prefetch: the last K-step pair of a tile loads the first
+//     pair of the workgroup's next tile, together with that tile's row
+//     scales, column scales and bias (into one of two small LDS areas, by
+//     tile parity).
+//   * Epilogue: 32-row strips of the wave tile are converted, written to a
+//     4 KB per-wave LDS area (swizzled) and read back so every global store
+//     writes whole 128-byte rows (16 bytes a lane, 8 lanes a row); stores
+//     past row M or column N are dropped by the buffer range check or
+//     skipped.  Output stores are non-temporal.
 //   * Tile order: workgroup ids are dealt round-robin to the 8 XCDs; each
 //     XCD owns a contiguous run of tiles in every round, walked group_m
 //     tile-rows at a time, so its concurrent tiles share A and B in its L2.
@@ -49,21 +50,24 @@ typedef unsigned int u32x4 __attribute__((__vector_size__(4 * sizeof(unsigned in
 // Raw buffer resource word 3 for gfx9-family: 32-bit data format, no swizzle.
 constexpr int kRsrcWord3 = 0x00020000;
 
-constexpr int BM = 256, BN = 256, BK = 128;
-constexpr int STG = BM * BK;            // 32 KB per operand per stage
-constexpr int DL = STG / 1024 / 4;      // 8 loads per operand per wave per K-step
-constexpr int EBYTES = 3 * 1024;        // per parity: sa | sb | bias (4 waves x 256 B each)
-constexpr int CHUNK = 4096;             // per-wave epilogue staging
+constexpr int BK = 128;
+constexpr int EBYTES = 3 * 1024;  // per parity: sa | sb | bias (4 waves x 256 B each)
+constexpr int CHUNK = 4096;       // per-wave epilogue staging
 
 constexpr int SG_MFMA = 0x008, SG_DSR = 0x100, SG_VMEM_R = 0x020;
 
 // Cache policy of the output stores: non-temporal.  The output is written
 // once and never read back by this kernel; letting it allocate in L2 evicts
-// the A and B strips the XCD's other tiles are still reading, and every CU
-// finishing a tile at about the same time turns that into a write-back burst
-// the next K-step's loads queue behind (measured: 17 % of the kernel time at
-// 4352 x 12288 x 3072).
+// the A and B strips the XCD's other tiles are still reading.
 constexpr int kStoreNT = 2;
+
+template <int WT>
+struct Cfg {
+    static constexpr int NB = WT / 32;         // MFMA blocks per wave dimension
+    static constexpr int BM = 2 * WT;          // workgroup tile (square)
+    static constexpr int STG = BM * BK;        // bytes per operand per stage
+    static constexpr int DL = STG / 1024 / 4;  // loads per operand per wave per K-step
+};
 
 // s_waitcnt vmcnt(0) lgkmcnt(0) (gfx9 encoding; expcnt untouched).
 __device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8)); }
@@ -96,56 +100,18 @@ __device__ __forceinline__ void tile_mn(const Shape& s, int logical, int& tm, in
     tn = in_group / gsz;
 }
 
+template <int WT>
 struct Frag {
-    v4i a[4], b[4];
+    v4i a[Cfg<WT>::NB], b[Cfg<WT>::NB];
 };
 
-// The workgroup's work list.  Tiles [0, dp_tiles) are dealt whole, round
-// by round: workgroup r (after the XCD remap) takes tiles r, r + G, ...
-// The split phase covers the remaining sk_tiles tiles as U = sk_tiles * KT
-// K-steps ("units"), cut into G contiguous ranges of whole unit pairs (KT is
-// even, so a tile boundary is a pair boundary); range r is
-// [2 * (r * (U/2) / G), 2 * ((r + 1) * (U/2) / G)).  A range starts or ends
-// inside a tile at most once each, so a workgroup holds at most two partial
-// tiles.
-// The launcher guarantees U * G < 2^31, so all of this is 32-bit.
-struct Plan {
-    int G, r, KT, ntiles, dp_tiles, n_dp, n_sk, nseg;
-    int U, s, e;  // split-phase units and this workgroup's range
-    int sk_t0;    // first split-phase tile of the range
-};
-
-// One stretch of K-steps [kb, ke) of logical tile `tile`.
-struct Seg {
-    int tile, kb, ke;
-};
-
-__device__ __forceinline__ Seg seg_at(const Plan& P, int i) {
-    Seg g;
-    if (i < P.n_dp) {
-        g.tile = i * P.G + P.r;
-        g.kb = 0;
-        g.ke = P.KT;
-    } else {
-        const int jt = P.sk_t0 + (i - P.n_dp);
-        const int t0 = jt * P.KT;
-        g.tile = P.dp_tiles + jt;
-        g.kb = max(P.s, t0) - t0;
-        g.ke = min(P.e, t0 + P.KT) - t0;
-    }
-    return g;
-}
-
-// The workgroup whose range holds split-phase unit u.
-__device__ __forceinline__ int sk_owner(int u, const Plan& P) { return ((u / 2 + 1) * P.G - 1) / (P.U / 2); }
-
-// Per-wave state.  The load cursor runs one K-step pair ahead of the
-// multiply, so it enters a segment during the previous segment's last pair;
-// after the last segment it reloads that segment's last pair (harmless).
+// Per-wave state.  The load cursor is the tile whose K-steps are being
+// loaded: it moves to the workgroup's next tile during a tile's last K-step
+// pair; after the last tile it reloads that tile's last pair (harmless).
 struct Wv {
     int8_t* la[2];
     int8_t* lb[2];
-    int8_t* le;   // two 3 KB epilogue-operand areas, one per segment parity
+    int8_t* le;  // two 3 KB epilogue-operand areas, one per tile parity
     int8_t* lc;
     __amdgpu_buffer_rsrc_t rA, rB;  // the load cursor's tile
     int cm0, cn0;
@@ -155,23 +121,26 @@ struct Wv {
 };
 
 // Points the load cursor at logical tile t.
+template <int WT>
 __device__ __forceinline__ void cursor_tile(Wv& w, const GemmParams& p, const Shape& s, int t) {
+    constexpr int BM = Cfg<WT>::BM;
     int tm, tn;
     tile_mn(s, t, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = tn * BM;
     w.cm0 = m0;
     w.cn0 = n0;
-    const int rows = min(BM, p.M - m0), cols = min(BN, p.N - n0);
+    const int rows = min(BM, p.M - m0), cols = min(BM, p.N - n0);
     w.rA = __builtin_amdgcn_make_buffer_rsrc((void*)(p.A + (int64_t)m0 * p.lda), (short)0, rows * (int)p.lda, kRsrcWord3);
     w.rB = __builtin_amdgcn_make_buffer_rsrc((void*)(p.B + (int64_t)n0 * p.ldb), (short)0, cols * (int)p.ldb, kRsrcWord3);
 }
 
 // Epilogue operands of the cursor's tile into LDS area le: wave w loads row
 // scales 64w..64w+63, column scales / fp32 bias 64w..64w+63 and (waves 0-1)
-// the bf16 bias words; past M or N they read as zero.  Issued with the
-// first K-step load of a segment.
+// the bf16 bias words; past M or N (or the tile) they read as zero.
+template <int WT>
 __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8_t* le) {
-    const int rows = min(BM, p.M - w.cm0), cols = min(BN, p.N - w.cn0);
+    constexpr int BM = Cfg<WT>::BM;
+    const int rows = min(BM, p.M - w.cm0), cols = min(BM, p.N - w.cn0);
     const __amdgpu_buffer_rsrc_t rSA =
         __builtin_amdgcn_make_buffer_rsrc((void*)(p.sA ? p.sA + w.cm0 : (const float*)p.A), (short)0,
                                           p.sA ? rows * 4 : 0, kRsrcWord3);
@@ -190,89 +159,82 @@ __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8
                                              w.wave * 256, 0, 0);
 }
 
-// K-step kl of the cursor's tile into stage S: 8 A and 8 B loads per wave,
+// K-step kl of the cursor's tile into stage S: DL A and DL B loads per wave,
 // with EPI plus the tile's epilogue operands into area le.
-template <int S, bool EPI>
+template <int WT, int S, bool EPI>
 __device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, int8_t* le) {
+    constexpr int DL = Cfg<WT>::DL;
     const int koff = kl * BK;
 #pragma unroll
     for (int j = 0; j < DL; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(w.la[S] + w.wave * (DL * 1024) + j * 1024), 16,
-                                                 w.voA[j & 1], koff + (w.wave * 64 + j * 8) * (int)p.lda, 0, 0);
+                                                 w.voA[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.lda, 0, 0);
 #pragma unroll
     for (int j = 0; j < DL; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(w.lb[S] + w.wave * (DL * 1024) + j * 1024), 16,
-                                                 w.voB[j & 1], koff + (w.wave * 64 + j * 8) * (int)p.ldb, 0, 0);
-    if constexpr (EPI) issue_epi(w, p, le);
+                                                 w.voB[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.ldb, 0, 0);
+    if constexpr (EPI) issue_epi<WT>(w, p, le);
 }
 
-template <int S, int Q>
-__device__ __forceinline__ void frag(Frag& f, const Wv& w) {
+template <int WT, int S, int Q>
+__device__ __forceinline__ void frag(Frag<WT>& f, const Wv& w) {
+    constexpr int NB = Cfg<WT>::NB;
     const int8_t* cA = w.la[S] + w.oA[Q];
     const int8_t* cB = w.lb[S] + w.oB[Q];
 #pragma unroll
-    for (int i = 0; i < 4; i++) f.a[i] = *(const v4i*)(cA + i * 32 * BK);
+    for (int i = 0; i < NB; i++) f.a[i] = *(const v4i*)(cA + i * 32 * BK);
 #pragma unroll
-    for (int j = 0; j < 4; j++) f.b[j] = *(const v4i*)(cB + j * 32 * BK);
+    for (int j = 0; j < NB; j++) f.b[j] = *(const v4i*)(cB + j * 32 * BK);
 }
 
-// Keeps the accumulators in their AGPRs across a region the register
-// allocator would otherwise split them around.
-__device__ __forceinline__ void pin_acc(v16i (&acc)[4][4]) {
+template <int WT>
+__device__ __forceinline__ void zero_acc(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB]) {
+    constexpr int NB = Cfg<WT>::NB;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) asm volatile("" : "+a"(acc[j][i]));
+        for (int i = 0; i < NB; i++) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 }
 
-__device__ __forceinline__ void zero_acc(v16i (&acc)[4][4]) {
+template <int WT>
+__device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB]) {
+    constexpr int NB = Cfg<WT>::NB;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-}
-
-template <bool ZERO>
-__device__ __forceinline__ void mma16(const Frag& f, v16i (&acc)[4][4]) {
-#pragma unroll
-    for (int q = 0; q < 16; q++) {
-        const int j = q / 4, i = q % 4;
-        if constexpr (ZERO) {
-            const v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], z, 0, 0, 0);
-        } else {
-            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[j][i], 0, 0, 0);
-        }
+    for (int q = 0; q < NB * NB; q++) {
+        const int j = q / NB, i = q % NB;
+        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[j][i], 0, 0, 0);
     }
 }
 
-// A quarter K-step: 16 MFMAs on cur, the eight fragment reads of quarter QN
+// A quarter K-step: NB^2 MFMAs on cur, the 2 NB fragment reads of quarter QN
 // of stage SN into nxt; with LOADS the cursor's K-step into stage S.  The
 // first MFMA goes ahead of the reads because the compiler's wait for cur is
 // a full lgkmcnt(0) that must not cover reads issued after it.
-template <int S, int SN, int QN, bool ZERO, bool LOADS, bool EPI>
-__device__ __forceinline__ void quarter(const Frag& cur, Frag& nxt, v16i (&acc)[4][4], const Wv& w,
-                                        const GemmParams& p, int kl, int8_t* le) {
-    mma16<ZERO>(cur, acc);
-    if constexpr (LOADS) issue<S, EPI>(w, p, kl, le);
-    frag<SN, QN>(nxt, w);
+template <int WT, int S, int SN, int QN, bool LOADS, bool EPI>
+__device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB],
+                                        const Wv& w, const GemmParams& p, int kl, int8_t* le) {
+    constexpr int NB = Cfg<WT>::NB, DL = Cfg<WT>::DL;
+    mma<WT>(cur, acc);
+    if constexpr (LOADS) issue<WT, S, EPI>(w, p, kl, le);
+    frag<WT, SN, QN>(nxt, w);
     __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
     if constexpr (LOADS) {
+        // Between the remaining MFMAs: the 2 DL loads and the 2 NB reads.
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
+        for (int t = 0; t < 2 * NB; t++) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, DL / NB / 2, 0);
             __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
+            if constexpr (NB / 2 > 1) __builtin_amdgcn_sched_group_barrier(SG_MFMA, NB / 2 - 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, DL / NB / 2, 0);
         }
     } else {
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
+        for (int t = 0; t < 2 * NB; t++) {
             __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 7, 0);
+        if constexpr (NB * NB - 1 - 2 * NB > 0) __builtin_amdgcn_sched_group_barrier(SG_MFMA, NB * NB - 1 - 2 * NB, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -280,38 +242,21 @@ __device__ __forceinline__ void quarter(const Frag& cur, Frag& nxt, v16i (&acc)[
 // One K-step on stage S.  With two stages the wait before the barrier covers
 // every load in flight: the next stage's (issued one K-step earlier).  After
 // the barrier every wave is done reading stage S, which the last quarter
-// refills with K-step kl of the cursor's tile (epilogue operands into le).
-template <int S, bool EPI>
-__device__ __forceinline__ void step(Frag& f0, v16i (&acc)[4][4], const Wv& w, const GemmParams& p, int kl,
-                                     int8_t* le) {
-    Frag f1;
-    quarter<S, S, 1, false, false, false>(f0, f1, acc, w, p, kl, le);
-    quarter<S, S, 2, false, false, false>(f1, f0, acc, w, p, kl, le);
-    quarter<S, S, 3, false, false, false>(f0, f1, acc, w, p, kl, le);
+// refills with K-step kl of the cursor's tile (EPI: epilogue operands into le).
+template <int WT, int S, bool EPI>
+__device__ __forceinline__ void step(Frag<WT>& f0, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const Wv& w,
+                                     const GemmParams& p, int kl, int8_t* le) {
+    Frag<WT> f1;
+    quarter<WT, S, S, 1, false, false>(f0, f1, acc, w, p, kl, le);
+    quarter<WT, S, S, 2, false, false>(f1, f0, acc, w, p, kl, le);
+    quarter<WT, S, S, 3, false, false>(f0, f1, acc, w, p, kl, le);
     wait_all();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    quarter<S, S ^ 1, 0, false, true, EPI>(f1, f0, acc, w, p, kl, le);
+    quarter<WT, S, S ^ 1, 0, true, EPI>(f1, f0, acc, w, p, kl, le);
 }
 
-// Split-phase partial tiles.  Every split tile has exactly two shares (the
-// launcher keeps each range at least a tile long): the tail, the tile's last
-// K-steps, which its workgroup multiplies first in its range, and the head,
-// the first K-steps, which another workgroup multiplies last in its range.
-// The tail workgroup leaves its accumulators in its 256 KB slot and raises
-// the tile's ready word; the head workgroup waits for the word (the tail is
-// normally done long before), starts its accumulators from the slot instead
-// of zero, and runs the epilogue.  Slot layout: wave, block (j, i), register
-// quad g, lane -- 16 bytes a lane, so both sides move whole 1 KB rows per
-// instruction in the accumulators' own layout.  Slots and ready words are
-// shared across XCDs, whose L2s are not coherent with each other: every
-// access is device-scope (sc1), which writes through and reads past the
-// non-coherent caches.
-constexpr int kDevScope = 16;  // sc1
-constexpr int kReadyBase = 64;  // sk_cnt[0]: error count; ready words from here (one cache line apart)
-constexpr int kSlotBytes = BM * BN * 4;
-
-// Scaled epilogue operands of this lane's four columns of group g in block j.
+// Scaled epilogue operands of this lane's four columns starting at tile column ct.
 __device__ __forceinline__ void col_operands(const GemmParams& p, const int8_t* e, int ct, v4f& sb, v4f& bz) {
     if (p.sb_scalar) {
         const float v = *(const float*)(e + 1024);
@@ -329,45 +274,43 @@ __device__ __forceinline__ void col_operands(const GemmParams& p, const int8_t* 
     }
 }
 
-// Where an epilogue writes: the output tile, or (raw int32, device scope) a
-// tail share's slot as a 256 x 256 row-major matrix.
-struct Dst {
-    __amdgpu_buffer_rsrc_t rs;  // the tile's rows
-    int pitch;                  // bytes per row
-    int n0, N;                  // first column; columns at or past N are dropped
-    int kind;                   // C_BF16 / C_F32 / C_I32
-    int dev;                    // device-scope stores (slots) instead of non-temporal ones
-};
-
-// Epilogue (operands in the LDS area e).  Lane l holds row l % 32 of
-// each A block and, in registers 4g..4g+3, columns 8g + 4(l/32) + 0..3 of each
-// B block.  Each 32-row strip goes through the wave's LDS area (16-byte slots
-// swizzled by row) and is stored as whole rows: bf16 in 32 x 64-column
-// pieces (128 bytes a row), fp32 / int32 in 32 x 32-column pieces.
-__device__ __forceinline__ void epilogue(v16i (&acc)[4][4], const GemmParams& p, const Dst& d, const Wv& w,
-                                         const int8_t* e) {
+// Epilogue of logical tile t (operands in the LDS area e).  Lane l holds row
+// l % 32 of each A block and, in registers 4g..4g+3, columns 8g + 4(l/32) +
+// 0..3 of each B block.  Each 32-row strip goes through the wave's LDS area
+// (16-byte slots swizzled by row) and is stored as whole rows: bf16 in
+// 32 x 64-column pieces (128 bytes a row), fp32 / int32 in 32 x 32-column
+// pieces.
+template <int WT>
+__device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const GemmParams& p, const Shape& s,
+                                         int t, const Wv& w, const int8_t* e) {
+    constexpr int NB = Cfg<WT>::NB, BM = Cfg<WT>::BM;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) asm volatile("" : "+a"(acc[j][i]));
-    const __amdgpu_buffer_rsrc_t rs = d.rs;
-    const int pitch = d.pitch;
+        for (int i = 0; i < NB; i++) asm volatile("" : "+a"(acc[j][i]));
+    int tm, tn;
+    tile_mn(s, t, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BM;
+    const int esz = p.c_kind == C_BF16 ? 2 : 4;
+    const int pitch = (int)p.ldc * esz;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (int8_t*)p.C + (int64_t)m0 * pitch, (short)0, min(BM, p.M - m0) * pitch, kRsrcWord3);
     int8_t* lc = w.lc;
-    const int colw = d.n0 + w.wn * 128;  // first column of this wave
-    float sa[4];
+    const int colw = n0 + w.wn * WT;  // first column of this wave
+    float sa[NB];
 #pragma unroll
-    for (int i = 0; i < 4; i++) sa[i] = *(const float*)(e + (w.wm * 128 + i * 32 + w.lrow) * 4);
-    if (d.kind == C_BF16) {
+    for (int i = 0; i < NB; i++) sa[i] = *(const float*)(e + (w.wm * WT + i * 32 + w.lrow) * 4);
+    if (p.c_kind == C_BF16) {
 #pragma unroll
-        for (int jp = 0; jp < 2; jp++) {
+        for (int jp = 0; jp < NB / 2; jp++) {
             v4f sb[2][4], bz[2][4];
 #pragma unroll
             for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                 for (int g = 0; g < 4; g++)
-                    col_operands(p, e, w.wn * 128 + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
+                    col_operands(p, e, w.wn * WT + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < NB; i++) {
 #pragma unroll
                 for (int jj = 0; jj < 2; jj++) {
                     v16i blk = acc[2 * jp + jj][i];
@@ -389,8 +332,9 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[4][4], const GemmParams& p,
                     const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
                     const u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
                     const int col = colw + jp * 64 + sl * 8;
-                    if (col < d.N)
-                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * 128 + i * 32 + r) * pitch + col * 2, 0, kStoreNT);
+                    if (col < p.N)
+                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * WT + i * 32 + r) * pitch + col * 2, 0,
+                                                               kStoreNT);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -399,20 +343,20 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[4][4], const GemmParams& p,
     }
     // fp32 / int32: 32 x 32 pieces, one block at a time.
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < NB; j++) {
         v4f sb[4], bz[4];
-        if (d.kind == C_F32) {
+        if (p.c_kind == C_F32) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) col_operands(p, e, w.wn * 128 + j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
+            for (int g = 0; g < 4; g++) col_operands(p, e, w.wn * WT + j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NB; i++) {
             v16i blk = acc[j][i];
             asm volatile("" : "+v"(blk));
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 u32x4 o;
-                if (d.kind == C_F32) {
+                if (p.c_kind == C_F32) {
 #pragma unroll
                     for (int q = 0; q < 4; q++)
                         o[q] = __float_as_uint(fmaf((float)blk[4 * g + q] * sa[i], sb[g][q], bz[g][q]));
@@ -428,68 +372,24 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[4][4], const GemmParams& p,
                 const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
                 const u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
                 const int col = colw + j * 32 + sl * 4;
-                if (col < d.N) {
-                    if (d.dev)
-                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * 128 + i * 32 + r) * pitch + col * 4, 0, kDevScope);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * 128 + i * 32 + r) * pitch + col * 4, 0, kStoreNT);
-                }
+                if (col < p.N)
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * WT + i * 32 + r) * pitch + col * 4, 0,
+                                                           kStoreNT);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
 
-// Head share of split tile jt: waits (bounded) for the tail's ready word and
-// loads the tail's slot into the accumulators.  A wait that runs out counts
-// in the workspace's error word and starts from zero instead (the tile is
-// then wrong and the caller must clear the workspace before reusing it).
-__device__ __forceinline__ void head_acquire(v16i (&acc)[4][4], const GemmParams& p, const Plan& P, const Wv& w,
-                                             int jt, int* flag) {
-    if (w.wave == 0 && w.lane == 0) {
-        int ready = 0;
-        for (int n = 0; n < p.sk_spin; n++) {
-            ready = __hip_atomic_load(p.sk_cnt + kReadyBase + jt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (ready) break;
-            __builtin_amdgcn_s_sleep(2);
-        }
-        if (!ready) __hip_atomic_fetch_add(p.sk_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = ready;
-    }
-    __builtin_amdgcn_s_barrier();
-    if (__builtin_amdgcn_readfirstlane(*flag) == 0) {
-        zero_acc(acc);
-        return;
-    }
-    const int q = sk_owner(jt * P.KT + P.KT - 1, P);  // the tail's workgroup
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.sk_part + (int64_t)q * kSlotBytes), (short)0, kSlotBytes, kRsrcWord3);
-    // Element (row, col) of the slot is at (row * 256 + col) * 4; lane l holds
-    // row wm*128 + 32i + l%32 and columns wn*128 + 32j + 8g + 4(l/32) + 0..3.
-    const int base = ((w.wm * 128 + w.lrow) * BN + w.wn * 128 + 4 * w.lhalf) * 4;
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            v16i blk;
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                    r, base + (i * 32 * BN + j * 32 + 8 * g) * 4, 0, kDevScope);
-#pragma unroll
-                for (int e = 0; e < 4; e++) blk[4 * g + e] = (int)v[e];
-            }
-            acc[j][i] = blk;
-        }
-}
-
 }  // namespace
 
+template <int WT>
 __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
+    using C = Cfg<WT>;
+    constexpr int NB = C::NB, STG = C::STG, DL = C::DL;
     __shared__ __align__(16) int8_t a0[STG], a1[STG], b0[STG], b1[STG];
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
-    __shared__ int flag;
     Wv w;
     w.lane = threadIdx.x & 63;
     w.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -498,26 +398,16 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     w.lrow = w.lane & 31;
     w.lhalf = w.lane >> 5;
     Shape s;
-    s.tiles_m = (p.M + BM - 1) / BM;
-    s.tiles_n = (p.N + BN - 1) / BN;
+    s.tiles_m = (p.M + C::BM - 1) / C::BM;
+    s.tiles_n = (p.N + C::BM - 1) / C::BM;
     s.ntiles = s.tiles_m * s.tiles_n;
     s.KT = p.K / BK;
     s.group_m = p.group_m;
     s.G = gridDim.x;
-    Plan P;
-    P.G = gridDim.x;
-    P.r = xcd_remap(blockIdx.x, P.G);
-    P.KT = s.KT;
-    P.ntiles = s.ntiles;
-    P.dp_tiles = p.sk_tiles ? p.sk_dp_tiles : s.ntiles;
-    P.n_dp = P.dp_tiles > P.r ? (P.dp_tiles - P.r - 1) / P.G + 1 : 0;
-    P.U = p.sk_tiles * P.KT;
-    P.s = 2 * (P.r * (P.U / 2) / P.G);
-    P.e = 2 * ((P.r + 1) * (P.U / 2) / P.G);
-    P.sk_t0 = P.s / P.KT;
-    P.n_sk = P.e > P.s ? (P.e - 1) / P.KT - P.sk_t0 + 1 : 0;
-    P.nseg = P.n_dp + P.n_sk;
-    if (P.nseg == 0) return;
+    // Tiles r, r + G, ... of this workgroup (r after the XCD remap).
+    const int r = xcd_remap(blockIdx.x, s.G);
+    if (r >= s.ntiles) return;
+    const int ntile = (s.ntiles - r - 1) / s.G + 1;
     w.la[0] = a0;
     w.la[1] = a1;
     w.lb[0] = b0;
@@ -526,117 +416,66 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     w.lc = cbuf + w.wave * CHUNK;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        w.oA[q] = (w.wm * 128 + w.lrow) * BK + swz8(w.lrow, 2 * q + w.lhalf) * 16;
-        w.oB[q] = (w.wn * 128 + w.lrow) * BK + swz8(w.lrow, 2 * q + w.lhalf) * 16;
+        w.oA[q] = (w.wm * WT + w.lrow) * BK + swz8(w.lrow, 2 * q + w.lhalf) * 16;
+        w.oB[q] = (w.wn * WT + w.lrow) * BK + swz8(w.lrow, 2 * q + w.lhalf) * 16;
     }
     // A load instruction covers 8 rows; lane l fetches row l/8 and the chunk
     // whose swizzled slot is l % 8 (the swizzle depends on the row's parity
     // within the load's 16-row pair).
 #pragma unroll
     for (int par = 0; par < 2; par++) {
-        const int r = par * 8 + (w.lane >> 3);
-        w.voA[par] = (w.lane >> 3) * (int)p.lda + swz8(r, w.lane & 7) * 16;
-        w.voB[par] = (w.lane >> 3) * (int)p.ldb + swz8(r, w.lane & 7) * 16;
+        const int rr = par * 8 + (w.lane >> 3);
+        w.voA[par] = (w.lane >> 3) * (int)p.lda + swz8(rr, w.lane & 7) * 16;
+        w.voB[par] = (w.lane >> 3) * (int)p.ldb + swz8(rr, w.lane & 7) * 16;
     }
-    // Every segment holds at least one K-step pair.  The epilogue operands
-    // of segment i go to area i % 2, loaded with its first K-step (during
-    // segment i-1's last pair), so at least one barrier separates a
-    // segment's epilogue from the load into its area for segment i+2.
-    {
-        const Seg g = seg_at(P, 0);
-        cursor_tile(w, p, s, g.tile);
-        issue<0, true>(w, p, g.kb, w.le);
-        issue<1, false>(w, p, g.kb + 1, w.le);
-    }
+    // The epilogue operands of the workgroup's i-th tile go to area i % 2,
+    // loaded with its first K-step (during tile i-1's last pair), so at
+    // least one barrier separates a tile's epilogue from the load into its
+    // area for tile i+2.
+    cursor_tile<WT>(w, p, s, r);
+    issue<WT, 0, true>(w, p, 0, w.le);
+    issue<WT, 1, false>(w, p, 1, w.le);
     wait_vm_lgkm0<2 * DL>();  // the first K-step and its operands have landed
     __builtin_amdgcn_s_barrier();
-    Frag f0;
-    frag<0, 0>(f0, w);
-    v16i acc[4][4];
-    for (int seg = 0;;) {
-        const Seg g = seg_at(P, seg);
-        const bool whole = g.kb == 0 && g.ke == P.KT;
-        const int jt = g.tile - P.dp_tiles;  // split-phase tile index
-        if (!whole && g.kb == 0) head_acquire(acc, p, P, w, jt, &flag);
-        else zero_acc(acc);
-        int8_t* le = w.le + (seg & 1) * EBYTES;
-        for (int k = g.kb; k < g.ke - 2; k += 2) {
-            step<0, false>(f0, acc, w, p, k + 2, le);
-            step<1, false>(f0, acc, w, p, k + 3, le);
+    Frag<WT> f0;
+    frag<WT, 0, 0>(f0, w);
+    v16i acc[NB][NB];
+    for (int i = 0;;) {
+        const int t = r + i * s.G;
+        int8_t* le = w.le + (i & 1) * EBYTES;
+        zero_acc<WT>(acc);
+        for (int k = 0; k < s.KT - 2; k += 2) {
+            step<WT, 0, false>(f0, acc, w, p, k + 2, le);
+            step<WT, 1, false>(f0, acc, w, p, k + 3, le);
         }
-        // The last pair: the cursor moves to the next segment, if any.
-        int kn = g.ke - 2;
+        // The last pair: the cursor moves to the next tile, if any.
+        int kn = s.KT - 2;
         int8_t* ln = le;
-        if (seg + 1 < P.nseg) {
-            const Seg h = seg_at(P, seg + 1);
-            cursor_tile(w, p, s, h.tile);
-            kn = h.kb;
-            ln = w.le + ((seg + 1) & 1) * EBYTES;
+        if (i + 1 < ntile) {
+            cursor_tile<WT>(w, p, s, t + s.G);
+            kn = 0;
+            ln = w.le + ((i + 1) & 1) * EBYTES;
         }
-        step<0, true>(f0, acc, w, p, kn, ln);
-        step<1, false>(f0, acc, w, p, kn + 1, ln);
-        // A whole or head tile goes to C; a tail share goes to this
-        // workgroup's slot as raw int32 and then raises the ready word.
-        const bool tail = g.kb != 0;
-        Dst d;
-        if (!tail) {
-            int tm, tn;
-            tile_mn(s, g.tile, tm, tn);
-            const int m0 = tm * BM;
-            d.kind = p.c_kind;
-            d.pitch = (int)p.ldc * (p.c_kind == C_BF16 ? 2 : 4);
-            d.rs = __builtin_amdgcn_make_buffer_rsrc((int8_t*)p.C + (int64_t)m0 * d.pitch, (short)0,
-                                                     min(BM, p.M - m0) * d.pitch, kRsrcWord3);
-            d.n0 = tn * BN;
-            d.N = p.N;
-            d.dev = 0;
-        } else {
-            d.kind = C_I32;
-            d.pitch = BN * 4;
-            d.rs = __builtin_amdgcn_make_buffer_rsrc(p.sk_part + (int64_t)P.r * kSlotBytes, (short)0, kSlotBytes,
-                                                     kRsrcWord3);
-            d.n0 = 0;
-            d.N = BN;
-            d.dev = 1;
-        }
-        epilogue(acc, p, d, w, le);
-        if (tail) {
-            wait_all();  // every row of this wave's share has reached device scope
-            __builtin_amdgcn_s_barrier();
-            if (w.wave == 0 && w.lane == 0)
-                __hip_atomic_store(p.sk_cnt + kReadyBase + jt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else if (!whole && w.wave == 0 && w.lane == 0) {
-            __hip_atomic_store(p.sk_cnt + kReadyBase + jt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (++seg == P.nseg) break;
+        step<WT, 0, true>(f0, acc, w, p, kn, ln);
+        step<WT, 1, false>(f0, acc, w, p, kn + 1, ln);
+        epilogue<WT>(acc, p, s, t, w, le);
+        if (++i == ntile) break;
     }
     // The reloads past the last K-step still write LDS: let them land.
     wait_all();
 }
 
-hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus) {
-    if (p.K % (2 * BK) != 0 || p.K < 4 * BK) return hipErrorInvalidValue;
-    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    int grid = tiles < num_cus ? tiles : num_cus;
-    if (p.sk_tiles) {
-        // The split phase takes the whole device, and every range must be at
-        // least a tile long (so a tile has at most two shares) and fewer than
-        // two tiles (one ready word per tile fits the counter area).
-        const int64_t units = (int64_t)p.sk_tiles * (p.K / BK);
-        if (p.sk_dp_tiles % num_cus != 0 || p.sk_dp_tiles + p.sk_tiles != tiles || p.sk_tiles < num_cus ||
-            p.sk_tiles >= 2 * num_cus || units * num_cus >= ((int64_t)1 << 31) ||
-            (int64_t)(kReadyBase + p.sk_tiles) * 4 > (int64_t)kPersistCounterBytes || p.sk_spin < 0 || !p.sk_cnt ||
-            !p.sk_part)
-            return hipErrorInvalidValue;
-        grid = num_cus;
-    }
-    hipLaunchKernelGGL(i8_gemm_persist_kernel, dim3(grid), dim3(256), 0, stream, p);
+hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile) {
+    if (p.K % (2 * BK) != 0 || p.K < 2 * BK) return hipErrorInvalidValue;
+    if (wave_tile != 128 && wave_tile != 64) return hipErrorInvalidValue;
+    const int bm = 2 * wave_tile;
+    const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
+    const int grid = tiles < num_cus ? tiles : num_cus;
+    if (wave_tile == 128)
+        hipLaunchKernelGGL(i8_gemm_persist_kernel<128>, dim3(grid), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(i8_gemm_persist_kernel<64>, dim3(grid), dim3(256), 0, stream, p);
     return hipGetLastError();
-}
-
-size_t persist_workspace_bytes(int num_cus) {
-    // The error word and ready words, then one tail slot per workgroup.
-    return kPersistCounterBytes + (size_t)num_cus * kSlotBytes;
 }
 
 }  // namespace phi_dev

@@ -149,31 +149,7 @@ def quant_rotate(x: torch.Tensor, *, qmax: float = 127.0, round_mode: int = ROUN
 
 
 # ---------------------------------------------------------------- A4-A6
-_workspaces: dict = {}
-
-
-def workspace_for(M: int, N: int, K: int, device, stream=None) -> torch.Tensor | None:
-    """The GEMM workspace phi_hip_workspace_bytes asks for (None when it asks
-    for none), one zero-filled buffer per (device, stream), grown on demand.
-    The library leaves it zeroed after every call; calls that share one on
-    different streams at the same time would race, hence one per stream."""
-    n = load().phi_hip_workspace_bytes(M, N, K)
-    if n == 0:
-        return None
-    dev = torch.device(device)
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(), _stream(stream).value)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < n:
-        ws = torch.zeros(n, dtype=torch.uint8, device=dev)
-        _workspaces[key] = ws
-    return ws
-
-
-def _ws(workspace, M, N, K, device, stream):
-    if isinstance(workspace, str):
-        if workspace != "auto":
-            raise ValueError("workspace must be a tensor, None or 'auto'")
-        workspace = workspace_for(M, N, K, device, stream)
+def _ws(workspace):
     if workspace is None:
         return None, 0
     _require_device(workspace)
@@ -182,18 +158,16 @@ def _ws(workspace, M, N, K, device, stream):
 
 def i8_gemm(A: torch.Tensor, B: torch.Tensor, sA: torch.Tensor | None, sB: torch.Tensor | None,
             bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
-            C: torch.Tensor | None = None, workspace="auto", stream=None) -> torch.Tensor:
-    """C = fma((float)(A . B^T) * sA, sB, bias) in out_dtype (int32: raw acc).
-
-    workspace: 'auto' (a cached zero-filled buffer sized by
-    phi_hip_workspace_bytes), None (no split schedule) or a device tensor."""
+            C: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+            stream=None) -> torch.Tensor:
+    """C = fma((float)(A . B^T) * sA, sB, bias) in out_dtype (int32: raw acc)."""
     _require_device(A, B, sA, sB, bias, C)
     M, K = A.shape
     N = B.shape[0]
     if C is None:
         C = torch.empty((M, N), dtype=out_dtype, device=A.device)
     sb_scalar = 1 if (sB is not None and sB.numel() == 1) else 0
-    wp, wn = _ws(workspace, M, N, K, A.device, stream)
+    wp, wn = _ws(workspace)
     _check(load().phi_hip_i8_gemm(_stream(stream), _ptr(A), A.stride(0), _ptr(B), B.stride(0),
                                   _ptr(sA), _ptr(sB), sb_scalar, _ptr(bias),
                                   _dt(bias) if bias is not None else F32, _ptr(C), _dt(C),
@@ -205,7 +179,7 @@ def q8_linear(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
               bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
               q8: torch.Tensor | None = None, s8: torch.Tensor | None = None,
               C: torch.Tensor | None = None, round_mode: int = ROUND_HALF_AWAY,
-              workspace="auto", stream=None) -> torch.Tensor:
+              workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
     """The W8A8 linear: rotate+quantise x into q8/s8, int8 GEMM, epilogue."""
     _require_device(x, W, sW, bias, q8, s8, C)
     M, K = x.shape
@@ -216,7 +190,7 @@ def q8_linear(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
         s8 = torch.empty((M,), dtype=torch.float32, device=x.device)
     if C is None:
         C = torch.empty((M, N), dtype=out_dtype, device=x.device)
-    wp, wn = _ws(workspace, M, N, K, x.device, stream)
+    wp, wn = _ws(workspace)
     _check(load().phi_hip_q8_linear(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(W),
                                     W.stride(0), _ptr(sW), 1 if sW.numel() == 1 else 0,
                                     _ptr(bias), _dt(bias) if bias is not None else F32, N,

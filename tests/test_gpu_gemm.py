@@ -27,7 +27,7 @@ def rand_i8(shape, seed):
     return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
 
 
-KERNELS = ["auto", "persist", "tile256", "tile256w4", "tile128"]
+KERNELS = ["auto", "persist", "persist256", "persist128", "tile256", "tile256w4", "tile128"]
 
 
 @pytest.fixture(params=KERNELS)
@@ -43,11 +43,12 @@ def kernel(request, monkeypatch):
 @pytest.mark.parametrize("M,N,K", [(1, 1, 64), (1, 37, 128), (5, 300, 192), (256, 256, 3072),
                                    (257, 129, 640), (300, 1000, 256), (512, 384, 1024),
                                    (33, 4100, 64), (1000, 70, 576), (513, 777, 320),
-                                   # shapes the persistent kernel takes (K % 256 == 0, K >= 512,
-                                   # N % 4 == 0): partial tiles in M and N, one to several tiles
-                                   # per workgroup, the shortest K it accepts
+                                   # shapes the persistent kernel takes (K % 256 == 0, N % 4 == 0):
+                                   # partial tiles in M and N, one to several tiles per workgroup,
+                                   # the shortest K it accepts
                                    (1, 4, 512), (300, 1000, 512), (257, 264, 768), (777, 520, 1280),
-                                   (2049, 2052, 512), (4100, 4104, 1024)])
+                                   (2049, 2052, 512), (4100, 4104, 1024), (129, 136, 256),
+                                   (640, 384, 256)])
 def test_int32_accumulators_exact(dev, orc, kernel, M, N, K):
     A, B = rand_i8((M, K), M + K), rand_i8((N, K), N + 7)
     C = Q.i8_gemm(A.to(dev), B.to(dev), None, None, out_dtype=torch.int32)
@@ -185,42 +186,35 @@ def test_contract_errors(dev):
         Q.i8_gemm(A, B[:, :64].contiguous(), None, None, out_dtype=torch.int32)
 
 
-# ---------------------------------------------------------------- split schedule
+# ---------------------------------------------------------------- two tile sizes
 # Shapes whose 256 x 256 tiles leave a partial last round on 256 CUs: the
-# persistent kernel then cuts the last rounds into K-step ranges and a tile's
-# two shares meet through the workspace.
-SPLIT_SHAPES = [(4352, 4352, 512), (4352, 12288, 512), (2304, 8192, 1024), (4352, 9216, 768),
-                (4100, 4104, 1536)]
+# persistent path then covers the bottom rows with 128 x 128 tiles in a second
+# launch.  The default plan, each tile size alone, and the register-staged
+# kernel must all give the same exact product.
+MIXED_SHAPES = [(4352, 12288, 512), (4352, 9216, 768), (4352, 4352, 256), (4100, 4104, 512),
+                (2304, 8192, 1024), (300, 1000, 512)]
 
 
 def exact_product(A, B):
     return (A.double() @ B.double().t()).to(torch.int64)
 
 
-@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
-def test_split_schedule_exact(dev, lib, monkeypatch, M, N, K):
-    monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
-    monkeypatch.setenv("PHI_GEMM_SPLIT", "1")
-    n = lib.phi_hip_workspace_bytes(M, N, K)
-    assert n > 0, "shape expected to take the split schedule"
+@pytest.mark.parametrize("M,N,K", MIXED_SHAPES)
+def test_tile_size_plans_exact(dev, monkeypatch, M, N, K):
     A = rand_i8((M, K), M + 3).to(dev)
     B = rand_i8((N, K), N + 5).to(dev)
-    ws = torch.zeros(n, dtype=torch.uint8, device=dev)
     want = exact_product(A, B)
-    for call in range(2):  # the second call reuses the ready words the first left clear
-        C = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=ws)
+    for kern in ("persist", "persist256", "persist128"):
+        monkeypatch.setenv("PHI_GEMM_KERNEL", kern)
+        C = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
         torch.cuda.synchronize()
-        assert torch.equal(C.to(torch.int64), want), f"call {call}"
-        assert torch.count_nonzero(ws[:4096]) == 0, "error or ready words left set"
-    C0 = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=None)  # whole tiles only
-    assert torch.equal(C0.to(torch.int64), want)
+        assert torch.equal(C.to(torch.int64), want), kern
 
 
 @pytest.mark.parametrize("out", ["bf16", "f32"])
-def test_split_schedule_epilogue(dev, orc, monkeypatch, out):
-    """Head tiles run the scaled epilogue on the sum of both shares."""
+def test_tile_size_plan_epilogue(dev, orc, monkeypatch, out):
+    """The second launch's row offset reaches the row scales and the output."""
     monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
-    monkeypatch.setenv("PHI_GEMM_SPLIT", "1")
     M, N, K = 4352, 4352, 512
     A, B = rand_i8((M, K), 41), rand_i8((N, K), 42)
     g = torch.Generator().manual_seed(43)
@@ -233,24 +227,3 @@ def test_split_schedule_epilogue(dev, orc, monkeypatch, out):
     want = orc.epilogue(acc, sa.numpy(), sb.numpy(), u16(bias), out=out)
     got = u16(C) if out == "bf16" else C.cpu().numpy().view(np.uint32)
     assert np.array_equal(got, want if out == "bf16" else want.view(np.uint32))
-
-
-def test_split_schedule_gives_up_without_hanging(dev, lib, monkeypatch):
-    """A head share whose wait runs out (forced from the host: zero polls)
-    counts the failure in the workspace's error word instead of waiting; the
-    kernel still finishes, and the whole-tile schedule is unaffected."""
-    monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
-    monkeypatch.setenv("PHI_GEMM_SPLIT", "1")
-    M, N, K = 4352, 4352, 512
-    A, B = rand_i8((M, K), 51).to(dev), rand_i8((N, K), 52).to(dev)
-    n = lib.phi_hip_workspace_bytes(M, N, K)
-    assert n > 0
-    ws = torch.zeros(n, dtype=torch.uint8, device=dev)
-    monkeypatch.setenv("PHI_GEMM_SPLIT_SPIN", "0")
-    Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=ws)
-    torch.cuda.synchronize()
-    errors = int(ws[:4].view(torch.int32).item())
-    assert errors > 0
-    monkeypatch.delenv("PHI_GEMM_SPLIT_SPIN")
-    C = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32, workspace=None)
-    assert torch.equal(C.to(torch.int64), exact_product(A, B))
