@@ -158,10 +158,14 @@ phi_status phi_hip_w4a8_prepare(phi_stream_t stream, const phi_w4a8_weight* w, i
                                 float* s);
 
 /*
- * W4A8 linear with nibbles unpacked in registers through the prepared table.
+ * W4A8 linear with nibbles unpacked through the prepared table.
  * Equal, bit for bit, to phi_hip_w4a8_expand followed by phi_hip_q8_linear.
  *   codes [N, codes_row_bytes] nibble4; lut [N, K/group, 16]; s_w [N].
  *   group % 64 == 0.
+ *   workspace: optional, phi_hip_w4a8_workspace_bytes() bytes (16-byte
+ *     aligned).  Given it, a call with many rows expands the codes once into
+ *     it (int8 [N, K]) and runs the W8A8 GEMM; without it, or for few rows,
+ *     the GEMM expands the codes in registers tile by tile.  Same bits either way.
  */
 phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,
                                int64_t M, int64_t K, const uint8_t* codes,
@@ -192,6 +196,11 @@ phi_status phi_hip_i8_gemv_batched(phi_stream_t stream, const int8_t* q8, const 
                                    int64_t M, int64_t K, int64_t N, const phi_gemv_item* items,
                                    int n_items, int bias_dtype, int c_dtype, void* workspace,
                                    size_t ws_bytes);
+
+/* Workspace with which phi_hip_w4a8_linear expands the codes once per call
+ * (N*K bytes; 0 when the shape keeps the in-register expansion).  No reference
+ * counterpart: the reference expands at load time (dispatch_w4a8_expand). */
+size_t phi_hip_w4a8_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 
 /* Workspace for phi_hip_i8_gemv_batched (holds the item table on the device). */
 size_t phi_hip_gemv_workspace_bytes(int n_items);

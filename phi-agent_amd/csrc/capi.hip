@@ -75,7 +75,10 @@ int c_kind_of(int c_dtype) {
 
 size_t c_elem_bytes(int c_dtype) { return c_dtype == PHI_BF16 ? 2 : 4; }
 
-constexpr int64_t kMaxRotK = 24576;  // rotated row held in LDS: 96 groups = 129 KB
+constexpr int64_t kMaxRotK = 24576;
+// Rows from which phi_hip_w4a8_linear expands the codes into the workspace
+// (when given one) rather than in registers per tile.
+constexpr int64_t kW4ExpandMinRows = 512;  // rotated row held in LDS: 96 groups = 129 KB
 
 // Shared validation of the GEMM operands (A [M,lda], B [N,ldb]).
 phi_status check_gemm(const char* who, const int8_t* A, int64_t lda, const void* B, int64_t ldb,
@@ -185,6 +188,28 @@ int64_t big_tile_rows(int64_t M, int64_t N, int G) {
     return best_r * 256 < M ? best_r * 256 : M;
 }
 
+// The persistent kernel over the whole problem: 256 x 256 tiles for the rows
+// big_tile_rows() gives it, then 128 x 128 tiles for the rest (A, sA, C and
+// the output rows offset; B, sB and bias are shared).
+hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p, GemmKernel gk, bool w4, int c_dtype,
+                               int64_t ldc) {
+    const int G = num_cus();
+    const int64_t M = p.M;
+    const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, p.N, G) : gk == GK_PERSIST256 ? M : 0;
+    if (rows > 0) {
+        phi_dev::GemmParams q = p;
+        q.M = (int)rows;
+        const hipError_t e = phi_dev::launch_i8_gemm_persist(stream, q, G, 128, w4);
+        if (e != hipSuccess || rows == M) return e;
+    }
+    phi_dev::GemmParams q = p;
+    q.M = (int)(M - rows);
+    q.A = p.A + rows * p.lda;
+    if (q.sA) q.sA = p.sA + rows;
+    q.C = (int8_t*)p.C + rows * ldc * (int64_t)c_elem_bytes(c_dtype);
+    return phi_dev::launch_i8_gemm_persist(stream, q, G, 64, w4);
+}
+
 // Vector-store / vector-load eligibility of the epilogue operands.
 void set_vec_flags(phi_dev::GemmParams& p, int c_dtype, int64_t ldc) {
     const size_t cal = c_dtype == PHI_BF16 ? 8 : 16;
@@ -266,23 +291,8 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.group_m = 4;
     set_vec_flags(p, c_dtype, ldc);
     const GemmKernel gk = gemm_kernel_for(M, N, K, persist_ok(C, c_dtype, N, K, lda, ldb, ldc));
-    if (gk == GK_PERSIST || gk == GK_PERSIST256 || gk == GK_PERSIST128) {
-        const int G = num_cus();
-        const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, N, G) : gk == GK_PERSIST256 ? M : 0;
-        if (rows > 0) {
-            phi_dev::GemmParams q = p;
-            q.M = (int)rows;
-            st = check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, q, G, 128), who);
-            if (st != PHI_OK || rows == M) return st;
-        }
-        // The remaining rows: A, sA and C start `rows` rows down.
-        phi_dev::GemmParams q = p;
-        q.M = (int)(M - rows);
-        q.A = A + rows * lda;
-        if (q.sA) q.sA = sA + rows;
-        q.C = (int8_t*)C + rows * ldc * (int64_t)c_elem_bytes(c_dtype);
-        return check_hip(phi_dev::launch_i8_gemm_persist((hipStream_t)stream, q, G, 64), who);
-    }
+    if (gk == GK_PERSIST || gk == GK_PERSIST256 || gk == GK_PERSIST128)
+        return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, false, c_dtype, ldc), who);
     if (gk != GK_TILE128) {
         p.schedule = gk == GK_TILE256W4 ? 1 : 0;
         return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);
@@ -378,7 +388,6 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
                                void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8,
                                int round_mode, void* workspace, size_t ws_bytes) {
     static const char* who = "w4a8_linear";
-    (void)workspace;
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     if (!q8 || !s8) return fail(PHI_ERR_ARG, "%s: the int8 path needs activation scratch", who);
     if (!lut || !s_w) return fail(PHI_ERR_ARG, "%s: missing prepared table or row scales", who);
@@ -387,7 +396,6 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     if (group <= 0 || group % 64 != 0 || K % group != 0 || (group & (group - 1)) != 0)
         return fail(PHI_ERR_SHAPE, "%s: group=%lld must be a power of two, a multiple of 64 and divide K", who, (long long)group);
     if (!aligned(lut, 16)) return fail(PHI_ERR_ALIGN, "%s: lut must be 16-byte aligned", who);
-    (void)ws_bytes;  // the in-register W4A8 kernel needs no workspace
     const int bk = bias_kind_of(bias, bias_dtype, &st);
     if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
     st = phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
@@ -414,7 +422,44 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     int sh = 0;
     while ((1ll << sh) < group) sh++;
     p.group_shift = sh;
+    const char* e = getenv("PHI_GEMM_KERNEL");
+    const bool force_staged = e && strcmp(e, "tile128") == 0;
+    // With a workspace (phi_hip_w4a8_workspace_bytes), large M expands the
+    // codes once into it and runs the W8A8 GEMM: one table lookup per weight
+    // instead of one per weight per 256-row tile.
+    const size_t need = phi_hip_w4a8_workspace_bytes(M, N, K, group);
+    if (!force_staged && need > 0 && workspace && ws_bytes >= need && aligned(workspace, 16) &&
+        aligned(codes, 16) && codes_row_bytes % 16 == 0 && persist_ok(C, c_dtype, N, K, K, K, ldc)) {
+        st = check_hip(phi_dev::launch_w4_lut_expand((hipStream_t)stream, p, (int8_t*)workspace), who);
+        if (st != PHI_OK) return st;
+        phi_dev::GemmParams g = p;
+        g.B = (const int8_t*)workspace;
+        g.ldb = K;
+        g.lut = nullptr;
+        set_vec_flags(g, c_dtype, ldc);
+        GemmKernel gk = GK_PERSIST;
+        if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;
+        if (e && strcmp(e, "persist128") == 0) gk = GK_PERSIST128;
+        return check_hip(launch_persist_plan((hipStream_t)stream, g, gk, false, c_dtype, ldc), who);
+    }
+    // In registers: the persistent kernel takes whole 128-column groups and
+    // 16-byte code rows; PHI_GEMM_KERNEL=tile128 forces the register-staged
+    // kernel (A/B switch).
+    if (!force_staged && group % 128 == 0 && aligned(codes, 16) && codes_row_bytes % 16 == 0 &&
+        persist_ok(C, c_dtype, N, K, K, codes_row_bytes, ldc)) {
+        set_vec_flags(p, c_dtype, ldc);
+        GemmKernel gk = GK_PERSIST;
+        if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;
+        if (e && strcmp(e, "persist128") == 0) gk = GK_PERSIST128;
+        return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, true, c_dtype, ldc), who);
+    }
     return check_hip(phi_dev::launch_w4a8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
+}
+
+size_t phi_hip_w4a8_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
+    // The expand-then-W8A8 path pays off once enough rows share each weight.
+    if (M < kW4ExpandMinRows || N <= 0 || K <= 0 || K % 256 != 0 || group <= 0 || group % 128 != 0) return 0;
+    return (size_t)N * (size_t)K;
 }
 
 size_t phi_hip_gemv_workspace_bytes(int n_items) {

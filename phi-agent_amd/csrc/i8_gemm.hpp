@@ -36,8 +36,11 @@ hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
 // Persistent kernel (K % 256 == 0): square tiles of 2 * wave_tile (128 -> 256 x 256,
-// 64 -> 128 x 128), min(tiles, num_cus) workgroups.
-hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile);
+// 64 -> 128 x 128), min(tiles, num_cus) workgroups.  w4: B is packed codes plus
+// the per-(row, group) table (group a multiple of 128, code rows 16-byte aligned).
+hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile, bool w4);
+// The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
+hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);
 
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,

@@ -54,12 +54,16 @@ constexpr int BK = 128;
 constexpr int EBYTES = 3 * 1024;  // per parity: sa | sb | bias (4 waves x 256 B each)
 constexpr int CHUNK = 4096;       // per-wave epilogue staging
 
-constexpr int SG_MFMA = 0x008, SG_DSR = 0x100, SG_VMEM_R = 0x020;
+constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_R = 0x020, SG_DSR = 0x100, SG_DSW = 0x200;
 
 // Cache policy of the output stores: non-temporal.  The output is written
 // once and never read back by this kernel; letting it allocate in L2 evicts
 // the A and B strips the XCD's other tiles are still reading.
 constexpr int kStoreNT = 2;
+
+#ifndef W4_Q1
+#define W4_Q1 1
+#endif
 
 template <int WT>
 struct Cfg {
@@ -105,6 +109,43 @@ struct Frag {
     v4i a[Cfg<WT>::NB], b[Cfg<WT>::NB];
 };
 
+// W4 operand: B is packed 4-bit codes (low nibble = even column) with a
+// per-(row, group) 16-entry int8 table.  Each thread owns BM/256 of a B row
+// per K-step: it loads that row's codes (64 bytes for a 256-row tile, 32 for
+// 128) and the row's table for the K-step's group into registers one K-step
+// ahead, and expands them into the int8 B stage between the next step's
+// MFMAs, so the MFMA core is unchanged.
+template <int WT>
+struct W4Regs {
+    static constexpr int C = Cfg<WT>::BM / 64;  // 16-byte code loads per thread per K-step
+    u32x4 c[C];
+    u32x4 t;
+};
+
+// Four codes (bytes of x, each 0..15) -> four int8 through the 16-byte table
+// t: v_perm_b32 picks from entries 0..7 and 8..15 by the low three bits, and
+// bit 3 chooses (selector bytes 0x0c / 0x0d give 0x00 / 0xff).
+__device__ __forceinline__ uint32_t lut4b(uint32_t x, const u32x4& t) {
+    const uint32_t sel = x & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t[3], t[2], sel);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((x >> 3) & 0x01010101u) | 0x0c0c0c0cu);
+    return (hi & m) | (lo & ~m);
+}
+
+// 16 codes (8 bytes) -> 16 int8 operand bytes in column order.
+__device__ __forceinline__ v4i expand16b(uint32_t c0, uint32_t c1, const u32x4& t) {
+    const uint32_t e0 = lut4b(c0 & 0x0f0f0f0fu, t), o0 = lut4b((c0 >> 4) & 0x0f0f0f0fu, t);
+    const uint32_t e1 = lut4b(c1 & 0x0f0f0f0fu, t), o1 = lut4b((c1 >> 4) & 0x0f0f0f0fu, t);
+    // e holds columns 0,2,4,6 and o columns 1,3,5,7: interleave.
+    v4i r;
+    r.x = (int)__builtin_amdgcn_perm(o0, e0, 0x05010400u);
+    r.y = (int)__builtin_amdgcn_perm(o0, e0, 0x07030602u);
+    r.z = (int)__builtin_amdgcn_perm(o1, e1, 0x05010400u);
+    r.w = (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u);
+    return r;
+}
+
 // Per-wave state.  The load cursor is the tile whose K-steps are being
 // loaded: it moves to the workgroup's next tile during a tile's last K-step
 // pair; after the last tile it reloads that tile's last pair (harmless).
@@ -113,15 +154,17 @@ struct Wv {
     int8_t* lb[2];
     int8_t* le;  // two 3 KB epilogue-operand areas, one per tile parity
     int8_t* lc;
-    __amdgpu_buffer_rsrc_t rA, rB;  // the load cursor's tile
+    __amdgpu_buffer_rsrc_t rA, rB;  // the load cursor's tile (W4: rB over the codes)
+    __amdgpu_buffer_rsrc_t rL;      // W4: the cursor's tile's table rows
     int cm0, cn0;
     int voA[2], voB[2];
+    int w4row, w4half, vo4, voL;    // W4: this thread's B row, half, code and table offsets
     int wave, wm, wn, lane, lrow, lhalf;
     int oA[4], oB[4];
 };
 
 // Points the load cursor at logical tile t.
-template <int WT>
+template <int WT, bool W4>
 __device__ __forceinline__ void cursor_tile(Wv& w, const GemmParams& p, const Shape& s, int t) {
     constexpr int BM = Cfg<WT>::BM;
     int tm, tn;
@@ -132,6 +175,10 @@ __device__ __forceinline__ void cursor_tile(Wv& w, const GemmParams& p, const Sh
     const int rows = min(BM, p.M - m0), cols = min(BM, p.N - n0);
     w.rA = __builtin_amdgcn_make_buffer_rsrc((void*)(p.A + (int64_t)m0 * p.lda), (short)0, rows * (int)p.lda, kRsrcWord3);
     w.rB = __builtin_amdgcn_make_buffer_rsrc((void*)(p.B + (int64_t)n0 * p.ldb), (short)0, cols * (int)p.ldb, kRsrcWord3);
+    if constexpr (W4) {
+        const int lrow = (int)p.lut_groups * 16;
+        w.rL = __builtin_amdgcn_make_buffer_rsrc((void*)(p.lut + (int64_t)n0 * lrow), (short)0, cols * lrow, kRsrcWord3);
+    }
 }
 
 // Epilogue operands of the cursor's tile into LDS area le: wave w loads row
@@ -159,21 +206,43 @@ __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8
                                              w.wave * 256, 0, 0);
 }
 
-// K-step kl of the cursor's tile into stage S: DL A and DL B loads per wave,
-// with EPI plus the tile's epilogue operands into area le.
-template <int WT, int S, bool EPI>
-__device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, int8_t* le) {
+// K-step kl of the cursor's tile into stage S: DL A loads per wave and DL B
+// loads (W4: the thread's codes and table into r instead), with EPI plus the
+// tile's epilogue operands into area le.
+template <int WT, int S, bool EPI, bool W4>
+__device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int DL = Cfg<WT>::DL;
     const int koff = kl * BK;
 #pragma unroll
     for (int j = 0; j < DL; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(w.la[S] + w.wave * (DL * 1024) + j * 1024), 16,
                                                  w.voA[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.lda, 0, 0);
+    if constexpr (W4) {
 #pragma unroll
-    for (int j = 0; j < DL; j++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(w.lb[S] + w.wave * (DL * 1024) + j * 1024), 16,
-                                                 w.voB[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.ldb, 0, 0);
+        for (int q = 0; q < W4Regs<WT>::C; q++)
+            r.c[q] = __builtin_amdgcn_raw_buffer_load_b128(w.rB, w.vo4 + q * 16, kl * (BK / 2), 0);
+        r.t = __builtin_amdgcn_raw_buffer_load_b128(w.rL, w.voL, ((kl * BK) >> p.group_shift) * 16, 0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < DL; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(w.lb[S] + w.wave * (DL * 1024) + j * 1024), 16,
+                                                     w.voB[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.ldb, 0, 0);
+    }
     if constexpr (EPI) issue_epi<WT>(w, p, le);
+}
+
+// W4: chunks [P0, P1) of the thread's 2C 16-column chunks of one K-step,
+// expanded from r into the int8 B stage S at their swizzled slots.
+template <int WT, int S, int P0, int P1>
+__device__ __forceinline__ void expand(const W4Regs<WT>& r, const Wv& w) {
+    constexpr int C = W4Regs<WT>::C;
+    int8_t* dst = w.lb[S] + w.w4row * BK;
+#pragma unroll
+    for (int x = P0; x < P1; x++) {
+        const int q = x / 2, h = x % 2;
+        const int c = w.w4half * 2 * C + x;
+        *(v4i*)(dst + swz8(w.w4row, c) * 16) = expand16b(r.c[q][2 * h], r.c[q][2 * h + 1], r.t);
+    }
 }
 
 template <int WT, int S, int Q>
@@ -210,13 +279,29 @@ __device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[Cfg<WT>::NB][
 // of stage SN into nxt; with LOADS the cursor's K-step into stage S.  The
 // first MFMA goes ahead of the reads because the compiler's wait for cur is
 // a full lgkmcnt(0) that must not cover reads issued after it.
-template <int WT, int S, int SN, int QN, bool LOADS, bool EPI>
+template <int WT, int S, int SN, int QN, bool LOADS, bool EPI, bool W4, int X0, int X1>
 __device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB],
-                                        const Wv& w, const GemmParams& p, int kl, int8_t* le) {
+                                        const Wv& w, const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int NB = Cfg<WT>::NB, DL = Cfg<WT>::DL;
     mma<WT>(cur, acc);
-    if constexpr (LOADS) issue<WT, S, EPI>(w, p, kl, le);
+    if constexpr (LOADS) issue<WT, S, EPI, W4>(w, p, kl, le, r);
     frag<WT, SN, QN>(nxt, w);
+    if constexpr (X1 > X0) {
+        // Chunks [X0, X1) of the previous step's codes into the other stage,
+        // spread between the MFMAs (about 38 VALU ops and one LDS write each).
+        expand<WT, S ^ 1, X0, X1>(r, w);
+        constexpr int V = (38 * (X1 - X0) + NB * NB - 1) / (NB * NB);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+#pragma unroll
+        for (int t = 0; t < NB * NB; t++) {
+            __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_VALU, V, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DSW, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        return;
+    }
     __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
     if constexpr (LOADS) {
         // Between the remaining MFMAs: the 2 DL loads and the 2 NB reads.
@@ -243,17 +328,20 @@ __device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i
 // every load in flight: the next stage's (issued one K-step earlier).  After
 // the barrier every wave is done reading stage S, which the last quarter
 // refills with K-step kl of the cursor's tile (EPI: epilogue operands into le).
-template <int WT, int S, bool EPI>
+// W4: the codes loaded by the previous step are expanded into stage S^1 over
+// quarters 1-3, before the barrier that hands that stage to the next step.
+template <int WT, int S, bool EPI, bool W4>
 __device__ __forceinline__ void step(Frag<WT>& f0, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const Wv& w,
-                                     const GemmParams& p, int kl, int8_t* le) {
+                                     const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
+    constexpr int X = W4 ? 2 * W4Regs<WT>::C : 0;  // chunks to expand, over quarters 1-3
     Frag<WT> f1;
-    quarter<WT, S, S, 1, false, false>(f0, f1, acc, w, p, kl, le);
-    quarter<WT, S, S, 2, false, false>(f1, f0, acc, w, p, kl, le);
-    quarter<WT, S, S, 3, false, false>(f0, f1, acc, w, p, kl, le);
+    quarter<WT, S, S, 1, false, false, W4, 0, W4_Q1 * X / 3>(f0, f1, acc, w, p, kl, le, r);
+    quarter<WT, S, S, 2, false, false, W4, W4_Q1 * X / 3, W4_Q1 ? 2 * X / 3 : X / 2>(f1, f0, acc, w, p, kl, le, r);
+    quarter<WT, S, S, 3, false, false, W4, W4_Q1 ? 2 * X / 3 : X / 2, X>(f0, f1, acc, w, p, kl, le, r);
     wait_all();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    quarter<WT, S, S ^ 1, 0, true, EPI>(f1, f0, acc, w, p, kl, le);
+    quarter<WT, S, S ^ 1, 0, true, EPI, W4, 0, 0>(f1, f0, acc, w, p, kl, le, r);
 }
 
 // Scaled epilogue operands of this lane's four columns starting at tile column ct.
@@ -383,7 +471,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
 
 }  // namespace
 
-template <int WT>
+template <int WT, bool W4>
 __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     using C = Cfg<WT>;
     constexpr int NB = C::NB, STG = C::STG, DL = C::DL;
@@ -428,14 +516,29 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
         w.voA[par] = (w.lane >> 3) * (int)p.lda + swz8(rr, w.lane & 7) * 16;
         w.voB[par] = (w.lane >> 3) * (int)p.ldb + swz8(rr, w.lane & 7) * 16;
     }
+    if constexpr (W4) {
+        constexpr int TPR = 256 / C::BM;  // threads per B row
+        w.w4row = threadIdx.x / TPR;
+        w.w4half = threadIdx.x % TPR;
+        w.vo4 = w.w4row * (int)p.ldb + w.w4half * (BK / 2 / TPR);
+        w.voL = w.w4row * (int)p.lut_groups * 16;
+    }
     // The epilogue operands of the workgroup's i-th tile go to area i % 2,
     // loaded with its first K-step (during tile i-1's last pair), so at
     // least one barrier separates a tile's epilogue from the load into its
     // area for tile i+2.
-    cursor_tile<WT>(w, p, s, r);
-    issue<WT, 0, true>(w, p, 0, w.le);
-    issue<WT, 1, false>(w, p, 1, w.le);
-    wait_vm_lgkm0<2 * DL>();  // the first K-step and its operands have landed
+    W4Regs<WT> w4r;
+    cursor_tile<WT, W4>(w, p, s, r);
+    issue<WT, 0, true, W4>(w, p, 0, w.le, w4r);
+    if constexpr (W4) {
+        wait_all();
+        expand<WT, 0, 0, 2 * W4Regs<WT>::C>(w4r, w);
+        issue<WT, 1, false, W4>(w, p, 1, w.le, w4r);
+        wait_vm_lgkm0<DL + W4Regs<WT>::C + 1>();  // stage 0, its operands and its expansion are done
+    } else {
+        issue<WT, 1, false, W4>(w, p, 1, w.le, w4r);
+        wait_vm_lgkm0<2 * DL>();  // the first K-step and its operands have landed
+    }
     __builtin_amdgcn_s_barrier();
     Frag<WT> f0;
     frag<WT, 0, 0>(f0, w);
@@ -445,19 +548,19 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
         int8_t* le = w.le + (i & 1) * EBYTES;
         zero_acc<WT>(acc);
         for (int k = 0; k < s.KT - 2; k += 2) {
-            step<WT, 0, false>(f0, acc, w, p, k + 2, le);
-            step<WT, 1, false>(f0, acc, w, p, k + 3, le);
+            step<WT, 0, false, W4>(f0, acc, w, p, k + 2, le, w4r);
+            step<WT, 1, false, W4>(f0, acc, w, p, k + 3, le, w4r);
         }
         // The last pair: the cursor moves to the next tile, if any.
         int kn = s.KT - 2;
         int8_t* ln = le;
         if (i + 1 < ntile) {
-            cursor_tile<WT>(w, p, s, t + s.G);
+            cursor_tile<WT, W4>(w, p, s, t + s.G);
             kn = 0;
             ln = w.le + ((i + 1) & 1) * EBYTES;
         }
-        step<WT, 0, true>(f0, acc, w, p, kn, ln);
-        step<WT, 1, false>(f0, acc, w, p, kn + 1, ln);
+        step<WT, 0, true, W4>(f0, acc, w, p, kn, ln, w4r);
+        step<WT, 1, false, W4>(f0, acc, w, p, kn + 1, ln, w4r);
         epilogue<WT>(acc, p, s, t, w, le);
         if (++i == ntile) break;
     }
@@ -465,16 +568,50 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     wait_all();
 }
 
-hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile) {
+// The W4 operand expanded once into an int8 [N, K] buffer (out, row pitch K):
+// each thread turns 32 consecutive codes of one row (16 bytes, one table
+// since group % 32 == 0) into 32 int8, the same bytes the in-register path
+// writes to LDS.
+__global__ __launch_bounds__(256) void w4_lut_expand_kernel(const uint8_t* __restrict__ codes, int64_t ldb,
+                                                            const int8_t* __restrict__ lut, int64_t lut_groups,
+                                                            int group_shift, int64_t N, int64_t K,
+                                                            int8_t* __restrict__ out) {
+    const int64_t per_row = K / 32;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= N * per_row) return;
+    const int64_t row = idx / per_row, c32 = idx - row * per_row;
+    const u32x4 c = *(const u32x4*)(codes + row * ldb + c32 * 16);
+    const u32x4 t = *(const u32x4*)(lut + (row * lut_groups + ((c32 * 32) >> group_shift)) * 16);
+    int8_t* o = out + row * K + c32 * 32;
+    *(v4i*)o = expand16b(c[0], c[1], t);
+    *(v4i*)(o + 16) = expand16b(c[2], c[3], t);
+}
+
+hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out) {
+    if (p.K % 32 != 0 || p.group_shift < 5 || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 ||
+        ((uintptr_t)out & 15) != 0 || !p.lut)
+        return hipErrorInvalidValue;
+    const int64_t threads = (int64_t)p.N * (p.K / 32);
+    hipLaunchKernelGGL(w4_lut_expand_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                       (const uint8_t*)p.B, p.ldb, p.lut, p.lut_groups, p.group_shift, (int64_t)p.N, (int64_t)p.K, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile, bool w4) {
     if (p.K % (2 * BK) != 0 || p.K < 2 * BK) return hipErrorInvalidValue;
     if (wave_tile != 128 && wave_tile != 64) return hipErrorInvalidValue;
+    // W4: one table per K-step (group a multiple of 128), 16-byte code loads.
+    if (w4 && (p.group_shift < 7 || !p.lut || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0)) return hipErrorInvalidValue;
     const int bm = 2 * wave_tile;
     const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
     const int grid = tiles < num_cus ? tiles : num_cus;
-    if (wave_tile == 128)
-        hipLaunchKernelGGL(i8_gemm_persist_kernel<128>, dim3(grid), dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL(i8_gemm_persist_kernel<64>, dim3(grid), dim3(256), 0, stream, p);
+    if (wave_tile == 128) {
+        if (w4) hipLaunchKernelGGL((i8_gemm_persist_kernel<128, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_persist_kernel<128, false>), dim3(grid), dim3(256), 0, stream, p);
+    } else {
+        if (w4) hipLaunchKernelGGL((i8_gemm_persist_kernel<64, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_persist_kernel<64, false>), dim3(grid), dim3(256), 0, stream, p);
+    }
     return hipGetLastError();
 }
 

@@ -60,7 +60,7 @@ class GemvItem(ctypes.Structure):
 EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", "phi_hip_i8_gemm",
            "phi_hip_workspace_bytes", "phi_hip_q8_linear", "phi_hip_w4a8_expand",
            "phi_hip_w4a8_prepare", "phi_hip_w4a8_linear", "phi_hip_i8_gemv_batched",
-           "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh"]
+           "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes"]
 
 _lib = None
 
@@ -88,6 +88,8 @@ def load() -> ctypes.CDLL:
                                       I64, P, P, I, P, SZ]
     L.phi_hip_i8_gemv_batched.argtypes = [P, P, P, I64, I64, I64, ctypes.POINTER(GemvItem), I, I,
                                           I, P, SZ]
+    L.phi_hip_w4a8_workspace_bytes.argtypes = [I64, I64, I64, I64]
+    L.phi_hip_w4a8_workspace_bytes.restype = SZ
     L.phi_hip_gemv_workspace_bytes.argtypes = [I]
     L.phi_hip_gemv_workspace_bytes.restype = SZ
     L.phi_hip_gelu_tanh.argtypes = [P, P, I, P, I, I64]
@@ -240,7 +242,9 @@ def w4a8_prepare(codes, s_rel, s_rel_dtype, s_channel=None, *, k, group, codeboo
 
 
 def w4a8_linear(x, codes, lut, s_w, *, group, bias=None, out_dtype=torch.bfloat16, q8=None,
-                s8=None, C=None, round_mode=ROUND_HALF_AWAY, stream=None):
+                s8=None, C=None, round_mode=ROUND_HALF_AWAY, workspace=None, stream=None):
+    """W4A8 linear; workspace (phi_hip_w4a8_workspace_bytes bytes) lets a call
+    with many rows expand the codes once instead of per tile."""
     _require_device(x, codes, lut, s_w, bias, q8, s8, C)
     M, K = x.shape
     N = codes.shape[0]
@@ -254,8 +258,14 @@ def w4a8_linear(x, codes, lut, s_w, *, group, bias=None, out_dtype=torch.bfloat1
                                       _ptr(codes), codes.stride(0), _ptr(lut), group, _ptr(s_w),
                                       _ptr(bias), _dt(bias) if bias is not None else F32, N,
                                       _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8),
-                                      round_mode, None, 0))
+                                      round_mode, *_ws(workspace)))
     return C
+
+
+def w4a8_workspace(M: int, N: int, K: int, group: int, device) -> torch.Tensor | None:
+    """A buffer of phi_hip_w4a8_workspace_bytes bytes (None when 0)."""
+    n = load().phi_hip_w4a8_workspace_bytes(M, N, K, group)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 
 # ---------------------------------------------------------------- GEMV

@@ -112,16 +112,28 @@ def test_prepare_table_reproduces_expand(dev, orc):
     assert torch.equal(looked, q.cpu())
 
 
+@pytest.mark.parametrize("with_ws", [False, True])
+@pytest.mark.parametrize("kernel", ["auto", "persist256", "persist128", "tile128"])
 @pytest.mark.parametrize("M,N,K,group", [(64, 256, 1024, 128), (300, 520, 3072, 128),
-                                         (1, 64, 512, 64), (130, 128, 2048, 256)])
-def test_in_register_linear_equals_expand_then_w8a8(dev, M, N, K, group):
+                                         (1, 64, 512, 64), (130, 128, 2048, 256),
+                                         (777, 1032, 768, 128), (4352, 2304, 512, 256)])
+def test_in_register_linear_equals_expand_then_w8a8(dev, monkeypatch, kernel, with_ws, M, N, K, group):
+    """Every W4A8 GEMM (persistent in both tile sizes and their mix, the
+    register-staged kernel, and with a workspace the expand-once path for
+    many rows) against expand-then-W8A8."""
+    if kernel == "auto":
+        monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("PHI_GEMM_KERNEL", kernel)
     codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=M + N)
     cd, rd, sd, kd = codes.to(dev), s_rel.to(dev), sch.to(dev), corr.to(dev)
     x = synth.activations(M, K, seed=M, device=dev)
     q, s = Q.w4a8_expand(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
     lut, s2 = Q.w4a8_prepare(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    ws = Q.w4a8_workspace(M, N, K, group, dev) if with_ws else None
+    y = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
+    monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
     y_ref = Q.q8_linear(x, q, s)
-    y = Q.w4a8_linear(x, cd, lut, s2, group=group)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
 
