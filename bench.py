@@ -44,6 +44,9 @@ CONFIGS = {
     "c3_attn": dict(kind="w8a8", M=32760, K=5120, N=5120),
     "c3_mlp": dict(kind="w8a8", M=32760, K=5120, N=13824),
     "c4": dict(kind="gemv", M=1, K=3072, N=18432, items=60),
+    # Config 1's MLP as a DiT sub-block: adaLN modulate -> up (bf16) -> GELU-tanh
+    # -> down into the fp32 residual stream through the gate.
+    "c1_block": dict(kind="block", M=4352, K=3072, N=12288),
 }
 
 
@@ -153,6 +156,76 @@ def bench_w8a8(cfg, steps, warmup):
     }
 
 
+def bench_block(cfg, steps, warmup):
+    """Config 1's MLP pair as the DiT runs it, fused against unfused.
+
+    Fused: quant_rotate_mod -> GEMM up (bf16) -> GELU-tanh -> quant_rotate ->
+    GEMM down with the gated residual (phi_hip_i8_gemm_residual).  Unfused:
+    the modulation and the residual update as separate elementwise passes
+    (torch), the projections as plain linears.  Reported: the fused block."""
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    Wu = synth.int8_weight(N, K, seed=1, device=dev)
+    Wd = synth.int8_weight(K, N, seed=2, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    bu = synth.bias(N, seed=3, device=dev)
+    g = torch.Generator(device=dev).manual_seed(4)
+    msc = torch.randn(K, generator=g, device=dev) * 0.1
+    msh = torch.randn(K, generator=g, device=dev) * 0.1
+    gate = torch.randn(K, generator=g, device=dev) * 0.1
+    H = torch.randn(M, K, generator=g, device=dev)
+    q8u = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8u = torch.empty((M,), dtype=torch.float32, device=dev)
+    q8d = torch.empty((M, N), dtype=torch.int8, device=dev)
+    s8d = torch.empty((M,), dtype=torch.float32, device=dev)
+    up = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    act = torch.empty_like(up)
+    proj = torch.empty((M, K), dtype=torch.float32, device=dev)
+
+    def fused():
+        Q.quant_rotate(x, q=q8u, s=s8u, mod_scale=msc, mod_shift=msh)
+        Q.i8_gemm(q8u, Wu, s8u, sW, bu, C=up)
+        Q.gelu_tanh(up, out=act)
+        Q.quant_rotate(act, q=q8d, s=s8d)
+        Q.i8_gemm_residual(q8d, Wd, s8d, sW, None, gate, H)
+
+    def unfused():
+        xm = torch.addcmul(msh, x.float(), 1.0 + msc)  # the separate ModAdd pass
+        Q.quant_rotate(xm, q=q8u, s=s8u)
+        Q.i8_gemm(q8u, Wu, s8u, sW, bu, C=up)
+        Q.gelu_tanh(up, out=act)
+        Q.quant_rotate(act, q=q8d, s=s8d)
+        Q.i8_gemm(q8d, Wd, s8d, sW, None, C=proj)
+        H.addcmul_(proj, gate)  # the separate AddMul pass
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    ms_un = timed(unfused)
+    ms = timed(fused)
+    ops = 2 * 2.0 * M * N * K
+    return {"value": ops / (ms * 1e-3) / 1e12, "ms": ms, "dtype": "int8",
+            "roofline": {"bound": "mfma", "achieved": ops / (ms * 1e-3) / 1e12, "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                         "traffic": None},
+            "extra": {"fused_us": ms * 1e3, "unfused_us": ms_un * 1e3}}
+
+
 def bench_w4a8(cfg, steps, warmup):
     import torch
 
@@ -250,6 +323,8 @@ def main() -> int:
     log(f"bench: config {args.config} {cfg}, warmup {args.warmup}, steps {args.steps}")
     if cfg["kind"] == "w8a8":
         r = bench_w8a8(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "block":
+        r = bench_block(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "w4a8":
         r = bench_w4a8(cfg, args.steps, args.warmup)
     else:

@@ -82,6 +82,21 @@ phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype,
                                 float qmax, int round_mode, int rotate);
 
 /*
+ * phi_hip_quant_rotate with the DiT's adaLN modulation fused in front:
+ * every element first becomes fma(x, 1 + mod_scale[k], mod_shift[k]) in fp32
+ * (either vector may be NULL, meaning 0; both [K] fp32, 16-byte aligned).
+ * Replaces dispatch_elem(ElemOp::ModAdd, Row, Row) followed by
+ * dispatch_quant_convrot (core/models/av_dit.cpp:1264-1267; ModAdd
+ * core/kernels/gpu_ops.hpp:29-35, maths core/kernels/ops.cpp:82 as NVRTC's
+ * default --fmad=true contracts it), without the modulated tensor's round
+ * trip through memory.
+ */
+phi_status phi_hip_quant_rotate_mod(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                    int64_t K, int64_t ldx, const float* mod_scale, const float* mod_shift,
+                                    int8_t* q, int64_t ldq, float* s, float qmax, int round_mode,
+                                    int rotate);
+
+/*
  * int8 GEMM with the fused dequant epilogue:
  *   C[m,n] = fma((float)acc[m,n] * sA[m], sB[n], bias[n])   (bias = 0 when NULL)
  *   acc[m,n] = sum_k A[m,k] * B[n,k]   (int32, exact)
@@ -102,6 +117,22 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
                            int64_t ldb, const float* sA, const float* sB, int sb_scalar,
                            const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
                            int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes);
+
+/*
+ * phi_hip_i8_gemm into a gated residual stream, in place:
+ *   H[m,n] = fma(linear[m,n], gate[n], H[m,n]),  linear = fma((float)acc*sA, sB, bias)
+ * H is fp32 [M, ldh] (16-byte aligned rows), gate fp32 [N].  Replaces
+ * dispatch_int8_gemm into a scratch projection followed by
+ * dispatch_elem(ElemOp::AddMul, Flat, Row) onto the residual
+ * (core/models/av_dit.cpp:1382-1390, :1410-1412; maths core/kernels/ops.cpp:80
+ * as NVRTC's default --fmad=true contracts it).  Needs K % 256 == 0 and
+ * N % 4 == 0 (the persistent kernel); otherwise PHI_ERR_UNSUPPORTED.
+ */
+phi_status phi_hip_i8_gemm_residual(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
+                                    int64_t ldb, const float* sA, const float* sB, int sb_scalar,
+                                    const void* bias, int bias_dtype, const float* gate, float* H,
+                                    int64_t ldh, int64_t M, int64_t N, int64_t K, void* workspace,
+                                    size_t ws_bytes);
 
 /* Workspace (bytes) phi_hip_i8_gemm / phi_hip_q8_linear need for this shape. */
 size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K);

@@ -50,6 +50,8 @@ def lib() -> ctypes.CDLL:
         L.orc_w4a8_expand.argtypes = [P, I64, P, I, I64, P, I, P, P, I64, I64, I64, I, P, P, P]
         L.orc_w4a8_expand.restype = I
         L.orc_gelu_tanh.argtypes = [P, P, I64]
+        L.orc_mod_add.argtypes = [P, P, P, P, I64, I64]
+        L.orc_add_mul.argtypes = [P, P, P, P, I64, I64]
         L.orc_f32_to_bf16_n.argtypes = [P, P, I64]
         L.orc_bf16_to_f32_n.argtypes = [P, P, I64]
         L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -205,6 +207,28 @@ def w4a8_expand(codes, s_rel, s_rel_dtype, s_channel, *, k, group, codebook=None
     if rc != 0:
         raise ValueError("w4a8_expand: bad geometry")
     return (q, s, vals) if return_values else (q, s)
+
+
+def mod_add(a, b, c) -> np.ndarray:
+    """adaLN ModAdd per column: fma(a, 1 + b[col], c[col]) (b, c may be None)."""
+    a = _c(a, np.float32)
+    rows, cols = a.shape
+    b = None if b is None else _c(b, np.float32).reshape(-1)
+    c = None if c is None else _c(c, np.float32).reshape(-1)
+    y = np.empty_like(a)
+    lib().orc_mod_add(_p(a), _p(b), _p(c), _p(y), rows, cols)
+    return y
+
+
+def add_mul(a, b, c) -> np.ndarray:
+    """Gated residual AddMul per column: fma(b, c[col], a)."""
+    a = _c(a, np.float32)
+    rows, cols = a.shape
+    b = _c(b, np.float32)
+    c = _c(c, np.float32).reshape(-1)
+    y = np.empty_like(a)
+    lib().orc_add_mul(_p(a), _p(b), _p(c), _p(y), rows, cols)
+    return y
 
 
 def gelu_tanh(x) -> np.ndarray:

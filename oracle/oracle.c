@@ -302,3 +302,17 @@ void orc_gelu_tanh(const float* x, float* y, int64_t n) {
         y[i] = 0.5f * a * (1.0f + tanhf(t));
     }
 }
+
+/* ---- fused neighbours: ModAdd and AddMul (core/kernels/ops.cpp:80-82) ---- */
+void orc_mod_add(const float* a, const float* b, const float* c, float* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t k = 0; k < cols; k++) {
+            const float one_b = 1.0f + (b ? b[k] : 0.0f);
+            y[r * cols + k] = fmaf(a[r * cols + k], one_b, c ? c[k] : 0.0f);
+        }
+}
+
+void orc_add_mul(const float* a, const float* b, const float* c, float* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t k = 0; k < cols; k++) y[r * cols + k] = fmaf(b[r * cols + k], c[k], a[r * cols + k]);
+}

@@ -87,6 +87,17 @@ int orc_w4a8_expand(const uint8_t* codes, int64_t codes_row_bytes, const void* s
                     int64_t rows, int64_t k, int64_t group, int layout, int8_t* q, float* s,
                     float* values);
 
+/* ---- fused neighbours of the linear (core/kernels/ops.cpp:71-92, the opcode
+ *      table; NVRTC compiles it with its default --fmad=true, which contracts
+ *      each multiply-add below into one fma) ----
+ * ModAdd (op 12, Row/Row modes, the adaLN modulation before a projection,
+ * core/models/av_dit.cpp:1264):  y = fma(a, 1 + b[col], c[col])
+ * AddMul (op 6, Flat/Row modes, the gated residual after a projection,
+ * core/models/av_dit.cpp:1389):  y = fma(b, c[col], a)
+ * b or c may be NULL (0).  a, b, y are [rows, cols]. */
+void orc_mod_add(const float* a, const float* b, const float* c, float* y, int64_t rows, int64_t cols);
+void orc_add_mul(const float* a, const float* b, const float* c, float* y, int64_t rows, int64_t cols);
+
 /* ---- A9: GELU-tanh (core/kernels/ops.cpp:83-89) ---- */
 void orc_gelu_tanh(const float* x, float* y, int64_t n);
 

@@ -229,10 +229,9 @@ const char* phi_hip_last_error(void) { return g_err.c_str(); }
 
 int phi_hip_abi_version(void) { return PHI_QLINEAR_ABI_VERSION; }
 
-phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
-                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                                float qmax, int round_mode, int rotate) {
-    static const char* who = "quant_rotate";
+static phi_status quant_rotate_impl(const char* who, phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                    int64_t K, int64_t ldx, const float* msc, const float* msh, int8_t* q,
+                                    int64_t ldq, float* s, float qmax, int round_mode, int rotate) {
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     if (rows < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
     if (rows == 0) return ok();
@@ -248,9 +247,26 @@ phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype,
     const size_t esz = x_dtype == PHI_BF16 ? 2 : 4;
     if (!aligned(x, 16) || (ldx * (int64_t)esz) % 16 != 0 || !aligned(q, 16) || ldq % 16 != 0 || !aligned(s, 4))
         return fail(PHI_ERR_ALIGN, "%s: x and q rows must be 16-byte aligned", who);
+    if ((msc && !aligned(msc, 16)) || (msh && !aligned(msh, 16)))
+        return fail(PHI_ERR_ALIGN, "%s: modulation vectors must be 16-byte aligned", who);
     return check_hip(phi_dev::launch_quant_rotate((hipStream_t)stream, x, x_dtype == PHI_BF16, rows, K, ldx, q, ldq, s,
-                                                  qmax, round_mode == PHI_ROUND_HALF_EVEN, rotate ? 1 : 0),
+                                                  qmax, round_mode == PHI_ROUND_HALF_EVEN, rotate ? 1 : 0, msc, msh),
                      who);
+}
+
+phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
+                                float qmax, int round_mode, int rotate) {
+    return quant_rotate_impl("quant_rotate", stream, x, x_dtype, rows, K, ldx, nullptr, nullptr, q, ldq, s, qmax,
+                             round_mode, rotate);
+}
+
+phi_status phi_hip_quant_rotate_mod(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                    int64_t K, int64_t ldx, const float* mod_scale, const float* mod_shift,
+                                    int8_t* q, int64_t ldq, float* s, float qmax, int round_mode,
+                                    int rotate) {
+    return quant_rotate_impl("quant_rotate_mod", stream, x, x_dtype, rows, K, ldx, mod_scale, mod_shift, q, ldq, s,
+                             qmax, round_mode, rotate);
 }
 
 size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K) {
@@ -298,6 +314,49 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
         return check_hip(phi_dev::launch_i8_gemm_256((hipStream_t)stream, p), who);
     }
     return check_hip(phi_dev::launch_i8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
+}
+
+phi_status phi_hip_i8_gemm_residual(phi_stream_t stream, const int8_t* A, int64_t lda, const int8_t* B,
+                                    int64_t ldb, const float* sA, const float* sB, int sb_scalar,
+                                    const void* bias, int bias_dtype, const float* gate, float* H,
+                                    int64_t ldh, int64_t M, int64_t N, int64_t K, void* workspace,
+                                    size_t ws_bytes) {
+    static const char* who = "int8_gemm_residual";
+    (void)workspace;
+    (void)ws_bytes;
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, H, PHI_F32, ldh, false);
+    if (st != PHI_OK) return st;
+    if (!gate) return fail(PHI_ERR_ARG, "%s: null gate", who);
+    if (!aligned(gate, 4)) return fail(PHI_ERR_ALIGN, "%s: gate must be 4-byte aligned", who);
+    if (!persist_ok(H, PHI_F32, N, K, lda, ldb, ldh))
+        return fail(PHI_ERR_UNSUPPORTED, "%s: needs K %% 256 == 0, N %% 4 == 0 and 16-byte aligned H rows", who);
+    const int bk = bias_kind_of(bias, bias_dtype, &st);
+    if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    phi_dev::GemmParams p{};
+    p.A = A;
+    p.B = B;
+    p.sA = sA;
+    p.sB = sB;
+    p.bias = bias;
+    p.C = H;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.ldc = ldh;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.sb_scalar = sb_scalar ? 1 : 0;
+    p.bias_kind = bk;
+    p.c_kind = phi_dev::C_F32;
+    p.group_m = 4;
+    p.gate = gate;
+    set_vec_flags(p, PHI_F32, ldh);
+    GemmKernel gk = GK_PERSIST;
+    const char* e = getenv("PHI_GEMM_KERNEL");
+    if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;
+    if (e && strcmp(e, "persist128") == 0) gk = GK_PERSIST128;
+    return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, false, PHI_F32, ldh), who);
 }
 
 phi_status phi_hip_q8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,

@@ -30,6 +30,8 @@ struct GemmParams {
     int c_vec16;         // C rows allow 16-byte stores (16-byte aligned, row pitch a multiple of 16 bytes)
     int s_vec;           // sB and bias allow 4-element vector loads (16-byte / 8-byte aligned)
     int schedule;        // 256x256 kernel: 0 = eight waves, 64-deep K; 1 = four waves, 128-deep K
+    // Persistent kernel, fp32 output: C = fma(linear, gate[n], C) in place (gated residual).
+    const float* gate;
 };
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
@@ -42,9 +44,10 @@ hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int n
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);
 
+// msc / msh: optional per-column modulation applied first, v*(1+msc)+msh (fma).
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                               float qmax, int half_even, int rotate);
+                               float qmax, int half_even, int rotate, const float* msc, const float* msh);
 size_t quant_rotate_lds_bytes(int64_t K);
 
 }  // namespace phi_dev

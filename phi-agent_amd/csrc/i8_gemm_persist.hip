@@ -51,7 +51,7 @@ typedef unsigned int u32x4 __attribute__((__vector_size__(4 * sizeof(unsigned in
 constexpr int kRsrcWord3 = 0x00020000;
 
 constexpr int BK = 128;
-constexpr int EBYTES = 3 * 1024;  // per parity: sa | sb | bias (4 waves x 256 B each)
+constexpr int EBYTES = 4 * 1024;  // per parity: sa | sb | bias | gate (4 waves x 256 B each)
 constexpr int CHUNK = 4096;       // per-wave epilogue staging
 
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_R = 0x020, SG_DSR = 0x100, SG_DSW = 0x200;
@@ -204,6 +204,12 @@ __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8
         p.bias_kind != BIAS_NONE ? cols * bsz : 0, kRsrcWord3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rBZ, (lptr_t)(le + 2048 + w.wave * 256), 4, w.lane * 4,
                                              w.wave * 256, 0, 0);
+    if (p.gate) {
+        const __amdgpu_buffer_rsrc_t rG =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(p.gate + w.cn0), (short)0, cols * 4, kRsrcWord3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rG, (lptr_t)(le + 3072 + w.wave * 256), 4, w.lane * 4,
+                                                 w.wave * 256, 0, 0);
+    }
 }
 
 // K-step kl of the cursor's tile into stage S: DL A loads per wave and DL B
@@ -429,7 +435,12 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
         }
         return;
     }
-    // fp32 / int32: 32 x 32 pieces, one block at a time.
+    // fp32 / int32: 32 x 32 pieces, one block at a time.  With a gate the
+    // fp32 output is the residual stream, updated in place:
+    // C = fma(v, gate[n], C), the reference's AddMul `a + b * c`
+    // (core/kernels/ops.cpp:80, applied after the projection at
+    // core/models/av_dit.cpp:1389) as NVRTC's default --fmad=true contracts it.
+    const bool gated = p.gate != nullptr;
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         v4f sb[4], bz[4];
@@ -439,6 +450,16 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
+            // The residual rows this lane stores, fetched before the conversion
+            // so their latency overlaps it.
+            u32x4 res[4];
+            if (gated) {
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) {
+                    const int r = tt * 8 + (w.lane >> 3), col = colw + j * 32 + (w.lane & 7) * 4;
+                    res[tt] = __builtin_amdgcn_raw_buffer_load_b128(rs, (w.wm * WT + i * 32 + r) * pitch + col * 4, 0, 0);
+                }
+            }
             v16i blk = acc[j][i];
             asm volatile("" : "+v"(blk));
 #pragma unroll
@@ -458,8 +479,14 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
                 const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
-                const u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
+                u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
                 const int col = colw + j * 32 + sl * 4;
+                if (gated) {
+                    const v4f gt = *(const v4f*)(e + 3072 + (w.wn * WT + j * 32 + sl * 4) * 4);
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        v[q] = __float_as_uint(fmaf(__uint_as_float(v[q]), gt[q], __uint_as_float(res[tt][q])));
+                }
                 if (col < p.N)
                     __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * WT + i * 32 + r) * pitch + col * 4, 0,
                                                            kStoreNT);

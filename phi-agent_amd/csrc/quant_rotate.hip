@@ -46,11 +46,31 @@ __device__ __forceinline__ void bfly16(float (&v)[16]) {
     }
 }
 
+// Modulation before the rotation (the DiT's adaLN ModAdd, fused):
+// v = fma(v, 1 + scale[col], shift[col]), the reference's `a * (1 + b) + c`
+// (core/kernels/ops.cpp:82, ModAdd core/kernels/gpu_ops.hpp:29-35) as NVRTC's
+// default --fmad=true contracts it.  scale or shift may be NULL (0).
+__device__ __forceinline__ void modulate16(float (&v)[16], const float* __restrict__ sc, const float* __restrict__ sh,
+                                           int64_t col) {
+    float b[16], c[16];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 tb = sc ? *(const float4*)(sc + col + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 tc = sh ? *(const float4*)(sh + col + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        b[4 * i] = tb.x, b[4 * i + 1] = tb.y, b[4 * i + 2] = tb.z, b[4 * i + 3] = tb.w;
+        c[4 * i] = tc.x, c[4 * i + 1] = tc.y, c[4 * i + 2] = tc.z, c[4 * i + 3] = tc.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) v[i] = fmaf(v[i], 1.0f + b[i], c[i]);
+}
+
 template <bool BF16_IN>
 __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict__ x, int64_t ldx,
                                                           int K, int8_t* __restrict__ q,
                                                           int64_t ldq, float* __restrict__ s,
-                                                          float qmax, int half_even, int rotate) {
+                                                          float qmax, int half_even, int rotate,
+                                                          const float* __restrict__ msc,
+                                                          const float* __restrict__ msh) {
     extern __shared__ __align__(16) float lds[];
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
@@ -83,6 +103,7 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
                 v[4 * i + 3] = t.w;
             }
         }
+        if (msc || msh) modulate16(v, msc, msh, e0);
         if (rotate) {
             bfly16<1>(v);
             bfly16<4>(v);
@@ -230,7 +251,9 @@ __device__ __forceinline__ uint32_t cvt_pack4(float a, float b, float c, float d
 template <bool BF16_IN, bool HALF_EVEN, int R>
 __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
                                                            int G, int8_t* __restrict__ q, int64_t ldq,
-                                                           float* __restrict__ s, float qmax, int rotate) {
+                                                           float* __restrict__ s, float qmax, int rotate,
+                                                           const float* __restrict__ msc,
+                                                           const float* __restrict__ msh) {
     extern __shared__ __align__(16) float lds[];
     constexpr int NW = BF16_IN ? 8 : 16;  // input dwords per lane per round
     const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
@@ -270,6 +293,7 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
             if (BF16_IN) v[i] = __uint_as_float(i & 1 ? raw[r][i >> 1] & 0xffff0000u : raw[r][i >> 1] << 16);
             else v[i] = __uint_as_float(raw[r][i]);
         }
+        if (msc || msh) modulate16(v, msc, msh, (int64_t)min(g0 + 4 * r, G - 1) * 256 + tl * 16);
         if (rotate) {
             bfly16f<1>(v);
             bfly16f<4>(v);
@@ -371,7 +395,7 @@ static int tile_rounds(int64_t rows, int G) {
 
 template <bool BF16_IN, bool HALF_EVEN, int R>
 static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                                 int64_t ldq, float* s, float qmax, int rotate) {
+                                 int64_t ldq, float* s, float qmax, int rotate, const float* msc, const float* msh) {
     const int wpr = (G + 4 * R - 1) / (4 * R);
     const int rpb = wpr >= 8 ? 1 : 8 / wpr;
     const size_t lds = ((size_t)rpb * wpr * QT_WAVE + 16) * sizeof(float);
@@ -385,34 +409,37 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
     }
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
     hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R>), grid, block, lds, stream, x, ldx, (int)rows, G, q,
-                       ldq, s, qmax, rotate);
+                       ldq, s, qmax, rotate, msc, msh);
     return hipGetLastError();
 }
 
 template <bool BF16_IN, bool HALF_EVEN>
 static hipError_t launch_tiles(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                               int64_t ldq, float* s, float qmax, int rotate) {
-    switch (tile_rounds(rows, G)) {
-        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
-        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
-        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
-        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
-        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+                               int64_t ldq, float* s, float qmax, int rotate, const float* msc, const float* msh) {
+    // With a modulation the per-round scale/shift registers cap R at 2.
+    int R = tile_rounds(rows, G);
+    if ((msc || msh) && R > 2 && (G + 7) / 8 <= 16) R = 2;
+    switch (R) {
+        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
     }
 }
 
 // Host-side launcher.  Validation is done by the C ABI layer.
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                               float qmax, int half_even, int rotate) {
+                               float qmax, int half_even, int rotate, const float* msc, const float* msh) {
     const int G = (int)(K / 256);
     if (rows == 0) return hipSuccess;
     if (G <= 64) {
         if (bf16_in)
-            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate)
-                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
-        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate)
-                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate);
+            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh)
+                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh)
+                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
     }
     int threads = ((16 * G + 63) / 64) * 64;
     if (threads > 1024) threads = 1024;
@@ -424,10 +451,10 @@ hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, 
     }
     if (bf16_in) {
         hipLaunchKernelGGL(quant_rotate_rows<true>, dim3((unsigned)rows), dim3(threads), lds_bytes,
-                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate);
+                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate, msc, msh);
     } else {
         hipLaunchKernelGGL(quant_rotate_rows<false>, dim3((unsigned)rows), dim3(threads), lds_bytes,
-                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate);
+                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate, msc, msh);
     }
     return hipGetLastError();
 }

@@ -60,7 +60,8 @@ class GemvItem(ctypes.Structure):
 EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", "phi_hip_i8_gemm",
            "phi_hip_workspace_bytes", "phi_hip_q8_linear", "phi_hip_w4a8_expand",
            "phi_hip_w4a8_prepare", "phi_hip_w4a8_linear", "phi_hip_i8_gemv_batched",
-           "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes"]
+           "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes",
+           "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual"]
 
 _lib = None
 
@@ -88,6 +89,8 @@ def load() -> ctypes.CDLL:
                                       I64, P, P, I, P, SZ]
     L.phi_hip_i8_gemv_batched.argtypes = [P, P, P, I64, I64, I64, ctypes.POINTER(GemvItem), I, I,
                                           I, P, SZ]
+    L.phi_hip_quant_rotate_mod.argtypes = [P, P, I, I64, I64, I64, P, P, P, I64, P, ctypes.c_float, I, I]
+    L.phi_hip_i8_gemm_residual.argtypes = [P, P, I64, P, I64, P, P, I, P, I, P, P, I64, I64, I64, I64, P, SZ]
     L.phi_hip_w4a8_workspace_bytes.argtypes = [I64, I64, I64, I64]
     L.phi_hip_w4a8_workspace_bytes.restype = SZ
     L.phi_hip_gemv_workspace_bytes.argtypes = [I]
@@ -134,19 +137,28 @@ def _require_device(*ts):
 # ---------------------------------------------------------------- A1-A3
 def quant_rotate(x: torch.Tensor, *, qmax: float = 127.0, round_mode: int = ROUND_HALF_AWAY,
                  rotate: bool = True, q: torch.Tensor | None = None,
-                 s: torch.Tensor | None = None, stream=None):
+                 s: torch.Tensor | None = None, mod_scale: torch.Tensor | None = None,
+                 mod_shift: torch.Tensor | None = None, stream=None):
     """Rotate (256-wide convrot) and quantise rows of x [rows, K] (f32/bf16).
 
+    mod_scale / mod_shift ([K] fp32): the adaLN modulation fma(x, 1 + scale,
+    shift) applied first (phi_hip_quant_rotate_mod).
     Returns (q int8 [rows, K], s f32 [rows])."""
-    _require_device(x)
+    _require_device(x, mod_scale, mod_shift)
     rows, K = x.shape
     if q is None:
         q = torch.empty((rows, K), dtype=torch.int8, device=x.device)
     if s is None:
         s = torch.empty((rows,), dtype=torch.float32, device=x.device)
-    _check(load().phi_hip_quant_rotate(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0),
-                                       _ptr(q), q.stride(0), _ptr(s), float(qmax), round_mode,
-                                       1 if rotate else 0))
+    if mod_scale is None and mod_shift is None:
+        _check(load().phi_hip_quant_rotate(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0),
+                                           _ptr(q), q.stride(0), _ptr(s), float(qmax), round_mode,
+                                           1 if rotate else 0))
+    else:
+        _check(load().phi_hip_quant_rotate_mod(_stream(stream), _ptr(x), _dt(x), rows, K,
+                                               x.stride(0), _ptr(mod_scale), _ptr(mod_shift),
+                                               _ptr(q), q.stride(0), _ptr(s), float(qmax),
+                                               round_mode, 1 if rotate else 0))
     return q, s
 
 
@@ -175,6 +187,21 @@ def i8_gemm(A: torch.Tensor, B: torch.Tensor, sA: torch.Tensor | None, sB: torch
                                   _dt(bias) if bias is not None else F32, _ptr(C), _dt(C),
                                   C.stride(0), M, N, K, wp, wn))
     return C
+
+
+def i8_gemm_residual(A: torch.Tensor, B: torch.Tensor, sA: torch.Tensor, sB: torch.Tensor,
+                     bias: torch.Tensor | None, gate: torch.Tensor, H: torch.Tensor,
+                     stream=None) -> torch.Tensor:
+    """H = fma(fma((float)(A . B^T) * sA, sB, bias), gate, H) in place (fp32 H)."""
+    _require_device(A, B, sA, sB, bias, gate, H)
+    M, K = A.shape
+    N = B.shape[0]
+    sb_scalar = 1 if sB.numel() == 1 else 0
+    _check(load().phi_hip_i8_gemm_residual(_stream(stream), _ptr(A), A.stride(0), _ptr(B),
+                                           B.stride(0), _ptr(sA), _ptr(sB), sb_scalar, _ptr(bias),
+                                           _dt(bias) if bias is not None else F32, _ptr(gate),
+                                           _ptr(H), H.stride(0), M, N, K, None, 0))
+    return H
 
 
 def q8_linear(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
