@@ -159,10 +159,11 @@ def bench_w8a8(cfg, steps, warmup):
 def bench_block(cfg, steps, warmup):
     """Config 1's MLP pair as the DiT runs it, fused against unfused.
 
-    Fused: quant_rotate_mod -> GEMM up (bf16) -> GELU-tanh -> quant_rotate ->
-    GEMM down with the gated residual (phi_hip_i8_gemm_residual).  Unfused:
-    the modulation and the residual update as separate elementwise passes
-    (torch), the projections as plain linears.  Reported: the fused block."""
+    Fused: quant_rotate_mod -> GEMM up (bf16) -> quant_rotate with GELU-tanh
+    in front (phi_hip_quant_rotate_act) -> GEMM down with the gated residual
+    (phi_hip_i8_gemm_residual): four launches.  Unfused: the modulation, the
+    GELU (bf16 out) and the residual update as separate elementwise passes,
+    the projections as plain linears.  Reported: the fused block."""
     import torch
 
     import phi_qlinear as Q
@@ -191,8 +192,7 @@ def bench_block(cfg, steps, warmup):
     def fused():
         Q.quant_rotate(x, q=q8u, s=s8u, mod_scale=msc, mod_shift=msh)
         Q.i8_gemm(q8u, Wu, s8u, sW, bu, C=up)
-        Q.gelu_tanh(up, out=act)
-        Q.quant_rotate(act, q=q8d, s=s8d)
+        Q.quant_rotate(up, q=q8d, s=s8d, act="gelu_tanh")
         Q.i8_gemm_residual(q8d, Wd, s8d, sW, None, gate, H)
 
     def unfused():

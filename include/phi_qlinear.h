@@ -60,6 +60,12 @@ typedef enum phi_round {
     PHI_ROUND_HALF_EVEN = 1  /* documented alternative */
 } phi_round;
 
+/* Activation fused in front of phi_hip_quant_rotate_act. */
+typedef enum phi_act {
+    PHI_ACT_GELU_TANH = 1, /* ElemOp::GeluTanh (core/kernels/ops.cpp:83-89) */
+    PHI_ACT_SILU_GATE = 2  /* silu_gate_fused (core/kernels/conv3d_causal.cpp:997-1013) */
+} phi_act;
+
 /* Message for the last failing call on this thread ("" after success). */
 const char* phi_hip_last_error(void);
 int phi_hip_abi_version(void);
@@ -95,6 +101,23 @@ phi_status phi_hip_quant_rotate_mod(phi_stream_t stream, const void* x, int x_dt
                                     int64_t K, int64_t ldx, const float* mod_scale, const float* mod_shift,
                                     int8_t* q, int64_t ldq, float* s, float qmax, int round_mode,
                                     int rotate);
+
+/*
+ * phi_hip_quant_rotate with the MLP's activation fused in front, so the
+ * activated tensor never goes through memory:
+ *   PHI_ACT_GELU_TANH  x [rows, ldx >= K]: v = gelu_tanh(x[r][k]).  Replaces
+ *     dispatch_elem(ElemOp::GeluTanh) followed by dispatch_quant_convrot
+ *     (core/kernels/ops.cpp:83-89).
+ *   PHI_ACT_SILU_GATE  x [rows, ldx >= 2K], gate then value halves:
+ *     v = silu(x[r][k]) * x[r][K + k].  Replaces dispatch_silu_gate_fused
+ *     (core/kernels/h3_kernels.hpp:116-129) followed by dispatch_quant_convrot.
+ * The activation is computed in fp32 with the same functions as
+ * phi_hip_gelu_tanh / phi_hip_silu_gate, so the codes and scales equal the
+ * unfused pair's bit for bit when that pair's intermediate is fp32.
+ */
+phi_status phi_hip_quant_rotate_act(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                    int64_t ldx, int act, int8_t* q, int64_t ldq, float* s, float qmax,
+                                    int round_mode, int rotate);
 
 /*
  * int8 GEMM with the fused dequant epilogue:
@@ -237,9 +260,16 @@ size_t phi_hip_w4a8_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gro
 size_t phi_hip_gemv_workspace_bytes(int n_items);
 
 /* GELU-tanh over bf16 or fp32 [n] (core/kernels/ops.cpp:83-89), in place
- * allowed; out_dtype PHI_BF16 rounds RNE. */
+ * allowed when the dtypes are equal; out_dtype PHI_BF16 rounds RNE. */
 phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, void* y,
                              int y_dtype, int64_t n);
+
+/* SiLU gate: out[r][c] = silu(gx[r][c]) * gx[r][cols + c], gx [rows, ldx >= 2*cols],
+ * out [rows, ldo >= cols], each f32 or bf16 (RNE), out not overlapping gx.
+ * Replaces dispatch_silu_gate_fused (core/kernels/h3_kernels.hpp:116-129,
+ * kernel core/kernels/conv3d_causal.cpp:997-1013). */
+phi_status phi_hip_silu_gate(phi_stream_t stream, const void* gx, int x_dtype, int64_t rows, int64_t cols,
+                             int64_t ldx, void* out, int out_dtype, int64_t ldo);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
         L.orc_w4a8_expand.argtypes = [P, I64, P, I, I64, P, I, P, P, I64, I64, I64, I, P, P, P]
         L.orc_w4a8_expand.restype = I
         L.orc_gelu_tanh.argtypes = [P, P, I64]
+        L.orc_silu_gate.argtypes = [P, P, I64, I64]
         L.orc_mod_add.argtypes = [P, P, P, P, I64, I64]
         L.orc_add_mul.argtypes = [P, P, P, P, I64, I64]
         L.orc_f32_to_bf16_n.argtypes = [P, P, I64]
@@ -236,6 +237,15 @@ def gelu_tanh(x) -> np.ndarray:
     y = np.empty_like(x)
     lib().orc_gelu_tanh(_p(x), _p(y), x.size)
     return y
+
+
+def silu_gate(gx) -> np.ndarray:
+    """silu(gx[:, :cols]) * gx[:, cols:] for gx [rows, 2 cols], fp32."""
+    gx = _c(gx, np.float32)
+    rows, two = gx.shape
+    out = np.empty((rows, two // 2), dtype=np.float32)
+    lib().orc_silu_gate(_p(gx), _p(out), rows, two // 2)
+    return out
 
 
 # ---------------------------------------------------------------- _ref driver

@@ -294,13 +294,27 @@ int orc_w4a8_expand(const uint8_t* codes, int64_t codes_row_bytes, const void* s
 /* ------------------------------------------------------------------------ */
 
 /* 0.5 x (1 + tanh(0.7978845608028654 (x + 0.044715 x^3))), fp32, the
- * operation order of core/kernels/ops.cpp:83-89. */
+ * operation order of core/kernels/ops.cpp:83-89, with the one contraction
+ * NVRTC's default --fmad=true makes there: the cube's last product fused into
+ * the add, fma(0.044715 x x, x, x). */
 void orc_gelu_tanh(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; i++) {
         const float a = x[i];
-        const float t = 0.7978845608028654f * (a + 0.044715f * a * a * a);
+        const float t = 0.7978845608028654f * fmaf(0.044715f * a * a, a, a);
         y[i] = 0.5f * a * (1.0f + tanhf(t));
     }
+}
+
+/* SiLU gate over gx [rows, 2 cols]: out[r][c] = (g / (1 + exp(-g))) * v with
+ * g = gx[r][c], v = gx[r][cols + c] (core/kernels/conv3d_causal.cpp:997-1013;
+ * OP_SILU_GATE core/kernels/ops.cpp:75).  No product feeds an add, so there is
+ * nothing to contract. */
+void orc_silu_gate(const float* gx, float* out, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c++) {
+            const float g = gx[r * 2 * cols + c], v = gx[r * 2 * cols + cols + c];
+            out[r * cols + c] = (g / (1.0f + expf(-g))) * v;
+        }
 }
 
 /* ---- fused neighbours: ModAdd and AddMul (core/kernels/ops.cpp:80-82) ---- */

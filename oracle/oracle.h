@@ -100,6 +100,7 @@ void orc_add_mul(const float* a, const float* b, const float* c, float* y, int64
 
 /* ---- A9: GELU-tanh (core/kernels/ops.cpp:83-89) ---- */
 void orc_gelu_tanh(const float* x, float* y, int64_t n);
+void orc_silu_gate(const float* gx, float* out, int64_t rows, int64_t cols);
 
 #ifdef __cplusplus
 }

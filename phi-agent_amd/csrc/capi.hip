@@ -230,7 +230,7 @@ const char* phi_hip_last_error(void) { return g_err.c_str(); }
 int phi_hip_abi_version(void) { return PHI_QLINEAR_ABI_VERSION; }
 
 static phi_status quant_rotate_impl(const char* who, phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
-                                    int64_t K, int64_t ldx, const float* msc, const float* msh, int8_t* q,
+                                    int64_t K, int64_t ldx, const phi_dev::QrPre& pre, int8_t* q,
                                     int64_t ldq, float* s, float qmax, int round_mode, int rotate) {
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     if (rows < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
@@ -243,30 +243,44 @@ static phi_status quant_rotate_impl(const char* who, phi_stream_t stream, const 
     if (K > kMaxRotK) return fail(PHI_ERR_UNSUPPORTED, "%s: K=%lld exceeds %lld", who, (long long)K, (long long)kMaxRotK);
     if (rows > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: rows exceeds 2^31", who);
     if (!(qmax >= 1.0f && qmax <= 127.0f) || qmax != (float)(int)qmax) return fail(PHI_ERR_ARG, "%s: qmax must be an integer in [1,127]", who);
-    if (ldx < K || ldq < K) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than K", who);
+    const int64_t xcols = pre.op == phi_dev::QR_SILU_GATE ? 2 * K : K;
+    if (ldx < xcols || ldq < K)
+        return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than %s", who,
+                    pre.op == phi_dev::QR_SILU_GATE ? "2K (gate and value halves)" : "K");
     const size_t esz = x_dtype == PHI_BF16 ? 2 : 4;
     if (!aligned(x, 16) || (ldx * (int64_t)esz) % 16 != 0 || !aligned(q, 16) || ldq % 16 != 0 || !aligned(s, 4))
         return fail(PHI_ERR_ALIGN, "%s: x and q rows must be 16-byte aligned", who);
-    if ((msc && !aligned(msc, 16)) || (msh && !aligned(msh, 16)))
+    if ((pre.sc && !aligned(pre.sc, 16)) || (pre.sh && !aligned(pre.sh, 16)))
         return fail(PHI_ERR_ALIGN, "%s: modulation vectors must be 16-byte aligned", who);
     return check_hip(phi_dev::launch_quant_rotate((hipStream_t)stream, x, x_dtype == PHI_BF16, rows, K, ldx, q, ldq, s,
-                                                  qmax, round_mode == PHI_ROUND_HALF_EVEN, rotate ? 1 : 0, msc, msh),
+                                                  qmax, round_mode == PHI_ROUND_HALF_EVEN, rotate ? 1 : 0, pre),
                      who);
 }
 
 phi_status phi_hip_quant_rotate(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
                                 int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
                                 float qmax, int round_mode, int rotate) {
-    return quant_rotate_impl("quant_rotate", stream, x, x_dtype, rows, K, ldx, nullptr, nullptr, q, ldq, s, qmax,
-                             round_mode, rotate);
+    const phi_dev::QrPre pre = {phi_dev::QR_PLAIN, nullptr, nullptr, 0};
+    return quant_rotate_impl("quant_rotate", stream, x, x_dtype, rows, K, ldx, pre, q, ldq, s, qmax, round_mode, rotate);
 }
 
 phi_status phi_hip_quant_rotate_mod(phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
                                     int64_t K, int64_t ldx, const float* mod_scale, const float* mod_shift,
                                     int8_t* q, int64_t ldq, float* s, float qmax, int round_mode,
                                     int rotate) {
-    return quant_rotate_impl("quant_rotate_mod", stream, x, x_dtype, rows, K, ldx, mod_scale, mod_shift, q, ldq, s,
-                             qmax, round_mode, rotate);
+    const phi_dev::QrPre pre = {mod_scale || mod_shift ? phi_dev::QR_MOD : phi_dev::QR_PLAIN, mod_scale, mod_shift, 0};
+    return quant_rotate_impl("quant_rotate_mod", stream, x, x_dtype, rows, K, ldx, pre, q, ldq, s, qmax, round_mode,
+                             rotate);
+}
+
+phi_status phi_hip_quant_rotate_act(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                    int64_t ldx, int act, int8_t* q, int64_t ldq, float* s, float qmax,
+                                    int round_mode, int rotate) {
+    if (act != PHI_ACT_GELU_TANH && act != PHI_ACT_SILU_GATE)
+        return fail(PHI_ERR_ARG, "quant_rotate_act: act must be PHI_ACT_GELU_TANH or PHI_ACT_SILU_GATE");
+    const phi_dev::QrPre pre = {act == PHI_ACT_GELU_TANH ? phi_dev::QR_GELU : phi_dev::QR_SILU_GATE, nullptr, nullptr, K};
+    return quant_rotate_impl("quant_rotate_act", stream, x, x_dtype, rows, K, ldx, pre, q, ldq, s, qmax, round_mode,
+                             rotate);
 }
 
 size_t phi_hip_workspace_bytes(int64_t M, int64_t N, int64_t K) {
@@ -590,7 +604,28 @@ phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, vo
     if (!x || !y) return fail(PHI_ERR_ARG, "%s: null pointer", who);
     if ((x_dtype != PHI_F32 && x_dtype != PHI_BF16) || (y_dtype != PHI_F32 && y_dtype != PHI_BF16))
         return fail(PHI_ERR_ARG, "%s: dtypes must be f32 or bf16", who);
+    if (x == y && x_dtype != y_dtype) return fail(PHI_ERR_ARG, "%s: in place needs equal dtypes", who);
     return check_hip(phi_dev::launch_gelu((hipStream_t)stream, x, x_dtype == PHI_BF16, y, y_dtype == PHI_BF16, n), who);
+}
+
+phi_status phi_hip_silu_gate(phi_stream_t stream, const void* gx, int x_dtype, int64_t rows, int64_t cols,
+                             int64_t ldx, void* out, int out_dtype, int64_t ldo) {
+    static const char* who = "silu_gate";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || cols < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0 || cols == 0) return ok();
+    if (!gx || !out) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if ((x_dtype != PHI_F32 && x_dtype != PHI_BF16) || (out_dtype != PHI_F32 && out_dtype != PHI_BF16))
+        return fail(PHI_ERR_ARG, "%s: dtypes must be f32 or bf16", who);
+    if (ldx < 2 * cols || ldo < cols) return fail(PHI_ERR_SHAPE, "%s: ldx must be >= 2*cols and ldo >= cols", who);
+    const int64_t xe = x_dtype == PHI_BF16 ? 2 : 4, ye = out_dtype == PHI_BF16 ? 2 : 4;
+    const char* xb = (const char*)gx;
+    const char* ob = (const char*)out;
+    if (ob < xb + ((rows - 1) * ldx + 2 * cols) * xe && xb < ob + ((rows - 1) * ldo + cols) * ye)
+        return fail(PHI_ERR_ARG, "%s: out must not overlap gx", who);
+    return check_hip(phi_dev::launch_silu_gate((hipStream_t)stream, gx, x_dtype == PHI_BF16, ldx, out,
+                                               out_dtype == PHI_BF16, ldo, rows, cols),
+                     who);
 }
 
 }  // extern "C"

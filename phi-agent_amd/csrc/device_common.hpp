@@ -82,6 +82,27 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
            ((uint32_t)d << 24);
 }
 
+// GELU, tanh form (core/kernels/ops.cpp:83-89):
+//   t = 0.7978845608028654 * (x + 0.044715 * x^3);  y = 0.5 * x * (1 + tanh(t)),
+// t with the one contraction NVRTC's default --fmad=true makes in it (the
+// cube's last product fused into the add).  y is evaluated through the
+// identity 0.5 (1 + tanh t) = 1 / (1 + e^(-2t)) as x * rcp(1 + exp2(-2 log2(e) t))
+// on v_exp_f32 and v_rcp_f32 (1 ulp each): branch-free, about a quarter of
+// the device library tanhf's instructions, and without the cancellation in
+// 1 + tanh(t) for t << 0.  It stays within 3e-7 |x| of the reference's
+// formula; where that formula cancels to 0 (x < -9) this gives the tiny
+// true value.  Every kernel that applies GELU calls this, so a fused form
+// equals the standalone op bit for bit.
+__device__ __forceinline__ float gelu_tanh(float a) {
+    const float t = 0.7978845608028654f * fmaf(0.044715f * a * a, a, a);
+    return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t * -2.8853900817779268f));
+}
+
+// The SiLU gate: silu(g) * v = (g / (1 + exp(-g))) * v, correctly rounded
+// division (core/kernels/conv3d_causal.cpp:997-1013, OP_SILU_GATE
+// core/kernels/ops.cpp:75).  expf is the device library's.
+__device__ __forceinline__ float silu_mul(float g, float v) { return (g / (1.0f + expf(-g))) * v; }
+
 // Wave-wide max over 64 lanes.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -28,4 +28,7 @@ hipError_t launch_gemv(hipStream_t stream, const GemvBatch& b);
 
 hipError_t launch_gelu(hipStream_t stream, const void* x, int x_bf16, void* y, int y_bf16, int64_t n);
 
+hipError_t launch_silu_gate(hipStream_t stream, const void* gx, int x_bf16, int64_t ldx, void* out, int y_bf16,
+                            int64_t ldo, int64_t rows, int64_t cols);
+
 }  // namespace phi_dev

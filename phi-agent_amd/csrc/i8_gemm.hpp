@@ -44,10 +44,17 @@ hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int n
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);
 
-// msc / msh: optional per-column modulation applied first, v*(1+msc)+msh (fma).
+// Element-wise operation applied to every input element before the rotation.
+enum QrPreOp { QR_PLAIN = 0, QR_MOD = 1, QR_GELU = 2, QR_SILU_GATE = 3 };
+struct QrPre {
+    int op;             // QrPreOp
+    const float* sc;    // QR_MOD: v = fma(v, 1 + sc[k], sh[k]); either may be NULL (0)
+    const float* sh;
+    int64_t off2;       // QR_SILU_GATE: v = silu(x[k]) * x[k + off2] (elements)
+};
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                               float qmax, int half_even, int rotate, const float* msc, const float* msh);
+                               float qmax, int half_even, int rotate, const QrPre& pre);
 size_t quant_rotate_lds_bytes(int64_t K);
 
 }  // namespace phi_dev

@@ -18,12 +18,20 @@
 // amax is reduced across the workgroup, and phase C quantises 16 contiguous
 // elements per lane and writes them with one 16-byte store.
 //
+// An element-wise pre-op can run on every input element before the rotation,
+// so the tensor between it and the linear never goes through memory: the
+// adaLN modulation (QR_MOD), GELU-tanh (QR_GELU) or the SiLU gate over a
+// [gate | value] row (QR_SILU_GATE).  They use the same per-element functions
+// as the standalone kernels, so fused and unfused agree bit for bit where the
+// unfused intermediate is fp32.
+//
 // LDS: a group's 256 floats sit as 16 slots of 20 floats (16 values + 4 pad,
 // so the 16-B slot accesses of 8 lanes land on 8 distinct 4-bank windows), and
 // groups are 336 floats apart (a 16-bank shift between the teams of a wave).
 #include <cstdlib>
 
 #include "device_common.hpp"
+#include "i8_gemm.hpp"
 
 namespace phi_dev {
 
@@ -64,13 +72,37 @@ __device__ __forceinline__ void modulate16(float (&v)[16], const float* __restri
     for (int i = 0; i < 16; i++) v[i] = fmaf(v[i], 1.0f + b[i], c[i]);
 }
 
+// 16 consecutive input elements at element offset off, as fp32.
+template <bool BF16_IN>
+__device__ __forceinline__ void load16(const void* __restrict__ x, int64_t off, float (&v)[16]) {
+    if (BF16_IN) {
+        const uint4* src = (const uint4*)((const uint16_t*)x + off);
+        const uint4 a = src[0], b = src[1];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            v[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+            v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+        }
+    } else {
+        const float4* src = (const float4*)((const float*)x + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = src[i];
+            v[4 * i] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+    }
+}
+
 template <bool BF16_IN>
 __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict__ x, int64_t ldx,
                                                           int K, int8_t* __restrict__ q,
                                                           int64_t ldq, float* __restrict__ s,
                                                           float qmax, int half_even, int rotate,
-                                                          const float* __restrict__ msc,
-                                                          const float* __restrict__ msh) {
+                                                          QrPre pre) {
     extern __shared__ __align__(16) float lds[];
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
@@ -83,27 +115,18 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
     for (int g = team; g < G; g += nteams) {
         float v[16];
         const int64_t e0 = (int64_t)g * 256 + tl * 16;
-        if (BF16_IN) {
-            const uint4* src = (const uint4*)((const uint16_t*)x + (int64_t)row * ldx + e0);
-            const uint4 a = src[0], b = src[1];
-            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        load16<BF16_IN>(x, (int64_t)row * ldx + e0, v);
+        if (pre.op == QR_MOD) {
+            modulate16(v, pre.sc, pre.sh, e0);
+        } else if (pre.op == QR_GELU) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                v[2 * i] = bf16_to_f32(w[i] & 0xffffu);
-                v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
-            }
-        } else {
-            const float4* src = (const float4*)((const float*)x + (int64_t)row * ldx + e0);
+            for (int i = 0; i < 16; i++) v[i] = gelu_tanh(v[i]);
+        } else if (pre.op == QR_SILU_GATE) {
+            float u[16];
+            load16<BF16_IN>(x, (int64_t)row * ldx + pre.off2 + e0, u);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 t = src[i];
-                v[4 * i] = t.x;
-                v[4 * i + 1] = t.y;
-                v[4 * i + 2] = t.z;
-                v[4 * i + 3] = t.w;
-            }
+            for (int i = 0; i < 16; i++) v[i] = silu_mul(v[i], u[i]);
         }
-        if (msc || msh) modulate16(v, msc, msh, e0);
         if (rotate) {
             bfly16<1>(v);
             bfly16<4>(v);
@@ -248,12 +271,11 @@ __device__ __forceinline__ uint32_t cvt_pack4(float a, float b, float c, float d
     return pack4((int)a, (int)b, (int)c, (int)d);
 }
 
-template <bool BF16_IN, bool HALF_EVEN, int R>
+template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
                                                            int G, int8_t* __restrict__ q, int64_t ldq,
                                                            float* __restrict__ s, float qmax, int rotate,
-                                                           const float* __restrict__ msc,
-                                                           const float* __restrict__ msh) {
+                                                           QrPre pre_op) {
     extern __shared__ __align__(16) float lds[];
     constexpr int NW = BF16_IN ? 8 : 16;  // input dwords per lane per round
     const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
@@ -268,20 +290,24 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
     // Every round's loads first.  Lanes past the row's last group, or in a
     // row past the last, read valid data of another group and discard it.
     const int64_t xrow = (int64_t)min(row, rows - 1) * ldx + tl * 16;
-    uint32_t raw[R][NW];
+    // The SiLU gate's value operand is a second set of the same loads.
+    constexpr int NS = OP == QR_SILU_GATE ? 2 : 1;
+    uint32_t raw[NS][R][NW];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int64_t off = xrow + (int64_t)min(g0 + 4 * r, G - 1) * 256;
-        const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)x + off) : (const uint4*)((const float*)x + off);
+    for (int h = 0; h < NS; h++)
 #pragma unroll
-        for (int i = 0; i < NW / 4; i++) {
-            const uint4 t = src[i];
-            raw[r][4 * i] = t.x;
-            raw[r][4 * i + 1] = t.y;
-            raw[r][4 * i + 2] = t.z;
-            raw[r][4 * i + 3] = t.w;
+        for (int r = 0; r < R; r++) {
+            const int64_t off = xrow + (int64_t)min(g0 + 4 * r, G - 1) * 256 + (h ? pre_op.off2 : 0);
+            const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)x + off) : (const uint4*)((const float*)x + off);
+#pragma unroll
+            for (int i = 0; i < NW / 4; i++) {
+                const uint4 t = src[i];
+                raw[h][r][4 * i] = t.x;
+                raw[h][r][4 * i + 1] = t.y;
+                raw[h][r][4 * i + 2] = t.z;
+                raw[h][r][4 * i + 3] = t.w;
+            }
         }
-    }
 
     float rot[R][16];
     uint32_t amax = 0;
@@ -290,10 +316,21 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
         float v[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            if (BF16_IN) v[i] = __uint_as_float(i & 1 ? raw[r][i >> 1] & 0xffff0000u : raw[r][i >> 1] << 16);
-            else v[i] = __uint_as_float(raw[r][i]);
+            if (BF16_IN) v[i] = __uint_as_float(i & 1 ? raw[0][r][i >> 1] & 0xffff0000u : raw[0][r][i >> 1] << 16);
+            else v[i] = __uint_as_float(raw[0][r][i]);
         }
-        if (msc || msh) modulate16(v, msc, msh, (int64_t)min(g0 + 4 * r, G - 1) * 256 + tl * 16);
+        if (OP == QR_MOD) modulate16(v, pre_op.sc, pre_op.sh, (int64_t)min(g0 + 4 * r, G - 1) * 256 + tl * 16);
+        if (OP == QR_GELU) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = gelu_tanh(v[i]);
+        }
+        if (OP == QR_SILU_GATE) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t u = raw[NS - 1][r][BF16_IN ? i >> 1 : i];
+                v[i] = silu_mul(v[i], __uint_as_float(BF16_IN ? (i & 1 ? u & 0xffff0000u : u << 16) : u));
+            }
+        }
         if (rotate) {
             bfly16f<1>(v);
             bfly16f<4>(v);
@@ -393,53 +430,68 @@ static int tile_rounds(int64_t rows, int G) {
     return best;
 }
 
-template <bool BF16_IN, bool HALF_EVEN, int R>
+template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                                 int64_t ldq, float* s, float qmax, int rotate, const float* msc, const float* msh) {
+                                 int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre) {
     const int wpr = (G + 4 * R - 1) / (4 * R);
     const int rpb = wpr >= 8 ? 1 : 8 / wpr;
     const size_t lds = ((size_t)rpb * wpr * QT_WAVE + 16) * sizeof(float);
     static bool lds_set = false;  // one attribute call per instantiation and process
     if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)quant_rotate_tiles<BF16_IN, HALF_EVEN, R>,
+        const hipError_t e = hipFuncSetAttribute((const void*)quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)((16 * QT_WAVE + 16) * sizeof(float)));
         if (e != hipSuccess) return e;
         lds_set = true;
     }
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
-    hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R>), grid, block, lds, stream, x, ldx, (int)rows, G, q,
-                       ldq, s, qmax, rotate, msc, msh);
+    hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows, G,
+                       q, ldq, s, qmax, rotate, pre);
     return hipGetLastError();
+}
+
+// A pre-op keeps R at 1 or 2: the modulation holds per-round scale/shift
+// registers and the SiLU gate a second set of loads, and GELU's VALU work
+// per element dwarfs the per-wave costs a larger R spreads.
+template <bool BF16_IN, bool HALF_EVEN, int OP>
+static hipError_t launch_tiles_op(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
+                                  int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre) {
+    if (tile_rounds(rows, G) == 1)
+        return launch_tiles_r<BF16_IN, HALF_EVEN, 1, OP>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+    return launch_tiles_r<BF16_IN, HALF_EVEN, 2, OP>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
 }
 
 template <bool BF16_IN, bool HALF_EVEN>
 static hipError_t launch_tiles(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                               int64_t ldq, float* s, float qmax, int rotate, const float* msc, const float* msh) {
-    // With a modulation the per-round scale/shift registers cap R at 2.
-    int R = tile_rounds(rows, G);
-    if ((msc || msh) && R > 2 && (G + 7) / 8 <= 16) R = 2;
-    switch (R) {
-        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
-        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
-        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
-        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
-        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+                               int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre) {
+    switch (pre.op) {
+        case QR_MOD: return launch_tiles_op<BF16_IN, HALF_EVEN, QR_MOD>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case QR_GELU: return launch_tiles_op<BF16_IN, HALF_EVEN, QR_GELU>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case QR_SILU_GATE:
+            return launch_tiles_op<BF16_IN, HALF_EVEN, QR_SILU_GATE>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        default: break;
+    }
+    switch (tile_rounds(rows, G)) {
+        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
     }
 }
 
 // Host-side launcher.  Validation is done by the C ABI layer.
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                               float qmax, int half_even, int rotate, const float* msc, const float* msh) {
+                               float qmax, int half_even, int rotate, const QrPre& pre) {
     const int G = (int)(K / 256);
     if (rows == 0) return hipSuccess;
     if (G <= 64) {
         if (bf16_in)
-            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh)
-                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
-        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh)
-                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, msc, msh);
+            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre)
+                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre)
+                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
     }
     int threads = ((16 * G + 63) / 64) * 64;
     if (threads > 1024) threads = 1024;
@@ -451,10 +503,10 @@ hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, 
     }
     if (bf16_in) {
         hipLaunchKernelGGL(quant_rotate_rows<true>, dim3((unsigned)rows), dim3(threads), lds_bytes,
-                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate, msc, msh);
+                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate, pre);
     } else {
         hipLaunchKernelGGL(quant_rotate_rows<false>, dim3((unsigned)rows), dim3(threads), lds_bytes,
-                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate, msc, msh);
+                           stream, x, ldx, (int)K, q, ldq, s, qmax, half_even, rotate, pre);
     }
     return hipGetLastError();
 }

@@ -28,6 +28,7 @@ INCLUDE_DIR = os.path.join(os.path.dirname(os.path.dirname(PKG_DIR)), "include")
 F32, BF16, F16, I32, I8, F8_E4M3, F8_E5M2, U8_E4M3 = range(8)
 # phi_round
 ROUND_HALF_AWAY, ROUND_HALF_EVEN = 0, 1
+ACT_GELU_TANH, ACT_SILU_GATE = 1, 2
 # phi_status
 STATUS = {0: "PHI_OK", 1: "PHI_ERR_ARG", 2: "PHI_ERR_SHAPE", 3: "PHI_ERR_ALIGN",
           4: "PHI_ERR_WORKSPACE", 5: "PHI_ERR_HIP", 6: "PHI_ERR_DEVICE_LOST",
@@ -61,7 +62,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_workspace_bytes", "phi_hip_q8_linear", "phi_hip_w4a8_expand",
            "phi_hip_w4a8_prepare", "phi_hip_w4a8_linear", "phi_hip_i8_gemv_batched",
            "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes",
-           "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual"]
+           "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual", "phi_hip_quant_rotate_act",
+           "phi_hip_silu_gate"]
 
 _lib = None
 
@@ -96,6 +98,8 @@ def load() -> ctypes.CDLL:
     L.phi_hip_gemv_workspace_bytes.argtypes = [I]
     L.phi_hip_gemv_workspace_bytes.restype = SZ
     L.phi_hip_gelu_tanh.argtypes = [P, P, I, P, I, I64]
+    L.phi_hip_quant_rotate_act.argtypes = [P, P, I, I64, I64, I64, I, P, I64, P, F, I, I]
+    L.phi_hip_silu_gate.argtypes = [P, P, I, I64, I64, I64, P, I, I64]
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:
@@ -138,14 +142,32 @@ def _require_device(*ts):
 def quant_rotate(x: torch.Tensor, *, qmax: float = 127.0, round_mode: int = ROUND_HALF_AWAY,
                  rotate: bool = True, q: torch.Tensor | None = None,
                  s: torch.Tensor | None = None, mod_scale: torch.Tensor | None = None,
-                 mod_shift: torch.Tensor | None = None, stream=None):
+                 mod_shift: torch.Tensor | None = None, act: str | None = None, stream=None):
     """Rotate (256-wide convrot) and quantise rows of x [rows, K] (f32/bf16).
 
     mod_scale / mod_shift ([K] fp32): the adaLN modulation fma(x, 1 + scale,
     shift) applied first (phi_hip_quant_rotate_mod).
+    act: "gelu_tanh" applies GELU-tanh first; "silu_gate" takes x [rows, 2K]
+    and quantises silu(x[:, :K]) * x[:, K:] (phi_hip_quant_rotate_act).
     Returns (q int8 [rows, K], s f32 [rows])."""
     _require_device(x, mod_scale, mod_shift)
     rows, K = x.shape
+    if act is not None:
+        if mod_scale is not None or mod_shift is not None:
+            raise ValueError("quant_rotate: act and modulation are exclusive")
+        code = {"gelu_tanh": ACT_GELU_TANH, "silu_gate": ACT_SILU_GATE}[act]
+        if act == "silu_gate":
+            if K % 2:
+                raise ValueError("quant_rotate: silu_gate needs an even number of columns")
+            K //= 2
+        if q is None:
+            q = torch.empty((rows, K), dtype=torch.int8, device=x.device)
+        if s is None:
+            s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+        _check(load().phi_hip_quant_rotate_act(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0), code,
+                                               _ptr(q), q.stride(0), _ptr(s), float(qmax), round_mode,
+                                               1 if rotate else 0))
+        return q, s
     if q is None:
         q = torch.empty((rows, K), dtype=torch.int8, device=x.device)
     if s is None:
@@ -323,9 +345,28 @@ def gemv_batched(q8: torch.Tensor, s8: torch.Tensor, weights, scales, *, biases=
 
 
 def gelu_tanh(x: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """GELU-tanh of a contiguous x into out (x's shape; f32 or bf16)."""
     _require_device(x, out)
     if out is None:
         out = torch.empty_like(x)
+    if not x.is_contiguous() or not out.is_contiguous() or out.numel() != x.numel():
+        raise ValueError("gelu_tanh: x and out must be contiguous and equally sized")
     _check(load().phi_hip_gelu_tanh(_stream(stream), _ptr(x), _dt(x), _ptr(out), _dt(out),
                                     x.numel()))
+    return out
+
+
+def silu_gate(gx: torch.Tensor, out: torch.Tensor | None = None, *, out_dtype=None,
+              stream=None) -> torch.Tensor:
+    """out [rows, cols] = silu(gx[:, :cols]) * gx[:, cols:] for gx [rows, 2*cols]
+    (phi_hip_silu_gate; dispatch_silu_gate_fused core/kernels/h3_kernels.hpp:116-129)."""
+    _require_device(gx, out)
+    rows, two = gx.shape
+    if two % 2:
+        raise ValueError("silu_gate: gx needs an even number of columns")
+    cols = two // 2
+    if out is None:
+        out = torch.empty((rows, cols), dtype=out_dtype or gx.dtype, device=gx.device)
+    _check(load().phi_hip_silu_gate(_stream(stream), _ptr(gx), _dt(gx), rows, cols, gx.stride(0), _ptr(out),
+                                    _dt(out), out.stride(0)))
     return out

@@ -78,6 +78,33 @@ def test_quant_rotate_contract(lib):
     assert Q.last_error() == ""
 
 
+def test_activation_contracts(lib):
+    # unknown activation
+    rc = lib.phi_hip_quant_rotate_act(None, FAKE, Q.F32, 4, 256, 512, 7, FAKE, 256, FAKE, 127.0, 0, 1)
+    assert rc == 1 and "act" in Q.last_error()
+    # the SiLU gate reads [gate | value]: ldx must cover 2K
+    rc = lib.phi_hip_quant_rotate_act(None, FAKE, Q.F32, 4, 256, 256, Q.ACT_SILU_GATE, FAKE, 256, FAKE,
+                                      127.0, 0, 1)
+    assert rc == 2 and "2K" in Q.last_error()
+    rc = lib.phi_hip_quant_rotate_act(None, FAKE, Q.F32, 4, 300, 600, Q.ACT_GELU_TANH, FAKE, 304, FAKE,
+                                      127.0, 0, 1)
+    assert rc == 2 and "K=300 is not a multiple of 256" in Q.last_error()
+    rc = lib.phi_hip_silu_gate(None, FAKE, Q.F32, 4, 64, 100, ctypes.c_void_p(0x900000), Q.F32, 64)
+    assert rc == 2
+    # out overlapping gx
+    rc = lib.phi_hip_silu_gate(None, FAKE, Q.F32, 4, 64, 128, ctypes.c_void_p(0x10000 + 256), Q.F32, 64)
+    assert rc == 1 and "overlap" in Q.last_error()
+    rc = lib.phi_hip_silu_gate(None, FAKE, Q.I8, 4, 64, 128, ctypes.c_void_p(0x900000), Q.F32, 64)
+    assert rc == 1
+    # in-place GELU only between equal dtypes
+    rc = lib.phi_hip_gelu_tanh(None, FAKE, Q.BF16, FAKE, Q.F32, 64)
+    assert rc == 1 and "in place" in Q.last_error()
+    # empty problems are no-ops
+    assert lib.phi_hip_silu_gate(None, None, Q.F32, 0, 64, 128, None, Q.F32, 64) == 0
+    assert lib.phi_hip_quant_rotate_act(None, None, Q.F32, 0, 256, 512, Q.ACT_SILU_GATE, None, 256, None,
+                                        127.0, 0, 1) == 0
+
+
 def test_gemm_contract(lib):
     g = lib.phi_hip_i8_gemm
     rc, msg = status_and_msg(lib, g(None, FAKE, 64, FAKE, 64, FAKE, FAKE, 0, None, 0, FAKE, Q.BF16, 64,

@@ -134,3 +134,121 @@ def test_contract_errors(dev):
     x = torch.zeros((2, 300), device=dev)
     with pytest.raises(Q.QLinearError, match="multiple of 256"):
         Q.quant_rotate(x, mod_scale=torch.zeros(300, device=dev))
+
+
+# ---------------------------------------------------------------- activations
+# GELU-tanh (core/kernels/ops.cpp:83-89) and the SiLU gate
+# (core/kernels/conv3d_causal.cpp:997-1013) in front of the rotation.  The
+# fused prologue must equal our own unfused pair (fp32 intermediate) bit for
+# bit; against the oracle the activation differs in its last bits (GELU's
+# sigmoid-form evaluation, expf of the device library vs the host's libm), so
+# codes may move by one step where a value sits on a rounding boundary, and
+# scales by a few ulps.
+ACT_SHAPES = [(1, 256), (37, 3072), (300, 1024), (129, 12288), (4, 16640), (3, 20480)]
+
+
+def act_input(M, K, dtype, seed):
+    x = synth.activations(M, K, seed=seed)
+    return x if dtype == torch.bfloat16 else x.float() * 1.5
+
+
+def close_to_oracle(q, s, qo, so):
+    q = q.cpu().numpy().astype(np.int32)
+    s = s.cpu().numpy()
+    d = np.abs(q - qo.astype(np.int32))
+    assert d.max() <= 1
+    assert (d > 0).mean() <= 1e-3
+    np.testing.assert_allclose(s, so, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,K", ACT_SHAPES)
+def test_quant_rotate_gelu_equals_gelu_then_quantise(dev, orc, dtype, M, K):
+    x = act_input(M, K, dtype, M * 7 + K).to(dev)
+    q, s = Q.quant_rotate(x, act="gelu_tanh")
+    h = Q.gelu_tanh(x, out=torch.empty(x.shape, dtype=torch.float32, device=dev))
+    qu, su = Q.quant_rotate(h)
+    torch.cuda.synchronize()
+    assert torch.equal(q, qu)
+    assert torch.equal(s.view(torch.int32), su.view(torch.int32))
+    qo, so = orc.quantize_rows(orc.gelu_tanh(x.float().cpu().numpy()))
+    close_to_oracle(q, s, qo, so)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,K", ACT_SHAPES)
+@pytest.mark.parametrize("pad", [0, 256])
+def test_quant_rotate_silu_equals_silu_then_quantise(dev, orc, dtype, M, K, pad):
+    wide = act_input(M, 2 * K + pad, dtype, M * 5 + K).to(dev)
+    gx = wide[:, :2 * K]  # row stride 2K + pad
+    q, s = Q.quant_rotate(gx, act="silu_gate")
+    h = Q.silu_gate(gx, out_dtype=torch.float32)
+    qu, su = Q.quant_rotate(h)
+    torch.cuda.synchronize()
+    assert torch.equal(q, qu)
+    assert torch.equal(s.view(torch.int32), su.view(torch.int32))
+    qo, so = orc.quantize_rows(orc.silu_gate(gx.float().cpu().numpy()))
+    close_to_oracle(q, s, qo, so)
+
+
+def test_quant_rotate_act_half_even_and_qmax(dev, orc):
+    x = act_input(64, 3072, torch.bfloat16, 11).to(dev)
+    for rm, qmax in [(Q.ROUND_HALF_EVEN, 127.0), (Q.ROUND_HALF_AWAY, 7.0)]:
+        q, s = Q.quant_rotate(x, act="gelu_tanh", round_mode=rm, qmax=qmax)
+        h = Q.gelu_tanh(x, out=torch.empty(x.shape, dtype=torch.float32, device=dev))
+        qu, su = Q.quant_rotate(h, round_mode=rm, qmax=qmax)
+        torch.cuda.synchronize()
+        assert torch.equal(q, qu) and torch.equal(s.view(torch.int32), su.view(torch.int32))
+        assert int(q.abs().max()) == int(qmax)
+
+
+def bf16_within_one_ulp(got_bf16, want_f32):
+    """got (bf16 tensor) is want rounded to bf16, or one bf16 step from it."""
+    want = torch.from_numpy(want_f32).to(torch.bfloat16)
+    a = u16(got_bf16).astype(np.int32)
+    b = want.view(torch.int16).numpy().view(np.uint16).astype(np.int32)
+    # sign-magnitude bf16 bits -> a monotone integer line
+    a = np.where(a & 0x8000, -(a & 0x7fff), a)
+    b = np.where(b & 0x8000, -(b & 0x7fff), b)
+    assert np.abs(a - b).max() <= 1
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,cols", [(1, 8), (5, 13), (300, 1024), (64, 3072)])
+def test_silu_gate_standalone(dev, orc, xdt, ydt, rows, cols):
+    gx = act_input(rows, 2 * cols, xdt, rows + cols).to(dev)
+    out = Q.silu_gate(gx, out_dtype=ydt)
+    torch.cuda.synchronize()
+    want = orc.silu_gate(gx.float().cpu().numpy())
+    if ydt == torch.float32:
+        np.testing.assert_allclose(out.cpu().numpy(), want, rtol=2e-6, atol=1e-30)
+    else:
+        bf16_within_one_ulp(out, want)
+
+
+def test_silu_gate_scalar_path_matches_vector_path(dev):
+    base = act_input(33, 2 * 1024 + 8, torch.bfloat16, 3).to(dev)
+    vec = Q.silu_gate(base[:, :2048], out_dtype=torch.float32)       # 16-B aligned rows
+    mis = Q.silu_gate(base[:, 1:2049], out_dtype=torch.float32)      # rows start 2 B in: scalar path
+    ref = Q.silu_gate(base[:, 1:2049].contiguous(), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(mis.view(torch.int32), ref.view(torch.int32))
+    assert vec.shape == mis.shape
+
+
+@pytest.mark.parametrize("n", [8, 100003, 4352 * 12288 // 64 + 5])
+def test_gelu_vector_tail_and_misaligned_paths_agree(dev, orc, n):
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(n + 1, generator=g) * 3).to(torch.bfloat16).to(dev)
+    full = Q.gelu_tanh(x)                                    # vector chunks + tail
+    mis = Q.gelu_tanh(x[1:])                                 # 2-byte offset: scalar path
+    torch.cuda.synchronize()
+    assert torch.equal(full[1:].view(torch.int16), mis.view(torch.int16))
+    xf = x.float().cpu().numpy()
+    err = np.abs(full.float().cpu().numpy() - orc.gelu_tanh(xf))
+    assert np.all(err <= 2.0 ** -8 * np.abs(orc.gelu_tanh(xf)) + 4e-7 * np.abs(xf))
+    inplace = x.clone()
+    Q.gelu_tanh(inplace, out=inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(inplace.view(torch.int16), full.view(torch.int16))

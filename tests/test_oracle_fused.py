@@ -80,3 +80,65 @@ def test_mod_add_b_minus_one_gives_shift():
     a = np.array([[3.5, -1e30, 7.0]], np.float32)
     y = oracle.mod_add(a, np.full(3, -1.0, np.float32), np.array([0.25, -2.0, 0.0], np.float32))
     assert np.array_equal(y, np.array([[0.25, -2.0, 0.0]], np.float32))
+
+
+# ---------------------------------------------------------------- activations
+def act_sample(n, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    x[:12] = [0.0, -0.0, 1.0, -1.0, 10.0, -10.0, 30.0, -30.0, 1e-3, -1e-3, 5.5, -5.5]
+    return x
+
+
+def test_gelu_tanh_oracle_against_torch_and_float64():
+    """GELU-tanh (core/kernels/ops.cpp:83-89) against torch's own tanh-GELU and
+    the float64 value of the same formula."""
+    torch = pytest.importorskip("torch")
+    x = act_sample(20000, 3)
+    y = oracle.gelu_tanh(x)
+    tref = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    np.testing.assert_allclose(y, tref, rtol=1e-5, atol=1e-6)
+    xd = x.astype(np.float64)
+    exact = 0.5 * xd * (1 + np.tanh(np.sqrt(2 / np.pi) * (xd + 0.044715 * xd ** 3)))
+    # 1 + tanh(t) cancels for t << 0, so the fp32 formula is good to ~1 ulp of |x|/2 there.
+    np.testing.assert_allclose(y, exact, rtol=2e-6, atol=2e-7 * np.abs(xd).max())
+
+
+def test_gelu_tanh_oracle_limits():
+    x = np.array([0.0, 10.0, 30.0, 1e4, -10.0, -30.0, -1e4], dtype=np.float32)
+    y = oracle.gelu_tanh(x)
+    assert y[0] == 0.0
+    # tanh(t) rounds to 1 for t > ~9: gelu(x) = 0.5 x * 2 = x exactly
+    assert np.array_equal(y[1:4], x[1:4])
+    # and to -1 for t < -9: 1 + tanh = 0, so gelu(x) = 0
+    assert np.all(y[4:] == 0.0)
+    # odd part: gelu(x) - gelu(-x) = x exactly in real arithmetic
+    z = act_sample(5000, 4)
+    d = oracle.gelu_tanh(z).astype(np.float64) - oracle.gelu_tanh(-z).astype(np.float64)
+    np.testing.assert_allclose(d, z, rtol=1e-6, atol=1e-6)
+
+
+def test_silu_gate_oracle_against_torch_and_float64():
+    """silu(g) * v over [gate | value] rows (core/kernels/conv3d_causal.cpp:997-1013)."""
+    torch = pytest.importorskip("torch")
+    rows, cols = 40, 500
+    gx = act_sample(rows * 2 * cols, 5).reshape(rows, 2 * cols)
+    out = oracle.silu_gate(gx)
+    g, v = gx[:, :cols], gx[:, cols:]
+    tref = (torch.nn.functional.silu(torch.from_numpy(g)) * torch.from_numpy(v)).numpy()
+    np.testing.assert_allclose(out, tref, rtol=1e-6, atol=1e-30)
+    gd, vd = g.astype(np.float64), v.astype(np.float64)
+    np.testing.assert_allclose(out, gd / (1 + np.exp(-gd)) * vd, rtol=1e-6, atol=1e-30)
+    # the pairing is per row: row r's value half, not the flat next block
+    assert not np.allclose(out[1], (g[1] / (1 + np.exp(-g[1].astype(np.float64)))) * gx[0, cols:])
+
+
+def test_silu_gate_oracle_limits():
+    g = np.array([0.0, 20.0, 100.0, -100.0, -200.0], dtype=np.float32)
+    v = np.array([3.0, 1.5, -2.0, 7.0, -7.0], dtype=np.float32)
+    out = oracle.silu_gate(np.concatenate([g, v])[None, :])[0]
+    assert out[0] == 0.0
+    # exp(-g) < 2^-24: 1 + exp(-g) rounds to 1, so silu(g) * v = g * v exactly
+    assert out[1] == np.float32(20.0 * 1.5) and out[2] == np.float32(-200.0)
+    # exp(-g) overflows: g / inf = 0
+    assert out[3] == 0.0 and out[4] == 0.0
