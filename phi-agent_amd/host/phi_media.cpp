@@ -105,6 +105,31 @@ void dispatch_quant_convrot(ComputeContext& ctx, const QuantConvrotArgs& a) {
               "quant_convrot");
 }
 
+// core/kernels/gpu_ops.cpp:14-47: the same opcode and size gates, GeluTanh served.
+void dispatch_elem(ComputeContext& ctx, const ElemArgs& a) {
+    if ((unsigned)a.op > 12u) throw MediaError("elem: unknown opcode " + std::to_string((int)a.op));
+    const i64 n = a.rows * a.cols;
+    if (n <= 0) throw MediaError("elem: empty");
+    if (a.y.bytes && (u64)n * 4 > a.y.bytes) throw MediaError("elem: output buffer is too small");
+    if (a.a.bytes && (u64)n * 4 > a.a.bytes)
+        throw MediaError("elem: operand A is too small for " + std::to_string(n) + " elements");
+    if (a.op != ElemOp::GeluTanh)
+        throw MediaError("elem: opcode " + std::to_string((int)a.op) +
+                         " is not served by the quantized-linear library (GeluTanh only)");
+    ctx.check(phi_hip_gelu_tanh(ctx.stream(), cat(a.a.res, a.a.off), PHI_F32, at(a.y.res, a.y.off), PHI_F32, n),
+              "elem");
+}
+
+// core/kernels/h3_kernels.cpp:466-482
+void dispatch_silu_gate_fused(ComputeContext& ctx, const GpuAlloc& gx, const GpuAlloc& out, i64 rows, i64 cols) {
+    if (rows <= 0 || cols <= 0) throw MediaError("silu_gate_fused: empty");
+    if (gx.bytes && (u64)(rows * 2 * cols) * 4 > gx.bytes) throw MediaError("silu_gate_fused: gx is too small");
+    if (out.bytes && (u64)(rows * cols) * 4 > out.bytes) throw MediaError("silu_gate_fused: out is too small");
+    ctx.check(phi_hip_silu_gate(ctx.stream(), cat(gx.res, gx.off), PHI_F32, rows, cols, 2 * cols, at(out.res, out.off),
+                                PHI_F32, cols),
+              "silu_gate_fused");
+}
+
 // core/kernels/w4a8_expand.cpp:263-303
 void dispatch_w4a8_expand(ComputeContext& ctx, const W4a8ExpandArgs& a) {
     if (a.rows <= 0 || a.k <= 0) return;

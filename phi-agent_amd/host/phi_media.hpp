@@ -139,6 +139,30 @@ struct W4a8ExpandArgs {
 
 void dispatch_w4a8_expand(ComputeContext& ctx, const W4a8ExpandArgs& args);
 
+// Elementwise ops (core/kernels/gpu_ops.hpp:14-48).  The opcode values are the
+// reference's; this library serves the one that sits between the MLP's two
+// linears (GeluTanh, flat) and refuses the others with MediaError.
+enum class ElemOp {
+    Add = 0, Mul = 1, SiluGate = 2, Tanh = 3, Silu = 4, Scale = 5, AddMul = 6, Copy = 7,
+    Modulate = 8, Exp = 9, AddScale = 10, GeluTanh = 11, ModAdd = 12,
+};
+enum class ElemMode { Flat = 0, Row = 1, Col = 2, Scalar = 3 };
+
+struct ElemArgs {
+    ElemOp op = ElemOp::Add;
+    GpuAlloc a, b, c, y;
+    i64 rows = 1, cols = 1;
+    ElemMode bMode = ElemMode::Flat;
+    ElemMode cMode = ElemMode::Flat;
+    float alpha = 0.0f;
+    float beta = 0.0f;
+};
+
+void dispatch_elem(ComputeContext& ctx, const ElemArgs& a);
+
+// out[r][c] = silu(gx[r][c]) * gx[r][cols + c], fp32 (core/kernels/h3_kernels.hpp:116-129).
+void dispatch_silu_gate_fused(ComputeContext& ctx, const GpuAlloc& gx, const GpuAlloc& out, i64 rows, i64 cols);
+
 // One linear weight in the int8 form the GEMM reads.
 struct QuantLinear {
     GpuAlloc w;      // [n,k] int8

@@ -137,6 +137,64 @@ static void test_w4a8_expand(ComputeContext& ctx) {
            failures == before ? "bit-exact" : "mismatch");
 }
 
+// dispatch_elem(GeluTanh) and dispatch_silu_gate_fused against the oracle.
+// The device evaluates GELU's 0.5 (1 + tanh t) as 1 / (1 + e^(-2t)) and takes
+// expf from its own library, so the bound is 4e-7 |x| (GELU) and 2e-6
+// relative (SiLU gate) instead of bit equality.
+static void test_activations(ComputeContext& ctx) {
+    const i64 rows = 33, cols = 1000;
+    std::mt19937 rng(11);
+    std::normal_distribution<float> nd(0.0f, 3.0f);
+    std::vector<float> gx(rows * 2 * cols);
+    for (auto& v : gx) v = nd(rng);
+    const u64 off_gx = 0, off_g = off_gx + gx.size() * 4, off_s = off_g + gx.size() * 4;
+    GpuBuffer* pool = ctx.create_device_buffer(off_s + rows * cols * 4);
+    ctx.upload(pool, gx.data(), gx.size() * 4, off_gx);
+    ctx.begin();
+    ElemArgs ea;
+    ea.op = ElemOp::GeluTanh;
+    ea.a = GpuAlloc{pool, off_gx, gx.size() * 4};
+    ea.y = GpuAlloc{pool, off_g, gx.size() * 4};
+    ea.rows = rows;
+    ea.cols = 2 * cols;
+    dispatch_elem(ctx, ea);
+    dispatch_silu_gate_fused(ctx, GpuAlloc{pool, off_gx, gx.size() * 4}, GpuAlloc{pool, off_s, (u64)(rows * cols * 4)},
+                             rows, cols);
+    ctx.submit();
+    std::vector<float> g(gx.size()), sg(rows * cols), go(gx.size()), so(rows * cols);
+    ctx.download(pool, g.data(), g.size() * 4, off_g);
+    ctx.download(pool, sg.data(), sg.size() * 4, off_s);
+    orc_gelu_tanh(gx.data(), go.data(), (int64_t)gx.size());
+    orc_silu_gate(gx.data(), so.data(), rows, cols);
+    int bad = 0;
+    for (size_t i = 0; i < g.size(); i++) bad += !(std::fabs(g[i] - go[i]) <= 4e-7f * std::fabs(gx[i]));
+    CHECK(bad == 0, "elem GeluTanh: %d values off the oracle", bad);
+    bad = 0;
+    for (size_t i = 0; i < sg.size(); i++) bad += !(std::fabs(sg[i] - so[i]) <= 2e-6f * std::fabs(so[i]) + 1e-30f);
+    CHECK(bad == 0, "silu_gate_fused: %d values off the oracle", bad);
+    ctx.release_buffer(pool);
+
+    bool threw = false;
+    try {
+        ElemArgs bad_op;
+        bad_op.op = ElemOp::Exp;
+        bad_op.rows = 1;
+        bad_op.cols = 4;
+        dispatch_elem(ctx, bad_op);
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "not served") != nullptr;
+    }
+    CHECK(threw, "elem Exp must throw MediaError");
+    threw = false;
+    try {
+        dispatch_silu_gate_fused(ctx, GpuAlloc{}, GpuAlloc{}, 0, 8);
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "empty") != nullptr;
+    }
+    CHECK(threw, "silu_gate_fused rows=0 must throw MediaError");
+    printf("activations: %s\n", failures ? "mismatch" : "within bounds");
+}
+
 static void test_errors(ComputeContext& ctx) {
     bool threw = false;
     try {
@@ -179,6 +237,7 @@ int main() {
         test_errors(ctx);
         test_linear_gemm(ctx);
         test_w4a8_expand(ctx);
+        test_activations(ctx);
     } catch (const std::exception& e) {
         printf("FAIL exception: %s\n", e.what());
         return 1;

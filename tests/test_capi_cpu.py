@@ -52,7 +52,8 @@ def test_host_layer_library_exports_reference_names():
                          text=True).stdout
     for name in ("phi::media::dispatch_int8_gemm", "phi::media::dispatch_quant_convrot",
                  "phi::media::dispatch_w4a8_expand", "phi::media::linear_gemm",
-                 "phi::media::ComputeContext::submit"):
+                 "phi::media::ComputeContext::submit", "phi::media::dispatch_elem",
+                 "phi::media::dispatch_silu_gate_fused"):
         assert name in out, name
 
 
