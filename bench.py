@@ -47,6 +47,9 @@ CONFIGS = {
     # Config 1's MLP as a DiT sub-block: adaLN modulate -> up (bf16) -> GELU-tanh
     # -> down into the fp32 residual stream through the gate.
     "c1_block": dict(kind="block", M=4352, K=3072, N=12288),
+    # The text encoder's convrot_w4a4 MLP up-projection (hidden 5120 -> 25600,
+    # a 1024-token prompt): rotate + quantise with qmax 7, then the int4 GEMM.
+    "c5_w4a4": dict(kind="w4a4", M=1024, K=5120, N=25600),
 }
 
 
@@ -268,6 +271,53 @@ def bench_w4a8(cfg, steps, warmup):
                       "expand_once_us": None if ms_ws is None else ms_ws * 1e3}}
 
 
+def bench_w4a4(cfg, steps, warmup):
+    """One step: phi_hip_quant_rotate (qmax 7) then phi_hip_i4_gemm (fp32 out,
+    as the reference), with and without the expand-once workspace; the faster
+    is reported."""
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    B = torch.randint(0, 256, (N, K // 2), generator=g, device=dev, dtype=torch.uint8)
+    sB = torch.rand(N, generator=g, device=dev) * 0.01 + 0.001
+    q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+
+    def run(ws):
+        def once():
+            Q.quant_rotate(x, q=q8, s=s8, qmax=7.0)
+            Q.i4_gemm(q8, B, s8, sB, C=y, workspace=ws)
+        for _ in range(warmup):
+            once()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            once()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    ms_reg = run(None)
+    ws = Q.i4_workspace(M, N, K, dev)
+    ms_ws = run(ws) if ws is not None else None
+    ms = min(ms_reg, ms_ws) if ms_ws is not None else ms_reg
+    ops = 2.0 * M * N * K
+    return {"value": ops / (ms * 1e-3) / 1e12, "ms": ms, "dtype": "int8",
+            "roofline": {"bound": "mfma", "achieved": ops / (ms * 1e-3) / 1e12, "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                         "traffic": None},
+            "extra": {"in_register_us": ms_reg * 1e3,
+                      "expand_once_us": None if ms_ws is None else ms_ws * 1e3}}
+
+
 def bench_gemv(cfg, steps, warmup):
     import torch
 
@@ -327,6 +377,8 @@ def main() -> int:
         r = bench_block(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "w4a8":
         r = bench_w4a8(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "w4a4":
+        r = bench_w4a4(cfg, args.steps, args.warmup)
     else:
         r = bench_gemv(cfg, args.steps, args.warmup)
     log(f"bench: {r['ms'] * 1e3:.1f} us per step")

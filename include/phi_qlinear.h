@@ -256,6 +256,27 @@ phi_status phi_hip_i8_gemv_batched(phi_stream_t stream, const int8_t* q8, const 
  * counterpart: the reference expands at load time (dispatch_w4a8_expand). */
 size_t phi_hip_w4a8_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group);
 
+/*
+ * int4 GEMM of the convrot_w4a4 family (the text encoder's weights):
+ *   C[m, n] = ((float)acc * sA[m]) * sB[n],  acc = sum_k A[m, k] * w[n, k]
+ * A [M, lda] int8 (activations rotated and quantised with qmax 7 by
+ * phi_hip_quant_rotate); B [N, ldb] bytes of packed signed nibbles, column 2j in
+ * the low nibble of byte j (w = code < 8 ? code : code - 16); sA [M], sB [N]
+ * fp32; C [M, ldc] of c_dtype (PHI_F32 as the reference, PHI_BF16 RNE, or
+ * PHI_I32 for the raw accumulators, which need no scales).  K % 512 == 0, as
+ * the reference requires.  workspace: optional, phi_hip_i4_workspace_bytes()
+ * bytes (the codes are then expanded once per call; same bits).
+ * Replaces dispatch_int4_gemm / Int4GemmArgs (core/kernels/h3_kernels.hpp:90-107,
+ * core/kernels/h3_kernels.cpp:546-662).
+ */
+phi_status phi_hip_i4_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb,
+                           const float* sA, const float* sB, void* C, int c_dtype, int64_t ldc, int64_t M,
+                           int64_t N, int64_t K, void* workspace, size_t ws_bytes);
+
+/* Workspace with which phi_hip_i4_gemm expands the codes once per call (N*K
+ * bytes from 512 rows up; 0 otherwise).  No reference counterpart. */
+size_t phi_hip_i4_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
 /* Workspace for phi_hip_i8_gemv_batched (holds the item table on the device). */
 size_t phi_hip_gemv_workspace_bytes(int n_items);
 

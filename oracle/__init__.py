@@ -51,6 +51,9 @@ def lib() -> ctypes.CDLL:
         L.orc_w4a8_expand.restype = I
         L.orc_gelu_tanh.argtypes = [P, P, I64]
         L.orc_silu_gate.argtypes = [P, P, I64, I64]
+        L.orc_quantize_convrot_w4a4.argtypes = [P, I64, I64, P, P]
+        L.orc_quantize_convrot_w4a4.restype = I
+        L.orc_int4_gemm.argtypes = [P, I64, P, I64, P, P, I64, I64, I64, P, I64]
         L.orc_mod_add.argtypes = [P, P, P, P, I64, I64]
         L.orc_add_mul.argtypes = [P, P, P, P, I64, I64]
         L.orc_f32_to_bf16_n.argtypes = [P, P, I64]
@@ -239,6 +242,28 @@ def gelu_tanh(x) -> np.ndarray:
     return y
 
 
+def quantize_convrot_w4a4(w):
+    """Signed-int4 weight packer (core/host/quant.cpp:247-272): (packed u8 [rows, cols/2], scales f32 [rows])."""
+    w = _c(w, np.float32)
+    rows, cols = w.shape
+    packed = np.empty((rows, cols // 2), dtype=np.uint8)
+    scales = np.empty(rows, dtype=np.float32)
+    if lib().orc_quantize_convrot_w4a4(_p(w), rows, cols, _p(packed), _p(scales)) != 0:
+        raise ValueError("quantize_convrot_w4a4: cols is not a multiple of 256")
+    return packed, scales
+
+
+def int4_gemm(a, b_packed, sa, sb) -> np.ndarray:
+    """C = ((float)(A . unpack(B)^T) * sa) * sb, fp32 (core/kernels/h3_kernels.cpp:546-635)."""
+    a, b = _c(a, np.int8), _c(b_packed, np.uint8)
+    M, K = a.shape
+    N = b.shape[0]
+    c = np.empty((M, N), dtype=np.float32)
+    lib().orc_int4_gemm(_p(a), K, _p(b), b.shape[1], _p(_c(sa, np.float32)), _p(_c(sb, np.float32)),
+                        M, N, K, _p(c), N)
+    return c
+
+
 def silu_gate(gx) -> np.ndarray:
     """silu(gx[:, :cols]) * gx[:, cols:] for gx [rows, 2 cols], fp32."""
     gx = _c(gx, np.float32)
@@ -311,6 +336,17 @@ def ref_grouped_decode(codes, s_rel_f32, s_channel, *, k, group, codebook=None,
             _ref_run(["w4", rows, k, group, 1 if codebook is not None else 0, hc, fc, fr, fs,
                       fcb, fco, fo])
         return np.fromfile(fo, np.float32).reshape(rows, k)
+
+
+def ref_w4a4pack(w):
+    """The reference's own quantize_convrot_w4a4 (group 256) on w [rows, cols]."""
+    w = _c(w, np.float32)
+    rows, cols = w.shape
+    with tempfile.TemporaryDirectory() as d:
+        fw, fp, fs = (os.path.join(d, n) for n in ("w", "p", "s"))
+        w.tofile(fw)
+        _ref_run(["w4a4pack", rows, cols, fw, fp, fs])
+        return (np.fromfile(fp, np.uint8).reshape(rows, cols // 2), np.fromfile(fs, np.float32))
 
 
 def ref_bench_q8(M, N, K, rows) -> float:

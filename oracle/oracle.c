@@ -290,6 +290,54 @@ int orc_w4a8_expand(const uint8_t* codes, int64_t codes_row_bytes, const void* s
 }
 
 /* ------------------------------------------------------------------------ */
+/* convrot_w4a4: signed int4 weights, absmax/7 activations                  */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_convrot_w4a4 (core/host/quant.cpp:247-272): rotate each 256-group,
+ * s = amax > 0 ? amax/7 : 1 per row, code = clamp(lround(v / s), +-7) (ties
+ * away from zero, a true division), two codes a byte with column 2j in the low
+ * nibble.  Returns 1 when cols is not a multiple of 256. */
+int orc_quantize_convrot_w4a4(const float* w, int64_t rows, int64_t cols, uint8_t* packed, float* scales) {
+    if (cols % 256 != 0) return 1;
+    float* rot = (float*)malloc(sizeof(float) * (size_t)cols);
+    for (int64_t r = 0; r < rows; r++) {
+        orc_convrot_rows(w + r * cols, rot, 1, cols);
+        float amax = 0.0f;
+        for (int64_t c = 0; c < cols; c++) amax = fmaxf(amax, fabsf(rot[c]));
+        const float s = amax > 0.0f ? amax / 7.0f : 1.0f;
+        scales[r] = s;
+        for (int64_t c = 0; c < cols; c += 2) {
+            long lo = lroundf(rot[c] / s), hi = lroundf(rot[c + 1] / s);
+            lo = lo < -7 ? -7 : (lo > 7 ? 7 : lo);
+            hi = hi < -7 ? -7 : (hi > 7 ? 7 : hi);
+            packed[r * (cols / 2) + c / 2] = (uint8_t)((lo & 0x0f) | ((hi & 0x0f) << 4));
+        }
+    }
+    free(rot);
+    return 0;
+}
+
+/* int4_gemm (core/kernels/h3_kernels.cpp:546-635): acc[m][n] = sum_k A[m][k] *
+ * nib(B[n], k), nib the signed low (even k) or high (odd k) nibble of byte k/2,
+ * then C = ((float)acc * sa[m]) * sb[n] in fp32, no bias. */
+void orc_int4_gemm(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, const float* sa,
+                   const float* sb, int64_t M, int64_t N, int64_t K, float* c, int64_t ldc) {
+    int8_t* row = (int8_t*)malloc((size_t)K);
+    for (int64_t n = 0; n < N; n++) {
+        for (int64_t k = 0; k < K; k++) {
+            int v = (b[n * ldb + k / 2] >> (4 * (k & 1))) & 0x0f;
+            row[k] = (int8_t)(v >= 8 ? v - 16 : v);
+        }
+        for (int64_t m = 0; m < M; m++) {
+            int32_t acc = 0;
+            for (int64_t k = 0; k < K; k++) acc += (int32_t)a[m * lda + k] * row[k];
+            c[m * ldc + n] = ((float)acc * sa[m]) * sb[n];
+        }
+    }
+    free(row);
+}
+
+/* ------------------------------------------------------------------------ */
 /* A9: GELU-tanh                                                            */
 /* ------------------------------------------------------------------------ */
 

@@ -12,6 +12,7 @@
 //   phiref gemm M N K a.i8 sa.f32 b.i8 sb.f32 y.f32
 //   phiref w4 ROWS K GROUP HAS_CB HAS_CORR codes.u8 srel.f32 sch.f32 cb.f32 corr.f32 out.f32
 //   phiref w6 ROWS K GROUP HAS_CORR codes.u8 srel.f32 sch.f32 corr.f32 out.f32
+//   phiref w4a4pack ROWS COLS w.f32 packed.u8 scales.f32   (quantize_convrot_w4a4, group 256)
 //   phiref bench_q8 M N K ROWS_TIMED       (prints seconds for ROWS_TIMED rows)
 #include <chrono>
 #include <cstdio>
@@ -127,6 +128,14 @@ int main(int argc, char** argv) {
                                               out.data() + r * k);
             }
             write_file(argv[ai], out.data(), out.size());
+        } else if (op == "w4a4pack" && argc == 7) {
+            const i64 rows = atoll(argv[2]), cols = atoll(argv[3]);
+            auto w = read_file<float>(argv[4], (size_t)(rows * cols));
+            std::vector<u8> packed((size_t)(rows * cols / 2));
+            std::vector<float> scales((size_t)rows);
+            quantize_convrot_w4a4(w.data(), rows, cols, packed.data(), scales.data(), 256);
+            write_file(argv[5], packed.data(), packed.size());
+            write_file(argv[6], scales.data(), scales.size());
         } else if (op == "bench_q8" && argc == 6) {
             // The reference CPU linear on a bounded row sample: rotate+quantise
             // ROWS rows of x, then the naive int8 GEMM against all N rows of W.

@@ -535,6 +535,62 @@ size_t phi_hip_w4a8_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gro
     return (size_t)N * (size_t)K;
 }
 
+size_t phi_hip_i4_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    // As for W4A8: from kW4ExpandMinRows rows the codes are expanded once.
+    if (M < kW4ExpandMinRows || N <= 0 || K <= 0 || K % 512 != 0) return 0;
+    return (size_t)N * (size_t)K;
+}
+
+phi_status phi_hip_i4_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb,
+                           const float* sA, const float* sB, void* C, int c_dtype, int64_t ldc, int64_t M,
+                           int64_t N, int64_t K, void* workspace, size_t ws_bytes) {
+    static const char* who = "int4_gemm";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (M <= 0 || N <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "int4_gemm: empty problem");
+    if (K % 512 != 0) return fail(PHI_ERR_SHAPE, "int4_gemm: K=%lld is not a multiple of 512", (long long)K);
+    phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, C, c_dtype, ldc, true);
+    if (st != PHI_OK) return st;
+    phi_dev::GemmParams p{};
+    p.A = A;
+    p.B = (const int8_t*)B;
+    p.sA = sA;
+    p.sB = sB;
+    p.C = C;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.ldc = ldc;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.bias_kind = phi_dev::BIAS_NONE;
+    p.c_kind = c_kind_of(c_dtype);
+    p.group_m = 4;
+    p.w4_signed = 1;
+    p.group_shift = 30;
+    const char* e = getenv("PHI_GEMM_KERNEL");
+    const bool force_staged = e && strcmp(e, "tile128") == 0;
+    GemmKernel gk = GK_PERSIST;
+    if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;
+    if (e && strcmp(e, "persist128") == 0) gk = GK_PERSIST128;
+    const bool codes16 = aligned(B, 16) && ldb % 16 == 0;
+    const size_t need = phi_hip_i4_workspace_bytes(M, N, K);
+    if (!force_staged && need > 0 && workspace && ws_bytes >= need && aligned(workspace, 16) && codes16 &&
+        persist_ok(C, c_dtype, N, K, lda, K, ldc)) {
+        st = check_hip(phi_dev::launch_w4_lut_expand((hipStream_t)stream, p, (int8_t*)workspace), who);
+        if (st != PHI_OK) return st;
+        phi_dev::GemmParams g = p;
+        g.B = (const int8_t*)workspace;
+        g.ldb = K;
+        g.w4_signed = 0;
+        set_vec_flags(g, c_dtype, ldc);
+        return check_hip(launch_persist_plan((hipStream_t)stream, g, gk, false, c_dtype, ldc), who);
+    }
+    set_vec_flags(p, c_dtype, ldc);
+    if (!force_staged && codes16 && persist_ok(C, c_dtype, N, K, lda, ldb, ldc))
+        return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, true, c_dtype, ldc), who);
+    return check_hip(phi_dev::launch_w4a8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
+}
+
 size_t phi_hip_gemv_workspace_bytes(int n_items) {
     (void)n_items;
     return 0;

@@ -80,7 +80,8 @@ __device__ __forceinline__ void tile_coords(int pid, int nblocks, int tiles_m, i
 }
 
 // W4 = true: B is packed nibbles (row stride ldb bytes, K/2 used) plus the
-// per-(row, group) table `lut`; each staged 16-byte B chunk is expanded in
+// per-(row, group) table `lut` (with p.w4_signed, the constant table of signed
+// nibbles instead); each staged 16-byte B chunk is expanded in
 // registers before it is written to LDS, so the MFMA core is unchanged.
 template <int BM, int BN, int WM, int WN, bool W4>
 __global__ __launch_bounds__(WM* WN * 64) void i8_gemm_kernel(GemmParams p) {
@@ -165,7 +166,8 @@ __global__ __launch_bounds__(WM* WN * 64) void i8_gemm_kernel(GemmParams p) {
         for (int i = 0; i < CB; i++) {
             if (W4) {
                 rc[i] = *(const uint2*)(gB[i] + (k >> 1));
-                rl[i] = *(const uint4*)(gL[i] + ((k >> p.group_shift) << 4));
+                rl[i] = p.w4_signed ? make_uint4(0x03020100u, 0x07060504u, 0xfbfaf9f8u, 0xfffefdfcu)
+                                    : *(const uint4*)(gL[i] + ((k >> p.group_shift) << 4));
             } else {
                 rb[i] = *(const v4i*)(gB[i] + k);
             }

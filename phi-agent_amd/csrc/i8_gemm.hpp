@@ -32,6 +32,9 @@ struct GemmParams {
     int schedule;        // 256x256 kernel: 0 = eight waves, 64-deep K; 1 = four waves, 128-deep K
     // Persistent kernel, fp32 output: C = fma(linear, gate[n], C) in place (gated residual).
     const float* gate;
+    // W4 operand of signed nibbles (convrot_w4a4): value = code < 8 ? code : code - 16,
+    // from a constant table in registers; lut is not read.
+    int w4_signed;
 };
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
@@ -39,7 +42,8 @@ hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
 // Persistent kernel (K % 256 == 0): square tiles of 2 * wave_tile (128 -> 256 x 256,
 // 64 -> 128 x 128), min(tiles, num_cus) workgroups.  w4: B is packed codes plus
-// the per-(row, group) table (group a multiple of 128, code rows 16-byte aligned).
+// the per-(row, group) table (group a multiple of 128, code rows 16-byte aligned),
+// or signed nibbles with p.w4_signed.
 hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile, bool w4);
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);

@@ -133,6 +133,9 @@ __device__ __forceinline__ uint32_t lut4b(uint32_t x, const u32x4& t) {
     return (hi & m) | (lo & ~m);
 }
 
+// The table of signed nibbles (convrot_w4a4): codes 0..7 are 0..7, 8..15 are -8..-1.
+__device__ __forceinline__ u32x4 signed_nibble_table() { return u32x4{0x03020100u, 0x07060504u, 0xfbfaf9f8u, 0xfffefdfcu}; }
+
 // 16 codes (8 bytes) -> 16 int8 operand bytes in column order.
 __device__ __forceinline__ v4i expand16b(uint32_t c0, uint32_t c1, const u32x4& t) {
     const uint32_t e0 = lut4b(c0 & 0x0f0f0f0fu, t), o0 = lut4b((c0 >> 4) & 0x0f0f0f0fu, t);
@@ -176,8 +179,11 @@ __device__ __forceinline__ void cursor_tile(Wv& w, const GemmParams& p, const Sh
     w.rA = __builtin_amdgcn_make_buffer_rsrc((void*)(p.A + (int64_t)m0 * p.lda), (short)0, rows * (int)p.lda, kRsrcWord3);
     w.rB = __builtin_amdgcn_make_buffer_rsrc((void*)(p.B + (int64_t)n0 * p.ldb), (short)0, cols * (int)p.ldb, kRsrcWord3);
     if constexpr (W4) {
-        const int lrow = (int)p.lut_groups * 16;
-        w.rL = __builtin_amdgcn_make_buffer_rsrc((void*)(p.lut + (int64_t)n0 * lrow), (short)0, cols * lrow, kRsrcWord3);
+        if (!p.w4_signed) {
+            const int lrow = (int)p.lut_groups * 16;
+            w.rL = __builtin_amdgcn_make_buffer_rsrc((void*)(p.lut + (int64_t)n0 * lrow), (short)0, cols * lrow,
+                                                     kRsrcWord3);
+        }
     }
 }
 
@@ -227,7 +233,8 @@ __device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, 
 #pragma unroll
         for (int q = 0; q < W4Regs<WT>::C; q++)
             r.c[q] = __builtin_amdgcn_raw_buffer_load_b128(w.rB, w.vo4 + q * 16, kl * (BK / 2), 0);
-        r.t = __builtin_amdgcn_raw_buffer_load_b128(w.rL, w.voL, ((kl * BK) >> p.group_shift) * 16, 0);
+        r.t = p.w4_signed ? signed_nibble_table()
+                          : __builtin_amdgcn_raw_buffer_load_b128(w.rL, w.voL, ((kl * BK) >> p.group_shift) * 16, 0);
     } else {
 #pragma unroll
         for (int j = 0; j < DL; j++)
@@ -601,26 +608,28 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
 // writes to LDS.
 __global__ __launch_bounds__(256) void w4_lut_expand_kernel(const uint8_t* __restrict__ codes, int64_t ldb,
                                                             const int8_t* __restrict__ lut, int64_t lut_groups,
-                                                            int group_shift, int64_t N, int64_t K,
+                                                            int group_shift, int w4_signed, int64_t N, int64_t K,
                                                             int8_t* __restrict__ out) {
     const int64_t per_row = K / 32;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= N * per_row) return;
     const int64_t row = idx / per_row, c32 = idx - row * per_row;
     const u32x4 c = *(const u32x4*)(codes + row * ldb + c32 * 16);
-    const u32x4 t = *(const u32x4*)(lut + (row * lut_groups + ((c32 * 32) >> group_shift)) * 16);
+    const u32x4 t = w4_signed ? signed_nibble_table()
+                              : *(const u32x4*)(lut + (row * lut_groups + ((c32 * 32) >> group_shift)) * 16);
     int8_t* o = out + row * K + c32 * 32;
     *(v4i*)o = expand16b(c[0], c[1], t);
     *(v4i*)(o + 16) = expand16b(c[2], c[3], t);
 }
 
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out) {
-    if (p.K % 32 != 0 || p.group_shift < 5 || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 ||
-        ((uintptr_t)out & 15) != 0 || !p.lut)
+    if (p.K % 32 != 0 || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 || ((uintptr_t)out & 15) != 0 ||
+        (!p.w4_signed && (p.group_shift < 5 || !p.lut)))
         return hipErrorInvalidValue;
     const int64_t threads = (int64_t)p.N * (p.K / 32);
     hipLaunchKernelGGL(w4_lut_expand_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                       (const uint8_t*)p.B, p.ldb, p.lut, p.lut_groups, p.group_shift, (int64_t)p.N, (int64_t)p.K, out);
+                       (const uint8_t*)p.B, p.ldb, p.lut, p.lut_groups, p.group_shift, p.w4_signed, (int64_t)p.N,
+                       (int64_t)p.K, out);
     return hipGetLastError();
 }
 
@@ -628,7 +637,8 @@ hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int n
     if (p.K % (2 * BK) != 0 || p.K < 2 * BK) return hipErrorInvalidValue;
     if (wave_tile != 128 && wave_tile != 64) return hipErrorInvalidValue;
     // W4: one table per K-step (group a multiple of 128), 16-byte code loads.
-    if (w4 && (p.group_shift < 7 || !p.lut || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0)) return hipErrorInvalidValue;
+    if (w4 && (p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 || (!p.w4_signed && (p.group_shift < 7 || !p.lut))))
+        return hipErrorInvalidValue;
     const int bm = 2 * wave_tile;
     const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
     const int grid = tiles < num_cus ? tiles : num_cus;

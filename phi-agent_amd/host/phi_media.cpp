@@ -130,6 +130,15 @@ void dispatch_silu_gate_fused(ComputeContext& ctx, const GpuAlloc& gx, const Gpu
               "silu_gate_fused");
 }
 
+// core/kernels/h3_kernels.cpp:637-662: the same contract (empty problem, K % 512).
+void dispatch_int4_gemm(ComputeContext& ctx, const Int4GemmArgs& a) {
+    ctx.check(phi_hip_i4_gemm(ctx.stream(), (const int8_t*)cat(a.a.res, a.a.off), a.k,
+                              (const uint8_t*)cat(a.b.res, a.b.off), a.k / 2, (const float*)cat(a.sa.res, a.sa.off),
+                              (const float*)cat(a.sb.res, a.sb.off), at(a.c.res, a.c.off), PHI_F32, a.n, a.m, a.n,
+                              a.k, nullptr, 0),
+              "int4_gemm");
+}
+
 // core/kernels/w4a8_expand.cpp:263-303
 void dispatch_w4a8_expand(ComputeContext& ctx, const W4a8ExpandArgs& a) {
     if (a.rows <= 0 || a.k <= 0) return;

@@ -163,6 +163,19 @@ void dispatch_elem(ComputeContext& ctx, const ElemArgs& a);
 // out[r][c] = silu(gx[r][c]) * gx[r][cols + c], fp32 (core/kernels/h3_kernels.hpp:116-129).
 void dispatch_silu_gate_fused(ComputeContext& ctx, const GpuAlloc& gx, const GpuAlloc& out, i64 rows, i64 cols);
 
+// int4 GEMM of the convrot_w4a4 family (core/kernels/h3_kernels.hpp:90-107):
+// C[M,N] fp32 = (A[M,K] int8 . B[N,K/2] signed nibbles) * sa[m] * sb[n].
+struct Int4GemmArgs {
+    GpuAlloc a;   // [M,K] int8 (rotated + quantised activations, qmax 7)
+    GpuAlloc b;   // [N,K/2] packed int4, column 2j in the low nibble of byte j
+    GpuAlloc sa;  // [M] fp32
+    GpuAlloc sb;  // [N] fp32
+    GpuAlloc c;   // [M,N] fp32
+    i64 m = 0, n = 0, k = 0;
+};
+
+void dispatch_int4_gemm(ComputeContext& ctx, const Int4GemmArgs& a);
+
 // One linear weight in the int8 form the GEMM reads.
 struct QuantLinear {
     GpuAlloc w;      // [n,k] int8

@@ -63,7 +63,7 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_w4a8_prepare", "phi_hip_w4a8_linear", "phi_hip_i8_gemv_batched",
            "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes",
            "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual", "phi_hip_quant_rotate_act",
-           "phi_hip_silu_gate"]
+           "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes"]
 
 _lib = None
 
@@ -100,6 +100,9 @@ def load() -> ctypes.CDLL:
     L.phi_hip_gelu_tanh.argtypes = [P, P, I, P, I, I64]
     L.phi_hip_quant_rotate_act.argtypes = [P, P, I, I64, I64, I64, I, P, I64, P, F, I, I]
     L.phi_hip_silu_gate.argtypes = [P, P, I, I64, I64, I64, P, I, I64]
+    L.phi_hip_i4_gemm.argtypes = [P, P, I64, P, I64, P, P, P, I, I64, I64, I64, I64, P, SZ]
+    L.phi_hip_i4_workspace_bytes.argtypes = [I64, I64, I64]
+    L.phi_hip_i4_workspace_bytes.restype = SZ
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:
@@ -370,3 +373,25 @@ def silu_gate(gx: torch.Tensor, out: torch.Tensor | None = None, *, out_dtype=No
     _check(load().phi_hip_silu_gate(_stream(stream), _ptr(gx), _dt(gx), rows, cols, gx.stride(0), _ptr(out),
                                     _dt(out), out.stride(0)))
     return out
+
+
+def i4_workspace(M: int, N: int, K: int, device) -> torch.Tensor | None:
+    """The optional expand-once buffer of i4_gemm (None when the shape takes none)."""
+    n = load().phi_hip_i4_workspace_bytes(M, N, K)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def i4_gemm(A: torch.Tensor, B: torch.Tensor, sA: torch.Tensor | None, sB: torch.Tensor | None, *,
+            out_dtype=torch.float32, C: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+            stream=None) -> torch.Tensor:
+    """convrot_w4a4 GEMM: C = ((float)(A . w^T) * sA) * sB, B uint8 [N, K/2] of signed
+    nibbles (low nibble = even column); int32 out_dtype gives the accumulators."""
+    _require_device(A, B, sA, sB, C)
+    M, K = A.shape
+    N = B.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=A.device)
+    ws, wsb = _ws(workspace)
+    _check(load().phi_hip_i4_gemm(_stream(stream), _ptr(A), A.stride(0), _ptr(B), B.stride(0), _ptr(sA),
+                                  _ptr(sB), _ptr(C), _dt(C), C.stride(0), M, N, K, ws, wsb))
+    return C

@@ -195,6 +195,73 @@ static void test_activations(ComputeContext& ctx) {
     printf("activations: %s\n", failures ? "mismatch" : "within bounds");
 }
 
+// dispatch_int4_gemm (the text encoder's convrot_w4a4 linear) after
+// dispatch_quant_convrot with qmax 7, against the oracle, bit for bit.
+static void test_int4_gemm(ComputeContext& ctx) {
+    const i64 m = 45, k = 1024, n = 200;
+    std::mt19937 rng(13);
+    std::normal_distribution<float> nd(0.0f, 1.5f);
+    std::vector<float> x(m * k), w(n * k);
+    for (auto& v : x) v = nd(rng);
+    for (auto& v : w) v = nd(rng);
+    std::vector<uint8_t> packed(n * k / 2);
+    std::vector<float> sw(n);
+    CHECK(orc_quantize_convrot_w4a4(w.data(), n, k, packed.data(), sw.data()) == 0, "w4a4 packer");
+    const u64 off_x = 0, off_b = off_x + m * k * 4, off_sw = off_b + n * k / 2, off_q = off_sw + 4096,
+              off_s = off_q + m * k, off_c = off_s + 4096;
+    GpuBuffer* pool = ctx.create_device_buffer(off_c + m * n * 4);
+    ctx.upload(pool, x.data(), m * k * 4, off_x);
+    ctx.upload(pool, packed.data(), packed.size(), off_b);
+    ctx.upload(pool, sw.data(), n * 4, off_sw);
+    ctx.begin();
+    QuantConvrotArgs qa;
+    qa.x = pool;
+    qa.x_offset = off_x;
+    qa.q = pool;
+    qa.q_offset = off_q;
+    qa.s = pool;
+    qa.s_offset = off_s;
+    qa.rows = m;
+    qa.K = k;
+    qa.qmax = 7.0f;
+    dispatch_quant_convrot(ctx, qa);
+    Int4GemmArgs ga;
+    ga.a = GpuAlloc{pool, off_q, (u64)(m * k)};
+    ga.b = GpuAlloc{pool, off_b, (u64)(n * k / 2)};
+    ga.sa = GpuAlloc{pool, off_s, (u64)(m * 4)};
+    ga.sb = GpuAlloc{pool, off_sw, (u64)(n * 4)};
+    ga.c = GpuAlloc{pool, off_c, (u64)(m * n * 4)};
+    ga.m = m;
+    ga.n = n;
+    ga.k = k;
+    dispatch_int4_gemm(ctx, ga);
+    ctx.submit();
+    std::vector<float> c(m * n), s(m), so(m), co(m * n);
+    std::vector<int8_t> q(m * k), qo(m * k);
+    ctx.download(pool, c.data(), c.size() * 4, off_c);
+    ctx.download(pool, q.data(), q.size(), off_q);
+    ctx.download(pool, s.data(), s.size() * 4, off_s);
+    orc_quantize_rows(x.data(), ORC_F32, m, k, k, 1, 7.0f, ORC_ROUND_HALF_AWAY, qo.data(), so.data());
+    orc_int4_gemm(qo.data(), k, packed.data(), k / 2, so.data(), sw.data(), m, n, k, co.data(), n);
+    CHECK(memcmp(q.data(), qo.data(), q.size()) == 0, "int4: qmax-7 activations differ");
+    CHECK(memcmp(s.data(), so.data(), s.size() * 4) == 0, "int4: activation scales differ");
+    CHECK(memcmp(c.data(), co.data(), c.size() * 4) == 0, "int4: fp32 outputs differ");
+    ctx.release_buffer(pool);
+    bool threw = false;
+    try {
+        Int4GemmArgs bad;
+        bad.m = 4;
+        bad.n = 4;
+        bad.k = 768;
+        dispatch_int4_gemm(ctx, bad);
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "not a multiple of 512") != nullptr;
+    }
+    CHECK(threw, "int4_gemm K=768 must throw MediaError");
+    printf("int4_gemm %lldx%lldx%lld: %s\n", (long long)m, (long long)n, (long long)k,
+           failures ? "mismatch" : "bit-exact");
+}
+
 static void test_errors(ComputeContext& ctx) {
     bool threw = false;
     try {
@@ -238,6 +305,7 @@ int main() {
         test_linear_gemm(ctx);
         test_w4a8_expand(ctx);
         test_activations(ctx);
+        test_int4_gemm(ctx);
     } catch (const std::exception& e) {
         printf("FAIL exception: %s\n", e.what());
         return 1;

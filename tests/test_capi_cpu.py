@@ -53,7 +53,7 @@ def test_host_layer_library_exports_reference_names():
     for name in ("phi::media::dispatch_int8_gemm", "phi::media::dispatch_quant_convrot",
                  "phi::media::dispatch_w4a8_expand", "phi::media::linear_gemm",
                  "phi::media::ComputeContext::submit", "phi::media::dispatch_elem",
-                 "phi::media::dispatch_silu_gate_fused"):
+                 "phi::media::dispatch_silu_gate_fused", "phi::media::dispatch_int4_gemm"):
         assert name in out, name
 
 
@@ -104,6 +104,20 @@ def test_activation_contracts(lib):
     assert lib.phi_hip_silu_gate(None, None, Q.F32, 0, 64, 128, None, Q.F32, 64) == 0
     assert lib.phi_hip_quant_rotate_act(None, None, Q.F32, 0, 256, 512, Q.ACT_SILU_GATE, None, 256, None,
                                         127.0, 0, 1) == 0
+
+
+def test_int4_gemm_contract(lib):
+    rc = lib.phi_hip_i4_gemm(None, FAKE, 512, FAKE, 256, FAKE, FAKE, FAKE, Q.F32, 64, 0, 64, 512, None, 0)
+    assert rc == 2 and Q.last_error() == "int4_gemm: empty problem"
+    rc = lib.phi_hip_i4_gemm(None, FAKE, 768, FAKE, 384, FAKE, FAKE, FAKE, Q.F32, 64, 4, 64, 768, None, 0)
+    assert rc == 2 and Q.last_error() == "int4_gemm: K=768 is not a multiple of 512"
+    rc = lib.phi_hip_i4_gemm(None, FAKE, 512, FAKE, 200, FAKE, FAKE, FAKE, Q.F32, 64, 4, 64, 512, None, 0)
+    assert rc == 2 and "nibble row" in Q.last_error()
+    rc = lib.phi_hip_i4_gemm(None, FAKE, 512, FAKE, 256, None, FAKE, FAKE, Q.F32, 64, 4, 64, 512, None, 0)
+    assert rc == 1 and "scales" in Q.last_error()
+    assert lib.phi_hip_i4_workspace_bytes(511, 64, 512) == 0
+    assert lib.phi_hip_i4_workspace_bytes(512, 64, 512) == 64 * 512
+    assert lib.phi_hip_i4_workspace_bytes(512, 64, 768) == 0
 
 
 def test_gemm_contract(lib):
