@@ -34,6 +34,7 @@ for _p in (ROOT, PKG):
 METRIC = "W8A8 linear TOPS & % int8 MFMA peak at M=4352,K=3072,N=12288"
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector (published; counts packed-fp32 issue)
 CPU_SAMPLE_ROWS = 4352    # rows of the reference CPU linear timed for the baseline (all of c1)
 
 CONFIGS = {
@@ -50,6 +51,9 @@ CONFIGS = {
     # The text encoder's convrot_w4a4 MLP up-projection (hidden 5120 -> 25600,
     # a 1024-token prompt): rotate + quantise with qmax 7, then the int4 GEMM.
     "c5_w4a4": dict(kind="w4a4", M=1024, K=5120, N=25600),
+    # A rank-64 LoRA correction on config 1's up-projection output (fp32, as
+    # the reference's apply_lora_tail runs it after the linear).
+    "c1_lora": dict(kind="lora", M=4352, K=3072, N=12288, rank=64),
 }
 
 
@@ -318,6 +322,39 @@ def bench_w4a4(cfg, steps, warmup):
                       "expand_once_us": None if ms_ws is None else ms_ws * 1e3}}
 
 
+def bench_lora(cfg, steps, warmup):
+    """One step: phi_hip_lora_tail, out [M, N] fp32 += (x A^T) B^T with exact
+    fp32 fma chains.  Throughput in TFLOP/s of fp32 fma work (2 (M R K + M N R)),
+    against MI355X's fp32 vector peak."""
+    import torch
+
+    import phi_qlinear as Q
+
+    dev = torch.device("cuda:0")
+    M, K, N, R = cfg["M"], cfg["K"], cfg["N"], cfg["rank"]
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(M, K, generator=g, device=dev)
+    A = torch.randn(R, K, generator=g, device=dev) * 0.02
+    B = torch.randn(N, R, generator=g, device=dev) * 0.02
+    out = torch.randn(M, N, generator=g, device=dev)
+    h = torch.empty((M, R), dtype=torch.float32, device=dev)
+    for _ in range(warmup):
+        Q.lora_tail(x, A, B, out, h=h)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        Q.lora_tail(x, A, B, out, h=h)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = 2.0 * (M * R * K + M * N * R)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"value": tf, "ms": ms, "dtype": "f32", "unit": "TFLOP/s",
+            "roofline": {"bound": "valu", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / FP32_PEAK_TFLOPS, "traffic": None}}
+
+
 def bench_gemv(cfg, steps, warmup):
     import torch
 
@@ -379,6 +416,8 @@ def main() -> int:
         r = bench_w4a8(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "w4a4":
         r = bench_w4a4(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "lora":
+        r = bench_lora(cfg, args.steps, args.warmup)
     else:
         r = bench_gemv(cfg, args.steps, args.warmup)
     log(f"bench: {r['ms'] * 1e3:.1f} us per step")

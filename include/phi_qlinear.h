@@ -277,6 +277,35 @@ phi_status phi_hip_i4_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
  * bytes from 512 rows up; 0 otherwise).  No reference counterpart. */
 size_t phi_hip_i4_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
+/*
+ * Runtime LoRA correction of a linear's output, out += (x A^T) B^T, as the
+ * reference's apply_lora_tail (core/models/model_common.cpp:1667-1700):
+ *   x   [M, ldx >= K] of x_dtype (PHI_F32 as the reference, or PHI_BF16): the linear's input
+ *   At  [R, K] fp32: the factors' A rows, stacked (LoraTail::at)
+ *   Bt  [N, R] fp32: the factors' B columns, scaled (LoraTail::bt)
+ *   out [M, ldo >= N] of out_dtype (PHI_F32 as the reference, or PHI_BF16), updated in place
+ *   h   caller scratch of h_bytes >= M*R*4 (the [M, R] fp32 hidden form)
+ * Both products are fp32 fma chains in the reference's order (k ascending from
+ * 0 for h; r ascending from out's value for the update), so an fp32 out is
+ * bit-exact.  M <= 0 or R <= 0 is a no-op (an inactive tail).  h must not
+ * overlap x or out.
+ */
+phi_status phi_hip_lora_tail(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                             const float* At, const float* Bt, int64_t R, int64_t N, void* out, int out_dtype,
+                             int64_t ldo, float* h, size_t h_bytes);
+
+/* The tail's first product, h [M, R] = x . At^T in fp32 (replaces dispatch_gemm_f16
+ * with fp32 operands and no bias, core/kernels/gemm_f16.cpp:56-200, as
+ * apply_lora_tail uses it). */
+phi_status phi_hip_lora_down(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                             const float* A, int64_t R, float* h);
+
+/* The tail's update, C [M, ldc] += h [M, R] . B [N, R]^T, fp32 chain from C's
+ * value (replaces dispatch_lora_rank_add / LoraRankAddArgs,
+ * core/kernels/gpu_ops.hpp:190-196, kernel core/kernels/gemm_f16.cpp:237-308). */
+phi_status phi_hip_lora_rank_add(phi_stream_t stream, const float* h, const float* B, void* C, int c_dtype,
+                                 int64_t ldc, int64_t M, int64_t N, int64_t R);
+
 /* Workspace for phi_hip_i8_gemv_batched (holds the item table on the device). */
 size_t phi_hip_gemv_workspace_bytes(int n_items);
 

@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L.orc_w4a8_expand.restype = I
         L.orc_gelu_tanh.argtypes = [P, P, I64]
         L.orc_silu_gate.argtypes = [P, P, I64, I64]
+        L.orc_lora_down.argtypes = [P, I64, P, P, I64, I64, I64]
+        L.orc_lora_rank_add.argtypes = [P, P, P, I64, I64, I64, I64]
         L.orc_quantize_convrot_w4a4.argtypes = [P, I64, I64, P, P]
         L.orc_quantize_convrot_w4a4.restype = I
         L.orc_int4_gemm.argtypes = [P, I64, P, I64, P, P, I64, I64, I64, P, I64]
@@ -262,6 +264,25 @@ def int4_gemm(a, b_packed, sa, sb) -> np.ndarray:
     lib().orc_int4_gemm(_p(a), K, _p(b), b.shape[1], _p(_c(sa, np.float32)), _p(_c(sb, np.float32)),
                         M, N, K, _p(c), N)
     return c
+
+
+def lora_down(x, a) -> np.ndarray:
+    """h [M, R] = x [M, K] . a [R, K]^T as k-ordered fp32 fma chains (fp32 x)."""
+    x, a = _c(x, np.float32), _c(a, np.float32)
+    M, K = x.shape
+    R = a.shape[0]
+    h = np.empty((M, R), dtype=np.float32)
+    lib().orc_lora_down(_p(x), K, _p(a), _p(h), M, K, R)
+    return h
+
+
+def lora_rank_add(h, b, c) -> np.ndarray:
+    """c + h . b^T as r-ordered fp32 fma chains starting from c (returns a new array)."""
+    h, b = _c(h, np.float32), _c(b, np.float32)
+    out = np.array(c, dtype=np.float32, copy=True, order="C")
+    M, N = out.shape
+    lib().orc_lora_rank_add(_p(h), _p(b), _p(out), N, M, N, h.shape[1])
+    return out
 
 
 def silu_gate(gx) -> np.ndarray:

@@ -338,6 +338,36 @@ void orc_int4_gemm(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, 
 }
 
 /* ------------------------------------------------------------------------ */
+/* LoRA tail: out += (x A^T) B^T (core/models/model_common.cpp:1667-1700)   */
+/* ------------------------------------------------------------------------ */
+
+/* h[m][r] = fma chain over k ascending of x[m][k] * A[r][k] from 0, as
+ * gemm_f16's `acc += av * bv` under NVRTC's --fmad=true
+ * (core/kernels/gemm_f16.cpp:56-200, fp32 operands, no bias).  That kernel
+ * walks whole 32-deep tiles with zero past K; the padding's only effect is
+ * fma(0, 0, -0) = +0, applied once when K % 32 != 0. */
+void orc_lora_down(const float* x, int64_t ldx, const float* a, float* h, int64_t M, int64_t K, int64_t R) {
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t r = 0; r < R; r++) {
+            float acc = 0.0f;
+            for (int64_t k = 0; k < K; k++) acc = fmaf(x[m * ldx + k], a[r * K + k], acc);
+            if (K % 32 != 0) acc = fmaf(0.0f, 0.0f, acc);
+            h[m * R + r] = acc;
+        }
+}
+
+/* c[m][n] = fma chain over r ascending of h[m][r] * b[n][r] from c[m][n]
+ * (lora_rank_add, core/kernels/gemm_f16.cpp:237-308). */
+void orc_lora_rank_add(const float* h, const float* b, float* c, int64_t ldc, int64_t M, int64_t N, int64_t R) {
+    for (int64_t m = 0; m < M; m++)
+        for (int64_t n = 0; n < N; n++) {
+            float acc = c[m * ldc + n];
+            for (int64_t r = 0; r < R; r++) acc = fmaf(h[m * R + r], b[n * R + r], acc);
+            c[m * ldc + n] = acc;
+        }
+}
+
+/* ------------------------------------------------------------------------ */
 /* A9: GELU-tanh                                                            */
 /* ------------------------------------------------------------------------ */
 

@@ -102,6 +102,8 @@ void orc_add_mul(const float* a, const float* b, const float* c, float* y, int64
 int orc_quantize_convrot_w4a4(const float* w, int64_t rows, int64_t cols, uint8_t* packed, float* scales);
 void orc_int4_gemm(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, const float* sa,
                    const float* sb, int64_t M, int64_t N, int64_t K, float* c, int64_t ldc);
+void orc_lora_down(const float* x, int64_t ldx, const float* a, float* h, int64_t M, int64_t K, int64_t R);
+void orc_lora_rank_add(const float* h, const float* b, float* c, int64_t ldc, int64_t M, int64_t N, int64_t R);
 void orc_gelu_tanh(const float* x, float* y, int64_t n);
 void orc_silu_gate(const float* gx, float* out, int64_t rows, int64_t cols);
 

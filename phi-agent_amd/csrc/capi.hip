@@ -18,6 +18,7 @@
 
 #include "../../include/phi_qlinear.h"
 #include "gemv.hpp"
+#include "lora.hpp"
 #include "i8_gemm.hpp"
 #include "w4a8.hpp"
 
@@ -650,6 +651,53 @@ phi_status phi_hip_i8_gemv_batched(phi_stream_t stream, const int8_t* q8, const 
         if (st != PHI_OK) return st;
     }
     return ok();
+}
+
+phi_status phi_hip_lora_down(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                             const float* A, int64_t R, float* h) {
+    static const char* who = "lora_down";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (M <= 0 || R <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
+    if (M > INT32_MAX || R > INT32_MAX || K > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: dimension exceeds 2^31", who);
+    if (!x || !A || !h) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (x_dtype != PHI_F32 && x_dtype != PHI_BF16) return fail(PHI_ERR_ARG, "%s: x dtype must be f32 or bf16", who);
+    if (ldx < K) return fail(PHI_ERR_SHAPE, "%s: ldx < K", who);
+    if (!aligned(x, x_dtype == PHI_BF16 ? 2 : 4) || !aligned(A, 4) || !aligned(h, 4))
+        return fail(PHI_ERR_ALIGN, "%s: misaligned operand", who);
+    return check_hip(phi_dev::launch_lora_down((hipStream_t)stream, x, x_dtype == PHI_BF16, ldx, A, h, (int)M, (int)K,
+                                               (int)R),
+                     who);
+}
+
+phi_status phi_hip_lora_rank_add(phi_stream_t stream, const float* h, const float* B, void* C, int c_dtype,
+                                 int64_t ldc, int64_t M, int64_t N, int64_t R) {
+    static const char* who = "lora_rank_add";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (M <= 0 || N <= 0 || R <= 0) return fail(PHI_ERR_SHAPE, "lora_rank_add: empty problem");
+    if (M > INT32_MAX || N > INT32_MAX || R > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: dimension exceeds 2^31", who);
+    if (!h || !B || !C) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (c_dtype != PHI_F32 && c_dtype != PHI_BF16) return fail(PHI_ERR_ARG, "%s: C dtype must be f32 or bf16", who);
+    if (ldc < N) return fail(PHI_ERR_SHAPE, "%s: ldc < N", who);
+    if (!aligned(C, c_dtype == PHI_BF16 ? 2 : 4) || !aligned(h, 4) || !aligned(B, 4))
+        return fail(PHI_ERR_ALIGN, "%s: misaligned operand", who);
+    return check_hip(phi_dev::launch_lora_rank_add((hipStream_t)stream, h, B, C, c_dtype == PHI_BF16, ldc, (int)M,
+                                                   (int)N, (int)R),
+                     who);
+}
+
+phi_status phi_hip_lora_tail(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                             const float* At, const float* Bt, int64_t R, int64_t N, void* out, int out_dtype,
+                             int64_t ldo, float* h, size_t h_bytes) {
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "lora_tail: device was lost earlier");
+    if (M <= 0 || R <= 0) return ok();  // an inactive tail or no rows: nothing to add
+    const uint64_t need = (uint64_t)M * (uint64_t)R * 4;
+    if (h_bytes < need)
+        return fail(PHI_ERR_WORKSPACE,
+                    "LoRA correction: the hidden-form scratch is %llu bytes; a [%lld, %lld] fp32 one needs %llu",
+                    (unsigned long long)h_bytes, (long long)M, (long long)R, (unsigned long long)need);
+    phi_status st = phi_hip_lora_down(stream, x, x_dtype, ldx, M, K, At, R, h);
+    if (st != PHI_OK) return st;
+    return phi_hip_lora_rank_add(stream, h, Bt, out, out_dtype, ldo, M, N, R);
 }
 
 phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, void* y, int y_dtype, int64_t n) {

@@ -1,0 +1,325 @@
+// The runtime LoRA correction of a linear, out += (x A^T) B^T, as the
+// reference runs it (apply_lora_tail, core/models/model_common.cpp:1667-1700):
+//
+//   lora_down      h[m, r] = sum_k x[m, k] * A[r, k]          (dispatch_gemm_f16 with
+//                  fp32 operands and no bias, core/kernels/gemm_f16.cpp:56-200)
+//   lora_rank_add  out[m, n] += sum_r h[m, r] * B[n, r]       (dispatch_lora_rank_add,
+//                  core/kernels/gemm_f16.cpp:237-308)
+//
+// Both are fp32 fma chains in a fixed order: the reference accumulates
+// acc = fma(a, b, acc) (NVRTC's default --fmad=true) with k ascending from 0
+// for h, and with r ascending from out's own value for the rank add.  Each
+// output here runs the same chain in one lane, so the bits are the
+// reference's; the tiling only decides which lane owns which outputs.
+// lora_down pads K to its 32-deep tiles with zero products; the only effect
+// of that padding is fma(0, 0, -0) = +0, reproduced by one extra fma when
+// K % 32 != 0.
+//
+// The chains are VALU work (R fmas per output element of the rank add), so
+// both kernels are sized for VALU issue: operands staged through LDS
+// transposed (k- or r-major), read with 16-byte loads, many accumulators per
+// lane.
+#include <cstdlib>
+
+#include "device_common.hpp"
+#include "lora.hpp"
+
+namespace phi_dev {
+
+// ---- lora_down: h [M, R] = x [M, K] . A [R, K]^T -------------------------
+// Main form (x rows 16-byte aligned, K % 64 == 0): a block owns 64 rows and
+// 4 LD_TR ranks, a wave LD_TR of the ranks and a lane one row.  LD_TR = 2 by
+// default: at 4352 x 3072 x 64 it runs in 112 us against 140 us for 4 (fewer
+// waves to cover the scalar loads' latency) and 170 us for 1 (twice the x
+// reads per fma).  The ranks are
+// wave-uniform, so their A values come through the scalar cache into SGPRs
+// and feed the fmas directly.  The rows' x values are staged 64 k at a time
+// through LDS (coalesced row loads, double-buffered), where a lane reads its
+// own row with a 65-float pitch (every lane on its own bank).
+constexpr int LD_KC = 64, LD_XP = LD_KC + 1;
+
+// The A values of TR ranks at k..k+7 (wave-uniform: scalar loads).
+template <int TR>
+__device__ __forceinline__ void load_a8(const float* const (&ar)[TR], int k, float (&av)[TR][8]) {
+#pragma unroll
+    for (int t = 0; t < TR; t++) {
+        const float4 a0 = *(const float4*)(ar[t] + k), a1 = *(const float4*)(ar[t] + k + 4);
+        av[t][0] = a0.x, av[t][1] = a0.y, av[t][2] = a0.z, av[t][3] = a0.w;
+        av[t][4] = a1.x, av[t][5] = a1.y, av[t][6] = a1.z, av[t][7] = a1.w;
+    }
+}
+
+// Scalar loads complete out of order, so their only wait is a full one.  The
+// two A operand sets alternate and this wait is placed before each set's
+// loads are issued, when it covers just the other set, so the fmas that
+// follow need no wait.
+__device__ __forceinline__ void wait_scalar_loads() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left open
+}
+
+// 64 rows x 64 k of x into registers: lane t holds row t / 4, k 16 (t % 4)..+15.
+template <bool XB>
+__device__ __forceinline__ void fetch_x_tile(const void* __restrict__ x, int64_t ldx, int m0, int M, int k0,
+                                             float (&v)[16]) {
+    const int row = threadIdx.x >> 2, kk = (threadIdx.x & 3) * 16;
+    const int64_t off = (int64_t)min(m0 + row, M - 1) * ldx + k0 + kk;
+    if (XB) {
+        const uint4 a = *(const uint4*)((const uint16_t*)x + off), b = *(const uint4*)((const uint16_t*)x + off + 8);
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            v[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+            v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 t = *(const float4*)((const float*)x + off + 4 * q);
+            v[4 * q] = t.x, v[4 * q + 1] = t.y, v[4 * q + 2] = t.z, v[4 * q + 3] = t.w;
+        }
+    }
+}
+
+template <bool XB, int LD_TR>
+__global__ __launch_bounds__(256) void lora_down_rows_kernel(const void* __restrict__ x, int64_t ldx,
+                                                             const float* __restrict__ A, float* __restrict__ h,
+                                                             int M, int K, int R) {
+    __shared__ float sx[2][64 * LD_XP];
+    const int lane = threadIdx.x & 63;
+    const int m0 = blockIdx.x * 64;
+    const int rb = __builtin_amdgcn_readfirstlane((blockIdx.y * 4 + (threadIdx.x >> 6)) * LD_TR);
+    const bool live = rb < R;  // wave-uniform; a dead wave still stages x for the others
+    const float* ar[LD_TR];
+#pragma unroll
+    for (int t = 0; t < LD_TR; t++) ar[t] = A + (int64_t)min(min(rb, R - 1) + t, R - 1) * K;
+    float acc[LD_TR];
+#pragma unroll
+    for (int t = 0; t < LD_TR; t++) acc[t] = 0.0f;
+    auto step = [&](const float* xr, int kk, const float(&av)[LD_TR][8]) {
+        float xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) xv[i] = xr[kk + i];
+#pragma unroll
+        for (int t = 0; t < LD_TR; t++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[t] = fmaf(xv[i], av[t][i], acc[t]);
+    };
+    float xt[16];
+    fetch_x_tile<XB>(x, ldx, m0, M, 0, xt);
+    float aa[LD_TR][8], ab[LD_TR][8];
+    if (live) load_a8<LD_TR>(ar, 0, aa);
+    const int srow = threadIdx.x >> 2, skk = (threadIdx.x & 3) * 16;
+    for (int k0 = 0, buf = 0; k0 < K; k0 += LD_KC, buf ^= 1) {
+        float* st = sx[buf] + srow * LD_XP + skk;
+#pragma unroll
+        for (int i = 0; i < 16; i++) st[i] = xt[i];
+        __syncthreads();
+        if (k0 + LD_KC < K) fetch_x_tile<XB>(x, ldx, m0, M, k0 + LD_KC, xt);
+        if (live) {
+            const float* xr = sx[buf] + lane * LD_XP;
+#pragma unroll
+            for (int kk = 0; kk < LD_KC; kk += 16) {
+                wait_scalar_loads();
+                load_a8<LD_TR>(ar, k0 + kk + 8, ab);
+                __builtin_amdgcn_sched_barrier(0);
+                step(xr, kk, aa);
+                __builtin_amdgcn_sched_barrier(0);
+                wait_scalar_loads();
+                load_a8<LD_TR>(ar, min(k0 + kk + 16, K - 8), aa);  // past the end: a harmless reload
+                __builtin_amdgcn_sched_barrier(0);
+                step(xr, kk + 8, ab);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        // The buffer written next iteration was last read two iterations ago,
+        // before this iteration's barrier: one barrier per chunk suffices.
+    }
+    const int m = m0 + lane;
+    if (!live || m >= M) return;
+    const bool pad = (K % 32) != 0;
+#pragma unroll
+    for (int t = 0; t < LD_TR; t++)
+        if (rb + t < R) h[(int64_t)m * R + rb + t] = pad ? fmaf(0.0f, 0.0f, acc[t]) : acc[t];
+}
+
+// General form (any alignment and K): block of 32 rows x 32 ranks, 256 lanes
+// of 2 x 2 outputs, K staged 64 deep through LDS, the next chunk's global
+// loads issued before the current chunk's fmas.
+constexpr int LD_BM = 32, LD_BR = 32, LD_BK = 64, LD_P = LD_BM + 4;
+
+template <bool XB>
+__device__ __forceinline__ void lora_down_fetch(const void* __restrict__ x, int64_t ldx, const float* __restrict__ A,
+                                                int M, int K, int R, int m0, int r0, int k0, int tid, float (&vx)[8],
+                                                float (&va)[8]) {
+    const int row = tid >> 3, k = k0 + (tid & 7) * 8;
+    const int m = m0 + row, r = r0 + row;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const bool in = m < M && k + i < K;
+        if (XB) vx[i] = in ? bf16_to_f32(((const uint16_t*)x)[(int64_t)m * ldx + k + i]) : 0.0f;
+        else vx[i] = in ? ((const float*)x)[(int64_t)m * ldx + k + i] : 0.0f;
+        va[i] = (r < R && k + i < K) ? A[(int64_t)r * K + k + i] : 0.0f;
+    }
+}
+
+template <bool XB>
+__global__ __launch_bounds__(256) void lora_down_kernel(const void* __restrict__ x, int64_t ldx,
+                                                        const float* __restrict__ A, float* __restrict__ h,
+                                                        int M, int K, int R) {
+    __shared__ __align__(16) float sx[LD_BK][LD_P];
+    __shared__ __align__(16) float sa[LD_BK][LD_P];
+    const int tid = threadIdx.x;
+    const int m0 = blockIdx.x * LD_BM, r0 = blockIdx.y * LD_BR;
+    const int tm = (tid & 15) * 2, tr = (tid >> 4) * 2;
+    const int srow = tid >> 3, skk = (tid & 7) * 8;
+    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
+    float vx[8], va[8];
+    lora_down_fetch<XB>(x, ldx, A, M, K, R, m0, r0, 0, tid, vx, va);
+    for (int k0 = 0; k0 < K; k0 += LD_BK) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sx[skk + i][srow] = vx[i];
+            sa[skk + i][srow] = va[i];
+        }
+        __syncthreads();
+        if (k0 + LD_BK < K) lora_down_fetch<XB>(x, ldx, A, M, K, R, m0, r0, k0 + LD_BK, tid, vx, va);
+        const int kn = min(LD_BK, K - k0);
+        if (kn == LD_BK) {
+#pragma unroll
+            for (int kk = 0; kk < LD_BK; kk++) {
+                const float2 xv = *(const float2*)&sx[kk][tm];
+                const float2 av = *(const float2*)&sa[kk][tr];
+                acc[0][0] = fmaf(xv.x, av.x, acc[0][0]);
+                acc[0][1] = fmaf(xv.x, av.y, acc[0][1]);
+                acc[1][0] = fmaf(xv.y, av.x, acc[1][0]);
+                acc[1][1] = fmaf(xv.y, av.y, acc[1][1]);
+            }
+        } else {
+            for (int kk = 0; kk < kn; kk++) {
+                const float2 xv = *(const float2*)&sx[kk][tm];
+                const float2 av = *(const float2*)&sa[kk][tr];
+                acc[0][0] = fmaf(xv.x, av.x, acc[0][0]);
+                acc[0][1] = fmaf(xv.x, av.y, acc[0][1]);
+                acc[1][0] = fmaf(xv.y, av.x, acc[1][0]);
+                acc[1][1] = fmaf(xv.y, av.y, acc[1][1]);
+            }
+        }
+        __syncthreads();
+    }
+    const bool pad = (K % 32) != 0;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int m = m0 + tm + i, r = r0 + tr + j;
+            if (m < M && r < R) h[(int64_t)m * R + r] = pad ? fmaf(0.0f, 0.0f, acc[i][j]) : acc[i][j];
+        }
+}
+
+// ---- lora_rank_add: C [M, N] += h [M, R] . B [N, R]^T ---------------------
+// Block: 128 x 128 outputs, 256 lanes of 8 x 8 (rows ty*8.., columns
+// tx*4.. and 64 + tx*4..), R staged 32 deep, r-major with a 132-float pitch.
+constexpr int RA_BM = 128, RA_BN = 128, RA_BR = 32, RA_P = 132;
+
+// One rank of the update: acc[i][j] = fma(h[row i], b[col j], acc[i][j]).
+__device__ __forceinline__ void rank_step(const float* __restrict__ hr, const float* __restrict__ br, int ty, int tx,
+                                          float (&acc)[8][8]) {
+    const float4 h0 = *(const float4*)&hr[ty * 8], h1 = *(const float4*)&hr[ty * 8 + 4];
+    const float4 b0 = *(const float4*)&br[tx * 4], b1 = *(const float4*)&br[64 + tx * 4];
+    const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[i][j] = fmaf(hv[i], bv[j], acc[i][j]);
+}
+
+template <bool CB>
+__global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restrict__ h, const float* __restrict__ B,
+                                                            void* __restrict__ C, int64_t ldc, int M, int N, int R) {
+    __shared__ __align__(16) float sh[RA_BR][RA_P];
+    __shared__ __align__(16) float sb[RA_BR][RA_P];
+    const int tid = threadIdx.x;
+    const int m0 = blockIdx.y * RA_BM, n0 = blockIdx.x * RA_BN;
+    const int ty = tid >> 4, tx = tid & 15;
+    float acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int m = m0 + ty * 8 + i;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int n = n0 + (j >> 2) * 64 + tx * 4 + (j & 3);
+            float v = 0.0f;
+            if (m < M && n < N) {
+                if (CB) v = bf16_to_f32(((const uint16_t*)C)[(int64_t)m * ldc + n]);
+                else v = ((const float*)C)[(int64_t)m * ldc + n];
+            }
+            acc[i][j] = v;
+        }
+    }
+    for (int r0 = 0; r0 < R; r0 += RA_BR) {
+        // 128 rows x 32 ranks of h and of B: lane t loads 4 consecutive ranks of
+        // rows t/8 + 32 s and stores them rank-major.
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int row = (tid >> 3) + 32 * s, rr = (tid & 7) * 4, r = r0 + rr;
+            const int m = m0 + row, n = n0 + row;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sh[rr + i][row] = (m < M && r + i < R) ? h[(int64_t)m * R + r + i] : 0.0f;
+                sb[rr + i][row] = (n < N && r + i < R) ? B[(int64_t)n * R + r + i] : 0.0f;
+            }
+        }
+        __syncthreads();
+        const int rn = min(RA_BR, R - r0);
+        for (int r = 0; r < rn; r++) rank_step(sh[r], sb[r], ty, tx, acc);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int m = m0 + ty * 8 + i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int n = n0 + (j >> 2) * 64 + tx * 4 + (j & 3);
+            if (n >= N) continue;
+            if (CB) ((uint16_t*)C)[(int64_t)m * ldc + n] = (uint16_t)f32_to_bf16(acc[i][j]);
+            else ((float*)C)[(int64_t)m * ldc + n] = acc[i][j];
+        }
+    }
+}
+
+template <int TR>
+static hipError_t launch_down_rows(hipStream_t stream, const void* x, bool x_bf16, int64_t ldx, const float* A,
+                                   float* h, int M, int K, int R) {
+    const dim3 grid((unsigned)((M + 63) / 64), (unsigned)((R + 4 * TR - 1) / (4 * TR)));
+    if (x_bf16) hipLaunchKernelGGL((lora_down_rows_kernel<true, TR>), grid, dim3(256), 0, stream, x, ldx, A, h, M, K, R);
+    else hipLaunchKernelGGL((lora_down_rows_kernel<false, TR>), grid, dim3(256), 0, stream, x, ldx, A, h, M, K, R);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_down(hipStream_t stream, const void* x, bool x_bf16, int64_t ldx, const float* A, float* h,
+                            int M, int K, int R) {
+    const int esz = x_bf16 ? 2 : 4;
+    if (K % LD_KC == 0 && (uintptr_t)x % 16 == 0 && (ldx * esz) % 16 == 0 && (uintptr_t)A % 16 == 0) {
+        const char* e = getenv("PHI_LORA_TR");  // A/B switch: ranks per wave (1, 2 or 4)
+        const int tr = e ? atoi(e) : 2;
+        if (tr == 1) return launch_down_rows<1>(stream, x, x_bf16, ldx, A, h, M, K, R);
+        if (tr == 2) return launch_down_rows<2>(stream, x, x_bf16, ldx, A, h, M, K, R);
+        return launch_down_rows<4>(stream, x, x_bf16, ldx, A, h, M, K, R);
+    }
+    const dim3 grid((unsigned)((M + LD_BM - 1) / LD_BM), (unsigned)((R + LD_BR - 1) / LD_BR));
+    if (x_bf16) hipLaunchKernelGGL(lora_down_kernel<true>, grid, dim3(256), 0, stream, x, ldx, A, h, M, K, R);
+    else hipLaunchKernelGGL(lora_down_kernel<false>, grid, dim3(256), 0, stream, x, ldx, A, h, M, K, R);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_rank_add(hipStream_t stream, const float* h, const float* B, void* C, bool c_bf16, int64_t ldc,
+                                int M, int N, int R) {
+    const dim3 grid((unsigned)((N + RA_BN - 1) / RA_BN), (unsigned)((M + RA_BM - 1) / RA_BM));
+    if (c_bf16) hipLaunchKernelGGL(lora_rank_add_kernel<true>, grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+    else hipLaunchKernelGGL(lora_rank_add_kernel<false>, grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+    return hipGetLastError();
+}
+
+}  // namespace phi_dev

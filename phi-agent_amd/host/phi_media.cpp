@@ -139,6 +139,27 @@ void dispatch_int4_gemm(ComputeContext& ctx, const Int4GemmArgs& a) {
               "int4_gemm");
 }
 
+// core/kernels/gpu_ops.cpp:505-522
+void dispatch_lora_rank_add(ComputeContext& ctx, const LoraRankAddArgs& a) {
+    if (a.m <= 0 || a.n <= 0 || a.rank <= 0) throw MediaError("lora_rank_add: empty problem");
+    ctx.check(phi_hip_lora_rank_add(ctx.stream(), (const float*)cat(a.h.res, a.h.off), (const float*)cat(a.b.res, a.b.off),
+                                    at(a.c.res, a.c.off), PHI_F32, a.n, a.m, a.n, a.rank),
+              "lora_rank_add");
+}
+
+// core/models/model_common.cpp:1667-1700: the same scratch check, then both products.
+void apply_lora_tail(GpuCtx& g, const LoraTail& t, const GpuAlloc& x, i64 m, const GpuAlloc& out, const GpuAlloc& h) {
+    if (!t.active || m <= 0) return;
+    const u64 need = (u64)m * (u64)t.rank * 4;
+    if (h.bytes < need)
+        throw MediaError("LoRA correction: the hidden-form scratch is " + std::to_string(h.bytes) + " bytes; a [" +
+                         std::to_string(m) + ", " + std::to_string(t.rank) + "] fp32 one needs " + std::to_string(need));
+    g.ctx->check(phi_hip_lora_tail(g.ctx->stream(), cat(x.res, x.off), PHI_F32, t.k, m, t.k,
+                                   (const float*)cat(t.at.res, t.at.off), (const float*)cat(t.bt.res, t.bt.off), t.rank,
+                                   t.n, at(out.res, out.off), PHI_F32, t.n, (float*)at(h.res, h.off), h.bytes),
+                 "lora_tail");
+}
+
 // core/kernels/w4a8_expand.cpp:263-303
 void dispatch_w4a8_expand(ComputeContext& ctx, const W4a8ExpandArgs& a) {
     if (a.rows <= 0 || a.k <= 0) return;

@@ -176,6 +176,22 @@ struct Int4GemmArgs {
 
 void dispatch_int4_gemm(ComputeContext& ctx, const Int4GemmArgs& a);
 
+// C[m, n] += H[m, rank] . B^T (core/kernels/gpu_ops.hpp:190-196), fp32.
+struct LoraRankAddArgs {
+    GpuAlloc h, b, c;
+    i64 m = 0, n = 0, rank = 0;
+};
+void dispatch_lora_rank_add(ComputeContext& ctx, const LoraRankAddArgs& a);
+
+// The runtime LoRA correction of one linear (core/models/model_common.hpp:245-251).
+struct LoraTail {
+    bool active = false;
+    i64 rank = 0;
+    i64 n = 0, k = 0;
+    GpuAlloc at;  // [rank, k] fp32: the factors' A rows, stacked
+    GpuAlloc bt;  // [n, rank] fp32: the factors' B columns, scaled, stacked
+};
+
 // One linear weight in the int8 form the GEMM reads.
 struct QuantLinear {
     GpuAlloc w;      // [n,k] int8
@@ -194,5 +210,9 @@ struct GpuCtx {
 // rotate+quantise x into q8/s8, then the int8 GEMM; out is [m, n] fp32.
 void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 k,
                  const GpuAlloc& out, const GpuAlloc& q8, const GpuAlloc& s8);
+
+// out [m, t.n] fp32 += (x [m, t.k] fp32 . at^T) . bt^T, with h the caller's
+// [m, rank] fp32 scratch (core/models/model_common.cpp:1667-1700).
+void apply_lora_tail(GpuCtx& g, const LoraTail& t, const GpuAlloc& x, i64 m, const GpuAlloc& out, const GpuAlloc& h);
 
 }  // namespace phi::media

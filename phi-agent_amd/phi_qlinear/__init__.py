@@ -63,7 +63,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_w4a8_prepare", "phi_hip_w4a8_linear", "phi_hip_i8_gemv_batched",
            "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes",
            "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual", "phi_hip_quant_rotate_act",
-           "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes"]
+           "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
+           "phi_hip_lora_down", "phi_hip_lora_rank_add"]
 
 _lib = None
 
@@ -102,6 +103,9 @@ def load() -> ctypes.CDLL:
     L.phi_hip_silu_gate.argtypes = [P, P, I, I64, I64, I64, P, I, I64]
     L.phi_hip_i4_gemm.argtypes = [P, P, I64, P, I64, P, P, P, I, I64, I64, I64, I64, P, SZ]
     L.phi_hip_i4_workspace_bytes.argtypes = [I64, I64, I64]
+    L.phi_hip_lora_tail.argtypes = [P, P, I, I64, I64, I64, P, P, I64, I64, P, I, I64, P, SZ]
+    L.phi_hip_lora_down.argtypes = [P, P, I, I64, I64, I64, P, I64, P]
+    L.phi_hip_lora_rank_add.argtypes = [P, P, P, P, I, I64, I64, I64, I64]
     L.phi_hip_i4_workspace_bytes.restype = SZ
     for name in EXPORTS:
         f = getattr(L, name)
@@ -395,3 +399,38 @@ def i4_gemm(A: torch.Tensor, B: torch.Tensor, sA: torch.Tensor | None, sB: torch
     _check(load().phi_hip_i4_gemm(_stream(stream), _ptr(A), A.stride(0), _ptr(B), B.stride(0), _ptr(sA),
                                   _ptr(sB), _ptr(C), _dt(C), C.stride(0), M, N, K, ws, wsb))
     return C
+
+
+def lora_down(x: torch.Tensor, A: torch.Tensor, h: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """h [M, R] = x [M, K] . A [R, K]^T in fp32, k-ordered fma chains (phi_hip_lora_down)."""
+    _require_device(x, A, h)
+    M, K = x.shape
+    R = A.shape[0]
+    if h is None:
+        h = torch.empty((M, R), dtype=torch.float32, device=x.device)
+    _check(load().phi_hip_lora_down(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(A), R, _ptr(h)))
+    return h
+
+
+def lora_rank_add(h: torch.Tensor, B: torch.Tensor, C: torch.Tensor, stream=None) -> torch.Tensor:
+    """C [M, N] += h [M, R] . B [N, R]^T in place, r-ordered fma chains from C (phi_hip_lora_rank_add)."""
+    _require_device(h, B, C)
+    M, N = C.shape
+    R = h.shape[1]
+    _check(load().phi_hip_lora_rank_add(_stream(stream), _ptr(h), _ptr(B), _ptr(C), _dt(C), C.stride(0), M, N, R))
+    return C
+
+
+def lora_tail(x: torch.Tensor, At: torch.Tensor, Bt: torch.Tensor, out: torch.Tensor,
+              h: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """out += (x . At^T) . Bt^T in place (phi_hip_lora_tail; apply_lora_tail
+    core/models/model_common.cpp:1667-1700); h is the [M, R] fp32 scratch."""
+    _require_device(x, At, Bt, out, h)
+    M, K = x.shape
+    R = At.shape[0]
+    N = out.shape[1]
+    if h is None:
+        h = torch.empty((M, R), dtype=torch.float32, device=x.device)
+    _check(load().phi_hip_lora_tail(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(At), _ptr(Bt), R, N,
+                                    _ptr(out), _dt(out), out.stride(0), _ptr(h), h.numel() * h.element_size()))
+    return out

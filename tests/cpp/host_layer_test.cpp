@@ -262,6 +262,66 @@ static void test_int4_gemm(ComputeContext& ctx) {
            failures ? "mismatch" : "bit-exact");
 }
 
+// linear_gemm then apply_lora_tail (core/models/image_dit.cpp:955-960), bit for bit.
+static void test_lora_tail(ComputeContext& ctx) {
+    const i64 m = 50, k = 512, n = 96, rank = 12;
+    std::mt19937 rng(17);
+    std::normal_distribution<float> nd(0.0f, 1.0f);
+    std::uniform_int_distribution<int> ud(-127, 127);
+    std::vector<float> x(m * k), sw(n, 0.002f), a(rank * k), b(n * rank);
+    std::vector<int8_t> w(n * k);
+    for (auto& v : x) v = nd(rng);
+    for (auto& v : w) v = (int8_t)ud(rng);
+    for (auto& v : a) v = 0.05f * nd(rng);
+    for (auto& v : b) v = 0.05f * nd(rng);
+    const u64 off_x = 0, off_w = off_x + m * k * 4, off_s = off_w + n * k, off_a = off_s + 4096,
+              off_b = off_a + rank * k * 4, off_q8 = off_b + n * rank * 4, off_s8 = off_q8 + m * k,
+              off_h = off_s8 + 4096, off_y = off_h + m * rank * 4;
+    GpuBuffer* pool = ctx.create_device_buffer(off_y + m * n * 4);
+    ctx.upload(pool, x.data(), m * k * 4, off_x);
+    ctx.upload(pool, w.data(), n * k, off_w);
+    ctx.upload(pool, sw.data(), n * 4, off_s);
+    ctx.upload(pool, a.data(), a.size() * 4, off_a);
+    ctx.upload(pool, b.data(), b.size() * 4, off_b);
+    GpuCtx g;
+    g.ctx = &ctx;
+    QuantLinear ql;
+    ql.w = GpuAlloc{pool, off_w, (u64)(n * k)};
+    ql.scale = GpuAlloc{pool, off_s, (u64)(n * 4)};
+    ql.n = n;
+    ql.k = k;
+    LoraTail t;
+    t.active = true;
+    t.rank = rank;
+    t.n = n;
+    t.k = k;
+    t.at = GpuAlloc{pool, off_a, (u64)(rank * k * 4)};
+    t.bt = GpuAlloc{pool, off_b, (u64)(n * rank * 4)};
+    const GpuAlloc xa{pool, off_x, (u64)(m * k * 4)}, ya{pool, off_y, (u64)(m * n * 4)};
+    ctx.begin();
+    linear_gemm(g, ql, xa, m, k, ya, GpuAlloc{pool, off_q8, (u64)(m * k)}, GpuAlloc{pool, off_s8, (u64)(m * 4)});
+    apply_lora_tail(g, t, xa, m, ya, GpuAlloc{pool, off_h, (u64)(m * rank * 4)});
+    ctx.submit();
+    std::vector<float> y(m * n), yo(m * n), so(m), h(m * rank);
+    std::vector<int8_t> qo(m * k);
+    ctx.download(pool, y.data(), y.size() * 4, off_y);
+    orc_q8_linear(x.data(), ORC_F32, m, k, w.data(), sw.data(), 0, nullptr, -1, n, ORC_ROUND_HALF_AWAY, yo.data(),
+                  ORC_F32, qo.data(), so.data(), nullptr);
+    orc_lora_down(x.data(), k, a.data(), h.data(), m, k, rank);
+    orc_lora_rank_add(h.data(), b.data(), yo.data(), n, m, n, rank);
+    CHECK(memcmp(y.data(), yo.data(), y.size() * 4) == 0, "lora tail: fp32 outputs differ");
+    bool threw = false;
+    try {
+        apply_lora_tail(g, t, xa, m, ya, GpuAlloc{pool, off_h, (u64)(m * rank * 4 - 4)});
+    } catch (const MediaError& e) {
+        threw = strstr(e.what(), "hidden-form scratch") != nullptr;
+    }
+    CHECK(threw, "a short LoRA scratch must throw MediaError");
+    ctx.release_buffer(pool);
+    printf("lora tail %lldx%lldx%lld rank %lld: %s\n", (long long)m, (long long)n, (long long)k, (long long)rank,
+           failures ? "mismatch" : "bit-exact");
+}
+
 static void test_errors(ComputeContext& ctx) {
     bool threw = false;
     try {
@@ -306,6 +366,7 @@ int main() {
         test_w4a8_expand(ctx);
         test_activations(ctx);
         test_int4_gemm(ctx);
+        test_lora_tail(ctx);
     } catch (const std::exception& e) {
         printf("FAIL exception: %s\n", e.what());
         return 1;

@@ -53,7 +53,8 @@ def test_host_layer_library_exports_reference_names():
     for name in ("phi::media::dispatch_int8_gemm", "phi::media::dispatch_quant_convrot",
                  "phi::media::dispatch_w4a8_expand", "phi::media::linear_gemm",
                  "phi::media::ComputeContext::submit", "phi::media::dispatch_elem",
-                 "phi::media::dispatch_silu_gate_fused", "phi::media::dispatch_int4_gemm"):
+                 "phi::media::dispatch_silu_gate_fused", "phi::media::dispatch_int4_gemm",
+                 "phi::media::dispatch_lora_rank_add", "phi::media::apply_lora_tail"):
         assert name in out, name
 
 
@@ -118,6 +119,20 @@ def test_int4_gemm_contract(lib):
     assert lib.phi_hip_i4_workspace_bytes(511, 64, 512) == 0
     assert lib.phi_hip_i4_workspace_bytes(512, 64, 512) == 64 * 512
     assert lib.phi_hip_i4_workspace_bytes(512, 64, 768) == 0
+
+
+def test_lora_contracts(lib):
+    rc = lib.phi_hip_lora_rank_add(None, FAKE, FAKE, FAKE, Q.F32, 16, 0, 16, 4)
+    assert rc == 2 and Q.last_error() == "lora_rank_add: empty problem"
+    rc = lib.phi_hip_lora_rank_add(None, FAKE, FAKE, FAKE, Q.I8, 16, 4, 16, 4)
+    assert rc == 1
+    rc = lib.phi_hip_lora_down(None, FAKE, Q.F32, 100, 4, 256, FAKE, 8, FAKE)
+    assert rc == 2 and "ldx" in Q.last_error()
+    rc = lib.phi_hip_lora_tail(None, FAKE, Q.F32, 256, 4, 256, FAKE, FAKE, 8, 16, FAKE, Q.F32, 16, FAKE, 127)
+    assert rc == 4 and "needs 128" in Q.last_error()
+    # an inactive tail or no rows: a no-op
+    assert lib.phi_hip_lora_tail(None, None, Q.F32, 256, 0, 256, None, None, 8, 16, None, Q.F32, 16, None, 0) == 0
+    assert lib.phi_hip_lora_tail(None, None, Q.F32, 256, 4, 256, None, None, 0, 16, None, Q.F32, 16, None, 0) == 0
 
 
 def test_gemm_contract(lib):
