@@ -2,6 +2,10 @@
 #include "phi_media.hpp"
 
 #include "phi_qlinear.h"
+#include "safetensors.hpp"
+
+#include <cstring>
+#include <vector>
 
 namespace phi::media {
 
@@ -158,6 +162,190 @@ void apply_lora_tail(GpuCtx& g, const LoraTail& t, const GpuAlloc& x, i64 m, con
                                    (const float*)cat(t.at.res, t.at.off), (const float*)cat(t.bt.res, t.bt.off), t.rank,
                                    t.n, at(out.res, out.off), PHI_F32, t.n, (float*)at(h.res, h.off), h.bytes),
                  "lora_tail");
+}
+
+GpuArena::GpuArena(ComputeContext& ctx, u64 bytes) : ctx_(ctx) { buf_ = ctx_.create_device_buffer(bytes); }
+
+GpuArena::~GpuArena() { ctx_.release_buffer(buf_); }
+
+GpuAlloc GpuArena::alloc(u64 bytes) {
+    const u64 off = (used_ + 255) & ~(u64)255;
+    if (!buf_ || off + bytes > buf_->bytes)
+        throw MediaError("arena: " + std::to_string(bytes) + " bytes do not fit (" + std::to_string(used_) + " of " +
+                         std::to_string(capacity()) + " used)");
+    used_ = off + bytes;
+    return GpuAlloc{buf_, off, bytes};
+}
+
+namespace {
+
+// The conditions of the reference's device-expand path (w4a8_plan_of,
+// core/models/model_common.cpp:605-680), each checked rather than trusted.
+struct W4a8Plan {
+    CodeLayout layout = CodeLayout::Nibble4;
+    const StTensor* codes = nullptr;
+    const StTensor* srel = nullptr;
+    const StTensor* sch = nullptr;
+    const StTensor* codebook = nullptr;
+    const StTensor* correction = nullptr;
+    i64 n = 0, k = 0, group = 0, srel_row_bytes = 0;
+    RelDType rel_dtype = RelDType::F32;
+};
+
+std::string w4a8_plan_of(const SafeTensors& st, const StTensor& t, W4a8Plan* out) {
+    const SafeTensors::WeightLayout L = st.weight_layout(t.name);
+    const std::string& f = L.spec.format;
+    const bool six = f == "w6a8_int8" || f == "w6a8";
+    if (t.shape.size() != 2 || (t.dtype != StDType::I8 && t.dtype != StDType::U8)) return "codes are not a 2-D byte tensor";
+    if (!L.spec.convrot) return "the weight is not convrot-rotated";
+    if (!L.rel_scale || L.rel_scale->shape.size() != 2) return "no 2-D weight_s_rel table";
+    RelDType rdt;
+    switch (L.rel_scale->dtype) {
+        case StDType::F32: rdt = RelDType::F32; break;
+        case StDType::F16: rdt = RelDType::F16; break;
+        case StDType::BF16: rdt = RelDType::BF16; break;
+        case StDType::F8_E4M3: rdt = RelDType::F8_E4M3; break;
+        case StDType::F8_E5M2: rdt = RelDType::F8_E5M2; break;
+        case StDType::U8: rdt = RelDType::U8_E4M3; break;
+        default: return std::string("weight_s_rel dtype ") + st_dtype_name(L.rel_scale->dtype) + " is not decodable";
+    }
+    const i64 n = t.shape[0], k = st.logical_cols(t);
+    const i64 group = L.group;
+    const i64 per = six ? 4 : 2;
+    if (group <= 0 || group % per != 0 || k % group != 0) return "group " + std::to_string(group) + " does not divide K";
+    const i64 need = six ? (k / 2 + k / 4) : k / 2;
+    if ((i64)t.row_bytes() < need) return "code rows are shorter than K needs";
+    if (L.rel_scale->shape[0] != n || L.rel_scale->shape[1] != k / group) return "weight_s_rel is not [N, K/group]";
+    if (six && L.codebook) return "a six-bit weight with a codebook";
+    if (!six && L.codebook && (L.codebook->dtype != StDType::F32 || L.codebook->numel != 16))
+        return "the codebook is not 16 fp32 levels";
+    if (L.row_scale && (L.row_scale->dtype != StDType::F32 || (L.row_scale->numel != 1 && L.row_scale->numel != n)))
+        return "the channel scale is not fp32 [N] or [1]";
+    if (L.correction) {
+        const i64 cg = L.correction->shape.empty() ? 0 : L.correction->shape[0];
+        const i64 cn = L.correction->shape.size() > 1 ? L.correction->shape[1] : 0;
+        if (L.correction->dtype != StDType::F32 || cg != k / group || cn != n)
+            return "weight_correction is not fp32 [K/group, N]";
+    }
+    out->layout = six ? CodeLayout::Packed6 : CodeLayout::Nibble4;
+    out->codes = &t;
+    out->srel = L.rel_scale;
+    out->sch = L.row_scale;
+    out->codebook = six ? nullptr : L.codebook;
+    out->correction = L.correction;
+    out->n = n;
+    out->k = k;
+    out->group = group;
+    out->srel_row_bytes = (i64)L.rel_scale->row_bytes();
+    out->rel_dtype = rdt;
+    return "";
+}
+
+}  // namespace
+
+// core/models/model_common.cpp:921-1010 (the int8 and device-expand branches)
+QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& into) {
+    if (!g.ok()) throw MediaError("load_quant_linear: no compute context");
+    const StTensor& t = st.require(base + ".weight");
+    if (t.shape.size() != 2) throw MediaError("load_quant_linear: '" + base + ".weight' is not a 2-D matrix");
+    const i64 n = t.shape[0], k = st.logical_cols(t);
+    QuantLinear q;
+    q.n = n;
+    q.k = k;
+    if (st.is_plain_int8(t)) {
+        // Shipped int8 tensorwise: the codes verbatim, one fp32 scale per row.
+        const StTensor& sc = st.require(base + ".weight_scale");
+        if (sc.numel != n) throw MediaError("weight_scale length mismatch: " + base);
+        if (t.nbytes != (u64)(n * k)) throw MediaError("load_quant_linear: '" + base + ".weight' is not [N, K] int8");
+        q.w = into.alloc((u64)(n * k));
+        g.ctx->upload(q.w.res, t.data, t.nbytes, q.w.off);
+        std::vector<float> s((size_t)n);
+        for (i64 r = 0; r < n; r++) s[(size_t)r] = st.row_scale_value(sc, r);
+        q.scale = into.alloc((u64)n * 4);
+        g.ctx->upload(q.scale.res, s.data(), (u64)n * 4, q.scale.off);
+        return q;
+    }
+    const SafeTensors::WeightLayout L = st.weight_layout(t.name);
+    if (L.packed) {
+        W4a8Plan pl;
+        const std::string why = w4a8_plan_of(st, t, &pl);
+        if (!why.empty()) throw MediaError("load_quant_linear: '" + base + "' (" + L.spec.format + "): " + why);
+        // Stage the stored parts on the device, 256-byte aligned, and expand.
+        auto up256 = [](u64 v) { return (v + 255) & ~(u64)255; };
+        const u64 cb = (u64)n * t.row_bytes(), sb = pl.srel->nbytes, hb = pl.sch ? (u64)n * 4 : 0,
+                  kb = pl.codebook ? 64 : 0, rb = pl.correction ? pl.correction->nbytes : 0;
+        const u64 o_codes = 0, o_srel = up256(cb), o_sch = o_srel + up256(sb), o_cb = o_sch + up256(hb),
+                  o_corr = o_cb + up256(kb), total = o_corr + up256(rb);
+        GpuBuffer* stage = g.ctx->create_device_buffer(total);
+        try {
+            g.ctx->upload(stage, t.data, cb, o_codes);
+            g.ctx->upload(stage, pl.srel->data, sb, o_srel);
+            if (pl.sch) {
+                std::vector<float> v((size_t)n);
+                for (i64 r = 0; r < n; r++) v[(size_t)r] = st.row_scale_value(*pl.sch, r);  // a [1] table broadcasts
+                g.ctx->upload(stage, v.data(), hb, o_sch);
+            }
+            if (pl.codebook) g.ctx->upload(stage, pl.codebook->data, kb, o_cb);
+            if (pl.correction) g.ctx->upload(stage, pl.correction->data, rb, o_corr);
+            q.w = into.alloc((u64)(n * k));
+            q.scale = into.alloc((u64)n * 4);
+            phi_w4a8_weight w{};
+            w.codes = (const uint8_t*)(stage->base + o_codes);
+            w.codes_row_bytes = (int64_t)t.row_bytes();
+            w.s_rel = (const void*)(stage->base + o_srel);
+            w.s_rel_dtype = phi_rel_dtype(pl.rel_dtype);
+            w.srel_row_bytes = pl.srel_row_bytes;
+            w.s_channel = pl.sch ? (const float*)(stage->base + o_sch) : nullptr;
+            w.codebook = pl.codebook ? (const float*)(stage->base + o_cb) : nullptr;
+            w.correction = pl.correction ? (const float*)(stage->base + o_corr) : nullptr;
+            w.rows = n;
+            w.k = k;
+            w.group = pl.group;
+            w.layout = pl.layout == CodeLayout::Nibble4 ? 0 : 1;
+            g.ctx->check(phi_hip_w4a8_expand(g.ctx->stream(), &w, (int8_t*)at(q.w.res, q.w.off),
+                                             (float*)at(q.scale.res, q.scale.off)),
+                         "w4a8_expand");
+            g.ctx->submit();
+        } catch (...) {
+            g.ctx->release_buffer(stage);
+            throw;
+        }
+        g.ctx->release_buffer(stage);
+        return q;
+    }
+    if (L.spec.valid && L.spec.format == "convrot_w4a4")
+        throw MediaError("load_quant_linear: '" + base + "' is convrot_w4a4: load it with upload_quant_linear_w4a4 "
+                         "for the int4 GEMM");
+    throw MediaError("load_quant_linear: '" + base + ".weight' is " + st_dtype_name(t.dtype) +
+                     (L.spec.valid ? " (" + L.spec.format + ")" : std::string(" without a comfy_quant spec")) +
+                     ": the quantized-linear library loads int8_tensorwise, asym_w4a8_int8 and w6a8_int8");
+}
+
+// core/models/model_common.cpp:1285-1340 (the verbatim, no-LoRA branch)
+I4Upload upload_quant_linear_w4a4(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& arena) {
+    if (!g.ok()) throw MediaError("upload_quant_linear_w4a4: no compute context");
+    const StTensor& t = st.require(base + ".weight");
+    if (t.shape.size() != 2)
+        throw MediaError("upload_quant_linear_w4a4: '" + base + ".weight' is not a 2-D matrix");
+    const i64 packed_k = t.shape[1], logical_k = st.logical_cols(t);
+    if (packed_k % 2 != 0 || packed_k % 256 != 0)
+        throw MediaError("qwen3vl: " + base + " has a packed width of " + std::to_string(packed_k) +
+                         ", not packable to convrot_w4a4");
+    if (logical_k != packed_k * 2 || logical_k % 256 != 0)
+        throw MediaError("qwen3vl: " + base + " has K=" + std::to_string(logical_k) +
+                         ", not a convrot_w4a4 matrix (it must be twice the packed width)");
+    if (st_dtype_bytes(t.dtype) != 1) throw MediaError("upload_quant_linear_w4a4: '" + base + ".weight' is not bytes");
+    const StTensor& sc = st.require(base + ".weight_scale");
+    I4Upload out;
+    out.n = t.shape[0];
+    out.k = packed_k;
+    out.w = arena.alloc((u64)out.n * (u64)packed_k);
+    g.ctx->upload(out.w.res, t.data, t.nbytes, out.w.off);
+    std::vector<float> s((size_t)out.n);
+    for (i64 r = 0; r < out.n; r++) s[(size_t)r] = st.row_scale_value(sc, r);
+    out.s = arena.alloc((u64)out.n * 4);
+    g.ctx->upload(out.s.res, s.data(), (u64)out.n * 4, out.s.off);
+    return out;
 }
 
 // core/kernels/w4a8_expand.cpp:263-303

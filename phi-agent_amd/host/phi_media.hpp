@@ -211,6 +211,46 @@ struct GpuCtx {
 void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 k,
                  const GpuAlloc& out, const GpuAlloc& q8, const GpuAlloc& s8);
 
+// ---- loading weights from checkpoints (safetensors.hpp reads the files) ----
+
+class SafeTensors;
+
+// A bump allocator over one device buffer, as the reference's GpuArena hands
+// out weight storage (core/runtime/sched.hpp:27-60): 256-byte aligned pieces,
+// MediaError when full.  Owns the buffer.
+class GpuArena {
+public:
+    GpuArena(ComputeContext& ctx, u64 bytes);
+    ~GpuArena();
+    GpuArena(const GpuArena&) = delete;
+    GpuArena& operator=(const GpuArena&) = delete;
+    GpuAlloc alloc(u64 bytes);
+    u64 used() const { return used_; }
+    u64 capacity() const { return buf_ ? buf_->bytes : 0; }
+
+private:
+    ComputeContext& ctx_;
+    GpuBuffer* buf_ = nullptr;
+    u64 used_ = 0;
+};
+
+// One linear from a checkpoint into the int8 form the GEMM reads
+// (core/models/model_common.cpp:921-1010, without the dense and LoRA-folding
+// branches): int8_tensorwise is uploaded verbatim with its weight_scale; the
+// grouped families (asym_w4a8_int8, w6a8_int8) are uploaded as stored and
+// expanded on the device (w4a8_plan_of / w4a8_pack_rows, :589-748).  Anything
+// else throws MediaError naming the family.
+QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& into);
+
+// convrot_w4a4 (signed int4, two per byte, one fp32 scale per row): the packed
+// bytes verbatim for the int4 GEMM (core/models/model_common.cpp:1285-1340);
+// k is the packed width K/2, as the reference's I4Upload records it.
+struct I4Upload {
+    GpuAlloc w, s;
+    i64 n = 0, k = 0;
+};
+I4Upload upload_quant_linear_w4a4(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& arena);
+
 // out [m, t.n] fp32 += (x [m, t.k] fp32 . at^T) . bt^T, with h the caller's
 // [m, rank] fp32 scratch (core/models/model_common.cpp:1667-1700).
 void apply_lora_tail(GpuCtx& g, const LoraTail& t, const GpuAlloc& x, i64 m, const GpuAlloc& out, const GpuAlloc& h);

@@ -1,0 +1,136 @@
+"""CPU checks of the checkpoint readers (phi-agent_amd/host/safetensors.cpp):
+the comfy_quant blob (core/host/quant.cpp:18-38), the weight-layout rules
+(core/host/st.cpp:839-935), scale-table decoding, and malformed files.  The
+files are written with the safetensors library (independent of this code)."""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+import ckpt_util as C
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _tool():
+    if not os.path.exists(C.ST_TOOL):
+        pytest.fail(f"{C.ST_TOOL} was not built (run __graft_entry__.build())")
+
+
+def spec(text):
+    return json.loads(C.run("spec", text).stdout)
+
+
+def test_quant_spec_blob():
+    s = spec('{"format": "asym_w4a8_int8", "group_size": 16, "convrot_groupsize": 256}    ')
+    assert s == {"valid": True, "format": "asym_w4a8_int8", "convrot": False, "convrot_groupsize": 256,
+                 "group_size": 16}
+    # defaults: int8_tensorwise, convrot off, group 256 / 0
+    assert spec("{}") == {"valid": True, "format": "int8_tensorwise", "convrot": False, "convrot_groupsize": 256,
+                          "group_size": 0}
+    s = spec('{"format": "int8_tensorwise", "convrot": true, "convrot_groupsize": -4, "group_size": -1}')
+    assert s["convrot"] and s["convrot_groupsize"] == 256 and s["group_size"] == 0
+    # text past the last '}' is padding; no '}' or bad JSON is an invalid spec
+    assert spec('{"format": "w6a8_int8"} trailing')["format"] == "w6a8_int8"
+    assert spec("no json here")["valid"] is False
+    assert spec('{"format": }')["valid"] is False
+
+
+def int8_file(tmp_path, N=24, K=512, scale_dtype=torch.float32, with_spec=True):
+    g = torch.Generator().manual_seed(1)
+    t = {"blk.0.mlp.weight": torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8),
+         "blk.0.mlp.weight_scale": (torch.rand(N, generator=g) * 0.01 + 0.001).to(scale_dtype),
+         "blk.0.other.bias": torch.zeros(N)}
+    if with_spec:
+        t["blk.0.mlp.comfy_quant"] = C.comfy_blob({"format": "int8_tensorwise", "convrot": True,
+                                                    "convrot_groupsize": 256})
+    return C.write(str(tmp_path / "int8.safetensors"), t), t
+
+
+def test_probe_int8_tensorwise(tmp_path):
+    path, t = int8_file(tmp_path)
+    p = C.probe(path, "blk.0.mlp")
+    assert p["tensors"] == 4 and p["dtype"] == "I8" and (p["n"], p["k"]) == (24, 512)
+    assert p["plain_int8"] and not p["packed"] and p["known"] and p["bits"] == 8 and p["group"] == 0
+    assert p["row_scale"] == "blk.0.mlp.weight_scale"
+    assert p["spec"]["format"] == "int8_tensorwise" and p["spec"]["convrot"]
+    assert np.float32(p["row_scale0"]) == t["blk.0.mlp.weight_scale"][0].item()
+    # no comfy_quant sidecar: still plain int8 (codes plus a weight_scale)
+    path2, _ = int8_file(tmp_path, with_spec=False)
+    assert C.probe(path2, "blk.0.mlp")["plain_int8"]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_scale_tables_decode(tmp_path, dt):
+    path, t = int8_file(tmp_path, scale_dtype=dt)
+    p = C.probe(path, "blk.0.mlp")
+    assert np.float32(p["row_scale0"]) == np.float32(t["blk.0.mlp.weight_scale"][0].float().item())
+
+
+def grouped_tensors(N, K, group, fmt, *, codebook=False, channel="s_channel", rel=torch.float16, spec_group=True):
+    g = torch.Generator().manual_seed(K + group)
+    six = fmt.startswith("w6a8")
+    stored = K // 2 + K // 4 if six else K // 2
+    t = {"m.weight": torch.randint(-128, 128, (N, stored), generator=g, dtype=torch.int8),
+         "m.weight_s_rel": (torch.rand(N, K // group, generator=g) * 4 + 0.5).to(rel)}
+    sp = {"format": fmt, "convrot_groupsize": 256}
+    if spec_group:
+        sp["group_size"] = group
+    t["m.comfy_quant"] = C.comfy_blob(sp)
+    if channel:
+        t[f"m.weight_{channel}"] = torch.rand(N, generator=g) * 0.01 + 0.001
+    if codebook:
+        t["m.weight_codebook"] = torch.randn(16, generator=g) * 3
+    return t
+
+
+def test_probe_asym_w4a8(tmp_path):
+    path = C.write(str(tmp_path / "w4.safetensors"), grouped_tensors(40, 1024, 128, "asym_w4a8_int8", codebook=True))
+    p = C.probe(path, "m")
+    assert (p["n"], p["k"]) == (40, 1024) and p["bits"] == 4 and p["packed"] and p["group"] == 128
+    assert p["codebook"] and not p["plain_int8"] and p["rel_scale"] == "m.weight_s_rel"
+    assert p["row_scale"] == "m.weight_s_channel"
+    assert p["spec"]["convrot"]  # the grouped families are stored rotated
+    # group_size absent: the family's default (16 for asym_w4a8_int8)
+    path = C.write(str(tmp_path / "w4d.safetensors"),
+                   grouped_tensors(8, 512, 16, "asym_w4a8_int8", spec_group=False))
+    assert C.probe(path, "m")["group"] == 16
+
+
+def test_probe_w6a8_and_scale_fallback(tmp_path):
+    # w6a8 with the channel scale under weight_scale (no weight_s_channel)
+    path = C.write(str(tmp_path / "w6.safetensors"),
+                   grouped_tensors(16, 1024, 32, "w6a8_int8", channel="scale", spec_group=False))
+    p = C.probe(path, "m")
+    assert (p["n"], p["k"]) == (16, 1024) and p["bits"] == 6 and p["group"] == 32
+    assert p["row_scale"] == "m.weight_scale"
+
+
+def test_probe_convrot_w4a4(tmp_path):
+    g = torch.Generator().manual_seed(3)
+    t = {"te.weight": torch.randint(-128, 128, (32, 512), generator=g, dtype=torch.int8),
+         "te.weight_scale": torch.rand(32, generator=g),
+         "te.comfy_quant": C.comfy_blob({"format": "convrot_w4a4"})}
+    p = C.probe(C.write(str(tmp_path / "w4a4.safetensors"), t), "te")
+    assert (p["n"], p["k"]) == (32, 1024) and not p["packed"] and p["spec"]["convrot"] and not p["plain_int8"]
+
+
+def test_malformed_files(tmp_path):
+    path, _ = int8_file(tmp_path)
+    raw = open(path, "rb").read()
+    hlen = struct.unpack("<Q", raw[:8])[0]
+    cases = {
+        "short": b"\x01\x02",
+        "hlen_past_end": struct.pack("<Q", len(raw)) + raw[8:],
+        "bad_json": struct.pack("<Q", 5) + b"{oops" + raw[8 + hlen:],
+        "truncated_data": raw[:-16],
+    }
+    for name, data in cases.items():
+        p = tmp_path / f"{name}.safetensors"
+        p.write_bytes(data)
+        out = C.run("probe", str(p), "blk.0.mlp", check=False)
+        assert out.returncode == 3 and out.stdout.startswith("error: safetensors"), (name, out.stdout)
+    out = C.run("probe", path, "nope", check=False)
+    assert out.returncode == 3 and "tensor not found: nope.weight" in out.stdout
