@@ -190,7 +190,7 @@ __device__ __forceinline__ void cursor_tile(Wv& w, const GemmParams& p, const Sh
 // Epilogue operands of the cursor's tile into LDS area le: wave w loads row
 // scales 64w..64w+63, column scales / fp32 bias 64w..64w+63 and (waves 0-1)
 // the bf16 bias words; past M or N (or the tile) they read as zero.
-template <int WT>
+template <int WT, bool G>
 __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8_t* le) {
     constexpr int BM = Cfg<WT>::BM;
     const int rows = min(BM, p.M - w.cm0), cols = min(BM, p.N - w.cn0);
@@ -210,7 +210,10 @@ __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8
         p.bias_kind != BIAS_NONE ? cols * bsz : 0, kRsrcWord3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rBZ, (lptr_t)(le + 2048 + w.wave * 256), 4, w.lane * 4,
                                              w.wave * 256, 0, 0);
-    if (p.gate) {
+    // G (the gated-residual instantiation): the gate, without a branch (a
+    // branch here would split the tile's last K-step pair, whose loads and
+    // MFMAs are scheduled as one block).
+    if constexpr (G) {
         const __amdgpu_buffer_rsrc_t rG =
             __builtin_amdgcn_make_buffer_rsrc((void*)(p.gate + w.cn0), (short)0, cols * 4, kRsrcWord3);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rG, (lptr_t)(le + 3072 + w.wave * 256), 4, w.lane * 4,
@@ -221,7 +224,7 @@ __device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8
 // K-step kl of the cursor's tile into stage S: DL A loads per wave and DL B
 // loads (W4: the thread's codes and table into r instead), with EPI plus the
 // tile's epilogue operands into area le.
-template <int WT, int S, bool EPI, bool W4>
+template <int WT, int S, bool EPI, bool W4, bool G>
 __device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int DL = Cfg<WT>::DL;
     const int koff = kl * BK;
@@ -241,7 +244,7 @@ __device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(w.lb[S] + w.wave * (DL * 1024) + j * 1024), 16,
                                                      w.voB[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.ldb, 0, 0);
     }
-    if constexpr (EPI) issue_epi<WT>(w, p, le);
+    if constexpr (EPI) issue_epi<WT, G>(w, p, le);
 }
 
 // W4: chunks [P0, P1) of the thread's 2C 16-column chunks of one K-step,
@@ -292,12 +295,12 @@ __device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[Cfg<WT>::NB][
 // of stage SN into nxt; with LOADS the cursor's K-step into stage S.  The
 // first MFMA goes ahead of the reads because the compiler's wait for cur is
 // a full lgkmcnt(0) that must not cover reads issued after it.
-template <int WT, int S, int SN, int QN, bool LOADS, bool EPI, bool W4, int X0, int X1>
+template <int WT, int S, int SN, int QN, bool LOADS, bool EPI, bool W4, bool G, int X0, int X1>
 __device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB],
                                         const Wv& w, const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int NB = Cfg<WT>::NB, DL = Cfg<WT>::DL;
     mma<WT>(cur, acc);
-    if constexpr (LOADS) issue<WT, S, EPI, W4>(w, p, kl, le, r);
+    if constexpr (LOADS) issue<WT, S, EPI, W4, G>(w, p, kl, le, r);
     frag<WT, SN, QN>(nxt, w);
     if constexpr (X1 > X0) {
         // Chunks [X0, X1) of the previous step's codes into the other stage,
@@ -343,18 +346,18 @@ __device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i
 // refills with K-step kl of the cursor's tile (EPI: epilogue operands into le).
 // W4: the codes loaded by the previous step are expanded into stage S^1 over
 // quarters 1-3, before the barrier that hands that stage to the next step.
-template <int WT, int S, bool EPI, bool W4>
+template <int WT, int S, bool EPI, bool W4, bool G>
 __device__ __forceinline__ void step(Frag<WT>& f0, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const Wv& w,
                                      const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int X = W4 ? 2 * W4Regs<WT>::C : 0;  // chunks to expand, over quarters 1-3
     Frag<WT> f1;
-    quarter<WT, S, S, 1, false, false, W4, 0, W4_Q1 * X / 3>(f0, f1, acc, w, p, kl, le, r);
-    quarter<WT, S, S, 2, false, false, W4, W4_Q1 * X / 3, W4_Q1 ? 2 * X / 3 : X / 2>(f1, f0, acc, w, p, kl, le, r);
-    quarter<WT, S, S, 3, false, false, W4, W4_Q1 ? 2 * X / 3 : X / 2, X>(f0, f1, acc, w, p, kl, le, r);
+    quarter<WT, S, S, 1, false, false, W4, G, 0, W4_Q1 * X / 3>(f0, f1, acc, w, p, kl, le, r);
+    quarter<WT, S, S, 2, false, false, W4, G, W4_Q1 * X / 3, W4_Q1 ? 2 * X / 3 : X / 2>(f1, f0, acc, w, p, kl, le, r);
+    quarter<WT, S, S, 3, false, false, W4, G, W4_Q1 ? 2 * X / 3 : X / 2, X>(f0, f1, acc, w, p, kl, le, r);
     wait_all();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    quarter<WT, S, S ^ 1, 0, true, EPI, W4, 0, 0>(f1, f0, acc, w, p, kl, le, r);
+    quarter<WT, S, S ^ 1, 0, true, EPI, W4, G, 0, 0>(f1, f0, acc, w, p, kl, le, r);
 }
 
 // Scaled epilogue operands of this lane's four columns starting at tile column ct.
@@ -381,7 +384,7 @@ __device__ __forceinline__ void col_operands(const GemmParams& p, const int8_t* 
 // (16-byte slots swizzled by row) and is stored as whole rows: bf16 in
 // 32 x 64-column pieces (128 bytes a row), fp32 / int32 in 32 x 32-column
 // pieces.
-template <int WT>
+template <int WT, bool G>
 __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const GemmParams& p, const Shape& s,
                                          int t, const Wv& w, const int8_t* e) {
     constexpr int NB = Cfg<WT>::NB, BM = Cfg<WT>::BM;
@@ -447,7 +450,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
     // C = fma(v, gate[n], C), the reference's AddMul `a + b * c`
     // (core/kernels/ops.cpp:80, applied after the projection at
     // core/models/av_dit.cpp:1389) as NVRTC's default --fmad=true contracts it.
-    const bool gated = p.gate != nullptr;
+    constexpr bool gated = G;
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         v4f sb[4], bz[4];
@@ -505,7 +508,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
 
 }  // namespace
 
-template <int WT, bool W4>
+template <int WT, bool W4, bool G>
 __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     using C = Cfg<WT>;
     constexpr int NB = C::NB, STG = C::STG, DL = C::DL;
@@ -563,14 +566,14 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     // area for tile i+2.
     W4Regs<WT> w4r;
     cursor_tile<WT, W4>(w, p, s, r);
-    issue<WT, 0, true, W4>(w, p, 0, w.le, w4r);
+    issue<WT, 0, true, W4, G>(w, p, 0, w.le, w4r);
     if constexpr (W4) {
         wait_all();
         expand<WT, 0, 0, 2 * W4Regs<WT>::C>(w4r, w);
-        issue<WT, 1, false, W4>(w, p, 1, w.le, w4r);
+        issue<WT, 1, false, W4, G>(w, p, 1, w.le, w4r);
         wait_vm_lgkm0<DL + W4Regs<WT>::C + 1>();  // stage 0, its operands and its expansion are done
     } else {
-        issue<WT, 1, false, W4>(w, p, 1, w.le, w4r);
+        issue<WT, 1, false, W4, G>(w, p, 1, w.le, w4r);
         wait_vm_lgkm0<2 * DL>();  // the first K-step and its operands have landed
     }
     __builtin_amdgcn_s_barrier();
@@ -582,8 +585,8 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
         int8_t* le = w.le + (i & 1) * EBYTES;
         zero_acc<WT>(acc);
         for (int k = 0; k < s.KT - 2; k += 2) {
-            step<WT, 0, false, W4>(f0, acc, w, p, k + 2, le, w4r);
-            step<WT, 1, false, W4>(f0, acc, w, p, k + 3, le, w4r);
+            step<WT, 0, false, W4, G>(f0, acc, w, p, k + 2, le, w4r);
+            step<WT, 1, false, W4, G>(f0, acc, w, p, k + 3, le, w4r);
         }
         // The last pair: the cursor moves to the next tile, if any.
         int kn = s.KT - 2;
@@ -593,9 +596,9 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
             kn = 0;
             ln = w.le + ((i + 1) & 1) * EBYTES;
         }
-        step<WT, 0, true, W4>(f0, acc, w, p, kn, ln, w4r);
-        step<WT, 1, false, W4>(f0, acc, w, p, kn + 1, ln, w4r);
-        epilogue<WT>(acc, p, s, t, w, le);
+        step<WT, 0, true, W4, G>(f0, acc, w, p, kn, ln, w4r);
+        step<WT, 1, false, W4, G>(f0, acc, w, p, kn + 1, ln, w4r);
+        epilogue<WT, G>(acc, p, s, t, w, le);
         if (++i == ntile) break;
     }
     // The reloads past the last K-step still write LDS: let them land.
@@ -642,12 +645,17 @@ hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int n
     const int bm = 2 * wave_tile;
     const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
     const int grid = tiles < num_cus ? tiles : num_cus;
+    // The gated residual (p.gate) is its own instantiation, so the plain
+    // kernels carry none of its registers.
+    if (w4 && p.gate) return hipErrorInvalidValue;
     if (wave_tile == 128) {
-        if (w4) hipLaunchKernelGGL((i8_gemm_persist_kernel<128, true>), dim3(grid), dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_persist_kernel<128, false>), dim3(grid), dim3(256), 0, stream, p);
+        if (w4) hipLaunchKernelGGL((i8_gemm_persist_kernel<128, true, false>), dim3(grid), dim3(256), 0, stream, p);
+        else if (p.gate) hipLaunchKernelGGL((i8_gemm_persist_kernel<128, false, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_persist_kernel<128, false, false>), dim3(grid), dim3(256), 0, stream, p);
     } else {
-        if (w4) hipLaunchKernelGGL((i8_gemm_persist_kernel<64, true>), dim3(grid), dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_persist_kernel<64, false>), dim3(grid), dim3(256), 0, stream, p);
+        if (w4) hipLaunchKernelGGL((i8_gemm_persist_kernel<64, true, false>), dim3(grid), dim3(256), 0, stream, p);
+        else if (p.gate) hipLaunchKernelGGL((i8_gemm_persist_kernel<64, false, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_persist_kernel<64, false, false>), dim3(grid), dim3(256), 0, stream, p);
     }
     return hipGetLastError();
 }
