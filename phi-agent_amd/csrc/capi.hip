@@ -197,17 +197,26 @@ hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p,
     const int G = num_cus();
     const int64_t M = p.M;
     const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, p.N, G) : gk == GK_PERSIST256 ? M : 0;
-    if (rows > 0) {
-        phi_dev::GemmParams q = p;
-        q.M = (int)rows;
-        const hipError_t e = phi_dev::launch_i8_gemm_persist(stream, q, G, 128, w4);
-        if (e != hipSuccess || rows == M) return e;
-    }
     phi_dev::GemmParams q = p;
     q.M = (int)(M - rows);
     q.A = p.A + rows * p.lda;
     if (q.sA) q.sA = p.sA + rows;
     q.C = (int8_t*)p.C + rows * ldc * (int64_t)c_elem_bytes(c_dtype);
+    if (rows > 0 && rows < M) {
+        // Both tile sizes: one launch (PHI_GEMM_MIXED=0 splits it in two, an A/B switch).
+        const char* e = getenv("PHI_GEMM_MIXED");
+        if (!(e && e[0] == '0')) {
+            phi_dev::GemmParams b = p;
+            b.M = (int)rows;
+            return phi_dev::launch_i8_gemm_persist_mixed(stream, b, q, G, w4);
+        }
+    }
+    if (rows > 0) {
+        phi_dev::GemmParams b = p;
+        b.M = (int)rows;
+        const hipError_t e = phi_dev::launch_i8_gemm_persist(stream, b, G, 128, w4);
+        if (e != hipSuccess || rows == M) return e;
+    }
     return phi_dev::launch_i8_gemm_persist(stream, q, G, 64, w4);
 }
 

@@ -45,6 +45,10 @@ hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
 // the per-(row, group) table (group a multiple of 128, code rows 16-byte aligned),
 // or signed nibbles with p.w4_signed.
 hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile, bool w4);
+// One launch of both tile sizes: pb's rows with 256 x 256 tiles, then ps's with
+// 128 x 128 tiles (same K, B, sB, bias; the caller offsets A, sA and C).
+hipError_t launch_i8_gemm_persist_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus,
+                                        bool w4);
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);
 

@@ -508,13 +508,14 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
 
 }  // namespace
 
+// The persistent loop over this workgroup's tiles of p, on LDS stages
+// a0/a1/b0/b1 (STG bytes each), the epilogue-operand areas eall and the
+// epilogue staging cbuf.  Returns at once when the workgroup has no tile.
 template <int WT, bool W4, bool G>
-__global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
+__device__ __forceinline__ void persist_tiles(const GemmParams& p, int8_t* a0, int8_t* a1, int8_t* b0, int8_t* b1,
+                                              int8_t* eall, int8_t* cbuf) {
     using C = Cfg<WT>;
-    constexpr int NB = C::NB, STG = C::STG, DL = C::DL;
-    __shared__ __align__(16) int8_t a0[STG], a1[STG], b0[STG], b1[STG];
-    __shared__ __align__(16) int8_t eall[2 * EBYTES];
-    __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    constexpr int NB = C::NB, DL = C::DL;
     Wv w;
     w.lane = threadIdx.x & 63;
     w.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -605,6 +606,32 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
     wait_all();
 }
 
+template <int WT, bool W4, bool G>
+__global__ __launch_bounds__(256) void i8_gemm_persist_kernel(GemmParams p) {
+    constexpr int STG = Cfg<WT>::STG;
+    __shared__ __align__(16) int8_t a0[STG], a1[STG], b0[STG], b1[STG];
+    __shared__ __align__(16) int8_t eall[2 * EBYTES];
+    __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    persist_tiles<WT, W4, G>(p, a0, a1, b0, b1, eall, cbuf);
+}
+
+// Both tile sizes in one launch: the workgroup's 256 x 256 tiles of pb, then
+// its 128 x 128 tiles of ps (the rows below pb's), in the same LDS.  One
+// launch instead of two saves a kernel boundary (about 6 us between dependent
+// launches on one stream), and a workgroup starts its small tile as soon as
+// its big ones are done.
+template <bool W4, bool G>
+__global__ __launch_bounds__(256) void i8_gemm_persist_mixed_kernel(GemmParams pb, GemmParams ps) {
+    constexpr int STG = Cfg<128>::STG, STG2 = Cfg<64>::STG;
+    static_assert(2 * STG2 <= STG, "the small tiles' stages fit in the big tiles' ones");
+    __shared__ __align__(16) int8_t a0[STG], a1[STG], b0[STG], b1[STG];
+    __shared__ __align__(16) int8_t eall[2 * EBYTES];
+    __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    persist_tiles<128, W4, G>(pb, a0, a1, b0, b1, eall, cbuf);
+    __syncthreads();  // every wave is done with the big tiles' LDS
+    persist_tiles<64, W4, G>(ps, a0, a1, b0, b1, eall, cbuf);
+}
+
 // The W4 operand expanded once into an int8 [N, K] buffer (out, row pitch K):
 // each thread turns 32 consecutive codes of one row (16 bytes, one table
 // since group % 32 == 0) into 32 int8, the same bytes the in-register path
@@ -657,6 +684,21 @@ hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int n
         else if (p.gate) hipLaunchKernelGGL((i8_gemm_persist_kernel<64, false, true>), dim3(grid), dim3(256), 0, stream, p);
         else hipLaunchKernelGGL((i8_gemm_persist_kernel<64, false, false>), dim3(grid), dim3(256), 0, stream, p);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_i8_gemm_persist_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus,
+                                        bool w4) {
+    if (pb.K != ps.K || pb.K % (2 * BK) != 0 || pb.K < 2 * BK) return hipErrorInvalidValue;
+    if (w4 && (pb.ldb % 16 != 0 || ((uintptr_t)pb.B & 15) != 0 || (!pb.w4_signed && (pb.group_shift < 7 || !pb.lut))))
+        return hipErrorInvalidValue;
+    if (w4 && pb.gate) return hipErrorInvalidValue;
+    const int big = ((pb.M + 255) / 256) * ((pb.N + 255) / 256), small = ((ps.M + 127) / 128) * ((ps.N + 127) / 128);
+    const int most = big > small ? big : small;
+    const int grid = most < num_cus ? most : num_cus;
+    if (w4) hipLaunchKernelGGL((i8_gemm_persist_mixed_kernel<true, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    else if (pb.gate) hipLaunchKernelGGL((i8_gemm_persist_mixed_kernel<false, true>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    else hipLaunchKernelGGL((i8_gemm_persist_mixed_kernel<false, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
     return hipGetLastError();
 }
 
