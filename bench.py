@@ -108,8 +108,16 @@ def cpu_baseline(cfg) -> dict | None:
         secs = time.perf_counter() - t0
         kind = "port"
     tops = 2.0 * rows * N * K / secs / 1e12
-    return {"value": tops, "unit": "TOPS", "cores": 1, "kind": kind,
-            "sample": f"{rows} of {M} rows x N={N} x K={K} (naive loop is linear in M), {secs:.2f} s"}
+    out = {"value": tops, "unit": "TOPS", "cores": 1, "kind": kind,
+           "sample": f"{rows} of {M} rows x N={N} x K={K} (naive loop is linear in M), {secs:.2f} s"}
+    if kind == "reference":
+        # The same rows over the host's cores (one row per task from a shared
+        # counter, as the reference's parallel_for), at most 16: the GPU box's share.
+        threads = max(1, min(16, os.cpu_count() or 1))
+        mt = oracle.ref_bench_q8_mt(M, N, K, rows, threads)
+        out["parallel"] = {"value": 2.0 * rows * N * K / mt / 1e12, "unit": "TOPS", "cores": threads,
+                           "seconds": round(mt, 3)}
+    return out
 
 
 def bench_w8a8(cfg, steps, warmup):

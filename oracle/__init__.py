@@ -373,3 +373,8 @@ def ref_w4a4pack(w):
 def ref_bench_q8(M, N, K, rows) -> float:
     """Seconds the reference CPU path takes for ``rows`` rows of an MxNxK linear."""
     return float(_ref_run(["bench_q8", M, N, K, rows]).split()[0])
+
+
+def ref_bench_q8_mt(M, N, K, rows, threads) -> float:
+    """The same rows spread over ``threads`` threads, one row per task."""
+    return float(_ref_run(["bench_q8_mt", M, N, K, rows, threads]).split()[0])

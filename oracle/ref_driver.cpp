@@ -14,7 +14,12 @@
 //   phiref w6 ROWS K GROUP HAS_CORR codes.u8 srel.f32 sch.f32 corr.f32 out.f32
 //   phiref w4a4pack ROWS COLS w.f32 packed.u8 scales.f32   (quantize_convrot_w4a4, group 256)
 //   phiref bench_q8 M N K ROWS_TIMED       (prints seconds for ROWS_TIMED rows)
+//   phiref bench_q8_mt M N K ROWS_TIMED THREADS
+//        the same rows spread over THREADS threads, one row per task from a
+//        shared counter (the shape of core/kernels/parallel_for.hpp:44-65)
+#include <atomic>
 #include <chrono>
+#include <thread>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -152,6 +157,36 @@ int main(int argc, char** argv) {
             const auto t0 = std::chrono::steady_clock::now();
             QuantInt8 qa = quantize_activation(x.data(), rows, K, spec_of(true));
             gemm_int8(qa.q.data(), qa.scale.data(), w.data(), sw.data(), rows, N, K, y.data());
+            const auto t1 = std::chrono::steady_clock::now();
+            double chk = 0;
+            for (float v : y) chk += v;
+            printf("%.6f %.6e\n", std::chrono::duration<double>(t1 - t0).count(), chk);
+        } else if (op == "bench_q8_mt" && argc == 7) {
+            const i64 M = atoll(argv[2]), N = atoll(argv[3]), K = atoll(argv[4]);
+            const i64 rows = std::min<i64>(M, atoll(argv[5]));
+            const int threads = std::max(1, atoi(argv[6]));
+            std::mt19937 rng(0);
+            std::normal_distribution<float> nd(0.0f, 1.0f);
+            std::uniform_int_distribution<int> ud(-127, 127);
+            std::vector<float> x((size_t)(rows * K));
+            for (auto& v : x) v = nd(rng);
+            std::vector<int8_t> w((size_t)(N * K));
+            for (auto& v : w) v = (int8_t)ud(rng);
+            std::vector<float> sw((size_t)N, 0.002f), y((size_t)(rows * N));
+            std::atomic<i64> next{0};
+            auto worker = [&] {
+                for (;;) {
+                    const i64 r = next.fetch_add(1, std::memory_order_relaxed);
+                    if (r >= rows) break;
+                    QuantInt8 qa = quantize_activation(x.data() + r * K, 1, K, spec_of(true));
+                    gemm_int8(qa.q.data(), qa.scale.data(), w.data(), sw.data(), 1, N, K, y.data() + r * N);
+                }
+            };
+            const auto t0 = std::chrono::steady_clock::now();
+            std::vector<std::thread> pool;
+            for (int t = 1; t < threads; t++) pool.emplace_back(worker);
+            worker();
+            for (auto& th : pool) th.join();
             const auto t1 = std::chrono::steady_clock::now();
             double chk = 0;
             for (float v : y) chk += v;
