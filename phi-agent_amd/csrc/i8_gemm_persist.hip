@@ -61,6 +61,13 @@ constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_R = 0x020, SG_DSR = 0x10
 // the A and B strips the XCD's other tiles are still reading.
 constexpr int kStoreNT = 2;
 
+// Offset of a store that must not land (a column past N): beyond any tile
+// buffer's range (those stay below 2^31 bytes), so the range check drops it.
+// Every epilogue store is issued, none is branched around: the epilogue has
+// no per-store blocks, and the number of memory operations it issues is
+// fixed, which the first wait of the next tile counts on.
+constexpr int kDropOffset = (int)0x80000000u;
+
 #ifndef W4_Q1
 #define W4_Q1 1
 #endif
@@ -83,6 +90,19 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 }
 
 __device__ __forceinline__ int swz8(int row, int c) { return c ^ ((row >> 1) & 7); }
+
+// An LDS pointer the compiler cannot fold into a constant address.  A ds_read
+// takes a 16-bit immediate offset: when the B stages sit above 64 KB, a known
+// base plus the block offset does not fit it, and each of a quarter's reads
+// would get an address register of its own (32 for the 256 x 256 tile, live
+// through the main loop).  With the base opaque, the stage and block offsets
+// stay immediates on one register per quarter.
+__device__ __forceinline__ int8_t* opaque_lds(int8_t* p) {
+    typedef __attribute__((address_space(3))) int8_t lds_i8;
+    uint32_t a = (uint32_t)(uintptr_t)(lds_i8*)p;
+    asm volatile("" : "+s"(a));
+    return (int8_t*)(lds_i8*)(uintptr_t)a;
+}
 
 __device__ __forceinline__ int xcd_remap(int pid, int nblocks) {
     const int xcd = pid & 7, idx = pid >> 3;
@@ -228,10 +248,14 @@ template <int WT, int S, bool EPI, bool W4, bool G>
 __device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int DL = Cfg<WT>::DL;
     const int koff = kl * BK;
+    // The LDS destinations (M0) come from bases made opaque here, one scalar
+    // add per load: hoisted out of the loop, the 2 x 2 DL destinations would
+    // hold as many SGPRs through it.
+    int8_t* dA = opaque_lds(w.la[S] + w.wave * (DL * 1024));
 #pragma unroll
     for (int j = 0; j < DL; j++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(w.la[S] + w.wave * (DL * 1024) + j * 1024), 16,
-                                                 w.voA[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.lda, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(dA + j * 1024), 16, w.voA[j & 1],
+                                                 koff + (w.wave * DL * 8 + j * 8) * (int)p.lda, 0, 0);
     if constexpr (W4) {
 #pragma unroll
         for (int q = 0; q < W4Regs<WT>::C; q++)
@@ -239,10 +263,11 @@ __device__ __forceinline__ void issue(const Wv& w, const GemmParams& p, int kl, 
         r.t = p.w4_signed ? signed_nibble_table()
                           : __builtin_amdgcn_raw_buffer_load_b128(w.rL, w.voL, ((kl * BK) >> p.group_shift) * 16, 0);
     } else {
+        int8_t* dB = opaque_lds(w.lb[S] + w.wave * (DL * 1024));
 #pragma unroll
         for (int j = 0; j < DL; j++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(w.lb[S] + w.wave * (DL * 1024) + j * 1024), 16,
-                                                     w.voB[j & 1], koff + (w.wave * DL * 8 + j * 8) * (int)p.ldb, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(dB + j * 1024), 16, w.voB[j & 1],
+                                                     koff + (w.wave * DL * 8 + j * 8) * (int)p.ldb, 0, 0);
     }
     if constexpr (EPI) issue_epi<WT, G>(w, p, le);
 }
@@ -281,13 +306,19 @@ __device__ __forceinline__ void zero_acc(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB]) 
         for (int i = 0; i < NB; i++) acc[j][i] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 }
 
-template <int WT>
+// MFMAs Q0 .. Q1-1 of the NB x NB block (column block j = q / NB outer).
+// Z: the tile's first MFMAs, which start the accumulators from an inline 0
+// instead of reading them (no zeroing of 16 NB^2 AGPRs per tile).
+template <int WT, int Q0 = 0, int Q1 = Cfg<WT>::NB * Cfg<WT>::NB, bool Z = false>
 __device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB]) {
     constexpr int NB = Cfg<WT>::NB;
 #pragma unroll
-    for (int q = 0; q < NB * NB; q++) {
+    for (int q = Q0; q < Q1; q++) {
         const int j = q / NB, i = q % NB;
-        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[j][i], 0, 0, 0);
+        if constexpr (Z)
+            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], v16i{}, 0, 0, 0);
+        else
+            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[j][i], 0, 0, 0);
     }
 }
 
@@ -295,13 +326,14 @@ __device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[Cfg<WT>::NB][
 // of stage SN into nxt; with LOADS the cursor's K-step into stage S.  The
 // first MFMA goes ahead of the reads because the compiler's wait for cur is
 // a full lgkmcnt(0) that must not cover reads issued after it.
-template <int WT, int S, int SN, int QN, bool LOADS, bool EPI, bool W4, bool G, int X0, int X1>
+template <int WT, int S, int SN, int QN, bool LOADS, bool EPI, bool W4, bool G, int X0, int X1, bool Z = false>
 __device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB],
                                         const Wv& w, const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int NB = Cfg<WT>::NB, DL = Cfg<WT>::DL;
-    mma<WT>(cur, acc);
+    mma<WT, 0, 1, Z>(cur, acc);
     if constexpr (LOADS) issue<WT, S, EPI, W4, G>(w, p, kl, le, r);
     frag<WT, SN, QN>(nxt, w);
+    mma<WT, 1, NB * NB, Z>(cur, acc);
     if constexpr (X1 > X0) {
         // Chunks [X0, X1) of the previous step's codes into the other stage,
         // spread between the MFMAs (about 38 VALU ops and one LDS write each).
@@ -346,36 +378,39 @@ __device__ __forceinline__ void quarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i
 // refills with K-step kl of the cursor's tile (EPI: epilogue operands into le).
 // W4: the codes loaded by the previous step are expanded into stage S^1 over
 // quarters 1-3, before the barrier that hands that stage to the next step.
-template <int WT, int S, bool EPI, bool W4, bool G>
+// Z: the tile's first K-step (its first quarter starts the accumulators).
+// VW: memory operations the wait before the barrier may leave in flight
+// (the first K-step after an epilogue: that epilogue's stores, issued after
+// the loads it waits for; memory operations complete in issue order).
+template <int WT, int S, bool EPI, bool W4, bool G, bool Z = false, int VW = 0>
 __device__ __forceinline__ void step(Frag<WT>& f0, v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const Wv& w,
                                      const GemmParams& p, int kl, int8_t* le, W4Regs<WT>& r) {
     constexpr int X = W4 ? 2 * W4Regs<WT>::C : 0;  // chunks to expand, over quarters 1-3
     Frag<WT> f1;
-    quarter<WT, S, S, 1, false, false, W4, G, 0, W4_Q1 * X / 3>(f0, f1, acc, w, p, kl, le, r);
+    quarter<WT, S, S, 1, false, false, W4, G, 0, W4_Q1 * X / 3, Z>(f0, f1, acc, w, p, kl, le, r);
     quarter<WT, S, S, 2, false, false, W4, G, W4_Q1 * X / 3, W4_Q1 ? 2 * X / 3 : X / 2>(f1, f0, acc, w, p, kl, le, r);
     quarter<WT, S, S, 3, false, false, W4, G, W4_Q1 ? 2 * X / 3 : X / 2, X>(f0, f1, acc, w, p, kl, le, r);
-    wait_all();
+    if constexpr (VW == 0) wait_all();
+    else wait_vm_lgkm0<VW>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     quarter<WT, S, S ^ 1, 0, true, EPI, W4, G, 0, 0>(f1, f0, acc, w, p, kl, le, r);
 }
 
-// Scaled epilogue operands of this lane's four columns starting at tile column ct.
-__device__ __forceinline__ void col_operands(const GemmParams& p, const int8_t* e, int ct, v4f& sb, v4f& bz) {
-    if (p.sb_scalar) {
-        const float v = *(const float*)(e + 1024);
-        sb = v4f{v, v, v, v};
-    } else {
-        sb = *(const v4f*)(e + 1024 + ct * 4);
-    }
-    if (p.bias_kind == BIAS_F32) {
-        bz = *(const v4f*)(e + 2048 + ct * 4);
-    } else if (p.bias_kind == BIAS_BF16) {
-        const uint2 h = *(const uint2*)(e + 2048 + ct * 2);
-        bz = v4f{bf16_to_f32(h.x & 0xffffu), bf16_to_f32(h.x >> 16), bf16_to_f32(h.y & 0xffffu), bf16_to_f32(h.y >> 16)};
-    } else {
-        bz = v4f{0.f, 0.f, 0.f, 0.f};
-    }
+// Scaled epilogue operands of this lane's four columns starting at tile
+// column ct.  The column-scale area holds one float per column: a scalar
+// scale was loaded into every slot.  The bias area holds bf16 pairs or fp32
+// words, which are zeros when there is no bias (its loads fell outside a
+// zero-length range).  Both views are read, at immediate offsets from two
+// per-lane bases, and the uniform format selects: no branch (branches here
+// split the epilogue into small blocks with waits of their own) and no
+// per-call offset for the compiler to keep live through the main loop.
+__device__ __forceinline__ void col_operands(bool bf, const int8_t* e, int ct, v4f& sb, v4f& bz) {
+    sb = *(const v4f*)(e + 1024 + ct * 4);
+    const v4f f = *(const v4f*)(e + 2048 + ct * 4);
+    const u32x2 h = *(const u32x2*)(e + 2048 + ct * 2);
+    bz = v4f{bf ? __uint_as_float(h[0] << 16) : f[0], bf ? __uint_as_float(h[0] & 0xffff0000u) : f[1],
+             bf ? __uint_as_float(h[1] << 16) : f[2], bf ? __uint_as_float(h[1] & 0xffff0000u) : f[3]};
 }
 
 // Epilogue of logical tile t (operands in the LDS area e).  Lane l holds row
@@ -396,6 +431,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
     tile_mn(s, t, tm, tn);
     const int m0 = tm * BM, n0 = tn * BM;
     const int esz = p.c_kind == C_BF16 ? 2 : 4;
+    const bool bf = p.bias_kind == BIAS_BF16;
     const int pitch = (int)p.ldc * esz;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (int8_t*)p.C + (int64_t)m0 * pitch, (short)0, min(BM, p.M - m0) * pitch, kRsrcWord3);
@@ -412,7 +448,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
             for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                 for (int g = 0; g < 4; g++)
-                    col_operands(p, e, w.wn * WT + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
+                    col_operands(bf, e, w.wn * WT + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
 #pragma unroll
             for (int i = 0; i < NB; i++) {
 #pragma unroll
@@ -436,9 +472,8 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
                     const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
                     const u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
                     const int col = colw + jp * 64 + sl * 8;
-                    if (col < p.N)
-                        __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * WT + i * 32 + r) * pitch + col * 2, 0,
-                                                               kStoreNT);
+                    const int off = col < p.N ? (w.wm * WT + i * 32 + r) * pitch + col * 2 : kDropOffset;
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -456,7 +491,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
         v4f sb[4], bz[4];
         if (p.c_kind == C_F32) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) col_operands(p, e, w.wn * WT + j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
+            for (int g = 0; g < 4; g++) col_operands(bf, e, w.wn * WT + j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
@@ -497,9 +532,8 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], 
                     for (int q = 0; q < 4; q++)
                         v[q] = __float_as_uint(fmaf(__uint_as_float(v[q]), gt[q], __uint_as_float(res[tt][q])));
                 }
-                if (col < p.N)
-                    __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w.wm * WT + i * 32 + r) * pitch + col * 4, 0,
-                                                           kStoreNT);
+                const int off = col < p.N ? (w.wm * WT + i * 32 + r) * pitch + col * 4 : kDropOffset;
+                __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -518,7 +552,7 @@ __device__ __forceinline__ void persist_tiles(const GemmParams& p, int8_t* a0, i
     constexpr int NB = C::NB, DL = C::DL;
     Wv w;
     w.lane = threadIdx.x & 63;
-    w.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    w.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;  // bounded, so LDS offsets fold
     w.wm = w.wave >> 1;
     w.wn = w.wave & 1;
     w.lrow = w.lane & 31;
@@ -536,8 +570,8 @@ __device__ __forceinline__ void persist_tiles(const GemmParams& p, int8_t* a0, i
     const int ntile = (s.ntiles - r - 1) / s.G + 1;
     w.la[0] = a0;
     w.la[1] = a1;
-    w.lb[0] = b0;
-    w.lb[1] = b1;
+    w.lb[0] = opaque_lds(b0);
+    w.lb[1] = w.lb[0] + (b1 - b0);
     w.le = eall;
     w.lc = cbuf + w.wave * CHUNK;
 #pragma unroll
@@ -584,8 +618,17 @@ __device__ __forceinline__ void persist_tiles(const GemmParams& p, int8_t* a0, i
     for (int i = 0;;) {
         const int t = r + i * s.G;
         int8_t* le = w.le + (i & 1) * EBYTES;
-        zero_acc<WT>(acc);
-        for (int k = 0; k < s.KT - 2; k += 2) {
+        if (s.KT > 2) {
+            // The first pair.  After an epilogue, its first wait leaves that
+            // epilogue's stores in flight: 2 NB^2 a wave on the bf16 path, the
+            // fewest of any output path (every store is issued, none skipped).
+            if (i > 0) step<WT, 0, false, W4, G, true, 2 * NB * NB>(f0, acc, w, p, 2, le, w4r);
+            else step<WT, 0, false, W4, G, true>(f0, acc, w, p, 2, le, w4r);
+            step<WT, 1, false, W4, G>(f0, acc, w, p, 3, le, w4r);
+        } else {
+            zero_acc<WT>(acc);
+        }
+        for (int k = 2; k < s.KT - 2; k += 2) {
             step<WT, 0, false, W4, G>(f0, acc, w, p, k + 2, le, w4r);
             step<WT, 1, false, W4, G>(f0, acc, w, p, k + 3, le, w4r);
         }
