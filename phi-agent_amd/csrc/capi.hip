@@ -195,6 +195,11 @@ int64_t big_tile_rows(int64_t M, int64_t N, int G) {
 hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p, GemmKernel gk, bool w4, int c_dtype,
                                int64_t ldc) {
     const int G = num_cus();
+    // int8 B runs on the four-stage pipeline; PHI_GEMM_PIPE=0 selects the
+    // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
+    // runs on the two-stage kernel.
+    const char* pe = getenv("PHI_GEMM_PIPE");
+    const bool pipe = !w4 && !(pe && pe[0] == '0');
     const int64_t M = p.M;
     const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, p.N, G) : gk == GK_PERSIST256 ? M : 0;
     phi_dev::GemmParams q = p;
@@ -208,16 +213,18 @@ hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p,
         if (!(e && e[0] == '0')) {
             phi_dev::GemmParams b = p;
             b.M = (int)rows;
-            return phi_dev::launch_i8_gemm_persist_mixed(stream, b, q, G, w4);
+            return pipe ? phi_dev::launch_i8_gemm_pipe_mixed(stream, b, q, G)
+                        : phi_dev::launch_i8_gemm_persist_mixed(stream, b, q, G, w4);
         }
     }
     if (rows > 0) {
         phi_dev::GemmParams b = p;
         b.M = (int)rows;
-        const hipError_t e = phi_dev::launch_i8_gemm_persist(stream, b, G, 128, w4);
+        const hipError_t e = pipe ? phi_dev::launch_i8_gemm_pipe(stream, b, G, 128)
+                                  : phi_dev::launch_i8_gemm_persist(stream, b, G, 128, w4);
         if (e != hipSuccess || rows == M) return e;
     }
-    return phi_dev::launch_i8_gemm_persist(stream, q, G, 64, w4);
+    return pipe ? phi_dev::launch_i8_gemm_pipe(stream, q, G, 64) : phi_dev::launch_i8_gemm_persist(stream, q, G, 64, w4);
 }
 
 // Vector-store / vector-load eligibility of the epilogue operands.

@@ -49,6 +49,10 @@ hipError_t launch_i8_gemm_persist(hipStream_t stream, const GemmParams& p, int n
 // 128 x 128 tiles (same K, B, sB, bias; the caller offsets A, sA and C).
 hipError_t launch_i8_gemm_persist_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus,
                                         bool w4);
+// The same contract without W4, on the four-stage 64-deep pipeline
+// (i8_gemm_pipe.hip).
+hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile);
+hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus);
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);
 

@@ -38,36 +38,15 @@
 //     tile-rows at a time, so its concurrent tiles share A and B in its L2.
 #include "device_common.hpp"
 #include "i8_gemm.hpp"
+#include "persist_common.hpp"
 
 namespace phi_dev {
 
 namespace {
 
-typedef __attribute__((address_space(3))) void* lptr_t;
-typedef unsigned int u32x2 __attribute__((__vector_size__(2 * sizeof(unsigned int))));
-typedef unsigned int u32x4 __attribute__((__vector_size__(4 * sizeof(unsigned int))));
-
-// Raw buffer resource word 3 for gfx9-family: 32-bit data format, no swizzle.
-constexpr int kRsrcWord3 = 0x00020000;
+using namespace persist;
 
 constexpr int BK = 128;
-constexpr int EBYTES = 4 * 1024;  // per parity: sa | sb | bias | gate (4 waves x 256 B each)
-constexpr int CHUNK = 4096;       // per-wave epilogue staging
-
-constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_R = 0x020, SG_DSR = 0x100, SG_DSW = 0x200;
-
-// Cache policy of the output stores: non-temporal.  The output is written
-// once and never read back by this kernel; letting it allocate in L2 evicts
-// the A and B strips the XCD's other tiles are still reading.
-constexpr int kStoreNT = 2;
-
-// Offset of a store that must not land (a column past N): beyond any tile
-// buffer's range (those stay below 2^31 bytes), so the range check drops it.
-// Every epilogue store is issued, none is branched around: the epilogue has
-// no per-store blocks, and the number of memory operations it issues is
-// fixed, which the first wait of the next tile counts on.
-constexpr int kDropOffset = (int)0x80000000u;
-
 #ifndef W4_Q1
 #define W4_Q1 1
 #endif
@@ -80,49 +59,7 @@ struct Cfg {
     static constexpr int DL = STG / 1024 / 4;  // loads per operand per wave per K-step
 };
 
-// s_waitcnt vmcnt(0) lgkmcnt(0) (gfx9 encoding; expcnt untouched).
-__device__ __forceinline__ void wait_all() { __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (0 << 8)); }
-// s_waitcnt vmcnt(N) lgkmcnt(0).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | (((N >> 4) & 3) << 14));
-}
-
 __device__ __forceinline__ int swz8(int row, int c) { return c ^ ((row >> 1) & 7); }
-
-// An LDS pointer the compiler cannot fold into a constant address.  A ds_read
-// takes a 16-bit immediate offset: when the B stages sit above 64 KB, a known
-// base plus the block offset does not fit it, and each of a quarter's reads
-// would get an address register of its own (32 for the 256 x 256 tile, live
-// through the main loop).  With the base opaque, the stage and block offsets
-// stay immediates on one register per quarter.
-__device__ __forceinline__ int8_t* opaque_lds(int8_t* p) {
-    typedef __attribute__((address_space(3))) int8_t lds_i8;
-    uint32_t a = (uint32_t)(uintptr_t)(lds_i8*)p;
-    asm volatile("" : "+s"(a));
-    return (int8_t*)(lds_i8*)(uintptr_t)a;
-}
-
-__device__ __forceinline__ int xcd_remap(int pid, int nblocks) {
-    const int xcd = pid & 7, idx = pid >> 3;
-    const int base = nblocks >> 3, rem = nblocks & 7;
-    return xcd < rem ? xcd * (base + 1) + idx : rem * (base + 1) + (xcd - rem) * base + idx;
-}
-
-struct Shape {
-    int tiles_m, tiles_n, ntiles, KT, group_m, G;
-};
-
-__device__ __forceinline__ void tile_mn(const Shape& s, int logical, int& tm, int& tn) {
-    const int per_group = s.group_m * s.tiles_n;
-    const int gid = logical / per_group;
-    const int first_m = gid * s.group_m;
-    const int gsz = min(s.tiles_m - first_m, s.group_m);
-    const int in_group = logical - gid * per_group;
-    tm = first_m + in_group % gsz;
-    tn = in_group / gsz;
-}
 
 template <int WT>
 struct Frag {
@@ -172,17 +109,14 @@ __device__ __forceinline__ v4i expand16b(uint32_t c0, uint32_t c1, const u32x4& 
 // Per-wave state.  The load cursor is the tile whose K-steps are being
 // loaded: it moves to the workgroup's next tile during a tile's last K-step
 // pair; after the last tile it reloads that tile's last pair (harmless).
-struct Wv {
+struct Wv : EpiWave {
     int8_t* la[2];
     int8_t* lb[2];
-    int8_t* le;  // two 3 KB epilogue-operand areas, one per tile parity
-    int8_t* lc;
+    int8_t* le;                     // two epilogue-operand areas, one per tile parity
     __amdgpu_buffer_rsrc_t rA, rB;  // the load cursor's tile (W4: rB over the codes)
     __amdgpu_buffer_rsrc_t rL;      // W4: the cursor's tile's table rows
-    int cm0, cn0;
     int voA[2], voB[2];
     int w4row, w4half, vo4, voL;    // W4: this thread's B row, half, code and table offsets
-    int wave, wm, wn, lane, lrow, lhalf;
     int oA[4], oB[4];
 };
 
@@ -204,40 +138,6 @@ __device__ __forceinline__ void cursor_tile(Wv& w, const GemmParams& p, const Sh
             w.rL = __builtin_amdgcn_make_buffer_rsrc((void*)(p.lut + (int64_t)n0 * lrow), (short)0, cols * lrow,
                                                      kRsrcWord3);
         }
-    }
-}
-
-// Epilogue operands of the cursor's tile into LDS area le: wave w loads row
-// scales 64w..64w+63, column scales / fp32 bias 64w..64w+63 and (waves 0-1)
-// the bf16 bias words; past M or N (or the tile) they read as zero.
-template <int WT, bool G>
-__device__ __forceinline__ void issue_epi(const Wv& w, const GemmParams& p, int8_t* le) {
-    constexpr int BM = Cfg<WT>::BM;
-    const int rows = min(BM, p.M - w.cm0), cols = min(BM, p.N - w.cn0);
-    const __amdgpu_buffer_rsrc_t rSA =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(p.sA ? p.sA + w.cm0 : (const float*)p.A), (short)0,
-                                          p.sA ? rows * 4 : 0, kRsrcWord3);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rSA, (lptr_t)(le + w.wave * 256), 4, w.lane * 4, w.wave * 256, 0, 0);
-    const bool sbs = p.sb_scalar != 0;
-    const __amdgpu_buffer_rsrc_t rSB = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.sB ? (sbs ? p.sB : p.sB + w.cn0) : (const float*)p.A), (short)0, p.sB ? (sbs ? 4 : cols * 4) : 0,
-        kRsrcWord3);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rSB, (lptr_t)(le + 1024 + w.wave * 256), 4, sbs ? 0 : w.lane * 4,
-                                             sbs ? 0 : w.wave * 256, 0, 0);
-    const int bsz = p.bias_kind == BIAS_F32 ? 4 : 2;
-    const __amdgpu_buffer_rsrc_t rBZ = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.bias_kind != BIAS_NONE ? (const int8_t*)p.bias + (int64_t)w.cn0 * bsz : (const int8_t*)p.A), (short)0,
-        p.bias_kind != BIAS_NONE ? cols * bsz : 0, kRsrcWord3);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rBZ, (lptr_t)(le + 2048 + w.wave * 256), 4, w.lane * 4,
-                                             w.wave * 256, 0, 0);
-    // G (the gated-residual instantiation): the gate, without a branch (a
-    // branch here would split the tile's last K-step pair, whose loads and
-    // MFMAs are scheduled as one block).
-    if constexpr (G) {
-        const __amdgpu_buffer_rsrc_t rG =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(p.gate + w.cn0), (short)0, cols * 4, kRsrcWord3);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rG, (lptr_t)(le + 3072 + w.wave * 256), 4, w.lane * 4,
-                                                 w.wave * 256, 0, 0);
     }
 }
 
@@ -395,149 +295,6 @@ __device__ __forceinline__ void step(Frag<WT>& f0, v16i (&acc)[Cfg<WT>::NB][Cfg<
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     quarter<WT, S, S ^ 1, 0, true, EPI, W4, G, 0, 0>(f1, f0, acc, w, p, kl, le, r);
-}
-
-// Scaled epilogue operands of this lane's four columns starting at tile
-// column ct.  The column-scale area holds one float per column: a scalar
-// scale was loaded into every slot.  The bias area holds bf16 pairs or fp32
-// words, which are zeros when there is no bias (its loads fell outside a
-// zero-length range).  Both views are read, at immediate offsets from two
-// per-lane bases, and the uniform format selects: no branch (branches here
-// split the epilogue into small blocks with waits of their own) and no
-// per-call offset for the compiler to keep live through the main loop.
-__device__ __forceinline__ void col_operands(bool bf, const int8_t* e, int ct, v4f& sb, v4f& bz) {
-    sb = *(const v4f*)(e + 1024 + ct * 4);
-    const v4f f = *(const v4f*)(e + 2048 + ct * 4);
-    const u32x2 h = *(const u32x2*)(e + 2048 + ct * 2);
-    bz = v4f{bf ? __uint_as_float(h[0] << 16) : f[0], bf ? __uint_as_float(h[0] & 0xffff0000u) : f[1],
-             bf ? __uint_as_float(h[1] << 16) : f[2], bf ? __uint_as_float(h[1] & 0xffff0000u) : f[3]};
-}
-
-// Epilogue of logical tile t (operands in the LDS area e).  Lane l holds row
-// l % 32 of each A block and, in registers 4g..4g+3, columns 8g + 4(l/32) +
-// 0..3 of each B block.  Each 32-row strip goes through the wave's LDS area
-// (16-byte slots swizzled by row) and is stored as whole rows: bf16 in
-// 32 x 64-column pieces (128 bytes a row), fp32 / int32 in 32 x 32-column
-// pieces.
-template <int WT, bool G>
-__device__ __forceinline__ void epilogue(v16i (&acc)[Cfg<WT>::NB][Cfg<WT>::NB], const GemmParams& p, const Shape& s,
-                                         int t, const Wv& w, const int8_t* e) {
-    constexpr int NB = Cfg<WT>::NB, BM = Cfg<WT>::BM;
-#pragma unroll
-    for (int j = 0; j < NB; j++)
-#pragma unroll
-        for (int i = 0; i < NB; i++) asm volatile("" : "+a"(acc[j][i]));
-    int tm, tn;
-    tile_mn(s, t, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BM;
-    const int esz = p.c_kind == C_BF16 ? 2 : 4;
-    const bool bf = p.bias_kind == BIAS_BF16;
-    const int pitch = (int)p.ldc * esz;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (int8_t*)p.C + (int64_t)m0 * pitch, (short)0, min(BM, p.M - m0) * pitch, kRsrcWord3);
-    int8_t* lc = w.lc;
-    const int colw = n0 + w.wn * WT;  // first column of this wave
-    float sa[NB];
-#pragma unroll
-    for (int i = 0; i < NB; i++) sa[i] = *(const float*)(e + (w.wm * WT + i * 32 + w.lrow) * 4);
-    if (p.c_kind == C_BF16) {
-#pragma unroll
-        for (int jp = 0; jp < NB / 2; jp++) {
-            v4f sb[2][4], bz[2][4];
-#pragma unroll
-            for (int jj = 0; jj < 2; jj++)
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                    col_operands(bf, e, w.wn * WT + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
-#pragma unroll
-            for (int i = 0; i < NB; i++) {
-#pragma unroll
-                for (int jj = 0; jj < 2; jj++) {
-                    v16i blk = acc[2 * jp + jj][i];
-                    asm volatile("" : "+v"(blk));
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        float v[4];
-#pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            v[q] = fmaf((float)blk[4 * g + q] * sa[i], sb[jj][g][q], bz[jj][g][q]);
-                        const int slot = (jj * 4 + g) ^ (w.lrow & 7);
-                        *(u32x2*)(lc + w.lrow * 128 + slot * 16 + w.lhalf * 8) =
-                            u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
-                    }
-                }
-                // A wave's LDS accesses complete in order: these reads see its writes.
-#pragma unroll
-                for (int tt = 0; tt < 4; tt++) {
-                    const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
-                    const u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
-                    const int col = colw + jp * 64 + sl * 8;
-                    const int off = col < p.N ? (w.wm * WT + i * 32 + r) * pitch + col * 2 : kDropOffset;
-                    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        return;
-    }
-    // fp32 / int32: 32 x 32 pieces, one block at a time.  With a gate the
-    // fp32 output is the residual stream, updated in place:
-    // C = fma(v, gate[n], C), the reference's AddMul `a + b * c`
-    // (core/kernels/ops.cpp:80, applied after the projection at
-    // core/models/av_dit.cpp:1389) as NVRTC's default --fmad=true contracts it.
-    constexpr bool gated = G;
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-        v4f sb[4], bz[4];
-        if (p.c_kind == C_F32) {
-#pragma unroll
-            for (int g = 0; g < 4; g++) col_operands(bf, e, w.wn * WT + j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
-        }
-#pragma unroll
-        for (int i = 0; i < NB; i++) {
-            // The residual rows this lane stores, fetched before the conversion
-            // so their latency overlaps it.
-            u32x4 res[4];
-            if (gated) {
-#pragma unroll
-                for (int tt = 0; tt < 4; tt++) {
-                    const int r = tt * 8 + (w.lane >> 3), col = colw + j * 32 + (w.lane & 7) * 4;
-                    res[tt] = __builtin_amdgcn_raw_buffer_load_b128(rs, (w.wm * WT + i * 32 + r) * pitch + col * 4, 0, 0);
-                }
-            }
-            v16i blk = acc[j][i];
-            asm volatile("" : "+v"(blk));
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                u32x4 o;
-                if (p.c_kind == C_F32) {
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        o[q] = __float_as_uint(fmaf((float)blk[4 * g + q] * sa[i], sb[g][q], bz[g][q]));
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; q++) o[q] = (unsigned)blk[4 * g + q];
-                }
-                const int slot = (2 * g + w.lhalf) ^ (w.lrow & 7);
-                *(u32x4*)(lc + w.lrow * 128 + slot * 16) = o;
-            }
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
-                u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
-                const int col = colw + j * 32 + sl * 4;
-                if (gated) {
-                    const v4f gt = *(const v4f*)(e + 3072 + (w.wn * WT + j * 32 + sl * 4) * 4);
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        v[q] = __float_as_uint(fmaf(__uint_as_float(v[q]), gt[q], __uint_as_float(res[tt][q])));
-                }
-                const int off = col < p.N ? (w.wm * WT + i * 32 + r) * pitch + col * 4 : kDropOffset;
-                __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
 }
 
 }  // namespace

@@ -1,0 +1,407 @@
+// Persistent int8 GEMM for gfx950 with a four-stage, 64-deep K pipeline:
+// one workgroup per CU walks square output tiles (256 x 256, or 128 x 128 for
+// the rows a whole number of 256-row rounds does not cover) as the
+// two-stage kernel of i8_gemm_persist.hip does, with a different main loop.
+//
+//   acc[m,n] = sum_k A[m,k] * B[n,k]                  (exact int32)
+//   C[m,n]   = fma((float)acc * sA[m], sB[n], bias[n])  -> bf16 (RNE) / fp32 / raw int32
+//
+// The product and epilogue are those of the reference's int8_gemm_tc
+// (core/kernels/int8_gemm.cpp:466-621, epilogue :588-620) and host gemm_int8
+// (core/host/quant.cpp:223-236).
+//
+// Why this loop.  A CU moves operands into LDS at about 57 bytes a clock;
+// a 256 x 256 tile needs 64 KB of A and B per 128 K, against 64 MFMAs a wave
+// (2048 clocks).  The two-stage kernel can refill a stage only after the
+// barrier that ends its K-step, so each wave issues its 16 loads of a K-step
+// in one quarter: the load queue backs up, and the MFMAs behind the loads in
+// the wave's instruction stream wait for it.  Here:
+//   * Four stages of 64 K (A and B 2WT rows x 64 bytes each: 128 KB for the
+//     256 x 256 tile).  K-step k works on stage k % 4.
+//   * A K-step is two quarters of NB^2 MFMAs.  Quarter 0 reads the second
+//     half of the step's fragments and issues B's loads for K-step k + 3;
+//     quarter 1 reads the first fragments of K-step k + 1 and issues A's
+//     loads for K-step k + 4 into stage k % 4, which the barrier between the
+//     quarters has released.  Loads are spread DL per quarter, and data is
+//     loaded four to five quarters before it is read.
+//   * Each load instruction moves 16 rows x 64 bytes.  64-byte row pieces
+//     stream faster than whole 128-byte rows at a 3072-byte pitch (14 against
+//     8 TB/s over a 48 MB operand, measured with the same instruction).
+//   * One barrier per K-step, between its quarters, after a wait for the
+//     wave's own loads of K-step k + 1 (the four later load groups may stay
+//     in flight: memory operations complete in issue order).
+//   * The A and B load cursors move to the workgroup's next tile on their
+//     own K-steps (A at K-step KT - 4, B at KT - 3): a tile's first K-steps
+//     are loaded while it finishes.  The next tile's epilogue operands are
+//     loaded with A's first K-step.
+//   * Chunk c (16 bytes) of row r sits in slot c ^ ((r >> 2) & 3) of the
+//     row's 64 bytes: the 16-byte fragment reads of 16 consecutive rows hit
+//     16 distinct bank windows.
+// The epilogue, the tile order and the epilogue-operand loads are those of
+// persist_common.hpp.
+#include "device_common.hpp"
+#include "i8_gemm.hpp"
+#include "persist_common.hpp"
+
+namespace phi_dev {
+
+namespace {
+
+using namespace persist;
+
+constexpr int PK = 64;   // K bytes per stage
+constexpr int NSTG = 4;  // stages
+
+template <int WT>
+struct PCfg {
+    static constexpr int NB = WT / 32;         // MFMA blocks per wave dimension
+    static constexpr int BM = 2 * WT;          // workgroup tile (square)
+    static constexpr int STG = BM * PK;        // bytes per operand per stage
+    static constexpr int DL = STG / 1024 / 4;  // loads per operand per wave per K-step
+    // Epilogue stores a wave issues on the bf16 path, the fewest of any
+    // output path (every store is issued: none is branched around).
+    static constexpr int NSTORE = 2 * NB * NB;
+    // Memory operations a K-step's wait may leave in flight: the four load
+    // groups issued after K-step k + 1's last one; in a tile's first two
+    // K-steps also the previous tile's epilogue stores, issued between them.
+    static constexpr int VWN = 4 * DL;
+    static constexpr int VWR = 4 * DL + NSTORE;
+    static_assert(VWR < 64, "vmcnt is six bits");
+};
+
+template <int WT>
+struct Frag {
+    v4i a[PCfg<WT>::NB], b[PCfg<WT>::NB];
+};
+
+// The next tile of the workgroup, if any (origins precomputed once a tile).
+struct NextTile {
+    int m0, n0;
+    bool valid;
+};
+
+// Per-wave state.  Each operand has its own load cursor: a buffer resource
+// over its tile's rows and the next K-step to load.
+struct Pw : EpiWave {
+    int8_t* la;  // A stage 0, stage s at la + s * STG (opaque, so fragment
+    int8_t* lb;  // B stage 0  offsets stay immediates wherever the stages sit)
+    int8_t* le;  // two epilogue-operand areas, one per tile parity
+    __amdgpu_buffer_rsrc_t rA, rB;
+    int voA, voB;  // per-lane global offset within a 16-row load
+    int oA[2], oB[2];
+    int kA, kB;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const int8_t* base, int64_t ld, int row0, int nrows) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)row0 * ld), (short)0, nrows * (int)ld,
+                                             kRsrcWord3);
+}
+
+// DL loads of operand A's K-step w.kA into stage ST (16 rows each); then the
+// cursor advances.
+template <int WT, int ST>
+__device__ __forceinline__ void load_a(Pw& w, const GemmParams& p) {
+    constexpr int DL = PCfg<WT>::DL, STG = PCfg<WT>::STG;
+    int8_t* d = opaque_lds(w.la + ST * STG + w.wave * (DL * 1024));
+    const int koff = w.kA * PK;
+#pragma unroll
+    for (int j = 0; j < DL; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(d + j * 1024), 16, w.voA,
+                                                 koff + (w.wave * DL + j) * 16 * (int)p.lda, 0, 0);
+    w.kA++;
+}
+
+template <int WT, int ST>
+__device__ __forceinline__ void load_b(Pw& w, const GemmParams& p) {
+    constexpr int DL = PCfg<WT>::DL, STG = PCfg<WT>::STG;
+    int8_t* d = opaque_lds(w.lb + ST * STG + w.wave * (DL * 1024));
+    const int koff = w.kB * PK;
+#pragma unroll
+    for (int j = 0; j < DL; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(d + j * 1024), 16, w.voB,
+                                                 koff + (w.wave * DL + j) * 16 * (int)p.ldb, 0, 0);
+    w.kB++;
+}
+
+// Cursor switches at a tile's end: to the next tile's K-step 0, or, after
+// the last tile, back to K-step 0 of the same tile (those loads land in
+// released stages and are never read).
+template <int WT>
+__device__ __forceinline__ void switch_a(Pw& w, const GemmParams& p, const NextTile& nt) {
+    constexpr int BM = PCfg<WT>::BM;
+    if (nt.valid) {
+        w.rA = rows_rsrc(p.A, p.lda, nt.m0, min(BM, p.M - nt.m0));
+        w.cm0 = nt.m0;
+        w.cn0 = nt.n0;
+    }
+    w.kA = 0;
+}
+
+template <int WT>
+__device__ __forceinline__ void switch_b(Pw& w, const GemmParams& p, const NextTile& nt) {
+    constexpr int BM = PCfg<WT>::BM;
+    if (nt.valid) w.rB = rows_rsrc(p.B, p.ldb, nt.n0, min(BM, p.N - nt.n0));
+    w.kB = 0;
+}
+
+template <int WT, int ST, int Q>
+__device__ __forceinline__ void frag(Frag<WT>& f, const Pw& w) {
+    constexpr int NB = PCfg<WT>::NB, STG = PCfg<WT>::STG;
+    const int8_t* cA = w.la + ST * STG + w.oA[Q];
+    const int8_t* cB = w.lb + ST * STG + w.oB[Q];
+#pragma unroll
+    for (int i = 0; i < NB; i++) f.a[i] = *(const v4i*)(cA + i * 32 * PK);
+#pragma unroll
+    for (int j = 0; j < NB; j++) f.b[j] = *(const v4i*)(cB + j * 32 * PK);
+}
+
+// MFMAs Q0 .. Q1-1 of the NB x NB block (column block j = q / NB outer).
+// Z: the tile's first MFMAs, which start the accumulators from an inline 0.
+template <int WT, int Q0, int Q1, bool Z>
+__device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB]) {
+    constexpr int NB = PCfg<WT>::NB;
+#pragma unroll
+    for (int q = Q0; q < Q1; q++) {
+        const int j = q / NB, i = q % NB;
+        if constexpr (Z)
+            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], v16i{}, 0, 0, 0);
+        else
+            acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.b[j], f.a[i], acc[j][i], 0, 0, 0);
+    }
+}
+
+// Places a quarter's R fragment reads and V loads between the NB^2 - 1
+// MFMAs after its first.  The reads go one a slot from the first (the next
+// quarter's first MFMAs need them: issued late, their latency would show);
+// the loads are spread over all slots, slot T taking those that bring the
+// running total to (T + 1) / (NB^2 - 1) of V.
+template <int NB, int R, int V, int T = 0>
+__device__ __forceinline__ void sched_quarter() {
+    constexpr int SLOTS = NB * NB - 1;
+    if constexpr (T < SLOTS) {
+        constexpr int r = R <= SLOTS ? (T < R ? 1 : 0) : (T + 1) * R / SLOTS - T * R / SLOTS;
+        constexpr int v = (T + 1) * V / SLOTS - T * V / SLOTS;
+        if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(SG_DSR, r, 0);
+        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, v, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+        sched_quarter<NB, R, V, T + 1>();
+    }
+}
+
+// A quarter: NB^2 MFMAs on cur, the fragment reads of (stage SR, half QR)
+// into nxt, and the loads issued by ld (V memory operations).  The first
+// MFMA goes ahead of the reads: the wait the compiler puts before it covers
+// cur's reads, which must not include reads issued after it.
+template <int WT, int SR, int QR, int V, bool Z, typename Ld>
+__device__ __forceinline__ void pquarter(const Frag<WT>& cur, Frag<WT>& nxt, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB],
+                                         Pw& w, Ld&& ld) {
+    constexpr int NB = PCfg<WT>::NB;
+    mma<WT, 0, 1, Z>(cur, acc);
+    ld();
+    frag<WT, SR, QR>(nxt, w);
+    mma<WT, 1, NB * NB, Z>(cur, acc);
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    sched_quarter<NB, 2 * NB, V>();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// K-step k on stage S = k % 4.  f0 holds the step's first-half fragments on
+// entry and the next step's on return.  Z: the tile's first K-step.  VW: the
+// wait's allowance.  SWA / SWB: the A / B cursor moves to the next tile
+// before its loads here (SWA also loads that tile's epilogue operands into
+// area ln).
+template <int WT, int S, bool Z, int VW, bool SWA, bool SWB, bool G>
+__device__ __forceinline__ void pstep(Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB], Pw& w,
+                                      const GemmParams& p, const NextTile& nt, int8_t* ln) {
+    constexpr int DL = PCfg<WT>::DL;
+    constexpr int NE = G ? 4 : 3;  // epilogue-operand loads
+    Frag<WT> f1;
+    pquarter<WT, S, 1, DL, Z>(f0, f1, acc, w, [&] {
+        if constexpr (SWB) switch_b<WT>(w, p, nt);
+        load_b<WT, (S + 3) % NSTG>(w, p);
+    });
+    wait_vm_lgkm0<VW>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    pquarter<WT, (S + 1) % NSTG, 0, DL + (SWA ? NE : 0), false>(f1, f0, acc, w, [&] {
+        if constexpr (SWA) {
+            switch_a<WT>(w, p, nt);
+            issue_epi<WT, G>(w, p, ln);
+        }
+        load_a<WT, S>(w, p);
+    });
+}
+
+template <int WT>
+__device__ __forceinline__ NextTile next_tile(const Shape& s, const GemmParams& p, int t, bool valid) {
+    NextTile nt{0, 0, valid};
+    if (valid) {
+        int tm, tn;
+        tile_mn(s, t, tm, tn);
+        nt.m0 = tm * PCfg<WT>::BM;
+        nt.n0 = tn * PCfg<WT>::BM;
+    }
+    return nt;
+}
+
+// The persistent loop over this workgroup's tiles of p, on four A stages at
+// la and four B stages at lb (STG bytes each), the epilogue-operand areas
+// eall and the epilogue staging cbuf.  K % 256 == 0.  Returns at once when
+// the workgroup has no tile.
+template <int WT, bool G>
+__device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8_t* lb, int8_t* eall, int8_t* cbuf) {
+    using C = PCfg<WT>;
+    constexpr int NB = C::NB, DL = C::DL, BM = C::BM;
+    Pw w;
+    w.lane = threadIdx.x & 63;
+    w.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+    w.wm = w.wave >> 1;
+    w.wn = w.wave & 1;
+    w.lrow = w.lane & 31;
+    w.lhalf = w.lane >> 5;
+    Shape s;
+    s.tiles_m = (p.M + BM - 1) / BM;
+    s.tiles_n = (p.N + BM - 1) / BM;
+    s.ntiles = s.tiles_m * s.tiles_n;
+    s.KT = p.K / PK;
+    s.group_m = p.group_m;
+    s.G = gridDim.x;
+    const int r = xcd_remap(blockIdx.x, s.G);
+    if (r >= s.ntiles) return;
+    const int ntile = (s.ntiles - r - 1) / s.G + 1;
+    w.la = opaque_lds(la);
+    w.lb = opaque_lds(lb);
+    w.le = eall;
+    w.lc = cbuf + w.wave * CHUNK;
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int c = (2 * q + w.lhalf) ^ ((w.lrow >> 2) & 3);
+        w.oA[q] = (w.wm * WT + w.lrow) * PK + c * 16;
+        w.oB[q] = (w.wn * WT + w.lrow) * PK + c * 16;
+    }
+    // A load covers 16 rows: lane l writes row l / 4, slot l % 4, and fetches
+    // the chunk that belongs in that slot.
+    {
+        const int row = w.lane >> 2, c = (w.lane & 3) ^ ((row >> 2) & 3);
+        w.voA = row * (int)p.lda + c * 16;
+        w.voB = row * (int)p.ldb + c * 16;
+    }
+    // Prologue: the first tile's K-steps 0-2 and A of K-step 3, with its
+    // epilogue operands; then NSTORE stores that land nowhere (offsets
+    // outside a zero-length range), standing where a previous tile's
+    // epilogue stores would stand, so every tile's first waits count alike.
+    const NextTile first = next_tile<WT>(s, p, r, true);
+    w.rA = rows_rsrc(p.A, p.lda, first.m0, min(BM, p.M - first.m0));
+    w.rB = rows_rsrc(p.B, p.ldb, first.n0, min(BM, p.N - first.n0));
+    w.cm0 = first.m0;
+    w.cn0 = first.n0;
+    w.kA = 0;
+    w.kB = 0;
+    load_a<WT, 0>(w, p);
+    issue_epi<WT, G>(w, p, w.le);
+    load_b<WT, 0>(w, p);
+    load_a<WT, 1>(w, p);
+    load_b<WT, 1>(w, p);
+    load_a<WT, 2>(w, p);
+    load_b<WT, 2>(w, p);
+    load_a<WT, 3>(w, p);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        const __amdgpu_buffer_rsrc_t nowhere = __builtin_amdgcn_make_buffer_rsrc((void*)p.C, (short)0, 0, kRsrcWord3);
+#pragma unroll
+        for (int d = 0; d < C::NSTORE; d++)
+            __builtin_amdgcn_raw_buffer_store_b32(0u, nowhere, w.lane * 4 + d * 256, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm0<5 * DL + C::NSTORE>();  // K-step 0 and the epilogue operands have landed
+    __builtin_amdgcn_s_barrier();
+    Frag<WT> f0;
+    frag<WT, 0, 0>(f0, w);
+    v16i acc[NB][NB];
+    for (int i = 0;;) {
+        const int t = r + i * s.G;
+        int8_t* le = w.le + (i & 1) * EBYTES;
+        int8_t* ln = w.le + ((i + 1) & 1) * EBYTES;
+        const NextTile nt = next_tile<WT>(s, p, t + s.G, i + 1 < ntile);
+        constexpr int VWR = C::VWR, VWN = C::VWN;
+        if (s.KT == 4) {
+            pstep<WT, 0, true, VWR, true, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 1, false, VWR, false, true, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+        } else {
+            pstep<WT, 0, true, VWR, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 1, false, VWR, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            for (int k = 4; k < s.KT - 4; k += 4) {
+                pstep<WT, 0, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+                pstep<WT, 1, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+                pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+                pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            }
+            pstep<WT, 0, false, VWN, true, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 1, false, VWN, false, true, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+        }
+        epilogue<WT, G>(acc, p, s, t, w, le);
+        if (++i == ntile) break;
+    }
+    // Loads past the last K-step (into released stages) and the epilogue's
+    // stores are still in flight: let them land before the LDS is released.
+    wait_all();
+}
+
+template <int WT, bool G>
+__global__ __launch_bounds__(256) void i8_gemm_pipe_kernel(GemmParams p) {
+    constexpr int STG = PCfg<WT>::STG;
+    __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
+    __shared__ __align__(16) int8_t eall[2 * EBYTES];
+    __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    pipe_tiles<WT, G>(p, la, lb, eall, cbuf);
+}
+
+// Both tile sizes in one launch: the workgroup's 256 x 256 tiles of pb, then
+// its 128 x 128 tiles of ps (the rows below pb's), in the same LDS.
+template <bool G>
+__global__ __launch_bounds__(256) void i8_gemm_pipe_mixed_kernel(GemmParams pb, GemmParams ps) {
+    constexpr int STG = PCfg<128>::STG;
+    static_assert(PCfg<64>::STG <= STG, "the small tiles' stages fit in the big tiles' ones");
+    __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
+    __shared__ __align__(16) int8_t eall[2 * EBYTES];
+    __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    pipe_tiles<128, G>(pb, la, lb, eall, cbuf);
+    __syncthreads();  // every wave is done with the big tiles' LDS
+    pipe_tiles<64, G>(ps, la, lb, eall, cbuf);
+}
+
+}  // namespace
+
+hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile) {
+    if (p.K % (NSTG * PK) != 0 || p.K < NSTG * PK) return hipErrorInvalidValue;
+    if (wave_tile != 128 && wave_tile != 64) return hipErrorInvalidValue;
+    const int bm = 2 * wave_tile;
+    const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
+    const int grid = tiles < num_cus ? tiles : num_cus;
+    if (wave_tile == 128) {
+        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false>), dim3(grid), dim3(256), 0, stream, p);
+    } else {
+        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false>), dim3(grid), dim3(256), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus) {
+    if (pb.K != ps.K || pb.K % (NSTG * PK) != 0 || pb.K < NSTG * PK) return hipErrorInvalidValue;
+    const int big = ((pb.M + 255) / 256) * ((pb.N + 255) / 256), small = ((ps.M + 127) / 128) * ((ps.N + 127) / 128);
+    const int most = big > small ? big : small;
+    const int grid = most < num_cus ? most : num_cus;
+    if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    return hipGetLastError();
+}
+
+}  // namespace phi_dev
