@@ -52,15 +52,20 @@ def test_quant_rotate_mod_zero_modulation_is_plain(dev):
     assert torch.equal(q0, q1) and torch.equal(s0.view(torch.int32), s1.view(torch.int32))
 
 
-@pytest.mark.parametrize("kernel", ["auto", "persist256", "persist128"])
+@pytest.mark.parametrize("kernel", ["auto", "persist256", "persist128", "auto:2stage"])
 @pytest.mark.parametrize("bias_kind", [None, "f32", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(64, 256, 512), (300, 1000, 1024), (4352, 3072, 512),
-                                   (777, 520, 768)])
+                                   (777, 520, 768), (300, 1000, 256)])
 def test_gemm_residual_matches_epilogue_then_addmul(dev, orc, monkeypatch, kernel, bias_kind, M, N, K):
-    if kernel == "auto":
+    kern, _, variant = kernel.partition(":")
+    if kern == "auto":
         monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
     else:
-        monkeypatch.setenv("PHI_GEMM_KERNEL", kernel)
+        monkeypatch.setenv("PHI_GEMM_KERNEL", kern)
+    if variant == "2stage":
+        monkeypatch.setenv("PHI_GEMM_PIPE", "0")
+    else:
+        monkeypatch.delenv("PHI_GEMM_PIPE", raising=False)
     g = torch.Generator().manual_seed(M * 7 + N)
     A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
     B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)

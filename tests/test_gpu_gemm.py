@@ -27,16 +27,29 @@ def rand_i8(shape, seed):
     return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
 
 
-KERNELS = ["auto", "persist", "persist256", "persist128", "tile256", "tile256w4", "tile128"]
+# "<kernel>:2stage" runs the persistent plan on the two-stage kernel
+# (PHI_GEMM_PIPE=0) instead of the four-stage pipeline.
+KERNELS = ["auto", "persist", "persist256", "persist128", "persist:2stage", "persist256:2stage",
+           "persist128:2stage", "tile256", "tile256w4", "tile128"]
+
+
+def select_kernel(monkeypatch, name):
+    """The PHI_GEMM_KERNEL / PHI_GEMM_PIPE A/B switches."""
+    kern, _, variant = name.partition(":")
+    if kern == "auto":
+        monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("PHI_GEMM_KERNEL", kern)
+    if variant == "2stage":
+        monkeypatch.setenv("PHI_GEMM_PIPE", "0")
+    else:
+        monkeypatch.delenv("PHI_GEMM_PIPE", raising=False)
 
 
 @pytest.fixture(params=KERNELS)
 def kernel(request, monkeypatch):
-    """The PHI_GEMM_KERNEL A/B switch: both GEMM kernels see every shape."""
-    if request.param == "auto":
-        monkeypatch.delenv("PHI_GEMM_KERNEL", raising=False)
-    else:
-        monkeypatch.setenv("PHI_GEMM_KERNEL", request.param)
+    """Every GEMM kernel sees every shape."""
+    select_kernel(monkeypatch, request.param)
     return request.param
 
 
@@ -204,8 +217,9 @@ def test_tile_size_plans_exact(dev, monkeypatch, M, N, K):
     A = rand_i8((M, K), M + 3).to(dev)
     B = rand_i8((N, K), N + 5).to(dev)
     want = exact_product(A, B)
-    for kern in ("persist", "persist256", "persist128"):
-        monkeypatch.setenv("PHI_GEMM_KERNEL", kern)
+    for kern in ("persist", "persist256", "persist128", "persist:2stage", "persist256:2stage",
+                 "persist128:2stage"):
+        select_kernel(monkeypatch, kern)
         C = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
         torch.cuda.synchronize()
         assert torch.equal(C.to(torch.int64), want), kern
