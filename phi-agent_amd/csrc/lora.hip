@@ -234,7 +234,9 @@ __device__ __forceinline__ void rank_step(const float* __restrict__ hr, const fl
         for (int j = 0; j < 8; j++) acc[i][j] = fmaf(hv[i], bv[j], acc[i][j]);
 }
 
-template <bool CB>
+// VEC: C's rows are 16-byte (fp32) or 8-byte (bf16) aligned and N % 4 == 0,
+// so each lane moves its four adjacent columns as one access.
+template <bool CB, bool VEC>
 __global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restrict__ h, const float* __restrict__ B,
                                                             void* __restrict__ C, int64_t ldc, int M, int N, int R) {
     __shared__ __align__(16) float sh[RA_BR][RA_P];
@@ -246,6 +248,31 @@ __global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restr
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int m = m0 + ty * 8 + i;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int g = 0; g < 2; g++) {
+                const int n = n0 + g * 64 + tx * 4;
+                float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (m < M && n < N) {
+                    if (CB) {
+                        const uint2 u = *(const uint2*)((const uint16_t*)C + (int64_t)m * ldc + n);
+                        v[0] = bf16_to_f32(u.x & 0xffffu);
+                        v[1] = bf16_to_f32(u.x >> 16);
+                        v[2] = bf16_to_f32(u.y & 0xffffu);
+                        v[3] = bf16_to_f32(u.y >> 16);
+                    } else {
+                        const float4 f = *(const float4*)((const float*)C + (int64_t)m * ldc + n);
+                        v[0] = f.x;
+                        v[1] = f.y;
+                        v[2] = f.z;
+                        v[3] = f.w;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][g * 4 + e] = v[e];
+            }
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int n = n0 + (j >> 2) * 64 + tx * 4 + (j & 3);
@@ -279,6 +306,20 @@ __global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restr
     for (int i = 0; i < 8; i++) {
         const int m = m0 + ty * 8 + i;
         if (m >= M) continue;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int g = 0; g < 2; g++) {
+                const int n = n0 + g * 64 + tx * 4;
+                if (n >= N) continue;
+                const float* a = &acc[i][g * 4];
+                if (CB)
+                    *(uint2*)((uint16_t*)C + (int64_t)m * ldc + n) = make_uint2(f32x2_to_bf16x2(a[0], a[1]),
+                                                                                f32x2_to_bf16x2(a[2], a[3]));
+                else
+                    *(float4*)((float*)C + (int64_t)m * ldc + n) = make_float4(a[0], a[1], a[2], a[3]);
+            }
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int n = n0 + (j >> 2) * 64 + tx * 4 + (j & 3);
@@ -317,8 +358,14 @@ hipError_t launch_lora_down(hipStream_t stream, const void* x, bool x_bf16, int6
 hipError_t launch_lora_rank_add(hipStream_t stream, const float* h, const float* B, void* C, bool c_bf16, int64_t ldc,
                                 int M, int N, int R) {
     const dim3 grid((unsigned)((N + RA_BN - 1) / RA_BN), (unsigned)((M + RA_BM - 1) / RA_BM));
-    if (c_bf16) hipLaunchKernelGGL(lora_rank_add_kernel<true>, grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
-    else hipLaunchKernelGGL(lora_rank_add_kernel<false>, grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+    const bool vec = N % 4 == 0 && ldc % 4 == 0 && (uintptr_t)C % (c_bf16 ? 8 : 16) == 0;
+    if (c_bf16) {
+        if (vec) hipLaunchKernelGGL((lora_rank_add_kernel<true, true>), grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+        else hipLaunchKernelGGL((lora_rank_add_kernel<true, false>), grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+    } else {
+        if (vec) hipLaunchKernelGGL((lora_rank_add_kernel<false, true>), grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+        else hipLaunchKernelGGL((lora_rank_add_kernel<false, false>), grid, dim3(256), 0, stream, h, B, C, ldc, M, N, R);
+    }
     return hipGetLastError();
 }
 
