@@ -28,33 +28,37 @@ namespace phi_dev {
 
 // ---- lora_down: h [M, R] = x [M, K] . A [R, K]^T -------------------------
 // Main form (x rows 16-byte aligned, K % 64 == 0): a block owns 64 rows and
-// 4 LD_TR ranks, a wave LD_TR of the ranks and a lane one row.  LD_TR = 2 by
-// default: at 4352 x 3072 x 64 it runs in 112 us against 140 us for 4 (fewer
-// waves to cover the scalar loads' latency) and 170 us for 1 (twice the x
-// reads per fma).  The ranks are
-// wave-uniform, so their A values come through the scalar cache into SGPRs
-// and feed the fmas directly.  The rows' x values are staged 64 k at a time
-// through LDS (coalesced row loads, double-buffered), where a lane reads its
-// own row with a 65-float pitch (every lane on its own bank).
-constexpr int LD_KC = 64, LD_XP = LD_KC + 1;
+// 4 LD_TR ranks, a wave LD_TR of the ranks and a lane one row.  Each 64-k
+// chunk of the rows' x and of the waves' A slices goes global -> registers ->
+// LDS, double-buffered with one barrier a chunk, the next chunk's global
+// loads in flight under the current chunk's fmas.  A lane reads its own row
+// of x (68-float pitch: 16-byte aligned rows, conflict-free 16-byte reads and
+// writes) and its wave's A values, which all the wave's lanes read at one
+// address (a broadcast).  Earlier the A values came through the scalar cache;
+// scalar loads complete out of order, so only a full wait covers them, and
+// each 8-k step waited on a batch that missed the scalar cache.  LD_TR = 2
+// by default (PHI_LORA_TR=1 or 4 as A/B switches).
+constexpr int LD_KC = 64, LD_XP = LD_KC + 4;
 
-// The A values of TR ranks at k..k+7 (wave-uniform: scalar loads).
+// TR consecutive floats (a TR * 4-byte aligned address) to and from registers.
 template <int TR>
-__device__ __forceinline__ void load_a8(const float* const (&ar)[TR], int k, float (&av)[TR][8]) {
-#pragma unroll
-    for (int t = 0; t < TR; t++) {
-        const float4 a0 = *(const float4*)(ar[t] + k), a1 = *(const float4*)(ar[t] + k + 4);
-        av[t][0] = a0.x, av[t][1] = a0.y, av[t][2] = a0.z, av[t][3] = a0.w;
-        av[t][4] = a1.x, av[t][5] = a1.y, av[t][6] = a1.z, av[t][7] = a1.w;
+__device__ __forceinline__ void load_tr(const float* __restrict__ p, float (&v)[TR]) {
+    if constexpr (TR == 4) {
+        const float4 t = *(const float4*)p;
+        v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+    } else if constexpr (TR == 2) {
+        const float2 t = *(const float2*)p;
+        v[0] = t.x, v[1] = t.y;
+    } else {
+        v[0] = *p;
     }
 }
 
-// Scalar loads complete out of order, so their only wait is a full one.  The
-// two A operand sets alternate and this wait is placed before each set's
-// loads are issued, when it covers just the other set, so the fmas that
-// follow need no wait.
-__device__ __forceinline__ void wait_scalar_loads() {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt left open
+template <int TR>
+__device__ __forceinline__ void store_tr(float* p, const float (&v)[TR]) {
+    if constexpr (TR == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+    else if constexpr (TR == 2) *(float2*)p = make_float2(v[0], v[1]);
+    else *p = v[0];
 }
 
 // 64 rows x 64 k of x into registers: lane t holds row t / 4, k 16 (t % 4)..+15.
@@ -84,51 +88,52 @@ template <bool XB, int LD_TR>
 __global__ __launch_bounds__(256) void lora_down_rows_kernel(const void* __restrict__ x, int64_t ldx,
                                                              const float* __restrict__ A, float* __restrict__ h,
                                                              int M, int K, int R) {
-    __shared__ float sx[2][64 * LD_XP];
-    const int lane = threadIdx.x & 63;
+    __shared__ __align__(16) float sx[2][64 * LD_XP];
+    __shared__ __align__(16) float sa[2][4][LD_TR * LD_KC];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * 64;
-    const int rb = __builtin_amdgcn_readfirstlane((blockIdx.y * 4 + (threadIdx.x >> 6)) * LD_TR);
+    const int rb = (blockIdx.y * 4 + wave) * LD_TR;
     const bool live = rb < R;  // wave-uniform; a dead wave still stages x for the others
-    const float* ar[LD_TR];
-#pragma unroll
-    for (int t = 0; t < LD_TR; t++) ar[t] = A + (int64_t)min(min(rb, R - 1) + t, R - 1) * K;
+    // The wave's A slice of a chunk (LD_TR ranks x 64 k, rank-major): lane l
+    // holds LD_TR consecutive k of rank l / LPR.  Ranks past R read rank R - 1.
+    constexpr int LPR = LD_KC / LD_TR;
+    const int at = lane / LPR, ak = (lane % LPR) * LD_TR;
+    const float* arow = A + (int64_t)min(rb + at, R - 1) * K + ak;
     float acc[LD_TR];
 #pragma unroll
     for (int t = 0; t < LD_TR; t++) acc[t] = 0.0f;
-    auto step = [&](const float* xr, int kk, const float(&av)[LD_TR][8]) {
-        float xv[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) xv[i] = xr[kk + i];
-#pragma unroll
-        for (int t = 0; t < LD_TR; t++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc[t] = fmaf(xv[i], av[t][i], acc[t]);
-    };
-    float xt[16];
+    float xt[16], ta[LD_TR];
     fetch_x_tile<XB>(x, ldx, m0, M, 0, xt);
-    float aa[LD_TR][8], ab[LD_TR][8];
-    if (live) load_a8<LD_TR>(ar, 0, aa);
+    load_tr<LD_TR>(arow, ta);
     const int srow = threadIdx.x >> 2, skk = (threadIdx.x & 3) * 16;
     for (int k0 = 0, buf = 0; k0 < K; k0 += LD_KC, buf ^= 1) {
         float* st = sx[buf] + srow * LD_XP + skk;
 #pragma unroll
-        for (int i = 0; i < 16; i++) st[i] = xt[i];
+        for (int q = 0; q < 4; q++) *(float4*)(st + 4 * q) = make_float4(xt[4 * q], xt[4 * q + 1], xt[4 * q + 2], xt[4 * q + 3]);
+        store_tr<LD_TR>(&sa[buf][wave][at * LD_KC + ak], ta);
         __syncthreads();
-        if (k0 + LD_KC < K) fetch_x_tile<XB>(x, ldx, m0, M, k0 + LD_KC, xt);
+        if (k0 + LD_KC < K) {
+            fetch_x_tile<XB>(x, ldx, m0, M, k0 + LD_KC, xt);
+            load_tr<LD_TR>(arow + k0 + LD_KC, ta);
+        }
         if (live) {
             const float* xr = sx[buf] + lane * LD_XP;
+            const float* as = sa[buf][wave];
 #pragma unroll
-            for (int kk = 0; kk < LD_KC; kk += 16) {
-                wait_scalar_loads();
-                load_a8<LD_TR>(ar, k0 + kk + 8, ab);
-                __builtin_amdgcn_sched_barrier(0);
-                step(xr, kk, aa);
-                __builtin_amdgcn_sched_barrier(0);
-                wait_scalar_loads();
-                load_a8<LD_TR>(ar, min(k0 + kk + 16, K - 8), aa);  // past the end: a harmless reload
-                __builtin_amdgcn_sched_barrier(0);
-                step(xr, kk + 8, ab);
-                __builtin_amdgcn_sched_barrier(0);
+            for (int kk = 0; kk < LD_KC; kk += 8) {
+                const float4 x0 = *(const float4*)(xr + kk), x1 = *(const float4*)(xr + kk + 4);
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                float av[LD_TR][8];
+#pragma unroll
+                for (int t = 0; t < LD_TR; t++) {
+                    const float4 a0 = *(const float4*)(as + t * LD_KC + kk), a1 = *(const float4*)(as + t * LD_KC + kk + 4);
+                    av[t][0] = a0.x, av[t][1] = a0.y, av[t][2] = a0.z, av[t][3] = a0.w;
+                    av[t][4] = a1.x, av[t][5] = a1.y, av[t][6] = a1.z, av[t][7] = a1.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+#pragma unroll
+                    for (int t = 0; t < LD_TR; t++) acc[t] = fmaf(xv[i], av[t][i], acc[t]);
             }
         }
         // The buffer written next iteration was last read two iterations ago,

@@ -29,9 +29,14 @@ def bits(t):
     return t.cpu().contiguous().view(torch.int32).numpy()
 
 
+@pytest.mark.parametrize("tr", ["1", "2", "4"])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,K,R", [(1, 256, 1), (37, 72, 17), (300, 3072, 64), (129, 1000, 256), (65, 33, 33)])
-def test_lora_down_bit_exact(dev, orc, xdt, M, K, R):
+@pytest.mark.parametrize("M,K,R", [(1, 256, 1), (37, 72, 17), (300, 3072, 64), (129, 1000, 256), (65, 33, 33),
+                                   (70, 640, 37)])
+def test_lora_down_bit_exact(dev, orc, monkeypatch, tr, xdt, M, K, R):
+    """tr: ranks per wave of the main form (the PHI_LORA_TR A/B switch); the
+    shapes with K % 64 == 0 take the main form, the others the general one."""
+    monkeypatch.setenv("PHI_LORA_TR", tr)
     x, A, _, _ = factors(M, K, R, 1, M + K + R)
     x = x.to(xdt)
     h = Q.lora_down(x.to(dev), A.to(dev))
