@@ -1,7 +1,10 @@
-// Persistent int8 GEMM for gfx950: one workgroup per CU walks square output
-// tiles (256 x 256, or 128 x 128 for the rows a whole number of 256-row
-// rounds does not cover), and the next tile's first K-steps are loaded while
-// the current tile finishes, so no tile starts on an empty pipeline.
+// Persistent int8 GEMM for gfx950, two-stage form: one workgroup per CU walks
+// square output tiles (256 x 256, or 128 x 128 for the rows a whole number of
+// 256-row rounds does not cover), and the next tile's first K-steps are
+// loaded while the current tile finishes, so no tile starts on an empty
+// pipeline.  It runs B as packed 4-bit codes expanded in registers (W4A8 and
+// int4); int8 B runs on the four-stage pipeline of i8_gemm_pipe.hip, with
+// this kernel as its A/B counterpart.
 //
 //   acc[m,n] = sum_k A[m,k] * B[n,k]                  (exact int32)
 //   C[m,n]   = fma((float)acc * sA[m], sB[n], bias[n])  -> bf16 (RNE) / fp32 / raw int32
