@@ -1,0 +1,79 @@
+"""GPU parity at the benchmark configs' full sizes, through the C ABI.
+
+* config 3: the fused W8A8 linear (bf16 x -> rotate + quantise -> int8 GEMM ->
+  bf16) at M=32760, K=5120 for both of its shapes (N=5120 attention out-proj and
+  N=13824 MLP up).  Sampled rows are compared bit for bit against the oracle
+  (int8 codes, fp32 scales, int32 accumulators, bf16 outputs); every row and
+  column of the int32 product is covered by the exact ABFT checksums.
+* config 4: the adaLN GEMV at M=2, K=3072, N=18432 against the oracle on every
+  output of several of the 60 weights.
+
+Reference: core/host/quant.cpp:109-169 (rotate + quantise), :223-236 (GEMM),
+core/kernels/int8_gemm.cpp:588-620 (epilogue), core/runtime/compute.cpp:551-684
+(the two dispatchers)."""
+import numpy as np
+import pytest
+import torch
+
+import phi_qlinear as Q
+from phi_qlinear import synth
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+
+def u16(t):
+    return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def checksums_ok(A, B, C32):
+    """sum_n C = A . (sum_n B) and sum_m C = (sum_m A) . B, exact in float64."""
+    Af, Bf, Cf = A.double(), B.double(), C32.double()
+    return torch.equal(Cf.sum(1), Af @ Bf.sum(0)) and torch.equal(Cf.sum(0), Bf @ Af.sum(0))
+
+
+@pytest.mark.parametrize("N", [5120, 13824])
+def test_config3_fused_linear(dev, orc, N):
+    M, K = 32760, 5120
+    print(f"config 3 fused linear M={M} K={K} N={N}", flush=True)
+    x = synth.activations(M, K, seed=0, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = Q.q8_linear(x, W, sW, b, q8=q8, s8=s8)
+    acc = Q.i8_gemm(q8, W, None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert checksums_ok(q8, W, acc)
+    # Rows spread over every 256-row tile band, the last row included.
+    rows = np.unique(np.concatenate([np.arange(0, M, 509), [M - 1, M - 256, 4095, 4096]]))
+    ri = torch.from_numpy(rows).to(dev)
+    qo, so = orc.quantize_rows(u16(x[ri]))
+    assert np.array_equal(q8[ri].cpu().numpy(), qo)
+    assert np.array_equal(s8[ri].cpu().numpy().view(np.uint32), so.view(np.uint32))
+    acco = orc.gemm_i8_i32_fast(qo, W.cpu().numpy())
+    assert np.array_equal(acc[ri].cpu().numpy(), acco)
+    yo = orc.epilogue(acco, so, sW.cpu().numpy(), u16(b))
+    assert np.array_equal(u16(y[ri]), yo)
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_config4_gemv_m2(dev, orc, out):
+    """M=2 timestep rows against 18432 x 3072 weights: every output of every
+    seventh weight of the 60 against the oracle."""
+    M, K, N, n_items = 2, 3072, 18432, 60
+    x = synth.activations(M, K, seed=4)
+    qo, so = orc.quantize_rows(u16(x))
+    q8, s8 = torch.from_numpy(qo).to(dev), torch.from_numpy(so).to(dev)
+    Ws = [synth.int8_weight(N, K, seed=300 + i, device=dev) for i in range(n_items)]
+    sc = [torch.full((1,), 0.002, device=dev) if i % 2 else torch.rand(N, device=dev) * 0.01 + 1e-3
+          for i in range(n_items)]
+    bs = [synth.bias(N, seed=400 + i, device=dev) for i in range(n_items)]
+    odt = torch.bfloat16 if out == "bf16" else torch.float32
+    outs = Q.gemv_batched(q8, s8, Ws, sc, biases=bs, out_dtype=odt)
+    torch.cuda.synchronize()
+    for i in range(0, n_items, 7):
+        acc = orc.gemm_i8_i32_fast(qo, Ws[i].cpu().numpy())
+        want = orc.epilogue(acc, so, sc[i].cpu().numpy(), u16(bs[i]), out=out)
+        got = u16(outs[i]) if out == "bf16" else outs[i].cpu().numpy().view(np.uint32)
+        assert np.array_equal(got, want if out == "bf16" else want.view(np.uint32)), i

@@ -169,7 +169,7 @@ def checksums_ok(A, B, C32):
 
 @pytest.mark.slow
 @pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4352, 3072, 12288), (4352, 9216, 3072),
-                                   (32760, 5120, 5120)])
+                                   (32760, 5120, 5120), (32760, 13824, 5120)])
 def test_full_size_checksums(dev, kernel, M, N, K):
     A = synth.int8_weight(M, K, seed=M, device=dev)
     B = synth.int8_weight(N, K, seed=N, device=dev)

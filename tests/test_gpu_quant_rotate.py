@@ -106,6 +106,77 @@ def test_exact_ties_and_the_half_boundary(dev, orc):
     assert list(q[0, :10]) == [1, -1, 2, -2, 3, -3, 127, -127, 0, 0]
 
 
+def near_ties(lo=-128, hi=128, ulps=3):
+    """Every half-integer in [lo, hi) and its fp32 neighbours within `ulps`
+    (the same set the oracle's own rounding pins use)."""
+    centres = np.arange(lo, hi) + 0.5
+    out = [centres.astype(np.float32)]
+    up = dn = centres.astype(np.float32)
+    for _ in range(ulps):
+        up = np.nextafter(up, np.float32(np.inf))
+        dn = np.nextafter(dn, np.float32(-np.inf))
+        out += [up, dn]
+    v = np.concatenate(out)
+    return v[np.abs(v) <= 127]
+
+
+def half_away(v):
+    """Round half away from zero, exactly (float64 holds every fp32 value)."""
+    d = v.astype(np.float64)
+    return np.clip(np.sign(d) * np.floor(np.abs(d) + 0.5), -127, 127).astype(np.int8)
+
+
+@pytest.mark.parametrize("round_mode", [Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN])
+@pytest.mark.parametrize("inv_pow", [0, 3, -2])
+def test_every_near_tie_unrotated(dev, orc, round_mode, inv_pow):
+    """The whole near-tie set in one row per scale: amax 127 * 2^-inv_pow makes
+    inv = 2^inv_pow exactly, so v * inv is exact and the rounding alone decides
+    each code (the kernel's add-0.49999997-then-truncate shortcut included)."""
+    v = near_ties()
+    K = 256 * ((v.size + 1 + 255) // 256)
+    row = np.zeros(K, np.float32)
+    row[:v.size] = v
+    row[-1] = 127.0
+    row *= np.float32(2.0 ** -inv_pow)
+    x = torch.from_numpy(np.stack([row, -row]))
+    q, s, qo, so = run(dev, orc, x, rotate=False, round_mode=round_mode)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    assert s[0] == np.float32(2.0 ** -inv_pow)
+    assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"
+    if round_mode == Q.ROUND_HALF_AWAY:
+        assert np.array_equal(q[0, :v.size], half_away(v))
+
+
+@pytest.mark.parametrize("round_mode", [Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN])
+def test_every_near_tie_through_the_rotation(dev, orc, round_mode):
+    """The near-tie set through the rotation and the folded inv/16.  A 256-group
+    holding one non-zero c at position p rotates to +-c in every element, times
+    1/16, with no rounding; with c = 16 t the group's values are exactly +-t.
+    One group per row holds 16 * 127, so amax = 127, scale = 1 and the kernel's
+    folded multiplier is 1/16: every code is the rounding of +-t."""
+    v = near_ties()
+    per_row = 95  # groups left in a 96-group (K = 24576) row after the amax group
+    rows = (v.size + per_row - 1) // per_row
+    K = 96 * 256
+    x = np.zeros((rows, K), np.float32)
+    want = np.zeros((rows, per_row), np.float32)
+    for i, t in enumerate(v):
+        r, g = divmod(i, per_row)
+        x[r, g * 256 + (i * 37) % 256] = np.float32(16.0) * t
+        want[r, g] = t
+    x[:, 95 * 256 + 5] = np.float32(16.0 * 127.0)
+    q, s, qo, so = run(dev, orc, torch.from_numpy(x), round_mode=round_mode)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    assert np.all(s == 1.0)
+    assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"
+    if round_mode == Q.ROUND_HALF_AWAY:
+        # Each group's codes are +-round(t); the sign pattern is the column's.
+        mag = np.abs(q[:, :95 * 256].reshape(rows, 95, 256).astype(np.int16))
+        n = v.size
+        got = mag.max(axis=2).reshape(-1)[:n]
+        assert np.array_equal(got, np.abs(half_away(want.reshape(-1)[:n])).astype(np.int16))
+
+
 def test_huge_rows(dev, orc):
     """Rows whose amax is so large that inv/16 would be subnormal (qmax 1,
     amax 1e37): the kernel then scales each element by 1/16 before inv, as the
