@@ -51,7 +51,8 @@ typedef enum phi_dtype {
     PHI_I8 = 4,
     PHI_F8_E4M3 = 5,
     PHI_F8_E5M2 = 6,
-    PHI_U8_E4M3 = 7 /* an E4M3 table in a byte container (RelDType::U8_E4M3) */
+    PHI_U8_E4M3 = 7, /* an E4M3 table in a byte container (RelDType::U8_E4M3) */
+    PHI_I4 = 8       /* two signed nibbles per byte, column 2j in the low nibble */
 } phi_dtype;
 
 /* Rounding of v * (1/scale) onto the integer grid. */
@@ -132,7 +133,11 @@ phi_status phi_hip_quant_rotate_act(phi_stream_t stream, const void* x, int x_dt
  *   bias: NULL, or [N] of bias_dtype (PHI_F32 / PHI_BF16).
  *   C [M, ldc] of c_dtype: PHI_F32 (reference), PHI_BF16 (RNE), or PHI_I32
  *     (raw accumulators; scales and bias are then ignored and may be NULL).
- *   A, B: 16-byte aligned; lda, ldb multiples of 16; K % 64 == 0.
+ *   Any K > 0 and any byte offset and pitch of A and B: K % 64 == 0 with
+ *     16-byte aligned rows takes the MFMA pipelines; anything else the same
+ *     MFMA tiles fed by byte-safe loads with the K tail zero-filled (the
+ *     reference's dp4a fallback, core/runtime/compute.cpp:566-575).
+ *   sA, sB, bias and C: naturally aligned (4 bytes; 2 for a bf16 bias or C).
  *   workspace: may be NULL when phi_hip_workspace_bytes() returns 0 (it
  *     does for every shape: the kernels keep all scratch in LDS).
  */
@@ -320,6 +325,40 @@ phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, vo
  * kernel core/kernels/conv3d_causal.cpp:997-1013). */
 phi_status phi_hip_silu_gate(phi_stream_t stream, const void* gx, int x_dtype, int64_t rows, int64_t cols,
                              int64_t ldx, void* out, int out_dtype, int64_t ldo);
+
+/*
+ * Load-time weight steps, on the device.  The reference runs these on the
+ * host while a loader turns a checkpoint tensor into the int8 GEMM operand;
+ * here the host layer's loaders (load_quant_linear, load_quant3_linear,
+ * upload_quant_linear_i8) chain them with phi_hip_quant_rotate, which is the
+ * reference's weight quantiser as well (quantize_weight and
+ * quantize_activation share quantize_impl_into, core/host/quant.cpp:134-195).
+ */
+
+/* The values of a stored tensor in fp32, as SafeTensors::dequant_rows
+ * computes them (core/host/st.cpp:601-700): PHI_I8 codes, or PHI_I4 signed
+ * nibbles (a bare packed int4), times their row's scale ((float)q * s;
+ * row_scale [rows], or [1] when scale_scalar; NULL means 1 for PHI_I4),
+ * PHI_F16 / PHI_BF16 widened exactly, PHI_F32 copied.  src [rows, lds]
+ * elements (bytes for PHI_I4), out [rows, ldo] fp32. */
+phi_status phi_hip_dequant_rows(phi_stream_t stream, const void* src, int src_dtype, int64_t rows, int64_t cols,
+                                int64_t lds, const float* row_scale, int scale_scalar, float* out, int64_t ldo);
+
+/* The 256-wide J-2R rotation of fp32 rows alone, y = H x per group with the
+ * reference's butterfly order and final 1/16 (convrot_forward,
+ * core/host/quant.cpp:66-100; H is an involution, so this is also
+ * convrot_inverse, core/host/quant.hpp:63-65).  K % 256 == 0; y == x (equal
+ * pitches) runs in place. */
+phi_status phi_hip_convrot_rows(phi_stream_t stream, const float* x, int64_t rows, int64_t K, int64_t ldx, float* y,
+                                int64_t ldy);
+
+/* Fold one LoRA factor into fp32 weight rows in place:
+ *   w[o][i] += (scale * B[o][r]) * A[r][i]  for r = 0..rank-1, skipping B[o][r] == 0,
+ * each product and sum rounded on its own (LoraSet::apply_rows_of,
+ * core/models/lora.cpp:182-201).  w [rows, ldw]; A [rank, k]; B [rows, rank]:
+ * the factor's B rows for these weight rows. */
+phi_status phi_hip_lora_fold(phi_stream_t stream, float* w, int64_t ldw, int64_t rows, int64_t k, const float* A,
+                             const float* B, int64_t rank, float scale);
 
 #ifdef __cplusplus
 }

@@ -84,22 +84,24 @@ constexpr int64_t kW4ExpandMinRows = 512;  // rotated row held in LDS: 96 groups
 // Shared validation of the GEMM operands (A [M,lda], B [N,ldb]).
 phi_status check_gemm(const char* who, const int8_t* A, int64_t lda, const void* B, int64_t ldb,
                       int64_t M, int64_t N, int64_t K, const float* sA, const float* sB,
-                      void* C, int c_dtype, int64_t ldc, bool w4) {
+                      void* C, int c_dtype, int64_t ldc, bool w4, bool any_k = false) {
     if (M <= 0 || N <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem (M=%lld N=%lld K=%lld)", who, (long long)M, (long long)N, (long long)K);
     if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: dimension exceeds 2^31", who);
     if (!A || !B || !C) return fail(PHI_ERR_ARG, "%s: null operand", who);
     if (c_kind_of(c_dtype) < 0) return fail(PHI_ERR_ARG, "%s: bad output dtype %d", who, c_dtype);
     if (c_dtype != PHI_I32 && (!sA || !sB)) return fail(PHI_ERR_ARG, "%s: scales are required for a scaled output", who);
-    if (K % 64 != 0) return fail(PHI_ERR_SHAPE, "%s: K=%lld is not a multiple of 64", who, (long long)K);
+    if (!any_k && K % 64 != 0) return fail(PHI_ERR_SHAPE, "%s: K=%lld is not a multiple of 64", who, (long long)K);
     if (lda < K || ldc < N) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than the row", who);
-    if (!aligned(A, 16) || lda % 16 != 0) return fail(PHI_ERR_ALIGN, "%s: A must be 16-byte aligned with lda %% 16 == 0", who);
+    if (!any_k && (!aligned(A, 16) || lda % 16 != 0)) return fail(PHI_ERR_ALIGN, "%s: A must be 16-byte aligned with lda %% 16 == 0", who);
     if (w4) {
         if (ldb < K / 2) return fail(PHI_ERR_SHAPE, "%s: a %lld-column nibble row needs %lld bytes, got %lld", who, (long long)K, (long long)(K / 2), (long long)ldb);
         if (!aligned(B, 8) || ldb % 8 != 0) return fail(PHI_ERR_ALIGN, "%s: codes must be 8-byte aligned with row bytes %% 8 == 0", who);
     } else {
         if (ldb < K) return fail(PHI_ERR_SHAPE, "%s: ldb < K", who);
-        if (!aligned(B, 16) || ldb % 16 != 0) return fail(PHI_ERR_ALIGN, "%s: B must be 16-byte aligned with ldb %% 16 == 0", who);
+        if (!any_k && (!aligned(B, 16) || ldb % 16 != 0)) return fail(PHI_ERR_ALIGN, "%s: B must be 16-byte aligned with ldb %% 16 == 0", who);
     }
+    if (sA && !aligned(sA, 4)) return fail(PHI_ERR_ALIGN, "%s: sA is misaligned", who);
+    if (sB && !aligned(sB, 4)) return fail(PHI_ERR_ALIGN, "%s: sB is misaligned", who);
     if (!aligned(C, c_elem_bytes(c_dtype))) return fail(PHI_ERR_ALIGN, "%s: C is misaligned", who);
     return PHI_OK;
 }
@@ -313,12 +315,20 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
                            int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes) {
     static const char* who = "int8_gemm";
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
-    phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, C, c_dtype, ldc, false);
+    phi_status st = check_gemm(who, A, lda, B, ldb, M, N, K, sA, sB, C, c_dtype, ldc, false, true);
     if (st != PHI_OK) return st;
     (void)workspace;  // no kernel needs one (phi_hip_workspace_bytes is 0)
     (void)ws_bytes;
     const int bk = bias_kind_of(bias, bias_dtype, &st);
     if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    if (bias && !aligned(bias, bk == phi_dev::BIAS_BF16 ? 2 : 4)) return fail(PHI_ERR_ALIGN, "%s: bias is misaligned", who);
+    // The MFMA kernels stage 16-byte chunks of whole 64-deep K-tiles.  Any
+    // other K, or an operand at an offset or pitch that is not a multiple of
+    // 16 bytes, takes the same kernel in its any-K form (the reference routes
+    // those to int8_gemm_dp4a, core/runtime/compute.cpp:566-575);
+    // PHI_GEMM_KERNEL=any forces it (an A/B switch, like PHI_INT8_DP4A).
+    const char* ek = getenv("PHI_GEMM_KERNEL");
+    const bool staged_ok = K % 64 == 0 && aligned(A, 16) && lda % 16 == 0 && aligned(B, 16) && ldb % 16 == 0;
     phi_dev::GemmParams p{};
     p.A = A;
     p.B = B;
@@ -337,6 +347,8 @@ phi_status phi_hip_i8_gemm(phi_stream_t stream, const int8_t* A, int64_t lda, co
     p.c_kind = c_kind_of(c_dtype);
     p.group_m = 4;
     set_vec_flags(p, c_dtype, ldc);
+    if (!staged_ok || (ek && strcmp(ek, "any") == 0))
+        return check_hip(phi_dev::launch_i8_gemm_any((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
     const GemmKernel gk = gemm_kernel_for(M, N, K, persist_ok(C, c_dtype, N, K, lda, ldb, ldc));
     if (gk == GK_PERSIST || gk == GK_PERSIST256 || gk == GK_PERSIST128)
         return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, false, c_dtype, ldc), who);
@@ -427,7 +439,7 @@ static phi_status check_w4a8(const char* who, const phi_w4a8_weight* w, bool lut
     const int64_t rsz = d == PHI_F32 ? 4 : (d == PHI_F16 || d == PHI_BF16) ? 2 : 1;
     if (w->s_rel && w->srel_row_bytes < (w->k / w->group) * rsz) return fail(PHI_ERR_SHAPE, "%s: relative-scale row too short", who);
     if (lut && w->layout != 0) return fail(PHI_ERR_UNSUPPORTED, "%s: the in-register table is for the nibble layout only", who);
-    if (w->rows > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: rows exceeds 2^31", who);
+    if (w->rows > INT32_MAX || w->k > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: rows or K exceeds 2^31", who);
     return PHI_OK;
 }
 
@@ -714,6 +726,64 @@ phi_status phi_hip_lora_tail(phi_stream_t stream, const void* x, int x_dtype, in
     phi_status st = phi_hip_lora_down(stream, x, x_dtype, ldx, M, K, At, R, h);
     if (st != PHI_OK) return st;
     return phi_hip_lora_rank_add(stream, h, Bt, out, out_dtype, ldo, M, N, R);
+}
+
+phi_status phi_hip_dequant_rows(phi_stream_t stream, const void* src, int src_dtype, int64_t rows, int64_t cols,
+                                int64_t lds, const float* row_scale, int scale_scalar, float* out, int64_t ldo) {
+    static const char* who = "dequant_rows";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || cols < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0 || cols == 0) return ok();
+    if (!src || !out) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    int kind;
+    size_t esz;
+    switch (src_dtype) {
+        case PHI_I8: kind = phi_dev::DQ_I8, esz = 1; break;
+        case PHI_I4: kind = phi_dev::DQ_I4, esz = 1; break;
+        case PHI_F16: kind = phi_dev::DQ_F16, esz = 2; break;
+        case PHI_BF16: kind = phi_dev::DQ_BF16, esz = 2; break;
+        case PHI_F32: kind = phi_dev::DQ_F32, esz = 4; break;
+        default: return fail(PHI_ERR_ARG, "%s: src dtype must be I8, I4, F16, BF16 or F32", who);
+    }
+    if (src_dtype == PHI_I8 && !row_scale) return fail(PHI_ERR_ARG, "%s: int8 codes need their row scales", who);
+    const int64_t src_cols = src_dtype == PHI_I4 ? (cols + 1) / 2 : cols;
+    if (lds < src_cols || ldo < cols) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than the row", who);
+    if (!aligned(src, esz) || !aligned(out, 4) || (row_scale && !aligned(row_scale, 4)))
+        return fail(PHI_ERR_ALIGN, "%s: misaligned operand", who);
+    return check_hip(phi_dev::launch_dequant_rows((hipStream_t)stream, src, kind, rows, cols, lds, row_scale,
+                                                  scale_scalar ? 1 : 0, out, ldo),
+                     who);
+}
+
+phi_status phi_hip_convrot_rows(phi_stream_t stream, const float* x, int64_t rows, int64_t K, int64_t ldx, float* y,
+                                int64_t ldy) {
+    static const char* who = "convrot";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0 || K == 0) return ok();
+    if (K % 256 != 0) return fail(PHI_ERR_SHAPE, "convrot: cols=%lld not a multiple of 256", (long long)K);
+    if (!x || !y) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (ldx < K || ldy < K) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than the row", who);
+    if (rows * (K / 256) > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: more than 2^31 groups", who);
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(PHI_ERR_ALIGN, "%s: misaligned operand", who);
+    const char* xb = (const char*)x;
+    const char* yb = (const char*)y;
+    const int64_t xe = ((rows - 1) * ldx + K) * 4, ye = ((rows - 1) * ldy + K) * 4;
+    if (x != y && yb < xb + xe && xb < yb + ye) return fail(PHI_ERR_ARG, "%s: y overlaps x without being x", who);
+    if (x == y && ldx != ldy) return fail(PHI_ERR_ARG, "%s: in place needs equal pitches", who);
+    return check_hip(phi_dev::launch_convrot_rows((hipStream_t)stream, x, ldx, y, ldy, rows, K), who);
+}
+
+phi_status phi_hip_lora_fold(phi_stream_t stream, float* w, int64_t ldw, int64_t rows, int64_t k, const float* A,
+                             const float* B, int64_t rank, float scale) {
+    static const char* who = "lora_fold";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || k < 0 || rank < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0 || k == 0 || rank == 0) return ok();
+    if (!w || !A || !B) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (ldw < k) return fail(PHI_ERR_SHAPE, "%s: ldw < k", who);
+    if (!aligned(w, 4) || !aligned(A, 4) || !aligned(B, 4)) return fail(PHI_ERR_ALIGN, "%s: misaligned operand", who);
+    return check_hip(phi_dev::launch_lora_fold((hipStream_t)stream, w, ldw, rows, k, A, B, rank, scale), who);
 }
 
 phi_status phi_hip_gelu_tanh(phi_stream_t stream, const void* x, int x_dtype, void* y, int y_dtype, int64_t n) {

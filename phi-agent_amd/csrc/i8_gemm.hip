@@ -62,6 +62,26 @@ __device__ __forceinline__ v4i expand16(const uint2& c, const uint4& t) {
     return r;
 }
 
+// 16 bytes of a row from byte k0 on, zero past K, from any address: one
+// 16-byte load when the address is aligned and the chunk lies inside the row,
+// byte loads otherwise (the ragged K tail, a row at an odd offset).
+__device__ __forceinline__ v4i load16_any(const int8_t* row, int64_t k0, int K) {
+    const int8_t* p = row + k0;
+    if (k0 + 16 <= K && ((uintptr_t)p & 15) == 0) return *(const v4i*)p;
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int64_t k = k0 + 4 * d + b;
+            v |= (k < K ? (uint32_t)(uint8_t)p[4 * d + b] : 0u) << (8 * b);
+        }
+        w[d] = v;
+    }
+    return v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+}
+
 // Workgroup id -> (tile_m, tile_n).  XCD remap then grouped walk.
 __device__ __forceinline__ void tile_coords(int pid, int nblocks, int tiles_m, int tiles_n,
                                             int group_m, int& tm, int& tn) {
@@ -83,7 +103,11 @@ __device__ __forceinline__ void tile_coords(int pid, int nblocks, int tiles_m, i
 // per-(row, group) table `lut` (with p.w4_signed, the constant table of signed
 // nibbles instead); each staged 16-byte B chunk is expanded in
 // registers before it is written to LDS, so the MFMA core is unchanged.
-template <int BM, int BN, int WM, int WN, bool W4>
+// ANY = true: any K > 0 and operands at any byte offset with any pitch (the
+// service the reference's dp4a kernel gives, core/kernels/int8_gemm.cpp:
+// 136-150): the last K-tile is zero-filled past K, which adds nothing to the
+// exact integer sums.
+template <int BM, int BN, int WM, int WN, bool W4, bool ANY = false>
 __global__ __launch_bounds__(WM* WN * 64) void i8_gemm_kernel(GemmParams p) {
     constexpr int NT = WM * WN * 64;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -156,10 +180,25 @@ __global__ __launch_bounds__(WM* WN * 64) void i8_gemm_kernel(GemmParams p) {
     v4i ra[CA], rb[CB];
     uint2 rc[W4 ? CB : 1];
     uint4 rl[W4 ? CB : 1];
-    const int KT = p.K / GEMM_BK;
+    const int KT = ANY ? (p.K + GEMM_BK - 1) / GEMM_BK : p.K / GEMM_BK;
 
     // Fetch the K-tile at byte offset k into registers.
     auto fetch = [&](int64_t k) {
+        if (ANY) {
+            // gA / gB point at chunk c of their rows: the chunk's own K offset
+            // is (tid + NT i) & 3 times 16, the same for every fetch.
+#pragma unroll
+            for (int i = 0; i < CA; i++) {
+                const int c = ((tid + NT * i) & 3) * 16;
+                ra[i] = load16_any(gA[i] - c, k + c, p.K);
+            }
+#pragma unroll
+            for (int i = 0; i < CB; i++) {
+                const int c = ((tid + NT * i) & 3) * 16;
+                rb[i] = load16_any(gB[i] - c, k + c, p.K);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < CA; i++) ra[i] = *(const v4i*)(gA[i] + k);
 #pragma unroll
@@ -244,10 +283,10 @@ __global__ __launch_bounds__(WM* WN * 64) void i8_gemm_kernel(GemmParams p) {
     }
 }
 
-template <int BM, int BN, int WM, int WN, bool W4>
+template <int BM, int BN, int WM, int WN, bool W4, bool ANY = false>
 static hipError_t launch_cfg(hipStream_t stream, const GemmParams& p) {
     const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-    hipLaunchKernelGGL((i8_gemm_kernel<BM, BN, WM, WN, W4>), dim3(tiles), dim3(WM * WN * 64), 0, stream, p);
+    hipLaunchKernelGGL((i8_gemm_kernel<BM, BN, WM, WN, W4, ANY>), dim3(tiles), dim3(WM * WN * 64), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -256,6 +295,13 @@ hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg) {
     switch (cfg) {
         case 1: return launch_cfg<128, 128, 2, 2, false>(stream, p);
         default: return launch_cfg<256, 128, 2, 2, false>(stream, p);
+    }
+}
+
+hipError_t launch_i8_gemm_any(hipStream_t stream, const GemmParams& p, int cfg) {
+    switch (cfg) {
+        case 1: return launch_cfg<128, 128, 2, 2, false, true>(stream, p);
+        default: return launch_cfg<256, 128, 2, 2, false, true>(stream, p);
     }
 }
 

@@ -39,6 +39,8 @@ struct GemmParams {
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
+// Any K > 0, operands at any byte offset and pitch (the K tail zero-filled).
+hipError_t launch_i8_gemm_any(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
 // Persistent kernel (K % 256 == 0): square tiles of 2 * wave_tile (128 -> 256 x 256,
 // 64 -> 128 x 128), min(tiles, num_cus) workgroups.  w4: B is packed codes plus

@@ -25,4 +25,13 @@ struct W4a8Params {
 
 hipError_t launch_w4a8_rows(hipStream_t stream, const W4a8Params& p, int8_t* out, float* s, bool lut);
 
+// Load-time weight kernels (weights.hip).
+enum DequantKind { DQ_F32 = 0, DQ_BF16 = 1, DQ_F16 = 2, DQ_I8 = 4, DQ_I4 = 8 };
+hipError_t launch_dequant_rows(hipStream_t stream, const void* src, int kind, int64_t rows, int64_t cols, int64_t lds,
+                               const float* row_scale, int scale_scalar, float* out, int64_t ldo);
+hipError_t launch_convrot_rows(hipStream_t stream, const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows,
+                               int64_t K);
+hipError_t launch_lora_fold(hipStream_t stream, float* w, int64_t ldw, int64_t rows, int64_t k, const float* A,
+                            const float* B, int64_t rank, float scale);
+
 }  // namespace phi_dev

@@ -1,0 +1,125 @@
+// Load-time weight kernels: the steps the reference's loaders run on the host
+// before a weight reaches the int8 GEMM, here on the device so a checkpoint
+// goes from its file bytes to the GEMM operand without an fp32 round trip
+// through host memory.
+//
+//   dequant_rows  a stored tensor's values in fp32 (SafeTensors::dequant_rows,
+//                 core/host/st.cpp:601-700: int8 codes or a bare int4's signed
+//                 nibbles times the row scale,
+//                 f16 / bf16 widened, fp32 copied)
+//   convrot_rows  the 256-wide J-2R rotation of fp32 rows with no quantiser
+//                 (convrot_forward, core/host/quant.cpp:66-100; its inverse is
+//                 the same map, core/host/quant.hpp:63-65)
+//   lora_fold     w[o][i] += (scale * B[o][r]) * A[r][i] for r ascending, rank
+//                 entries of B that are 0 skipped (LoraSet::apply_rows_of,
+//                 core/models/lora.cpp:182-201)
+//
+// The rotate + quantise that turns the result into int8 is quant_rotate, the
+// same kernel the activations take: the reference's weight and activation
+// quantisers are one function (quantize_impl_into, core/host/quant.cpp:134-169).
+//
+// All of this runs once per weight load and is bound by HBM at a few bytes per
+// element; the kernels are plain and exact (-ffp-contract=off: every product
+// and sum rounds on its own, as the reference's x86-64 host code does).
+#include "device_common.hpp"
+#include "w4a8.hpp"
+
+namespace phi_dev {
+
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const void* src, int kind, int64_t rows, int64_t cols,
+                                                           int64_t lds, const float* row_scale, int scale_scalar,
+                                                           float* out, int64_t ldo) {
+    const int64_t total = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / cols, c = i - r * cols;
+        const int64_t at = r * lds + c;
+        float v;
+        switch (kind) {
+            case DQ_I8: v = (float)((const int8_t*)src)[at] * row_scale[scale_scalar ? 0 : r]; break;
+            case DQ_I4: {
+                const uint32_t b = ((const uint8_t*)src)[r * lds + (c >> 1)];
+                const int nib = (int)((c & 1) ? b >> 4 : b & 15u);
+                const float sc = row_scale ? row_scale[scale_scalar ? 0 : r] : 1.0f;
+                v = (float)(nib >= 8 ? nib - 16 : nib) * sc;
+                break;
+            }
+            case DQ_F16: v = f16_to_f32(((const uint16_t*)src)[at]); break;
+            case DQ_BF16: v = bf16_to_f32(((const uint16_t*)src)[at]); break;
+            default: v = ((const float*)src)[at]; break;
+        }
+        out[r * ldo + c] = v;
+    }
+}
+
+// One 256-element group per workgroup, one element per thread.  Stage d
+// (stride 4^d) gives element j of each 4-tuple (((x0 + x1) + x2) + x3) - 2 x[3-j],
+// the reference's butterfly in its operation order; the 1/16 is a final
+// product, as in the reference.  x == y (same pitch) is allowed: a group is
+// read whole into LDS before any of it is written.
+__global__ __launch_bounds__(256) void convrot_rows_kernel(const float* x, int64_t ldx, float* y, int64_t ldy,
+                                                           int64_t groups_per_row) {
+    __shared__ float buf[256];
+    const int t = threadIdx.x;
+    const int64_t row = blockIdx.x / groups_per_row, g = blockIdx.x - row * groups_per_row;
+    buf[t] = x[row * ldx + g * 256 + t];
+    __syncthreads();
+#pragma unroll
+    for (int stride = 1; stride < 256; stride *= 4) {
+        const int j = (t / stride) & 3, b = t - j * stride;
+        const float x0 = buf[b], x1 = buf[b + stride], x2 = buf[b + 2 * stride], x3 = buf[b + 3 * stride];
+        const float s = ((x0 + x1) + x2) + x3;
+        const float mine = j == 0 ? x3 : j == 1 ? x2 : j == 2 ? x1 : x0;
+        const float v = s - 2.0f * mine;
+        __syncthreads();
+        buf[t] = v;
+        __syncthreads();
+    }
+    y[row * ldy + g * 256 + t] = buf[t] * (1.0f / 16.0f);
+}
+
+// One element per thread; the rank loop runs in one lane in the reference's
+// order.  B is indexed from the factor's row0.
+__global__ __launch_bounds__(256) void lora_fold_kernel(float* w, int64_t ldw, int64_t rows, int64_t k,
+                                                        const float* A, const float* B, int64_t rank, float scale) {
+    const int64_t total = rows * k;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t o = i / k, c = i - o * k;
+        float acc = w[o * ldw + c];
+        const float* brow = B + o * rank;
+        for (int64_t r = 0; r < rank; r++) {
+            const float br = brow[r];
+            if (br == 0.0f) continue;
+            const float s = scale * br;
+            acc = acc + s * A[r * k + c];
+        }
+        w[o * ldw + c] = acc;
+    }
+}
+
+static unsigned grid_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
+}
+
+hipError_t launch_dequant_rows(hipStream_t stream, const void* src, int kind, int64_t rows, int64_t cols, int64_t lds,
+                               const float* row_scale, int scale_scalar, float* out, int64_t ldo) {
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, stream, src, kind, rows, cols,
+                       lds, row_scale, scale_scalar, out, ldo);
+    return hipGetLastError();
+}
+
+hipError_t launch_convrot_rows(hipStream_t stream, const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows,
+                               int64_t K) {
+    const int64_t gpr = K / 256;
+    hipLaunchKernelGGL(convrot_rows_kernel, dim3((unsigned)(rows * gpr)), dim3(256), 0, stream, x, ldx, y, ldy, gpr);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_fold(hipStream_t stream, float* w, int64_t ldw, int64_t rows, int64_t k, const float* A,
+                            const float* B, int64_t rank, float scale) {
+    hipLaunchKernelGGL(lora_fold_kernel, dim3(grid_for(rows * k)), dim3(256), 0, stream, w, ldw, rows, k, A, B, rank,
+                       scale);
+    return hipGetLastError();
+}
+
+}  // namespace phi_dev

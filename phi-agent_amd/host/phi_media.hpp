@@ -20,6 +20,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace phi::media {
 
@@ -202,9 +203,33 @@ struct QuantLinear {
     bool dense() const { return dtype == DType::F16 || dtype == DType::BF16 || dtype == DType::F32; }
 };
 
+class GpuArena;
+class SafeTensors;
+class LoraSet;
+
+// What a model holds while it runs (core/models/model_common.hpp:51-63): the
+// compute context and three bump arenas.  The weight arena is reset per layer,
+// the activation arena per step, the keep arena holds long-lived buffers.  The
+// reference's upload ring is not needed: uploads here are stream-ordered
+// copies from the checkpoint's mapping.
 struct GpuCtx {
     ComputeContext* ctx = nullptr;
-    bool ok() const { return ctx != nullptr; }
+    GpuArena* wa = nullptr;    // weights, reset per layer
+    GpuArena* aa = nullptr;    // activations, reset per step
+    GpuArena* keep = nullptr;  // long-lived buffers
+    bool ok() const { return ctx && wa && aa; }
+
+    GpuAlloc walloc(u64 bytes);
+    GpuAlloc aalloc(u64 bytes);
+    GpuAlloc kalloc(u64 bytes);
+    // Bytes already in the form the kernels read, into an allocation.
+    void upload_into(const GpuAlloc& a, const void* src, u64 bytes);
+
+    void begin();      // a batch of dispatches (no-op: one stream)
+    void submit();     // fence
+    void new_layer();  // weight arena reset
+    void end_layer();  // submit
+    void new_step();   // activation arena reset
 };
 
 // rotate+quantise x into q8/s8, then the int8 GEMM; out is [m, n] fp32.
@@ -213,43 +238,177 @@ void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 
 
 // ---- loading weights from checkpoints (safetensors.hpp reads the files) ----
 
-class SafeTensors;
-
-// A bump allocator over one device buffer, as the reference's GpuArena hands
-// out weight storage (core/runtime/sched.hpp:27-60): 256-byte aligned pieces,
-// MediaError when full.  Owns the buffer.
+// A bump allocator over device memory chunks, as the reference's GpuArena
+// (core/runtime/sched.hpp:40-100): alloc() hands out aligned pieces (256 bytes
+// by default) and adds a chunk when the current one is full; reset()
+// invalidates every allocation and keeps the chunks; mark() / rewind_to() give
+// back what was allocated after a mark.  Owns its chunks.
 class GpuArena {
 public:
+    struct Mark {
+        size_t chunk = 0;
+        u64 off = 0;
+        u64 used = 0;
+    };
+    GpuArena() = default;
+    // init(&ctx, bytes) with the first chunk allocated now.
     GpuArena(ComputeContext& ctx, u64 bytes);
     ~GpuArena();
     GpuArena(const GpuArena&) = delete;
     GpuArena& operator=(const GpuArena&) = delete;
-    GpuAlloc alloc(u64 bytes);
+
+    void init(ComputeContext* ctx, u64 chunk_bytes = 192ull << 20);
+    // Size of future chunks (0 is ignored).
+    void set_chunk_bytes(u64 chunk_bytes) {
+        if (chunk_bytes) chunk_bytes_ = chunk_bytes;
+    }
+    u64 chunk_bytes() const { return chunk_bytes_; }
+    // Returns every chunk to the device; only legal when nothing in the arena is live.
+    void release_chunks();
+    void destroy() { release_chunks(); }
+    GpuAlloc alloc(u64 bytes, u64 align = 256);
+    void reset();
     u64 used() const { return used_; }
-    u64 capacity() const { return buf_ ? buf_->bytes : 0; }
+    u64 capacity() const { return capacity_; }
+    int chunks() const { return (int)chunks_.size(); }
+    Mark mark() const { return Mark{cur_, cur_off_, used_}; }
+    void rewind_to(const Mark& m);
 
 private:
-    ComputeContext& ctx_;
-    GpuBuffer* buf_ = nullptr;
+    ComputeContext* ctx_ = nullptr;
+    u64 chunk_bytes_ = 192ull << 20;
+    std::vector<GpuBuffer*> chunks_;
+    size_t cur_ = 0;
+    u64 cur_off_ = 0;
     u64 used_ = 0;
+    u64 capacity_ = 0;
 };
 
+// LoRA factor files (core/models/lora.hpp:102-186): per adapted module a
+// rank-r delta  W_eff = W + strength * (alpha / r) * B @ A  (A [r, k], B [n, r]).
+// Keys in the diffusers / peft (lora_A / lora_B), kohya (lora_down / lora_up)
+// and ComfyUI (display-name prefixes) conventions all normalise to the base
+// weight's name without ".weight".  Files are applied in the order added.
+inline constexpr int kMaxLoras = 2;
+inline constexpr i64 kLoraRankBound = 256;
+inline constexpr float kLoraStrengthDefault = 1.0f;
+
+class LoraSet {
+public:
+    // Loads a safetensors LoRA and appends it; MediaError when it holds no
+    // factor pair this loader can map.  strength scales the file's deltas.
+    void add(const std::string& path, float strength = kLoraStrengthDefault);
+    void clear() {
+        files_.clear();
+        paths_.clear();
+    }
+    bool empty() const { return files_.empty(); }
+    size_t size() const { return files_.size(); }
+    const std::vector<std::string>& paths() const { return paths_; }
+
+    // One factor as stored: W_eff = W + scale * b @ a, a [rank, k], b [n, rank],
+    // scale = strength * alpha / rank.
+    struct Delta {
+        i64 n = 0, k = 0, rank = 0;
+        float scale = 1.0f;
+        const float* a = nullptr;
+        const float* b = nullptr;
+    };
+    // Every factor of `target` whose (n, k) is exactly the weight's, in file order.
+    int deltas_for(const std::string& target, i64 n, i64 k, std::vector<Delta>* out) const;
+    // Every factor of `target` with width k covering rows [row0, row0 + rows):
+    // the factors apply_rows folds, in its order.
+    int deltas_for_rows(const std::string& target, i64 row0, i64 rows, i64 k, std::vector<Delta>* out) const;
+    // True if any factor could match `target`.
+    bool touches(const std::string& target) const;
+    // The folds on a host fp32 weight [n, k] (or its rows [row0, row0 + rows)):
+    // w[o][i] += (scale * B[o][r]) * A[r][i], r ascending, B entries of 0 skipped.
+    int apply(const std::string& target, float* w, i64 n, i64 k) const;
+    int apply_rows(const std::string& target, float* w, i64 row0, i64 rows, i64 k) const;
+
+private:
+    struct Factor {
+        std::string target;
+        i64 n = 0, k = 0, rank = 0;
+        float scale = 1.0f;
+        std::vector<float> A;  // [rank, k]
+        std::vector<float> B;  // [n, rank]
+    };
+    struct File {
+        std::string path;
+        float strength = kLoraStrengthDefault;
+        std::vector<Factor> factors;
+    };
+    std::vector<File> files_;
+    std::vector<std::string> paths_;
+};
+
+// A LoRA tensor key -> the module it adapts (no ".weight"), or "" when the key
+// is not a factor or alpha key.
+std::string lora_normalize_target(const std::string& key, bool* is_a, bool* is_b);
+
 // One linear from a checkpoint into the int8 form the GEMM reads
-// (core/models/model_common.cpp:921-1010, without the dense and LoRA-folding
-// branches): int8_tensorwise is uploaded verbatim with its weight_scale; the
-// grouped families (asym_w4a8_int8, w6a8_int8) are uploaded as stored and
-// expanded on the device (w4a8_plan_of / w4a8_pack_rows, :589-748).  Anything
-// else throws MediaError naming the family.
-QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& into);
+// (core/models/model_common.cpp:921-1090).  `into` null allocates from the
+// context's weight arena.
+//   int8_tensorwise: the codes verbatim with their weight_scale;
+//   asym_w4a8_int8 / w6a8_int8: stored parts staged on the device and
+//     expanded there (w4a8_plan_of / w4a8_pack_rows, :589-748);
+//   another integer form (an int8 weight without a convrot sidecar, a bare I4):
+//     decoded and requantised on the device with the reference's requant spec;
+//   a LoRA in `lora` that touches the module is folded first: the weight is
+//     decoded, rotated back to its original basis, the deltas added, then
+//     rotated and quantised (int8_tensorwise sources).
+// Dense float weights (f16 / bf16 / f32 / fp8 / nvfp4) belong to the dense GEMM
+// and throw MediaError naming the precision.
+QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::string& base,
+                              GpuArena* into = nullptr, const LoraSet* lora = nullptr);
+
+// The fused q|k|v form (core/models/model_common.cpp:1414-1578): one [3N, K]
+// int8 matrix whose rows are q then k then v, and the concatenated row scales.
+// Three plain int8 weights are concatenated verbatim; otherwise each part is
+// requantised into its rows (the grouped families through the device expand).
+QuantLinear load_quant3_linear(GpuCtx& g, const SafeTensors& st, const std::string& base_q,
+                               const std::string& base_k, const std::string& base_v,
+                               GpuArena* into = nullptr, const LoraSet* lora = nullptr);
+
+// The streaming int8 upload (core/models/model_common.cpp:1095-1283): a grouped
+// family expanded on the device; an int8_tensorwise weight whose file declares
+// convrot uploaded verbatim; anything else (f16 / bf16 / f32, int8 without a
+// convrot sidecar) decoded and requantised on the device, rotated unless the
+// file says it is stored rotated.  A LoRA that touches the module is folded.
+struct I8Upload {
+    GpuAlloc w, s;
+    i64 n = 0, k = 0;
+};
+I8Upload upload_quant_linear_i8(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& arena,
+                                const LoraSet* lora);
 
 // convrot_w4a4 (signed int4, two per byte, one fp32 scale per row): the packed
 // bytes verbatim for the int4 GEMM (core/models/model_common.cpp:1285-1340);
-// k is the packed width K/2, as the reference's I4Upload records it.
+// k is the packed width K/2, as the reference's I4Upload records it.  A LoRA is
+// not folded into int4 weights: it is applied by the runtime tail.
 struct I4Upload {
     GpuAlloc w, s;
     i64 n = 0, k = 0;
 };
-I4Upload upload_quant_linear_w4a4(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& arena);
+I4Upload upload_quant_linear_w4a4(GpuCtx& g, const SafeTensors& st, const std::string& base, GpuArena& arena,
+                                  const LoraSet* lora = nullptr);
+
+// One module of a (possibly fused) projection: `base` corrects the output rows
+// [row0, row0 + n) of the layer's weight (core/models/model_common.hpp:255-260).
+struct LoraModule {
+    std::string base;
+    i64 row0 = 0;
+    i64 n = 0;
+    const LoraSet* lora = nullptr;
+};
+
+// The runtime correction's operands (core/models/model_common.cpp:1587-1652):
+// every matching factor of every module stacked along the rank axis (A) and
+// placed at its module's output rows with its scale folded in (B).  Inactive
+// when no factor matches; MediaError past kLoraRankBound.
+LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::vector<LoraModule>& mods, i64 n, i64 k);
+LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::string& base, const LoraSet* lora, i64 n, i64 k);
 
 // out [m, t.n] fp32 += (x [m, t.k] fp32 . at^T) . bt^T, with h the caller's
 // [m, rank] fp32 scratch (core/models/model_common.cpp:1667-1700).

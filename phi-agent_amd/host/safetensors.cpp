@@ -234,11 +234,23 @@ bool ends_with(const std::string& s, const char* suf) {
 
 std::string weight_stem(const std::string& name) { return ends_with(name, ".weight") ? name.substr(0, name.size() - 7) : name; }
 
+// The dtype spellings a header may use: the safetensors names plus the torch
+// and short spellings the reference's reader accepts (dtype_from_name,
+// core/util/media_common.cpp:31-44).  I4 / U4 / int4 hold two values per byte;
+// their shape keeps the packed width.  Anything else is unknown, and such an
+// entry is skipped as the reference skips it (core/host/st.cpp:242).
 StDType dtype_of(const std::string& s) {
     static const std::pair<const char*, StDType> table[] = {
-        {"F64", StDType::F64}, {"F32", StDType::F32},   {"F16", StDType::F16},         {"BF16", StDType::BF16},
-        {"I64", StDType::I64}, {"I32", StDType::I32},   {"I16", StDType::I16},         {"I8", StDType::I8},
-        {"U8", StDType::U8},   {"BOOL", StDType::BOOL}, {"F8_E4M3", StDType::F8_E4M3}, {"F8_E5M2", StDType::F8_E5M2}};
+        {"F32", StDType::F32},         {"float32", StDType::F32},      {"float", StDType::F32},
+        {"F16", StDType::F16},         {"float16", StDType::F16},      {"BF16", StDType::BF16},
+        {"bfloat16", StDType::BF16},   {"I8", StDType::I8},            {"int8", StDType::I8},
+        {"U8", StDType::U8},           {"uint8", StDType::U8},         {"I4", StDType::I4},
+        {"int4", StDType::I4},         {"U4", StDType::I4},            {"F8_E4M3", StDType::F8_E4M3},
+        {"float8_e4m3fn", StDType::F8_E4M3}, {"float8_e4m3", StDType::F8_E4M3}, {"F8E4M3", StDType::F8_E4M3},
+        {"e4m3", StDType::F8_E4M3},    {"F8_E5M2", StDType::F8_E5M2},  {"float8_e5m2", StDType::F8_E5M2},
+        {"F8E5M2", StDType::F8_E5M2},  {"e5m2", StDType::F8_E5M2},     {"F64", StDType::F64},
+        {"I64", StDType::I64},         {"I32", StDType::I32},          {"I16", StDType::I16},
+        {"BOOL", StDType::BOOL}};
     for (const auto& e : table)
         if (s == e.first) return e.second;
     return StDType::Unknown;
@@ -296,6 +308,7 @@ const char* st_dtype_name(StDType t) {
         case StDType::BOOL: return "BOOL";
         case StDType::F8_E4M3: return "F8_E4M3";
         case StDType::F8_E5M2: return "F8_E5M2";
+        case StDType::I4: return "I4";
         default: return "?";
     }
 }
@@ -311,6 +324,7 @@ size_t st_dtype_bytes(StDType t) {
         case StDType::I16: return 2;
         case StDType::I8:
         case StDType::U8:
+        case StDType::I4:  // packed: two values per byte, the shape holds bytes
         case StDType::BOOL:
         case StDType::F8_E4M3:
         case StDType::F8_E5M2: return 1;
@@ -378,34 +392,49 @@ SafeTensors::SafeTensors(const std::string& path) : path_(path) {
     if (!JsonReader((const char*)base + 8, (size_t)hlen).parse(h) || h.kind != Json::Obj) fail("malformed header");
     const uint64_t data0 = 8 + hlen, data_bytes = map_bytes_ - data0;
     for (const auto& kv : h.obj) {
-        if (kv.first == "__metadata__") continue;
+        if (kv.first == "__metadata__") {
+            if (kv.second.kind == Json::Obj)
+                for (const auto& m : kv.second.obj)
+                    if (m.second.kind == Json::Str) metadata_[m.first] = m.second.str;
+            continue;
+        }
         const Json& e = kv.second;
+        // As the reference reads a header (core/host/st.cpp:231-271): entries that
+        // are not objects, whose dtype it cannot name or that have no two-element
+        // data_offsets are skipped; a malformed shape or offsets past the data
+        // are errors.
+        if (e.kind != Json::Obj) continue;
         const Json* dt = e.get("dtype");
         const Json* sh = e.get("shape");
         const Json* off = e.get("data_offsets");
-        if (!dt || dt->kind != Json::Str || !sh || sh->kind != Json::Arr || !off || off->kind != Json::Arr ||
-            off->arr.size() != 2)
-            fail("entry '" + kv.first + "' is malformed");
+        if (!dt || dt->kind != Json::Str) continue;
         StTensor t;
         t.name = kv.first;
         t.dtype = dtype_of(dt->str);
+        if (t.dtype == StDType::Unknown) continue;
+        if (!off || off->kind != Json::Arr || off->arr.size() != 2) continue;
+        if (!sh || sh->kind != Json::Arr) fail("entry '" + kv.first + "' has no shape");
         t.numel = 1;
         for (const Json& d : sh->arr) {
             if (d.kind != Json::Num || !d.integral || d.inum < 0) fail("entry '" + kv.first + "' has a bad shape");
             t.shape.push_back(d.inum);
-            t.numel *= d.inum;
+            if (__builtin_mul_overflow(t.numel, d.inum, &t.numel))
+                fail("entry '" + kv.first + "' has a shape whose element count overflows");
         }
         if (!off->arr[0].integral || !off->arr[1].integral) fail("entry '" + kv.first + "' has bad offsets");
         const int64_t b = off->arr[0].inum, en = off->arr[1].inum;
         if (b < 0 || en < b || (uint64_t)en > data_bytes) fail("entry '" + kv.first + "' lies outside the file");
         t.offset = data0 + (uint64_t)b;
         t.nbytes = (uint64_t)(en - b);
-        if (t.dtype != StDType::Unknown && (uint64_t)t.numel * st_dtype_bytes(t.dtype) != t.nbytes)
+        uint64_t want = 0;
+        if (__builtin_mul_overflow((uint64_t)t.numel, (uint64_t)st_dtype_bytes(t.dtype), &want) || want != t.nbytes)
             fail("entry '" + kv.first + "' has " + std::to_string(t.nbytes) + " bytes for " +
                  std::to_string(t.numel) + " " + st_dtype_name(t.dtype) + " values");
         t.data = base + t.offset;
+        if (!tensors_.count(t.name)) order_.push_back(t.name);
         tensors_[t.name] = std::move(t);
     }
+    if (tensors_.empty()) fail("no readable tensors");
 }
 
 SafeTensors::~SafeTensors() {
@@ -471,6 +500,8 @@ int64_t SafeTensors::logical_cols(const StTensor& t) const {
     const WeightLayout L = weight_layout(t.name);
     if (L.packed && L.bits > 0) return stored * 8 / L.bits;
     if (L.spec.valid && L.spec.format == "convrot_w4a4") return stored * 2;
+    // A bare packed int4 (I4 / U4 with no sidecar): two values per byte along K.
+    if (t.dtype == StDType::I4) return stored * 2;
     return stored;
 }
 
@@ -480,6 +511,32 @@ bool SafeTensors::is_plain_int8(const StTensor& t) const {
     if (L.packed || L.rel_scale) return false;
     if (L.spec.valid && !L.spec.format.empty() && L.spec.format != "int8_tensorwise") return false;
     return find(weight_stem(t.name) + ".weight_scale") != nullptr;
+}
+
+std::vector<float> SafeTensors::to_f32(const StTensor& t) const {
+    std::vector<float> v((size_t)t.numel);
+    for (int64_t i = 0; i < t.numel; i++) {
+        switch (t.dtype) {
+            case StDType::F32: std::memcpy(&v[(size_t)i], t.data + 4 * i, 4); break;
+            case StDType::F16: {
+                uint16_t h;
+                std::memcpy(&h, t.data + 2 * i, 2);
+                v[(size_t)i] = half_bits_to_f32(h);
+                break;
+            }
+            case StDType::BF16: {
+                uint16_t h;
+                std::memcpy(&h, t.data + 2 * i, 2);
+                const uint32_t u = (uint32_t)h << 16;
+                std::memcpy(&v[(size_t)i], &u, 4);
+                break;
+            }
+            case StDType::F8_E4M3: v[(size_t)i] = f8_to_f32(t.data[i], true); break;
+            case StDType::F8_E5M2: v[(size_t)i] = f8_to_f32(t.data[i], false); break;
+            default: throw MediaError("'" + t.name + "': " + st_dtype_name(t.dtype) + " is not a float tensor");
+        }
+    }
+    return v;
 }
 
 float SafeTensors::row_scale_value(const StTensor& scale, int64_t row) const {

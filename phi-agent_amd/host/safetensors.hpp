@@ -23,7 +23,8 @@
 
 namespace phi::media {
 
-enum class StDType { Unknown, F64, F32, F16, BF16, I64, I32, I16, I8, U8, BOOL, F8_E4M3, F8_E5M2 };
+// I4 is a packed dtype: two signed nibbles per byte, the shape holds the bytes.
+enum class StDType { Unknown, F64, F32, F16, BF16, I64, I32, I16, I8, U8, BOOL, F8_E4M3, F8_E5M2, I4 };
 
 const char* st_dtype_name(StDType t);
 size_t st_dtype_bytes(StDType t);
@@ -70,6 +71,12 @@ public:
     const StTensor& require(const std::string& name) const;
     const std::map<std::string, StTensor>& tensors() const { return tensors_; }
     const std::string& path() const { return path_; }
+    // Names of the readable entries in header order, and the header's
+    // __metadata__ strings (core/host/st.cpp:231-241).
+    const std::vector<std::string>& names() const { return order_; }
+    const std::map<std::string, std::string>& metadata() const { return metadata_; }
+    // Every value of a float tensor (F32 / F16 / BF16 / F8) as fp32, exactly.
+    std::vector<float> to_f32(const StTensor& t) const;
 
     // The comfy_quant spec of a weight ("<base>.weight" -> "<base>.comfy_quant").
     QuantSpec quant_spec_of(const std::string& weight_name) const;
@@ -104,6 +111,8 @@ private:
     void* map_ = nullptr;
     size_t map_bytes_ = 0;
     std::map<std::string, StTensor> tensors_;
+    std::vector<std::string> order_;
+    std::map<std::string, std::string> metadata_;
 };
 
 }  // namespace phi::media

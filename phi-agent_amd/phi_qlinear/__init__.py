@@ -25,7 +25,7 @@ MEDIA_LIB_PATH = os.path.join(LIB_DIR, "libphi_media.so")
 INCLUDE_DIR = os.path.join(os.path.dirname(os.path.dirname(PKG_DIR)), "include")
 
 # phi_dtype
-F32, BF16, F16, I32, I8, F8_E4M3, F8_E5M2, U8_E4M3 = range(8)
+F32, BF16, F16, I32, I8, F8_E4M3, F8_E5M2, U8_E4M3, I4 = range(9)
 # phi_round
 ROUND_HALF_AWAY, ROUND_HALF_EVEN = 0, 1
 ACT_GELU_TANH, ACT_SILU_GATE = 1, 2
@@ -64,7 +64,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_gemv_workspace_bytes", "phi_hip_gelu_tanh", "phi_hip_w4a8_workspace_bytes",
            "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual", "phi_hip_quant_rotate_act",
            "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
-           "phi_hip_lora_down", "phi_hip_lora_rank_add"]
+           "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
+           "phi_hip_lora_fold"]
 
 _lib = None
 
@@ -107,6 +108,9 @@ def load() -> ctypes.CDLL:
     L.phi_hip_lora_down.argtypes = [P, P, I, I64, I64, I64, P, I64, P]
     L.phi_hip_lora_rank_add.argtypes = [P, P, P, P, I, I64, I64, I64, I64]
     L.phi_hip_i4_workspace_bytes.restype = SZ
+    L.phi_hip_dequant_rows.argtypes = [P, P, I, I64, I64, I64, P, I, P, I64]
+    L.phi_hip_convrot_rows.argtypes = [P, P, I64, I64, I64, P, I64]
+    L.phi_hip_lora_fold.argtypes = [P, P, I64, I64, I64, P, P, I64, F]
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:

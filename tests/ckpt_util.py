@@ -34,3 +34,36 @@ def run(*args, check=True):
 
 def probe(path: str, base: str) -> dict:
     return json.loads(run("probe", path, base).stdout)
+
+
+def write_raw(path: str, entries, metadata=None) -> str:
+    """A safetensors file written by hand, so the header can use any dtype
+    spelling, shape or offsets.  entries: (name, dtype string, shape,
+    payload bytes or None for a header-only entry, extra header fields)."""
+    header, blobs, off = {}, [], 0
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for e in entries:
+        name, dt, shape, payload = e[:4]
+        extra = e[4] if len(e) > 4 else {}
+        ent = {"dtype": dt, "shape": list(shape)}
+        if payload is not None:
+            ent["data_offsets"] = [off, off + len(payload)]
+            blobs.append(payload)
+            off += len(payload)
+        ent.update(extra)
+        header[name] = ent
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little"))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+    return path
+
+
+def lora_file(path: str, tensors: dict, metadata=None) -> str:
+    """A LoRA factor file (safetensors, optional string metadata)."""
+    save_file({k: v.contiguous() for k, v in tensors.items()}, path, metadata=metadata)
+    return path

@@ -358,6 +358,120 @@ static void test_errors(ComputeContext& ctx) {
     printf("error contract: %s\n", failures ? "mismatch" : "ok");
 }
 
+// dispatch_int8_gemm at K values the MFMA tiles do not divide and at byte
+// offsets that are not multiples of 16 (the reference sends these to its dp4a
+// kernel, core/runtime/compute.cpp:566-575): int32-exact accumulators and the
+// reference's fp32 epilogue, bit for bit against the oracle.
+static void test_any_k_gemm(ComputeContext& ctx) {
+    std::mt19937 rng(11);
+    std::uniform_int_distribution<int> ud(-127, 127);
+    std::uniform_real_distribution<float> us(0.001f, 0.01f);
+    std::normal_distribution<float> nd(0.0f, 0.02f);
+    const i64 ks[] = {32, 96, 100, 3000, 64, 1};
+    const u64 aoffs[] = {1, 3, 16, 7, 5, 0};
+    const u64 boffs[] = {3, 0, 5, 1, 2, 9};
+    int cases = 0;
+    for (int t = 0; t < 6; t++) {
+        const i64 m = 37 + 20 * t, n = 45 + 31 * t, k = ks[t];
+        std::vector<int8_t> a(m * k), b(n * k);
+        std::vector<float> sa(m), sb(n), bias(n);
+        for (auto& v : a) v = (int8_t)ud(rng);
+        for (auto& v : b) v = (int8_t)ud(rng);
+        for (auto& v : sa) v = us(rng);
+        for (auto& v : sb) v = us(rng);
+        for (auto& v : bias) v = nd(rng);
+        const u64 o_a = aoffs[t], o_b = (((o_a + m * k) + 255) & ~(u64)255) + boffs[t];
+        const u64 o_sa = ((o_b + n * k) + 255) & ~(u64)255, o_sb = o_sa + ((m * 4 + 255) & ~(u64)255),
+                  o_bias = o_sb + ((n * 4 + 255) & ~(u64)255), o_c = o_bias + ((n * 4 + 255) & ~(u64)255);
+        GpuBuffer* pool = ctx.create_device_buffer(o_c + (u64)m * n * 4 + 256);
+        ctx.upload(pool, a.data(), a.size(), o_a);
+        ctx.upload(pool, b.data(), b.size(), o_b);
+        ctx.upload(pool, sa.data(), sa.size() * 4, o_sa);
+        ctx.upload(pool, sb.data(), sb.size() * 4, o_sb);
+        ctx.upload(pool, bias.data(), bias.size() * 4, o_bias);
+        for (int with_bias = 0; with_bias < 2; with_bias++) {
+            Int8GemmArgs ga;
+            ga.a = pool;
+            ga.a_offset = o_a;
+            ga.b = pool;
+            ga.b_offset = o_b;
+            ga.sa = pool;
+            ga.sa_offset = o_sa;
+            ga.sb = pool;
+            ga.sb_offset = o_sb;
+            ga.c = pool;
+            ga.c_offset = o_c;
+            if (with_bias) {
+                ga.bias = pool;
+                ga.bias_offset = o_bias;
+            }
+            ga.M = m;
+            ga.N = n;
+            ga.K = k;
+            ctx.begin();
+            dispatch_int8_gemm(ctx, ga);
+            ctx.submit();
+            std::vector<float> c(m * n), want(m * n);
+            std::vector<int32_t> acc(m * n);
+            ctx.download(pool, c.data(), c.size() * 4, o_c);
+            orc_gemm_i8_i32(a.data(), k, b.data(), k, m, n, k, acc.data());
+            orc_epilogue(acc.data(), m, n, sa.data(), sb.data(), 0, with_bias ? bias.data() : nullptr,
+                         with_bias ? ORC_F32 : -1, 1, want.data(), ORC_F32);
+            CHECK(memcmp(c.data(), want.data(), c.size() * 4) == 0,
+                  "any-K gemm K=%lld a_off=%llu b_off=%llu bias=%d differs", (long long)k, (unsigned long long)o_a,
+                  (unsigned long long)o_b, with_bias);
+            cases++;
+        }
+        ctx.release_buffer(pool);
+    }
+    printf("any-K int8 gemm: %d cases %s\n", cases, failures ? "mismatch" : "bit-exact");
+}
+
+// GpuArena as the reference's (core/runtime/sched.hpp:40-100): aligned pieces,
+// a new chunk when one is full, reset keeps the chunks, rewind to a mark; and
+// GpuCtx's arenas.
+static void test_arena(ComputeContext& ctx) {
+    GpuArena a;
+    a.init(&ctx, 1 << 20);
+    const GpuAlloc p = a.alloc(100);
+    const GpuAlloc q = a.alloc(1000, 1024);
+    CHECK(p.off == 0 && q.res == p.res && q.off == 1024, "arena alignment: offsets %llu %llu",
+          (unsigned long long)p.off, (unsigned long long)q.off);
+    CHECK(a.chunks() == 1 && a.capacity() == (1u << 20), "arena: one chunk of the chunk size");
+    const GpuArena::Mark m = a.mark();
+    const GpuAlloc big = a.alloc(3u << 20);
+    CHECK(a.chunks() == 2 && big.res != p.res && big.off == 0 && big.res->bytes >= (3u << 20),
+          "arena: a request past the chunk size gets its own chunk");
+    a.rewind_to(m);
+    const GpuAlloc r = a.alloc(64);
+    CHECK(r.res == p.res && r.off == 2048, "arena: rewind returns to the mark (off %llu)", (unsigned long long)r.off);
+    a.reset();
+    CHECK(a.used() == 0 && a.chunks() == 2, "arena: reset keeps the chunks");
+    const GpuAlloc s2 = a.alloc(2u << 20);
+    CHECK(s2.res == big.res && a.chunks() == 2, "arena: a reset arena reuses a later chunk that fits");
+    GpuArena wa, aa;
+    wa.init(&ctx, 1 << 16);
+    aa.init(&ctx, 1 << 16);
+    GpuCtx g;
+    g.ctx = &ctx;
+    CHECK(!g.ok(), "GpuCtx without arenas is not ok");
+    g.wa = &wa;
+    g.aa = &aa;
+    CHECK(g.ok(), "GpuCtx with both arenas is ok");
+    const GpuAlloc w1 = g.walloc(4096), a1 = g.aalloc(4096), k1 = g.kalloc(16);
+    CHECK(w1.res != a1.res && k1.res == a1.res, "GpuCtx: weights and activations in their own arenas");
+    const float v[4] = {1.f, 2.f, 3.f, 4.f};
+    float back[4] = {};
+    g.upload_into(w1, v, sizeof v);
+    ctx.download(w1.res, back, sizeof back, w1.off);
+    CHECK(memcmp(v, back, sizeof v) == 0, "GpuCtx::upload_into");
+    g.new_layer();
+    CHECK(wa.used() == 0 && aa.used() > 0, "new_layer resets the weight arena only");
+    g.new_step();
+    CHECK(aa.used() == 0, "new_step resets the activation arena");
+    printf("arena and context: %s\n", failures ? "mismatch" : "ok");
+}
+
 int main() {
     try {
         ComputeContext ctx(0);
@@ -367,6 +481,8 @@ int main() {
         test_activations(ctx);
         test_int4_gemm(ctx);
         test_lora_tail(ctx);
+        test_any_k_gemm(ctx);
+        test_arena(ctx);
     } catch (const std::exception& e) {
         printf("FAIL exception: %s\n", e.what());
         return 1;

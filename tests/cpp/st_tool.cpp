@@ -9,6 +9,15 @@
 //        load_quant_linear, then linear_gemm of x [M, K] fp32 into out [M, N] fp32 (GPU)
 //   st_tool int4 <file> <base> <x.f32> <M> <out.f32>
 //        upload_quant_linear_w4a4, quant_convrot (qmax 7), int4 GEMM into out (GPU)
+//   st_tool weights <how> <file> <out.bin> <base> [<base_k> <base_v>] [lora <path> <strength>]...
+//        how = load (load_quant_linear), load3 (load_quant3_linear) or upload_i8
+//        (upload_quant_linear_i8), with an optional LoraSet; writes n, k (int64)
+//        then the int8 weight [n, k] and its fp32 scales [n] (GPU)
+//   st_tool lora_probe <target> <n> <k> lora <path> <strength>...
+//        LoraSet::touches / deltas_for -> JSON line (no GPU)
+//   st_tool tail <out.bin> <n> <k> <base>:<row0>:<rows>... lora <path> <strength>...
+//        load_lora_tail over the modules; writes rank (int64), at [rank, k] and
+//        bt [n, rank] fp32 (GPU)
 // Exit code 0 on success; a MediaError prints "error: <message>" and exits 3.
 #include <cstdio>
 #include <cstdlib>
@@ -40,6 +49,107 @@ static void write_f32(const char* path, const std::vector<float>& v) {
     fclose(f);
 }
 
+static void write_bytes(FILE* f, const void* p, size_t n) {
+    if (fwrite(p, 1, n, f) != n) throw MediaError("short write");
+}
+
+// Splits trailing "lora <path> <strength>" triples off argv[from..argc).
+static int lora_args(int argc, char** argv, int from, LoraSet& lora) {
+    int end = argc;
+    for (int i = from; i < argc; i++)
+        if (std::string(argv[i]) == "lora") {
+            if (end == argc) end = i;
+            if (i + 2 >= argc) throw MediaError("lora needs <path> <strength>");
+            lora.add(argv[i + 1], (float)atof(argv[i + 2]));
+            i += 2;
+        }
+    return end;
+}
+
+static int weights(int argc, char** argv) {
+    const std::string how = argv[2];
+    SafeTensors st(argv[3]);
+    const char* out = argv[4];
+    LoraSet lora;
+    const int end = lora_args(argc, argv, 5, lora);
+    const LoraSet* lp = lora.empty() ? nullptr : &lora;
+    ComputeContext ctx(0);
+    GpuArena wa, aa;
+    wa.init(&ctx, 64ull << 20);
+    aa.init(&ctx, 1 << 20);
+    GpuCtx g;
+    g.ctx = &ctx;
+    g.wa = &wa;
+    g.aa = &aa;
+    GpuAlloc w, s;
+    i64 n = 0, k = 0;
+    if (how == "load" && end == 6) {
+        const QuantLinear q = load_quant_linear(g, st, argv[5], nullptr, lp);
+        w = q.w, s = q.scale, n = q.n, k = q.k;
+    } else if (how == "load3" && end == 8) {
+        const QuantLinear q = load_quant3_linear(g, st, argv[5], argv[6], argv[7], nullptr, lp);
+        w = q.w, s = q.scale, n = q.n, k = q.k;
+    } else if (how == "upload_i8" && end == 6) {
+        const I8Upload u = upload_quant_linear_i8(g, st, argv[5], wa, lp);
+        w = u.w, s = u.s, n = u.n, k = u.k;
+    } else {
+        fprintf(stderr, "st_tool weights: bad arguments\n");
+        return 2;
+    }
+    ctx.submit();
+    std::vector<int8_t> wq((size_t)(n * k));
+    std::vector<float> sc((size_t)n);
+    ctx.download(w.res, wq.data(), wq.size(), w.off);
+    ctx.download(s.res, sc.data(), sc.size() * 4, s.off);
+    FILE* f = fopen(out, "wb");
+    if (!f) throw MediaError(std::string("cannot write ") + out);
+    write_bytes(f, &n, 8);
+    write_bytes(f, &k, 8);
+    write_bytes(f, wq.data(), wq.size());
+    write_bytes(f, sc.data(), sc.size() * 4);
+    fclose(f);
+    printf("{\"n\": %lld, \"k\": %lld, \"arena_used\": %llu}\n", (long long)n, (long long)k,
+           (unsigned long long)wa.used());
+    return 0;
+}
+
+static int tail(int argc, char** argv) {
+    const char* out = argv[2];
+    const i64 n = atoll(argv[3]), k = atoll(argv[4]);
+    LoraSet lora;
+    const int end = lora_args(argc, argv, 5, lora);
+    std::vector<LoraModule> mods;
+    for (int i = 5; i < end; i++) {
+        const std::string spec = argv[i];
+        const size_t a = spec.find(':'), b = spec.rfind(':');
+        if (a == std::string::npos || a == b) throw MediaError("module spec is base:row0:rows");
+        mods.push_back(LoraModule{spec.substr(0, a), atoll(spec.substr(a + 1, b - a - 1).c_str()),
+                                  atoll(spec.substr(b + 1).c_str()), &lora});
+    }
+    ComputeContext ctx(0);
+    GpuArena arena;
+    arena.init(&ctx, 16ull << 20);
+    GpuCtx g;
+    g.ctx = &ctx;
+    const LoraTail t = load_lora_tail(g, arena, mods, n, k);
+    ctx.submit();
+    FILE* f = fopen(out, "wb");
+    if (!f) throw MediaError(std::string("cannot write ") + out);
+    const i64 rank = t.active ? t.rank : 0;
+    write_bytes(f, &rank, 8);
+    if (rank > 0) {
+        std::vector<float> at((size_t)(rank * k)), bt((size_t)(n * rank));
+        ctx.download(t.at.res, at.data(), at.size() * 4, t.at.off);
+        ctx.download(t.bt.res, bt.data(), bt.size() * 4, t.bt.off);
+        write_bytes(f, at.data(), at.size() * 4);
+        write_bytes(f, bt.data(), bt.size() * 4);
+    }
+    fclose(f);
+    printf("{\"rank\": %lld, \"touches\": %s}\n", (long long)rank,
+           mods.empty() ? "false" : (lora.touches(mods[0].base) ? "true" : "false"));
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc < 3) {
         fprintf(stderr, "usage: st_tool spec|probe|linear|int4 ...\n");
@@ -50,6 +160,21 @@ int main(int argc, char** argv) {
         if (op == "spec") {
             const std::string text = argv[2];
             print_spec(parse_quant_spec(text.data(), text.size()), "\n");
+            return 0;
+        }
+        if (op == "weights" && argc >= 6) return weights(argc, argv);
+        if (op == "tail" && argc >= 6) return tail(argc, argv);
+        if (op == "lora_probe" && argc >= 8) {
+            LoraSet lora;
+            lora_args(argc, argv, 5, lora);
+            std::vector<LoraSet::Delta> d;
+            lora.deltas_for(argv[2], atoll(argv[3]), atoll(argv[4]), &d);
+            printf("{\"files\": %zu, \"touches\": %s, \"deltas\": [", lora.size(),
+                   lora.touches(argv[2]) ? "true" : "false");
+            for (size_t i = 0; i < d.size(); i++)
+                printf("%s{\"rank\": %lld, \"scale\": %.9g, \"a0\": %.9g, \"b0\": %.9g}", i ? ", " : "",
+                       (long long)d[i].rank, d[i].scale, d[i].a[0], d[i].b[0]);
+            printf("]}\n");
             return 0;
         }
         if (argc < 4) return 2;
@@ -71,7 +196,7 @@ int main(int argc, char** argv) {
             fflush(stdout);
             return 0;
         }
-        if ((op == "linear" || op == "int4") && argc == 7) {
+        if ((op == "linear" && argc >= 7 && (argc - 7) % 2 == 0) || (op == "int4" && argc == 7)) {
             const i64 M = atoll(argv[5]);
             ComputeContext ctx(0);
             GpuCtx g;
@@ -80,12 +205,18 @@ int main(int argc, char** argv) {
             const i64 K = st.logical_cols(t), N = t.shape[0];
             std::vector<float> x = read_f32(argv[4], (size_t)(M * K)), y((size_t)(M * N));
             GpuArena arena(ctx, (u64)(N * K + N * 4 + 1024));
+            GpuArena acts;
+            acts.init(&ctx, 1 << 20);
+            g.wa = &arena;
+            g.aa = &acts;
             GpuBuffer* work = ctx.create_device_buffer((u64)(M * K * 4 + M * K + M * 4 + M * N * 4 + 4096));
             const u64 o_x = 0, o_q = (u64)M * K * 4, o_s = (o_q + M * K + 255) & ~(u64)255,
                       o_y = (o_s + M * 4 + 255) & ~(u64)255;
             ctx.upload(work, x.data(), x.size() * 4, o_x);
             if (op == "linear") {
-                const QuantLinear ql = load_quant_linear(g, st, base, arena);
+                LoraSet lora;
+                for (int i = 7; i + 1 < argc; i += 2) lora.add(argv[i], (float)atof(argv[i + 1]));
+                const QuantLinear ql = load_quant_linear(g, st, base, nullptr, lora.empty() ? nullptr : &lora);
                 linear_gemm(g, ql, GpuAlloc{work, o_x, (u64)M * K * 4}, M, K, GpuAlloc{work, o_y, (u64)M * N * 4},
                             GpuAlloc{work, o_q, (u64)M * K}, GpuAlloc{work, o_s, (u64)M * 4});
             } else {

@@ -134,3 +134,91 @@ def test_malformed_files(tmp_path):
         assert out.returncode == 3 and out.stdout.startswith("error: safetensors"), (name, out.stdout)
     out = C.run("probe", path, "nope", check=False)
     assert out.returncode == 3 and "tensor not found: nope.weight" in out.stdout
+
+
+def test_dtype_spellings_and_skipped_entries(tmp_path):
+    """The header spellings the reference's reader accepts
+    (dtype_from_name, core/util/media_common.cpp:31-44): torch names
+    (float8_e4m3fn, bfloat16, int8) and the packed I4; entries whose dtype it
+    cannot name, or without data_offsets, are skipped (core/host/st.cpp:242,
+    :257), not errors."""
+    N, K = 8, 512
+    g = torch.Generator().manual_seed(4)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sc = (torch.rand(N, generator=g) * 4 + 0.5).to(torch.float8_e4m3fn)
+    path = C.write_raw(str(tmp_path / "sp.safetensors"), [
+        ("a.weight", "int8", (N, K), w.numpy().tobytes()),
+        ("a.weight_scale", "float8_e4m3fn", (N,), sc.view(torch.uint8).numpy().tobytes()),
+        ("junk.x", "complex64", (2,), b"\0" * 16),
+        ("nodata.x", "F32", (2,), None),
+        ("b.weight", "I4", (N, K // 2), bytes(range(256)) * (N * K // 2 // 256)),
+        ("b.weight_scale", "bfloat16", (N,), torch.ones(N, dtype=torch.bfloat16).view(torch.int16).numpy().tobytes()),
+    ])
+    p = C.probe(path, "a")
+    assert p["tensors"] == 4, p  # complex64 and the offset-less entry are skipped
+    assert p["dtype"] == "I8" and p["plain_int8"] and (p["n"], p["k"]) == (N, K)
+    assert np.float32(p["row_scale0"]) == np.float32(sc[0].float().item())
+    q = C.probe(path, "b")
+    assert q["dtype"] == "I4" and (q["n"], q["k"]) == (N, K), q  # two values per packed byte
+    out = C.run("probe", path, "junk", check=False)
+    assert out.returncode == 3 and "tensor not found" in out.stdout
+
+
+def test_header_overflow_is_refused(tmp_path):
+    """A shape whose element count wraps 64 bits must not pass the size check."""
+    path = C.write_raw(str(tmp_path / "ov.safetensors"), [
+        ("o.weight", "I8", (2 ** 32, 2 ** 32), b""),
+        ("o.weight_scale", "F32", (1,), b"\0\0\x80\x3f"),
+    ])
+    out = C.run("probe", path, "o", check=False)
+    assert out.returncode == 3 and "overflows" in out.stdout, out.stdout
+    path = C.write_raw(str(tmp_path / "ov2.safetensors"), [
+        ("o.weight", "F32", (2 ** 62,), b""),
+    ])
+    out = C.run("probe", path, "o", check=False)
+    assert out.returncode == 3 and "error: safetensors" in out.stdout, out.stdout
+
+
+def lora_probe(target, n, k, *files):
+    args = ["lora_probe", target, n, k]
+    for path, strength in files:
+        args += ["lora", path, strength]
+    return json.loads(C.run(*args).stdout)
+
+
+def test_lora_key_conventions(tmp_path):
+    """The three key conventions normalise to the module name
+    (core/models/lora.cpp:14-84), alpha from a per-module tensor, then the file
+    metadata, then the rank; strength multiplies the delta's scale."""
+    n, k, r = 16, 64, 4
+    g = torch.Generator().manual_seed(2)
+    A = torch.randn(r, k, generator=g)
+    B = torch.randn(n, r, generator=g)
+    peft = C.lora_file(str(tmp_path / "peft.safetensors"), {
+        "diffusion_model.blocks.0.attn.to_q.lora_A.weight": A,
+        "diffusion_model.blocks.0.attn.to_q.lora_B.weight": B})
+    # kohya's lora_unet_ form: every '_' of the module path stands for '.'
+    kohya = C.lora_file(str(tmp_path / "kohya.safetensors"), {
+        "lora_unet_blocks_0_attn_qkv.lora_down.weight": A * 2,
+        "lora_unet_blocks_0_attn_qkv.lora_up.weight": B,
+        "lora_unet_blocks_0_attn_qkv.alpha": torch.tensor(2.0)})
+    meta = C.lora_file(str(tmp_path / "meta.safetensors"), {
+        "transformer.blocks.0.attn.to_q.lora_A.weight": A,
+        "transformer.blocks.0.attn.to_q.lora_B.weight": B}, metadata={"ss_network_alpha": "8"})
+    p = lora_probe("blocks.0.attn.to_q", n, k, (peft, 1.0))
+    assert p["touches"] and len(p["deltas"]) == 1
+    d = p["deltas"][0]
+    assert d["rank"] == r and np.float32(d["scale"]) == np.float32(1.0)  # alpha = rank
+    assert np.float32(d["a0"]) == A[0, 0].item() and np.float32(d["b0"]) == B[0, 0].item()
+    p = lora_probe("blocks.0.attn.qkv", n, k, (kohya, 0.5))
+    assert np.float32(p["deltas"][0]["scale"]) == np.float32(0.5 * 2.0 / r)
+    assert np.float32(p["deltas"][0]["a0"]) == np.float32(2 * A[0, 0].item())
+    p = lora_probe("model.blocks.0.attn.to_q", n, k, (meta, 1.0), (peft, -1.0))
+    assert p["touches"] and [np.float32(x["scale"]) for x in p["deltas"]] == [np.float32(2.0), np.float32(-1.0)]
+    # a factor whose shape disagrees with the weight is never returned
+    p = lora_probe("blocks.0.attn.to_q", n + 1, k, (peft, 1.0))
+    assert p["touches"] and p["deltas"] == []
+    assert not lora_probe("blocks.0.attn.to_k", n, k, (peft, 1.0))["touches"]
+    empty = C.lora_file(str(tmp_path / "none.safetensors"), {"x.weight": torch.zeros(2)})
+    out = C.run("lora_probe", "t", 1, 1, "lora", empty, 1.0, check=False)
+    assert out.returncode == 3 and "holds no A/B factor pairs" in out.stdout

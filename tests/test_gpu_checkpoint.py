@@ -7,6 +7,7 @@ stored codes and scales.  asym_w4a8_int8 / w6a8_int8: the oracle's decode +
 row requantise (core/host/quant.cpp:315-389) of the stored codes, relative
 scales, channel scale, codebook and correction, then the W8A8 linear.
 convrot_w4a4: quantise with qmax 7, then the int4 GEMM."""
+import json
 import os
 
 import numpy as np
@@ -114,7 +115,7 @@ def test_unsupported_families_are_named(dev, tmp_path):
     np.zeros((4, 256), np.float32).tofile(xf)
     dense = C.write(str(tmp_path / "d.safetensors"), {"d.weight": torch.randn(8, 256)})
     out = C.run("linear", dense, "d", xf, 4, str(tmp_path / "y.f32"), check=False)
-    assert out.returncode == 3 and "F32 without a comfy_quant spec" in out.stdout
+    assert out.returncode == 3 and "is f32: a dense float weight runs the dense GEMM" in out.stdout
     w4a4 = C.write(str(tmp_path / "e.safetensors"), {
         "e.weight": torch.zeros(8, 128, dtype=torch.int8), "e.weight_scale": torch.ones(8),
         "e.comfy_quant": C.comfy_blob({"format": "convrot_w4a4"})})
@@ -125,3 +126,238 @@ def test_unsupported_families_are_named(dev, tmp_path):
         "f.comfy_quant": C.comfy_blob({"format": "asym_w4a8_int8", "group_size": 64})})
     out = C.run("linear", bad, "f", xf, 4, str(tmp_path / "y.f32"), check=False)
     assert out.returncode == 3 and "weight_s_rel is not [N, K/group]" in out.stdout
+
+
+# ---------------------------------------------------------------- the loaders' other paths
+import struct  # noqa: E402
+
+
+def loaded(tmp_path, how, path, *bases, loras=()):
+    """st_tool weights: the int8 weight and row scales a loader produced."""
+    out = str(tmp_path / f"{how}.bin")
+    args = ["weights", how, path, out, *bases]
+    for lp, strength in loras:
+        args += ["lora", lp, strength]
+    C.run(*args)
+    raw = open(out, "rb").read()
+    n, k = struct.unpack("<qq", raw[:16])
+    q = np.frombuffer(raw[16:16 + n * k], np.int8).reshape(n, k)
+    s = np.frombuffer(raw[16 + n * k:16 + n * k + 4 * n], np.float32)
+    return q, s
+
+
+def int8_weight_tensors(prefix, N, K, seed, convrot=True, spec=True):
+    g = torch.Generator().manual_seed(seed)
+    t = {f"{prefix}.weight": torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8),
+         f"{prefix}.weight_scale": torch.rand(N, generator=g) * 0.004 + 0.001}
+    if spec:
+        t[f"{prefix}.comfy_quant"] = C.comfy_blob({"format": "int8_tensorwise", "convrot": convrot,
+                                                   "convrot_groupsize": 256})
+    return t
+
+
+def dequant_i8(t, prefix):
+    """SafeTensors::dequant_rows of an int8 weight: (float)q * s per row."""
+    return t[f"{prefix}.weight"].numpy().astype(np.float32) * t[f"{prefix}.weight_scale"].numpy()[:, None]
+
+
+def grouped_weight_tensors(prefix, N, K, group, seed):
+    g = torch.Generator().manual_seed(seed)
+    return {f"{prefix}.weight": torch.randint(-128, 128, (N, K // 2), generator=g, dtype=torch.int8),
+            f"{prefix}.weight_s_rel": (torch.rand(N, K // group, generator=g) * 6 + 0.5).to(torch.float16),
+            f"{prefix}.weight_s_channel": torch.rand(N, generator=g) * 0.01 + 0.001,
+            f"{prefix}.comfy_quant": C.comfy_blob({"format": "asym_w4a8_int8", "group_size": group,
+                                                   "convrot_groupsize": 256})}
+
+
+def oracle_grouped(orc, t, prefix, K, group):
+    return orc.w4a8_expand(t[f"{prefix}.weight"].view(torch.uint8).numpy(),
+                           t[f"{prefix}.weight_s_rel"].view(torch.int16).numpy().view(np.uint16), Q.F16,
+                           t[f"{prefix}.weight_s_channel"].numpy(), k=K, group=group)
+
+
+def test_load3_int8_concatenates(dev, tmp_path):
+    """Three int8_tensorwise weights: rows q then k then v, scales likewise,
+    verbatim (core/models/model_common.cpp:1457-1480)."""
+    K = 512
+    t = {**int8_weight_tensors("a.to_q", 96, K, 1), **int8_weight_tensors("a.to_k", 32, K, 2),
+         **int8_weight_tensors("a.to_v", 64, K, 3)}
+    path = C.write(str(tmp_path / "qkv.safetensors"), t)
+    q, s = loaded(tmp_path, "load3", path, "a.to_q", "a.to_k", "a.to_v")
+    want_q = np.concatenate([t[f"a.to_{x}.weight"].numpy() for x in "qkv"])
+    want_s = np.concatenate([t[f"a.to_{x}.weight_scale"].numpy() for x in "qkv"])
+    assert np.array_equal(q, want_q) and np.array_equal(s.view(np.uint32), want_s.view(np.uint32))
+
+
+def test_load3_grouped_and_mixed(dev, orc, tmp_path):
+    """Grouped q|k|v: each part's rows are its decode + row requantise; a plain
+    int8 part among them is decoded and requantised without a rotation (the
+    requant spec of a stored-rotated base_q), as the reference's requant path."""
+    K, group = 1024, 128
+    t = {**grouped_weight_tensors("b.q", 64, K, group, 4), **grouped_weight_tensors("b.k", 32, K, group, 5),
+         **grouped_weight_tensors("b.v", 48, K, group, 6)}
+    path = C.write(str(tmp_path / "g.safetensors"), t)
+    q, s = loaded(tmp_path, "load3", path, "b.q", "b.k", "b.v")
+    parts = [oracle_grouped(orc, t, x, K, group) for x in ("b.q", "b.k", "b.v")]
+    assert np.array_equal(q, np.concatenate([p[0] for p in parts]))
+    assert np.array_equal(s.view(np.uint32), np.concatenate([p[1] for p in parts]).view(np.uint32))
+    t2 = {**grouped_weight_tensors("c.q", 64, K, group, 7), **int8_weight_tensors("c.k", 40, K, 8),
+          **grouped_weight_tensors("c.v", 48, K, group, 9)}
+    path = C.write(str(tmp_path / "m.safetensors"), t2)
+    q, s = loaded(tmp_path, "load3", path, "c.q", "c.k", "c.v")
+    qk, sk = orc.quantize_rows(dequant_i8(t2, "c.k"), rotate=False)
+    assert np.array_equal(q[64:104], qk) and np.array_equal(s[64:104].view(np.uint32), sk.view(np.uint32))
+    qq, sq = oracle_grouped(orc, t2, "c.q", K, group)
+    assert np.array_equal(q[:64], qq) and np.array_equal(s[:64].view(np.uint32), sq.view(np.uint32))
+
+
+@pytest.mark.parametrize("src", ["int8_convrot", "int8_plain", "int8_nospec", "bf16", "f16", "f32",
+                                 "f32_rotated", "grouped"])
+def test_upload_quant_linear_i8(dev, orc, tmp_path, src):
+    """The streaming upload's three paths (core/models/model_common.cpp:1095-1283):
+    a grouped weight expanded, an int8 weight whose file declares convrot
+    verbatim, anything else decoded and requantised (rotated unless the file
+    says it is stored rotated)."""
+    N, K = 72, 768
+    g = torch.Generator().manual_seed(11)
+    if src.startswith("int8"):
+        t = int8_weight_tensors("u", N, K, 12, convrot=src == "int8_convrot", spec=src != "int8_nospec")
+        vals, rotated = dequant_i8(t, "u"), src == "int8_convrot"
+    elif src == "grouped":
+        t = grouped_weight_tensors("u", N, K, 128, 13)
+    else:
+        dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32, "f32_rotated": torch.float32}[src]
+        w = (torch.randn(N, K, generator=g) * 0.05).to(dt)
+        t = {"u.weight": w}
+        if src == "f32_rotated":
+            t["u.comfy_quant"] = C.comfy_blob({"format": "int8_tensorwise", "convrot": True})
+        vals, rotated = w.float().numpy(), src == "f32_rotated"
+    path = C.write(str(tmp_path / "u.safetensors"), t)
+    q, s = loaded(tmp_path, "upload_i8", path, "u")
+    if src == "grouped":
+        wq, ws = oracle_grouped(orc, t, "u", K, 128)
+    elif src == "int8_convrot":
+        wq, ws = t["u.weight"].numpy(), t["u.weight_scale"].numpy()
+    else:
+        wq, ws = orc.quantize_rows(vals, rotate=not rotated)
+    assert np.array_equal(q, wq) and np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+
+
+def test_bare_int4_weight(dev, orc, tmp_path):
+    """A bare I4 tensor (no comfy_quant): two signed nibbles a byte times the
+    row scale, then the requantiser with a rotation (core/host/st.cpp:636-656)."""
+    N, K = 40, 512
+    g = torch.Generator().manual_seed(14)
+    packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    sc = torch.rand(N, generator=g) * 0.01 + 0.001
+    path = C.write_raw(str(tmp_path / "i4.safetensors"), [
+        ("n.weight", "I4", (N, K // 2), packed.numpy().tobytes()),
+        ("n.weight_scale", "F32", (N,), sc.numpy().tobytes())])
+    q, s = loaded(tmp_path, "load", path, "n")
+    p = packed.numpy().astype(np.int32)
+    nib = np.stack([p & 15, p >> 4], axis=2).reshape(N, K)
+    vals = np.where(nib >= 8, nib - 16, nib).astype(np.float32) * sc.numpy()[:, None]
+    wq, ws = orc.quantize_rows(vals, rotate=True)
+    assert np.array_equal(q, wq) and np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+
+
+def lora_tensors(prefix, n, k, r, seed, zero_row=None):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(r, k, generator=g) * 0.05
+    B = torch.randn(n, r, generator=g) * 0.05
+    if zero_row is not None:
+        B[zero_row, :] = 0.0
+    return {f"{prefix}.lora_A.weight": A, f"{prefix}.lora_B.weight": B}, A.numpy(), B.numpy()
+
+
+def fold(w, A, B, scale):
+    """w[o][i] += (scale * B[o][r]) * A[r][i], r ascending, B == 0 skipped,
+    every product and sum rounded to fp32 (core/models/lora.cpp:182-201)."""
+    w = w.copy()
+    scale = np.float32(scale)
+    for r in range(A.shape[0]):
+        s = (scale * B[:, r]).astype(np.float32)
+        upd = (w + (s[:, None] * A[r][None, :]).astype(np.float32)).astype(np.float32)
+        w = np.where((B[:, r] != 0)[:, None], upd, w)
+    return w
+
+
+def lora_scale(strength, alpha, rank):
+    return np.float32(np.float32(np.float32(strength) * np.float32(alpha)) / np.float32(rank))
+
+
+@pytest.mark.parametrize("convrot", [True, False])
+def test_lora_fold_load_quant_linear(dev, orc, tmp_path, convrot):
+    """load_quant_linear with a LoRA that touches the module: decode, rotate
+    back to the original basis, add the deltas file by file, rotate and
+    quantise (core/models/model_common.cpp:1011-1030)."""
+    N, K, r = 64, 512, 8
+    t = int8_weight_tensors("blk.attn", N, K, 15, convrot=convrot)
+    path = C.write(str(tmp_path / "w.safetensors"), t)
+    f1, A1, B1 = lora_tensors("blk.attn", N, K, r, 16, zero_row=3)
+    f2, A2, B2 = lora_tensors("diffusion_model.blk.attn", N, K, 4, 17)
+    l1 = C.lora_file(str(tmp_path / "l1.safetensors"), f1)
+    l2 = C.lora_file(str(tmp_path / "l2.safetensors"), f2, metadata={"lora_alpha": "2"})
+    q, s = loaded(tmp_path, "load", path, "blk.attn", loras=((l1, 0.7), (l2, 1.5)))
+    w = dequant_i8(t, "blk.attn")
+    if convrot:
+        w = orc.convrot(w)
+    w = fold(w, A1, B1, lora_scale(0.7, r, r))
+    w = fold(w, A2, B2, lora_scale(1.5, 2.0, 4))
+    wq, ws = orc.quantize_rows(w, rotate=True)
+    assert np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(q, wq), f"{(q != wq).sum()} code mismatches"
+    # A LoRA for another module leaves the weight verbatim.
+    f3, _, _ = lora_tensors("blk.mlp", N, K, r, 18)
+    l3 = C.lora_file(str(tmp_path / "l3.safetensors"), f3)
+    q, s = loaded(tmp_path, "load", path, "blk.attn", loras=((l3, 1.0),))
+    if convrot:
+        assert np.array_equal(q, t["blk.attn.weight"].numpy())
+
+
+def test_lora_fold_upload_and_load3(dev, orc, tmp_path):
+    """upload_quant_linear_i8 folds slab by slab (rotate back a stored-rotated
+    weight, add, rotate and quantise); load_quant3_linear folds each part in its
+    original basis and quantises the stack with base_q's requant spec, which
+    for a stored-rotated checkpoint does not rotate again
+    (core/models/model_common.cpp:1160-1216, :1486-1503)."""
+    N, K, r = 48, 512, 4
+    t = {**int8_weight_tensors("x.q", N, K, 19), **int8_weight_tensors("x.k", N, K, 20),
+         **int8_weight_tensors("x.v", N, K, 21)}
+    path = C.write(str(tmp_path / "w.safetensors"), t)
+    fq, Aq, Bq = lora_tensors("x.q", N, K, r, 22)
+    fv, Av, Bv = lora_tensors("x.v", N, K, r, 23)
+    lp = C.lora_file(str(tmp_path / "l.safetensors"), {**fq, **fv})
+    q, s = loaded(tmp_path, "upload_i8", path, "x.q", loras=((lp, 1.0),))
+    w = fold(orc.convrot(dequant_i8(t, "x.q")), Aq, Bq, lora_scale(1.0, r, r))
+    wq, ws = orc.quantize_rows(w, rotate=True)
+    assert np.array_equal(q, wq) and np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+    q, s = loaded(tmp_path, "load3", path, "x.q", "x.k", "x.v", loras=((lp, 1.0),))
+    parts = [fold(orc.convrot(dequant_i8(t, "x.q")), Aq, Bq, lora_scale(1.0, r, r)),
+             orc.convrot(dequant_i8(t, "x.k")),
+             fold(orc.convrot(dequant_i8(t, "x.v")), Av, Bv, lora_scale(1.0, r, r))]
+    wq, ws = orc.quantize_rows(np.concatenate(parts), rotate=False)
+    assert np.array_equal(q, wq) and np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+
+
+def test_load_lora_tail_layout(dev, tmp_path):
+    """load_lora_tail over a fused q|k|v: A stacked along the rank axis, B
+    placed at each module's output rows with its scale folded in
+    (core/models/model_common.cpp:1587-1652)."""
+    n1, k = 32, 256
+    fq, Aq, Bq = lora_tensors("blocks.0.attn.to_q", n1, k, 4, 24)
+    fv, Av, Bv = lora_tensors("blocks.0.attn.to_v", n1, k, 2, 25)
+    lp = C.lora_file(str(tmp_path / "l.safetensors"), {**fq, **fv})
+    out = str(tmp_path / "tail.bin")
+    res = json.loads(C.run("tail", out, 3 * n1, k, f"blocks.0.attn.to_q:0:{n1}", f"blocks.0.attn.to_k:{n1}:{n1}",
+                           f"blocks.0.attn.to_v:{2 * n1}:{n1}", "lora", lp, 0.5).stdout)
+    assert res["rank"] == 6 and res["touches"]
+    raw = open(out, "rb").read()
+    rank = struct.unpack("<q", raw[:8])[0]
+    at = np.frombuffer(raw[8:8 + rank * k * 4], np.float32).reshape(rank, k)
+    bt = np.frombuffer(raw[8 + rank * k * 4:], np.float32).reshape(3 * n1, rank)
+    assert np.array_equal(at, np.concatenate([Aq, Av]))
+    want = np.zeros((3 * n1, rank), np.float32)
+    want[:n1, :4] = lora_scale(0.5, 4, 4) * Bq
+    want[2 * n1:, 4:] = lora_scale(0.5, 2, 2) * Bv
+    assert np.array_equal(bt, want)

@@ -190,13 +190,65 @@ def test_full_size_checksums(dev, kernel, M, N, K):
 
 
 def test_contract_errors(dev):
-    A = torch.zeros((4, 100), dtype=torch.int8, device=dev)
-    B = torch.zeros((4, 100), dtype=torch.int8, device=dev)
-    with pytest.raises(Q.QLinearError, match="multiple of 64"):
-        Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
+    B = torch.zeros((4, 64), dtype=torch.int8, device=dev)
     A = torch.zeros((0, 64), dtype=torch.int8, device=dev)
     with pytest.raises(Q.QLinearError, match="empty problem"):
-        Q.i8_gemm(A, B[:, :64].contiguous(), None, None, out_dtype=torch.int32)
+        Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
+    # A row scale at an address that is not a multiple of 4.
+    A = torch.zeros((4, 64), dtype=torch.int8, device=dev)
+    s = torch.ones(8, device=dev)
+    C = torch.empty((4, 4), device=dev)
+    st = Q.load().phi_hip_i8_gemm(None, Q._ptr(A), 64, Q._ptr(B), 64, s.data_ptr() + 2, s.data_ptr(), 1, None,
+                                  Q.F32, Q._ptr(C), Q.F32, 4, 4, 4, 64, None, 0)
+    assert st == 3 and "sA is misaligned" in Q.last_error()
+
+
+# ---------------------------------------------------------------- any K, any offset
+# The reference serves any K > 0 at any byte offset through its dp4a kernel
+# (core/runtime/compute.cpp:566-575, core/kernels/int8_gemm.cpp:136-290); here
+# the register-staged MFMA kernel takes them with byte-safe loads and a
+# zero-filled K tail.
+def offset_view(t, off, device):
+    """t's bytes copied into a device buffer at byte offset `off` (any
+    alignment), viewed with t's shape and a row pitch of t.shape[1]."""
+    M, K = t.shape
+    buf = torch.zeros(M * K + off + 64, dtype=torch.int8, device=device)
+    buf[off:off + M * K] = t.reshape(-1).to(device)
+    return buf[off:off + M * K].view(M, K)
+
+
+@pytest.mark.parametrize("K", [1, 32, 96, 100, 127, 3000])
+@pytest.mark.parametrize("aoff,boff", [(1, 3), (0, 5), (7, 0), (16, 16)])
+@pytest.mark.parametrize("out", ["i32", "f32", "bf16"])
+def test_any_k_and_offsets(dev, orc, K, aoff, boff, out):
+    M, N = 77, 130
+    A, B = rand_i8((M, K), K + aoff), rand_i8((N, K), K + boff + 1)
+    Ad, Bd = offset_view(A, aoff, dev), offset_view(B, boff, dev)
+    assert (Ad.data_ptr() % 16 == 0) == (aoff % 16 == 0)
+    acc = orc.gemm_i8_i32_fast(A.numpy(), B.numpy())
+    if out == "i32":
+        C = Q.i8_gemm(Ad, Bd, None, None, out_dtype=torch.int32)
+        assert np.array_equal(C.cpu().numpy(), acc)
+        return
+    g = torch.Generator().manual_seed(K)
+    sa = torch.rand(M, generator=g) * 0.01 + 0.001
+    sb = torch.rand(N, generator=g) * 0.01 + 0.001
+    bias = torch.randn(N, generator=g) * 0.02
+    C = Q.i8_gemm(Ad, Bd, sa.to(dev), sb.to(dev), bias.to(dev),
+                  out_dtype=torch.float32 if out == "f32" else torch.bfloat16)
+    want = orc.epilogue(acc, sa.numpy(), sb.numpy(), bias.numpy(), out=out)
+    got = C.cpu().numpy().view(np.uint32) if out == "f32" else u16(C)
+    assert np.array_equal(got, want.view(np.uint32) if out == "f32" else want)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 3072), (300, 1000, 512), (1, 4, 64), (513, 777, 320)])
+def test_any_k_kernel_on_aligned_shapes(dev, orc, monkeypatch, M, N, K):
+    """PHI_GEMM_KERNEL=any forces the any-K kernel where the MFMA pipelines
+    would run (the reference's PHI_INT8_DP4A A/B switch): same exact product."""
+    monkeypatch.setenv("PHI_GEMM_KERNEL", "any")
+    A, B = rand_i8((M, K), M + 1), rand_i8((N, K), N + 2)
+    C = Q.i8_gemm(A.to(dev), B.to(dev), None, None, out_dtype=torch.int32)
+    assert np.array_equal(C.cpu().numpy(), orc.gemm_i8_i32_fast(A.numpy(), B.numpy()))
 
 
 # ---------------------------------------------------------------- two tile sizes
