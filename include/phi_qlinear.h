@@ -360,6 +360,24 @@ phi_status phi_hip_convrot_rows(phi_stream_t stream, const float* x, int64_t row
 phi_status phi_hip_lora_fold(phi_stream_t stream, float* w, int64_t ldw, int64_t rows, int64_t k, const float* A,
                              const float* B, int64_t rank, float scale);
 
+/*
+ * phi_hip_q8_linear without caller scratch, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, arithmetic
+ * and bits as phi_hip_q8_linear; its q8 [M, K] / s8 [M] activation scratch is
+ * a static device array of PHI_NOALLOC_SCRATCH_BYTES per GPU (held from the
+ * library's load until the process ends), so M * K (rounded up to 256) + 4 M
+ * must fit in it: larger calls return PHI_ERR_WORKSPACE.  Allocates nothing.
+ * All calls on one GPU share that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race.
+ */
+#define PHI_NOALLOC_SCRATCH_BYTES (64ull << 20)
+size_t phi_hip_noalloc_scratch_bytes(void);
+phi_status phi_hip_q8_linear_noalloc(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M,
+                                     int64_t K, const int8_t* W, int64_t ldw, const float* sW, int sw_scalar,
+                                     const void* bias, int bias_dtype, int64_t N, void* C, int c_dtype, int64_t ldc,
+                                     int round_mode);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,13 +27,18 @@ namespace {
 thread_local std::string g_err;
 std::atomic<bool> g_lost{false};
 
-phi_status fail(phi_status st, const char* fmt, ...) {
+phi_status vfail(phi_status st, const char* fmt, va_list ap) {
     char buf[512];
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    g_err = buf;
+    return st;
+}
+
+phi_status fail(phi_status st, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
+    vfail(st, fmt, ap);
     va_end(ap);
-    g_err = buf;
     return st;
 }
 
@@ -241,6 +246,21 @@ void set_vec_flags(phi_dev::GemmParams& p, int c_dtype, int64_t ldc) {
 }
 
 }  // namespace
+
+namespace phi_capi {
+
+// The error contract for entry points defined in other files of the library.
+phi_status fail(phi_status st, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vfail(st, fmt, ap);
+    va_end(ap);
+    return st;
+}
+
+bool device_lost() { return g_lost; }
+
+}  // namespace phi_capi
 
 extern "C" {
 

@@ -65,7 +65,7 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual", "phi_hip_quant_rotate_act",
            "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
            "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
-           "phi_hip_lora_fold"]
+           "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes"]
 
 _lib = None
 
@@ -111,6 +111,9 @@ def load() -> ctypes.CDLL:
     L.phi_hip_dequant_rows.argtypes = [P, P, I, I64, I64, I64, P, I, P, I64]
     L.phi_hip_convrot_rows.argtypes = [P, P, I64, I64, I64, P, I64]
     L.phi_hip_lora_fold.argtypes = [P, P, I64, I64, I64, P, P, I64, F]
+    L.phi_hip_q8_linear_noalloc.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, I]
+    L.phi_hip_noalloc_scratch_bytes.argtypes = []
+    L.phi_hip_noalloc_scratch_bytes.restype = SZ
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:
@@ -258,6 +261,25 @@ def q8_linear(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
                                     _ptr(bias), _dt(bias) if bias is not None else F32, N,
                                     _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8), round_mode,
                                     wp, wn))
+    return C
+
+
+def q8_linear_noalloc(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
+                      bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
+                      C: torch.Tensor | None = None, round_mode: int = ROUND_HALF_AWAY,
+                      stream=None) -> torch.Tensor:
+    """q8_linear with the activation scratch in the library's static device
+    array (phi_hip_q8_linear_noalloc): no caller scratch, nothing allocated
+    by the library.  Calls that overlap on one GPU race on that array."""
+    _require_device(x, W, sW, bias, C)
+    M, K = x.shape
+    N = W.shape[0]
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    _check(load().phi_hip_q8_linear_noalloc(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(W),
+                                            W.stride(0), _ptr(sW), 1 if sW.numel() == 1 else 0, _ptr(bias),
+                                            _dt(bias) if bias is not None else F32, N, _ptr(C), _dt(C),
+                                            C.stride(0), round_mode))
     return C
 
 

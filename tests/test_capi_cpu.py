@@ -249,3 +249,17 @@ def test_binding_refuses_host_tensors():
 
     with pytest.raises(ValueError):
         Q.quant_rotate(torch.zeros((2, 256)))
+
+
+def test_noalloc_contract(lib):
+    """The allocation-free linear refuses, before touching any device, a
+    problem whose activation scratch does not fit its static array."""
+    cap = lib.phi_hip_noalloc_scratch_bytes()
+    assert cap == 64 << 20
+    K = 4096
+    rc = lib.phi_hip_q8_linear_noalloc(None, FAKE, Q.BF16, K, cap // K + 1, K, FAKE, K, FAKE, 1, None, Q.F32, 64,
+                                       FAKE, Q.BF16, 64, 0)
+    assert rc == 4 and "static scratch" in Q.last_error()
+    rc = lib.phi_hip_q8_linear_noalloc(None, FAKE, Q.BF16, K, 0, K, FAKE, K, FAKE, 1, None, Q.F32, 64,
+                                       FAKE, Q.BF16, 64, 0)
+    assert rc == 2 and "empty problem" in Q.last_error()
