@@ -8,7 +8,7 @@
 
 namespace phi_dev {
 
-constexpr int GEMV_MAX_ITEMS = 48;  // items per launch (kernel-argument budget)
+constexpr int GEMV_MAX_ITEMS = 64;  // items per launch (kernel arguments: 64 x 40 bytes + the header, under 4 KB)
 
 struct GemvBatch {
     const int8_t* q8;
