@@ -45,6 +45,7 @@ CONFIGS = {
     "c3_attn": dict(kind="w8a8", M=32760, K=5120, N=5120),
     "c3_mlp": dict(kind="w8a8", M=32760, K=5120, N=13824),
     "c4": dict(kind="gemv", M=1, K=3072, N=18432, items=60),
+    "c4_m2": dict(kind="gemv", M=2, K=3072, N=18432, items=60),
     # Config 1's MLP as a DiT sub-block: adaLN modulate -> up (bf16) -> GELU-tanh
     # -> down into the fp32 residual stream through the gate.
     "c1_block": dict(kind="block", M=4352, K=3072, N=12288),
@@ -54,6 +55,9 @@ CONFIGS = {
     # A rank-64 LoRA correction on config 1's up-projection output (fp32, as
     # the reference's apply_lora_tail runs it after the linear).
     "c1_lora": dict(kind="lora", M=4352, K=3072, N=12288, rank=64),
+    # Ceilings, not a workload: int8 MFMAs with no data movement (zero, static
+    # and rotating random operands) and the operand stream into LDS alone.
+    "mfma_ceiling": dict(kind="ceiling"),
 }
 
 
@@ -120,7 +124,12 @@ def cpu_baseline(cfg) -> dict | None:
     return out
 
 
-def bench_w8a8(cfg, steps, warmup):
+def bench_w8a8(cfg, steps, warmup, layout="kt"):
+    """One step: rotate + quantise the activations, then the GEMM with the
+    dequant + bias epilogue to bf16.  layout "kt": the weight is packed into
+    the K-tiled operand layout once, before timing (a load-time step, like
+    the checkpoint's quantisation), and the prologue writes q8 K-tiled;
+    "row": row-major operands (the reference's layout)."""
     import torch
 
     import phi_qlinear as Q
@@ -135,12 +144,22 @@ def bench_w8a8(cfg, steps, warmup):
     q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
     s8 = torch.empty((M,), dtype=torch.float32, device=dev)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    if layout == "kt":
+        Wk = Q.pack_k_tiled(W)
+        qk = q8.view(-1)
+        torch.cuda.synchronize()
 
     def step():
-        Q.quant_rotate(x, q=q8, s=s8)
+        if layout == "kt":
+            Q.quant_rotate_kt(x, q=qk, s=s8)
+        else:
+            Q.quant_rotate(x, q=q8, s=s8)
         mid = torch.cuda.Event(enable_timing=True)
         mid.record()
-        Q.i8_gemm(q8, W, s8, sW, b, C=y)
+        if layout == "kt":
+            Q.i8_gemm_kt(qk, Wk, M, N, K, s8, sW, b, C=y)
+        else:
+            Q.i8_gemm(q8, W, s8, sW, b, C=y)
         return mid
 
     for _ in range(warmup):
@@ -393,6 +412,73 @@ def bench_gemv(cfg, steps, warmup):
                          "frac": gbs / HBM_PEAK_GBS, "traffic": None}}
 
 
+def bench_ceiling(steps, warmup):
+    """The two ceilings the headline GEMM is argued against, from the probe
+    kernels of lib/libphi_probe.so: every wave of every CU issues int8 MFMAs
+    back to back on 16 accumulators (zero operands; one static random fragment
+    pair; the GEMM's 8 + 8 random fragments, changed every K-step), and every
+    wave streams operands into LDS the way the GEMM's pipeline does (no
+    MFMAs), from a window that fits the MALL and one that does not."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(PKG, "lib", "libphi_probe.so"))
+    lib.phi_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_int]
+    lib.phi_probe_lds_dma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_int]
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device=dev).manual_seed(7)
+    ops = torch.randint(-127, 128, (64 * 1024,), generator=g, device=dev, dtype=torch.int8)
+    sink = torch.zeros(cus * 4, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def timed(launch):
+        for _ in range(warmup):
+            launch()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            launch()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps * 1e-3
+
+    iters = 2000  # 64000 MFMAs a wave, about 1 ms a launch
+    tops = {}
+    for mode, name in ((0, "zero"), (1, "static"), (2, "rotating")):
+        def launch(mode=mode):
+            rc = lib.phi_probe_mfma(stream, ctypes.c_void_p(ops.data_ptr()), mode, iters,
+                                    ctypes.c_void_p(sink.data_ptr()), cus)
+            if rc != 0:
+                raise RuntimeError(f"mfma probe launch failed ({rc})")
+        secs = timed(launch)
+        tops[name] = cus * 4 * iters * 32 * 65536 / secs / 1e12
+        log(f"bench: mfma ceiling ({name} operands) {tops[name]:.0f} TOPS")
+    dma = {}
+    for label, window in (("mall", 32 << 20), ("hbm", 1536 << 20)):
+        buf = torch.randint(-127, 128, (window,), generator=g, device=dev, dtype=torch.int8)
+        dma_iters = 4000
+
+        def launch(buf=buf, window=window):
+            rc = lib.phi_probe_lds_dma(stream, ctypes.c_void_p(buf.data_ptr()), window, dma_iters,
+                                       ctypes.c_void_p(sink.data_ptr()), cus)
+            if rc != 0:
+                raise RuntimeError(f"lds dma probe launch failed ({rc})")
+        secs = timed(launch)
+        dma[label] = cus * 4 * dma_iters * 8 * 1024 / secs / 1e9
+        log(f"bench: LDS DMA stream ({label} window) {dma[label]:.0f} GB/s")
+        del buf
+    value = tops["rotating"]
+    return {"value": value, "ms": None, "dtype": "int8", "unit": "TOPS",
+            "roofline": {"bound": "mfma", "achieved": value, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                         "frac": value / INT8_PEAK_TOPS, "traffic": None},
+            "extra": {"mfma_tops": tops, "lds_dma_gbs": dma, "cus": cus, "mfma_per_wave_per_launch": iters * 32}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -401,6 +487,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--config", default="c1_up", choices=sorted(CONFIGS))
+    ap.add_argument("--layout", default="kt", choices=["kt", "row"],
+                    help="W8A8 operands: K-tiled (weight packed before timing) or row-major")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
@@ -417,7 +505,7 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     log(f"bench: config {args.config} {cfg}, warmup {args.warmup}, steps {args.steps}")
     if cfg["kind"] == "w8a8":
-        r = bench_w8a8(cfg, args.steps, args.warmup)
+        r = bench_w8a8(cfg, args.steps, args.warmup, args.layout)
     elif cfg["kind"] == "block":
         r = bench_block(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "w4a8":
@@ -426,9 +514,12 @@ def main() -> int:
         r = bench_w4a4(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "lora":
         r = bench_lora(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "ceiling":
+        r = bench_ceiling(min(args.steps, 20), min(args.warmup, 20))
     else:
         r = bench_gemv(cfg, args.steps, args.warmup)
-    log(f"bench: {r['ms'] * 1e3:.1f} us per step")
+    if r["ms"] is not None:
+        log(f"bench: {r['ms'] * 1e3:.1f} us per step")
     if args.calibrate_copy:
         calibrate_copy(args.calibrate_copy)
     r["roofline"]["traffic"] = traffic_for(args.config)
@@ -448,6 +539,8 @@ def main() -> int:
         "data": "synthetic (seeded: bf16 N(0,1) activations with 0.1% x20 outlier channels, "
                 "int8 U[-127,127] weights, scale 0.002, bf16 N(0,0.02) bias)",
         "config": {"workload": workload, **{k: v for k, v in cfg.items() if k != "kind"},
+                   **({"operand_layout": "k-tiled" if args.layout == "kt" else "row-major"}
+                      if cfg["kind"] == "w8a8" else {}),
                    "parallelism": "single GPU"},
         "roofline": r["roofline"], "cpu_baseline": cpu,
     }

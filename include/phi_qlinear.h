@@ -177,6 +177,47 @@ phi_status phi_hip_q8_linear(phi_stream_t stream, const void* x, int x_dtype, in
                              int c_dtype, int64_t ldc, int8_t* q8, float* s8, int round_mode,
                              void* workspace, size_t ws_bytes);
 
+/*
+ * The K-tiled operand layout: an int8 [rows, K] matrix (K % 256 == 0) in
+ * strips of 256 rows (the last may hold fewer, h); within a strip, each
+ * 64-byte K-step of all h rows is one contiguous h x 64-byte block, and the
+ * 16-byte chunk c of row r sits in slot c ^ ((r >> 2) & 3) of the row's 64
+ * bytes.  Byte (r, k) of the matrix is at
+ *   256 K (r / 256) + h 64 (k / 64) + 64 (r % 256) + 16 (((k / 16) % 4) ^ ((r % 256 / 4) % 4)) + k % 16.
+ * It is the persistent GEMM's LDS stage layout, so each operand load moves
+ * 1 KB from one place instead of sixteen 64-byte row pieces.  It holds
+ * rows x K bytes, as the row-major matrix does.  No counterpart in the
+ * reference (its weights stay row-major, core/host/quant.cpp:223-236): these
+ * entries serve callers that pack each weight once at load time.
+ *
+ * phi_hip_pack_k_tiled: src (row-major, pitch ld >= K, ld % 16 == 0, 16-byte
+ * aligned) into dst (rows x K bytes, 16-byte aligned).  A pure re-layout.
+ */
+phi_status phi_hip_pack_k_tiled(phi_stream_t stream, const int8_t* src, int64_t ld, int64_t rows, int64_t K,
+                                int8_t* dst);
+
+/* phi_hip_quant_rotate (rotation on) writing q (rows x K bytes) K-tiled,
+ * for callers that feed one quantised activation to several K-tiled GEMMs.
+ * K % 256 == 0, K <= 16384. */
+phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                  int64_t ldx, int8_t* q, float* s, float qmax, int round_mode);
+
+/* phi_hip_i8_gemm with A [M, K] and B [N, K] both K-tiled: the same result,
+ * bit for bit, as phi_hip_i8_gemm on the row-major operands.  Needs
+ * K % 256 == 0, whole 16-byte output pieces (N % 8 for bf16, N % 4 else) on
+ * 16-byte aligned C rows; otherwise PHI_ERR_UNSUPPORTED. */
+phi_status phi_hip_i8_gemm_kt(phi_stream_t stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
+                              int sb_scalar, const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
+                              int64_t M, int64_t N, int64_t K);
+
+/* phi_hip_q8_linear with the weight W K-tiled (phi_hip_pack_k_tiled at load
+ * time): the prologue writes q8 (M x K bytes) K-tiled, then phi_hip_i8_gemm_kt.
+ * C is bit-identical to phi_hip_q8_linear's; s8 is the same; q8 holds the same
+ * bytes in the K-tiled layout.  Also needs K <= 16384. */
+phi_status phi_hip_q8_linear_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                                const int8_t* W, const float* sW, int sw_scalar, const void* bias, int bias_dtype,
+                                int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8, int round_mode);
+
 /* A grouped low-bit weight as the checkpoint stores it
  * (W4a8ExpandArgs, core/kernels/w4a8_expand.hpp:86-117). */
 typedef struct phi_w4a8_weight {

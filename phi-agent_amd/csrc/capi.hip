@@ -206,7 +206,7 @@ hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p,
     // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
     // runs on the two-stage kernel.
     const char* pe = getenv("PHI_GEMM_PIPE");
-    const bool pipe = !w4 && !(pe && pe[0] == '0');
+    const bool pipe = p.kt || (!w4 && !(pe && pe[0] == '0'));  // K-tiled operands: the pipeline only
     const int64_t M = p.M;
     const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, p.N, G) : gk == GK_PERSIST256 ? M : 0;
     phi_dev::GemmParams q = p;
@@ -268,12 +268,10 @@ const char* phi_hip_last_error(void) { return g_err.c_str(); }
 
 int phi_hip_abi_version(void) { return PHI_QLINEAR_ABI_VERSION; }
 
-static phi_status quant_rotate_impl(const char* who, phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
-                                    int64_t K, int64_t ldx, const phi_dev::QrPre& pre, int8_t* q,
-                                    int64_t ldq, float* s, float qmax, int round_mode, int rotate) {
-    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
-    if (rows < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
-    if (rows == 0) return ok();
+// The prologue's contract (rows > 0).
+static phi_status quant_rotate_check(const char* who, const void* x, int x_dtype, int64_t rows, int64_t K, int64_t ldx,
+                                     const phi_dev::QrPre& pre, int8_t* q, int64_t ldq, float* s, float qmax,
+                                     int round_mode) {
     if (x_dtype != PHI_F32 && x_dtype != PHI_BF16) return fail(PHI_ERR_ARG, "%s: x dtype must be f32 or bf16", who);
     if (round_mode != PHI_ROUND_HALF_AWAY && round_mode != PHI_ROUND_HALF_EVEN) return fail(PHI_ERR_ARG, "%s: bad round mode", who);
     if (!x || !q || !s) return fail(PHI_ERR_ARG, "%s: null pointer", who);
@@ -291,6 +289,17 @@ static phi_status quant_rotate_impl(const char* who, phi_stream_t stream, const 
         return fail(PHI_ERR_ALIGN, "%s: x and q rows must be 16-byte aligned", who);
     if ((pre.sc && !aligned(pre.sc, 16)) || (pre.sh && !aligned(pre.sh, 16)))
         return fail(PHI_ERR_ALIGN, "%s: modulation vectors must be 16-byte aligned", who);
+    return PHI_OK;
+}
+
+static phi_status quant_rotate_impl(const char* who, phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                    int64_t K, int64_t ldx, const phi_dev::QrPre& pre, int8_t* q,
+                                    int64_t ldq, float* s, float qmax, int round_mode, int rotate) {
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || K < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0) return ok();
+    const phi_status st = quant_rotate_check(who, x, x_dtype, rows, K, ldx, pre, q, ldq, s, qmax, round_mode);
+    if (st != PHI_OK) return st;
     return check_hip(phi_dev::launch_quant_rotate((hipStream_t)stream, x, x_dtype == PHI_BF16, rows, K, ldx, q, ldq, s,
                                                   qmax, round_mode == PHI_ROUND_HALF_EVEN, rotate ? 1 : 0, pre),
                      who);
@@ -437,6 +446,106 @@ phi_status phi_hip_q8_linear(phi_stream_t stream, const void* x, int x_dtype, in
     if (st != PHI_OK) return st;
     return phi_hip_i8_gemm(stream, q8, K, W, ldw, s8, sW, sw_scalar, bias, bias_dtype, C, c_dtype, ldc, M, N, K,
                            workspace, ws_bytes);
+}
+
+// The K-tiled operand contract: whole 256-deep K-steps (the pipeline's pairs
+// of 64-deep stages, and whole rotation groups), 16-byte aligned bases, and
+// strip offsets within 32 bits (256 x K < 2^31).
+static phi_status check_kt(const char* who, const void* A, const void* B, int64_t K) {
+    if (K % 256 != 0) return fail(PHI_ERR_SHAPE, "%s: K=%lld is not a multiple of 256", who, (long long)K);
+    if (K >= ((int64_t)1 << 23)) return fail(PHI_ERR_SHAPE, "%s: K=%lld is too large for the K-tiled layout", who, (long long)K);
+    if (!aligned(A, 16) || !aligned(B, 16)) return fail(PHI_ERR_ALIGN, "%s: K-tiled operands must be 16-byte aligned", who);
+    return PHI_OK;
+}
+
+static phi_status i8_gemm_kt_impl(const char* who, phi_stream_t stream, const int8_t* A, const int8_t* B,
+                                  const float* sA, const float* sB, int sb_scalar, const void* bias, int bias_dtype,
+                                  void* C, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K) {
+    phi_status st = check_gemm(who, A, K, B, K, M, N, K, sA, sB, C, c_dtype, ldc, false);
+    if (st != PHI_OK) return st;
+    if ((st = check_kt(who, A, B, K)) != PHI_OK) return st;
+    if (!persist_ok(C, c_dtype, N, K, K, K, ldc))
+        return fail(PHI_ERR_UNSUPPORTED, "%s: needs whole 16-byte output pieces on 16-byte aligned C rows", who);
+    const int bk = bias_kind_of(bias, bias_dtype, &st);
+    if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    if (bias && !aligned(bias, bk == phi_dev::BIAS_BF16 ? 2 : 4)) return fail(PHI_ERR_ALIGN, "%s: bias is misaligned", who);
+    phi_dev::GemmParams p{};
+    p.A = A;
+    p.B = B;
+    p.sA = sA;
+    p.sB = sB;
+    p.bias = bias;
+    p.C = C;
+    p.lda = K;
+    p.ldb = K;
+    p.ldc = ldc;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.sb_scalar = sb_scalar ? 1 : 0;
+    p.bias_kind = bk;
+    p.c_kind = c_kind_of(c_dtype);
+    p.group_m = 4;
+    p.kt = 1;
+    set_vec_flags(p, c_dtype, ldc);
+    GemmKernel gk = GK_PERSIST;
+    const char* e = getenv("PHI_GEMM_KERNEL");
+    if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;
+    if (e && strcmp(e, "persist128") == 0) gk = GK_PERSIST128;
+    return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, false, c_dtype, ldc), who);
+}
+
+phi_status phi_hip_pack_k_tiled(phi_stream_t stream, const int8_t* src, int64_t ld, int64_t rows, int64_t K,
+                                int8_t* dst) {
+    static const char* who = "pack_k_tiled";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty matrix (rows=%lld K=%lld)", who, (long long)rows, (long long)K);
+    if (rows > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: rows exceeds 2^31", who);
+    if (!src || !dst) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    phi_status st = check_kt(who, src, dst, K);
+    if (st != PHI_OK) return st;
+    if (ld < K || ld % 16 != 0) return fail(PHI_ERR_ALIGN, "%s: ld must be >= K and a multiple of 16", who);
+    return check_hip(phi_dev::launch_pack_k_tiled((hipStream_t)stream, src, ld, rows, K, dst), who);
+}
+
+phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                  int64_t ldx, int8_t* q, float* s, float qmax, int round_mode) {
+    static const char* who = "quant_convrot_kt";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem (rows=%lld)", who, (long long)rows);
+    phi_dev::QrPre pre{};
+    phi_status st = quant_rotate_check(who, x, x_dtype, rows, K, ldx, pre, q, K, s, qmax, round_mode);
+    if (st != PHI_OK) return st;
+    if (K > 16384) return fail(PHI_ERR_UNSUPPORTED, "%s: K=%lld exceeds 16384 (K-tiled activations)", who, (long long)K);
+    return check_hip(phi_dev::launch_quant_rotate((hipStream_t)stream, x, x_dtype == PHI_BF16, rows, K, ldx, q, K, s,
+                                                  qmax, round_mode == PHI_ROUND_HALF_EVEN, 1, pre, 1),
+                     who);
+}
+
+phi_status phi_hip_i8_gemm_kt(phi_stream_t stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
+                              int sb_scalar, const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
+                              int64_t M, int64_t N, int64_t K) {
+    static const char* who = "int8_gemm_kt";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    return i8_gemm_kt_impl(who, stream, A, B, sA, sB, sb_scalar, bias, bias_dtype, C, c_dtype, ldc, M, N, K);
+}
+
+phi_status phi_hip_q8_linear_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                                const int8_t* W, const float* sW, int sw_scalar, const void* bias, int bias_dtype,
+                                int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8, int round_mode) {
+    static const char* who = "linear_gemm_kt";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!q8 || !s8) return fail(PHI_ERR_ARG, "%s: the int8 path needs activation scratch", who);
+    if (M <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
+    phi_status st = check_gemm(who, q8, K, W, K, M, N, K, s8, sW, C, c_dtype, ldc, false);
+    if (st != PHI_OK) return st;
+    if ((st = check_kt(who, q8, W, K)) != PHI_OK) return st;
+    if (K > 16384) return fail(PHI_ERR_UNSUPPORTED, "%s: K=%lld exceeds 16384 (K-tiled activations)", who, (long long)K);
+    if (!persist_ok(C, c_dtype, N, K, K, K, ldc))
+        return fail(PHI_ERR_UNSUPPORTED, "%s: needs whole 16-byte output pieces on 16-byte aligned C rows", who);
+    st = phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode);
+    if (st != PHI_OK) return st;
+    return i8_gemm_kt_impl(who, stream, q8, W, s8, sW, sw_scalar, bias, bias_dtype, C, c_dtype, ldc, M, N, K);
 }
 
 static phi_status check_w4a8(const char* who, const phi_w4a8_weight* w, bool lut) {

@@ -35,7 +35,23 @@ struct GemmParams {
     // W4 operand of signed nibbles (convrot_w4a4): value = code < 8 ? code : code - 16,
     // from a constant table in registers; lut is not read.
     int w4_signed;
+    // Persistent pipeline: A and B in the K-tiled layout (k_tiled_offset) instead
+    // of row-major; lda / ldb are then K.
+    int kt;
 };
+
+// The K-tiled operand layout: rows in strips of 256 (the last strip may be
+// shorter, h rows); within a strip, each 64-byte K-step of all h rows is one
+// contiguous block of h x 64 bytes, and 16-byte chunk c of row r sits in slot
+// c ^ ((r >> 2) & 3) of the row's 64 bytes -- the persistent pipeline's LDS
+// stage layout, so a stage fills with contiguous 1 KB loads.  Byte offset of
+// row r, column c (K columns, `rows` rows in all):
+__host__ __device__ __forceinline__ int64_t k_tiled_offset(int64_t r, int64_t c, int64_t K, int64_t rows) {
+    const int64_t s = r >> 8, rr = r & 255;
+    const int64_t h = rows - (s << 8) < 256 ? rows - (s << 8) : 256;
+    const int64_t k = c >> 6, chunk = (c >> 4) & 3, slot = chunk ^ ((rr >> 2) & 3);
+    return s * 256 * K + k * h * 64 + rr * 64 + slot * 16 + (c & 15);
+}
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
@@ -66,9 +82,12 @@ struct QrPre {
     const float* sh;
     int64_t off2;       // QR_SILU_GATE: v = silu(x[k]) * x[k + off2] (elements)
 };
+// q_kt: q is written in the K-tiled layout of `rows` rows (ldq unused; K <= 16384).
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                               float qmax, int half_even, int rotate, const QrPre& pre);
+                               float qmax, int half_even, int rotate, const QrPre& pre, int q_kt = 0);
+// An int8 [rows, ld] row-major matrix into the K-tiled layout (16-byte aligned rows).
+hipError_t launch_pack_k_tiled(hipStream_t stream, const int8_t* src, int64_t ld, int64_t rows, int64_t K, int8_t* dst);
 size_t quant_rotate_lds_bytes(int64_t K);
 
 }  // namespace phi_dev

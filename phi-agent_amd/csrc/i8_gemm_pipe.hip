@@ -90,6 +90,9 @@ struct Pw : EpiWave {
     int voA, voB;  // per-lane global offset within a 16-row load
     int oA[2], oB[2];
     int kA, kB;
+    // K-tiled operands: bytes from one K-step's block to the next (strip
+    // height x 64), and the tile's offset within its 256-row strip's block.
+    int kstA, kstB, hoA, hoB;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const int8_t* base, int64_t ld, int row0, int nrows) {
@@ -97,50 +100,84 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const int8_t* base, 
                                              kRsrcWord3);
 }
 
+// A K-tiled operand of `rows` rows and K columns (k_tiled_offset): the
+// resource over the strip holding tile row row0, that strip's K-step stride,
+// and the tile's offset within the strip's K-step block (128-row tiles sit in
+// either half of a 256-row strip).
+__device__ __forceinline__ void kt_cursor(const int8_t* base, int K, int row0, int rows, __amdgpu_buffer_rsrc_t& r,
+                                          int& kst, int& ho) {
+    const int s = row0 >> 8, h = min(256, rows - (s << 8));
+    r = __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)s * 256 * K), (short)0, h * K, kRsrcWord3);
+    kst = h * 64;
+    ho = (row0 & 255) * 64;
+}
+
 // DL loads of operand A's K-step w.kA into stage ST (16 rows each); then the
 // cursor advances.
-template <int WT, int ST>
+// KT: the operand is K-tiled, so the wave's 16-row pieces of the K-step are
+// contiguous 1 KB blocks: each load fetches 1 KB from one place.
+template <int WT, int ST, bool KT>
 __device__ __forceinline__ void load_a(Pw& w, const GemmParams& p) {
     constexpr int DL = PCfg<WT>::DL, STG = PCfg<WT>::STG;
     int8_t* d = opaque_lds(w.la + ST * STG + w.wave * (DL * 1024));
-    const int koff = w.kA * PK;
+    if constexpr (KT) {
+        const int koff = w.kA * w.kstA + w.hoA;
 #pragma unroll
-    for (int j = 0; j < DL; j++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(d + j * 1024), 16, w.voA,
-                                                 koff + (w.wave * DL + j) * 16 * (int)p.lda, 0, 0);
+        for (int j = 0; j < DL; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(d + j * 1024), 16, w.voA,
+                                                     koff + (w.wave * DL + j) * 1024, 0, 0);
+    } else {
+        const int koff = w.kA * PK;
+#pragma unroll
+        for (int j = 0; j < DL; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(d + j * 1024), 16, w.voA,
+                                                     koff + (w.wave * DL + j) * 16 * (int)p.lda, 0, 0);
+    }
     w.kA++;
 }
 
-template <int WT, int ST>
+template <int WT, int ST, bool KT>
 __device__ __forceinline__ void load_b(Pw& w, const GemmParams& p) {
     constexpr int DL = PCfg<WT>::DL, STG = PCfg<WT>::STG;
     int8_t* d = opaque_lds(w.lb + ST * STG + w.wave * (DL * 1024));
-    const int koff = w.kB * PK;
+    if constexpr (KT) {
+        const int koff = w.kB * w.kstB + w.hoB;
 #pragma unroll
-    for (int j = 0; j < DL; j++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(d + j * 1024), 16, w.voB,
-                                                 koff + (w.wave * DL + j) * 16 * (int)p.ldb, 0, 0);
+        for (int j = 0; j < DL; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(d + j * 1024), 16, w.voB,
+                                                     koff + (w.wave * DL + j) * 1024, 0, 0);
+    } else {
+        const int koff = w.kB * PK;
+#pragma unroll
+        for (int j = 0; j < DL; j++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(d + j * 1024), 16, w.voB,
+                                                     koff + (w.wave * DL + j) * 16 * (int)p.ldb, 0, 0);
+    }
     w.kB++;
 }
 
 // Cursor switches at a tile's end: to the next tile's K-step 0, or, after
 // the last tile, back to K-step 0 of the same tile (those loads land in
 // released stages and are never read).
-template <int WT>
+template <int WT, bool KT>
 __device__ __forceinline__ void switch_a(Pw& w, const GemmParams& p, const NextTile& nt) {
     constexpr int BM = PCfg<WT>::BM;
     if (nt.valid) {
-        w.rA = rows_rsrc(p.A, p.lda, nt.m0, min(BM, p.M - nt.m0));
+        if constexpr (KT) kt_cursor(p.A, p.K, nt.m0, p.M, w.rA, w.kstA, w.hoA);
+        else w.rA = rows_rsrc(p.A, p.lda, nt.m0, min(BM, p.M - nt.m0));
         w.cm0 = nt.m0;
         w.cn0 = nt.n0;
     }
     w.kA = 0;
 }
 
-template <int WT>
+template <int WT, bool KT>
 __device__ __forceinline__ void switch_b(Pw& w, const GemmParams& p, const NextTile& nt) {
     constexpr int BM = PCfg<WT>::BM;
-    if (nt.valid) w.rB = rows_rsrc(p.B, p.ldb, nt.n0, min(BM, p.N - nt.n0));
+    if (nt.valid) {
+        if constexpr (KT) kt_cursor(p.B, p.K, nt.n0, p.N, w.rB, w.kstB, w.hoB);
+        else w.rB = rows_rsrc(p.B, p.ldb, nt.n0, min(BM, p.N - nt.n0));
+    }
     w.kB = 0;
 }
 
@@ -210,25 +247,25 @@ __device__ __forceinline__ void pquarter(const Frag<WT>& cur, Frag<WT>& nxt, v16
 // wait's allowance.  SWA / SWB: the A / B cursor moves to the next tile
 // before its loads here (SWA also loads that tile's epilogue operands into
 // area ln).
-template <int WT, int S, bool Z, int VW, bool SWA, bool SWB, bool G>
+template <int WT, int S, bool Z, int VW, bool SWA, bool SWB, bool G, bool KT>
 __device__ __forceinline__ void pstep(Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB], Pw& w,
                                       const GemmParams& p, const NextTile& nt, int8_t* ln) {
     constexpr int DL = PCfg<WT>::DL;
     constexpr int NE = G ? 4 : 3;  // epilogue-operand loads
     Frag<WT> f1;
     pquarter<WT, S, 1, DL, Z>(f0, f1, acc, w, [&] {
-        if constexpr (SWB) switch_b<WT>(w, p, nt);
-        load_b<WT, (S + 3) % NSTG>(w, p);
+        if constexpr (SWB) switch_b<WT, KT>(w, p, nt);
+        load_b<WT, (S + 3) % NSTG, KT>(w, p);
     });
     wait_vm_lgkm0<VW>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     pquarter<WT, (S + 1) % NSTG, 0, DL + (SWA ? NE : 0), false>(f1, f0, acc, w, [&] {
         if constexpr (SWA) {
-            switch_a<WT>(w, p, nt);
+            switch_a<WT, KT>(w, p, nt);
             issue_epi<WT, G>(w, p, ln);
         }
-        load_a<WT, S>(w, p);
+        load_a<WT, S, KT>(w, p);
     });
 }
 
@@ -248,7 +285,7 @@ __device__ __forceinline__ NextTile next_tile(const Shape& s, const GemmParams& 
 // la and four B stages at lb (STG bytes each), the epilogue-operand areas
 // eall and the epilogue staging cbuf.  K % 256 == 0.  Returns at once when
 // the workgroup has no tile.
-template <int WT, bool G>
+template <int WT, bool G, bool KT>
 __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8_t* lb, int8_t* eall, int8_t* cbuf) {
     using C = PCfg<WT>;
     constexpr int NB = C::NB, DL = C::DL, BM = C::BM;
@@ -280,8 +317,11 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
         w.oB[q] = (w.wn * WT + w.lrow) * PK + c * 16;
     }
     // A load covers 16 rows: lane l writes row l / 4, slot l % 4, and fetches
-    // the chunk that belongs in that slot.
-    {
+    // the chunk that belongs in that slot (K-tiled: the slot's bytes as stored).
+    if constexpr (KT) {
+        w.voA = w.lane * 16;
+        w.voB = w.lane * 16;
+    } else {
         const int row = w.lane >> 2, c = (w.lane & 3) ^ ((row >> 2) & 3);
         w.voA = row * (int)p.lda + c * 16;
         w.voB = row * (int)p.ldb + c * 16;
@@ -291,20 +331,25 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
     // outside a zero-length range), standing where a previous tile's
     // epilogue stores would stand, so every tile's first waits count alike.
     const NextTile first = next_tile<WT>(s, p, r, true);
-    w.rA = rows_rsrc(p.A, p.lda, first.m0, min(BM, p.M - first.m0));
-    w.rB = rows_rsrc(p.B, p.ldb, first.n0, min(BM, p.N - first.n0));
+    if constexpr (KT) {
+        kt_cursor(p.A, p.K, first.m0, p.M, w.rA, w.kstA, w.hoA);
+        kt_cursor(p.B, p.K, first.n0, p.N, w.rB, w.kstB, w.hoB);
+    } else {
+        w.rA = rows_rsrc(p.A, p.lda, first.m0, min(BM, p.M - first.m0));
+        w.rB = rows_rsrc(p.B, p.ldb, first.n0, min(BM, p.N - first.n0));
+    }
     w.cm0 = first.m0;
     w.cn0 = first.n0;
     w.kA = 0;
     w.kB = 0;
-    load_a<WT, 0>(w, p);
+    load_a<WT, 0, KT>(w, p);
     issue_epi<WT, G>(w, p, w.le);
-    load_b<WT, 0>(w, p);
-    load_a<WT, 1>(w, p);
-    load_b<WT, 1>(w, p);
-    load_a<WT, 2>(w, p);
-    load_b<WT, 2>(w, p);
-    load_a<WT, 3>(w, p);
+    load_b<WT, 0, KT>(w, p);
+    load_a<WT, 1, KT>(w, p);
+    load_b<WT, 1, KT>(w, p);
+    load_a<WT, 2, KT>(w, p);
+    load_b<WT, 2, KT>(w, p);
+    load_a<WT, 3, KT>(w, p);
     __builtin_amdgcn_sched_barrier(0);
     {
         const __amdgpu_buffer_rsrc_t nowhere = __builtin_amdgcn_make_buffer_rsrc((void*)p.C, (short)0, 0, kRsrcWord3);
@@ -325,25 +370,25 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
         const NextTile nt = next_tile<WT>(s, p, t + s.G, i + 1 < ntile);
         constexpr int VWR = C::VWR, VWN = C::VWN;
         if (s.KT == 4) {
-            pstep<WT, 0, true, VWR, true, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 1, false, VWR, false, true, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 0, true, VWR, true, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 1, false, VWR, false, true, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
         } else {
-            pstep<WT, 0, true, VWR, false, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 1, false, VWR, false, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 0, true, VWR, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 1, false, VWR, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             for (int k = 4; k < s.KT - 4; k += 4) {
-                pstep<WT, 0, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
-                pstep<WT, 1, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
-                pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
-                pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+                pstep<WT, 0, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 1, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             }
-            pstep<WT, 0, false, VWN, true, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 1, false, VWN, false, true, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 2, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
-            pstep<WT, 3, false, VWN, false, false, G>(f0, acc, w, p, nt, ln);
+            pstep<WT, 0, false, VWN, true, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 1, false, VWN, false, true, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
         }
         epilogue<WT, G>(acc, p, s, t, w, le);
         if (++i == ntile) break;
@@ -353,27 +398,27 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
     wait_all();
 }
 
-template <int WT, bool G>
+template <int WT, bool G, bool KT>
 __global__ __launch_bounds__(256) void i8_gemm_pipe_kernel(GemmParams p) {
     constexpr int STG = PCfg<WT>::STG;
     __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
-    pipe_tiles<WT, G>(p, la, lb, eall, cbuf);
+    pipe_tiles<WT, G, KT>(p, la, lb, eall, cbuf);
 }
 
 // Both tile sizes in one launch: the workgroup's 256 x 256 tiles of pb, then
 // its 128 x 128 tiles of ps (the rows below pb's), in the same LDS.
-template <bool G>
+template <bool G, bool KT>
 __global__ __launch_bounds__(256) void i8_gemm_pipe_mixed_kernel(GemmParams pb, GemmParams ps) {
     constexpr int STG = PCfg<128>::STG;
     static_assert(PCfg<64>::STG <= STG, "the small tiles' stages fit in the big tiles' ones");
     __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
-    pipe_tiles<128, G>(pb, la, lb, eall, cbuf);
+    pipe_tiles<128, G, KT>(pb, la, lb, eall, cbuf);
     __syncthreads();  // every wave is done with the big tiles' LDS
-    pipe_tiles<64, G>(ps, la, lb, eall, cbuf);
+    pipe_tiles<64, G, KT>(ps, la, lb, eall, cbuf);
 }
 
 }  // namespace
@@ -384,12 +429,15 @@ hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_
     const int bm = 2 * wave_tile;
     const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
     const int grid = tiles < num_cus ? tiles : num_cus;
+    if (p.kt && p.gate) return hipErrorInvalidValue;  // the gated residual reads row-major operands only
     if (wave_tile == 128) {
-        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true>), dim3(grid), dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false>), dim3(grid), dim3(256), 0, stream, p);
+        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true, false>), dim3(grid), dim3(256), 0, stream, p);
+        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, false>), dim3(grid), dim3(256), 0, stream, p);
     } else {
-        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true>), dim3(grid), dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false>), dim3(grid), dim3(256), 0, stream, p);
+        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true, false>), dim3(grid), dim3(256), 0, stream, p);
+        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, true>), dim3(grid), dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, false>), dim3(grid), dim3(256), 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -399,8 +447,10 @@ hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, c
     const int big = ((pb.M + 255) / 256) * ((pb.N + 255) / 256), small = ((ps.M + 127) / 128) * ((ps.N + 127) / 128);
     const int most = big > small ? big : small;
     const int grid = most < num_cus ? most : num_cus;
-    if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true>), dim3(grid), dim3(256), 0, stream, pb, ps);
-    else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    if (pb.kt != ps.kt || (pb.kt && pb.gate)) return hipErrorInvalidValue;
+    if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    else if (pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, true>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
     return hipGetLastError();
 }
 

@@ -275,7 +275,7 @@ template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
                                                            int G, int8_t* __restrict__ q, int64_t ldq,
                                                            float* __restrict__ s, float qmax, int rotate,
-                                                           QrPre pre_op) {
+                                                           QrPre pre_op, int qkt) {
     extern __shared__ __align__(16) float lds[];
     constexpr int NW = BF16_IN ? 8 : 16;  // input dwords per lane per round
     const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
@@ -377,7 +377,20 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
     const bool fold = !rotate || inv >= 0x1p-122f;
     const float pre = fold ? 1.0f : sixteenth, post = fold ? inv * sixteenth : inv;
 
-    int8_t* qrow = q + (int64_t)row * ldq + tl * 16;
+    // The lane's 16 bytes of group g land at qrow + g * gstep: row-major, or
+    // K-tiled (256-row strips of h rows; the group's four 64-byte K-steps are
+    // blocks h x 64 bytes apart; chunk tl & 3 of K-step tl >> 2 in slot
+    // (tl & 3) ^ ((row >> 2) & 3)).
+    int8_t* qrow;
+    int64_t gstep;
+    if (qkt) {
+        const int64_t st = row >> 8, rr = row & 255, h = min(256, rows - (int)(st << 8));
+        qrow = q + st * 256 * (int64_t)G * 256 + (tl >> 2) * h * 64 + rr * 64 + (((tl & 3) ^ ((rr >> 2) & 3)) * 16);
+        gstep = 4 * h * 64;
+    } else {
+        qrow = q + (int64_t)row * ldq + tl * 16;
+        gstep = 256;
+    }
 #pragma unroll
     for (int r = 0; r < R; r++) {
         // Column tl back into the tile, row tl out: 16 contiguous elements.
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
         }
         wave_lds_fence();
         if (row < rows && g0 + 4 * r < G)
-            *(uint4*)(qrow + (int64_t)(g0 + 4 * r) * 256) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            *(uint4*)(qrow + (int64_t)(g0 + 4 * r) * gstep) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
     }
     if (wr == 0 && lane == 0 && row < rows) s[row] = scale;
 }
@@ -432,7 +445,7 @@ static int tile_rounds(int64_t rows, int G) {
 
 template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                                 int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre) {
+                                 int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre, int qkt) {
     const int wpr = (G + 4 * R - 1) / (4 * R);
     const int rpb = wpr >= 8 ? 1 : 8 / wpr;
     const size_t lds = ((size_t)rpb * wpr * QT_WAVE + 16) * sizeof(float);
@@ -446,7 +459,7 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
     }
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
     hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows, G,
-                       q, ldq, s, qmax, rotate, pre);
+                       q, ldq, s, qmax, rotate, pre, qkt);
     return hipGetLastError();
 }
 
@@ -455,43 +468,44 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
 // per element dwarfs the per-wave costs a larger R spreads.
 template <bool BF16_IN, bool HALF_EVEN, int OP>
 static hipError_t launch_tiles_op(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                                  int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre) {
+                                  int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre, int qkt) {
     if (tile_rounds(rows, G) == 1)
-        return launch_tiles_r<BF16_IN, HALF_EVEN, 1, OP>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-    return launch_tiles_r<BF16_IN, HALF_EVEN, 2, OP>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        return launch_tiles_r<BF16_IN, HALF_EVEN, 1, OP>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+    return launch_tiles_r<BF16_IN, HALF_EVEN, 2, OP>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
 }
 
 template <bool BF16_IN, bool HALF_EVEN>
 static hipError_t launch_tiles(hipStream_t stream, const void* x, int64_t rows, int G, int64_t ldx, int8_t* q,
-                               int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre) {
+                               int64_t ldq, float* s, float qmax, int rotate, const QrPre& pre, int qkt) {
     switch (pre.op) {
-        case QR_MOD: return launch_tiles_op<BF16_IN, HALF_EVEN, QR_MOD>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-        case QR_GELU: return launch_tiles_op<BF16_IN, HALF_EVEN, QR_GELU>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case QR_MOD: return launch_tiles_op<BF16_IN, HALF_EVEN, QR_MOD>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+        case QR_GELU: return launch_tiles_op<BF16_IN, HALF_EVEN, QR_GELU>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
         case QR_SILU_GATE:
-            return launch_tiles_op<BF16_IN, HALF_EVEN, QR_SILU_GATE>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+            return launch_tiles_op<BF16_IN, HALF_EVEN, QR_SILU_GATE>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
         default: break;
     }
     switch (tile_rounds(rows, G)) {
-        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+        case 1: return launch_tiles_r<BF16_IN, HALF_EVEN, 1, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+        case 2: return launch_tiles_r<BF16_IN, HALF_EVEN, 2, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+        case 3: return launch_tiles_r<BF16_IN, HALF_EVEN, 3, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+        case 4: return launch_tiles_r<BF16_IN, HALF_EVEN, 4, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+        default: return launch_tiles_r<BF16_IN, HALF_EVEN, 5, QR_PLAIN>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
     }
 }
 
 // Host-side launcher.  Validation is done by the C ABI layer.
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,
                                int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* s,
-                               float qmax, int half_even, int rotate, const QrPre& pre) {
+                               float qmax, int half_even, int rotate, const QrPre& pre, int qkt) {
     const int G = (int)(K / 256);
     if (rows == 0) return hipSuccess;
+    if (qkt && G > 64) return hipErrorInvalidValue;  // the row kernel writes row-major q only
     if (G <= 64) {
         if (bf16_in)
-            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre)
-                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
-        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre)
-                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre);
+            return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt)
+                             : launch_tiles<true, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
+        return half_even ? launch_tiles<false, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt)
+                         : launch_tiles<false, false>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt);
     }
     int threads = ((16 * G + 63) / 64) * 64;
     if (threads > 1024) threads = 1024;

@@ -13,6 +13,8 @@
 //   lora_fold     w[o][i] += (scale * B[o][r]) * A[r][i] for r ascending, rank
 //                 entries of B that are 0 skipped (LoraSet::apply_rows_of,
 //                 core/models/lora.cpp:182-201)
+//   pack_k_tiled  an int8 row-major weight into the K-tiled operand layout of
+//                 the persistent pipeline (k_tiled_offset); a pure re-layout
 //
 // The rotate + quantise that turns the result into int8 is quant_rotate, the
 // same kernel the activations take: the reference's weight and activation
@@ -22,6 +24,7 @@
 // element; the kernels are plain and exact (-ffp-contract=off: every product
 // and sum rounds on its own, as the reference's x86-64 host code does).
 #include "device_common.hpp"
+#include "i8_gemm.hpp"
 #include "w4a8.hpp"
 
 namespace phi_dev {
@@ -96,6 +99,17 @@ __global__ __launch_bounds__(256) void lora_fold_kernel(float* w, int64_t ldw, i
     }
 }
 
+// One 16-byte chunk a thread, read in row order (coalesced), written to its
+// K-tiled slot.  src rows are 16-byte aligned; K % 64 == 0.
+__global__ __launch_bounds__(256) void pack_k_tiled_kernel(const int8_t* __restrict__ src, int64_t ld, int64_t rows,
+                                                           int64_t K, int8_t* __restrict__ dst) {
+    const int64_t cpr = K >> 4, total = rows * cpr;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / cpr, c = (i - r * cpr) << 4;
+        *(uint4*)(dst + k_tiled_offset(r, c, K, rows)) = *(const uint4*)(src + r * ld + c);
+    }
+}
+
 static unsigned grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -119,6 +133,13 @@ hipError_t launch_lora_fold(hipStream_t stream, float* w, int64_t ldw, int64_t r
                             const float* B, int64_t rank, float scale) {
     hipLaunchKernelGGL(lora_fold_kernel, dim3(grid_for(rows * k)), dim3(256), 0, stream, w, ldw, rows, k, A, B, rank,
                        scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_k_tiled(hipStream_t stream, const int8_t* src, int64_t ld, int64_t rows, int64_t K,
+                               int8_t* dst) {
+    hipLaunchKernelGGL(pack_k_tiled_kernel, dim3(grid_for(rows * (K >> 4))), dim3(256), 0, stream, src, ld, rows, K,
+                       dst);
     return hipGetLastError();
 }
 

@@ -65,7 +65,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_quant_rotate_mod", "phi_hip_i8_gemm_residual", "phi_hip_quant_rotate_act",
            "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
            "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
-           "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes"]
+           "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes",
+           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt"]
 
 _lib = None
 
@@ -114,6 +115,10 @@ def load() -> ctypes.CDLL:
     L.phi_hip_q8_linear_noalloc.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, I]
     L.phi_hip_noalloc_scratch_bytes.argtypes = []
     L.phi_hip_noalloc_scratch_bytes.restype = SZ
+    L.phi_hip_pack_k_tiled.argtypes = [P, P, I64, I64, I64, P]
+    L.phi_hip_quant_rotate_kt.argtypes = [P, P, I, I64, I64, I64, P, P, F, I]
+    L.phi_hip_i8_gemm_kt.argtypes = [P, P, P, P, P, I, P, I, P, I, I64, I64, I64, I64]
+    L.phi_hip_q8_linear_kt.argtypes = [P, P, I, I64, I64, I64, P, P, I, P, I, I64, P, I, I64, P, P, I]
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:
@@ -460,3 +465,76 @@ def lora_tail(x: torch.Tensor, At: torch.Tensor, Bt: torch.Tensor, out: torch.Te
     _check(load().phi_hip_lora_tail(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(At), _ptr(Bt), R, N,
                                     _ptr(out), _dt(out), out.stride(0), _ptr(h), h.numel() * h.element_size()))
     return out
+
+
+def pack_k_tiled(W: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """An int8 [rows, K] matrix (row pitch a multiple of 16) in the K-tiled
+    operand layout of the persistent GEMM (phi_hip_pack_k_tiled): a flat
+    int8 tensor of rows * K bytes."""
+    _require_device(W, out)
+    rows, K = W.shape
+    if out is None:
+        out = torch.empty((rows * K,), dtype=torch.int8, device=W.device)
+    if out.numel() < rows * K:
+        raise ValueError(f"pack_k_tiled: out holds {out.numel()} bytes, needs {rows * K}")
+    _check(load().phi_hip_pack_k_tiled(_stream(stream), _ptr(W), W.stride(0), rows, K, _ptr(out)))
+    return out
+
+
+def quant_rotate_kt(x: torch.Tensor, q: torch.Tensor | None = None, s: torch.Tensor | None = None,
+                    qmax: float = 127.0, round_mode: int = ROUND_HALF_AWAY, stream=None):
+    """quant_rotate with q (rows * K bytes) written K-tiled (phi_hip_quant_rotate_kt)."""
+    _require_device(x, q, s)
+    rows, K = x.shape
+    if q is None:
+        q = torch.empty((rows * K,), dtype=torch.int8, device=x.device)
+    if s is None:
+        s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    if q.numel() < rows * K:
+        raise ValueError(f"quant_rotate_kt: q holds {q.numel()} bytes, needs {rows * K}")
+    _check(load().phi_hip_quant_rotate_kt(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0), _ptr(q),
+                                          _ptr(s), qmax, round_mode))
+    return q, s
+
+
+def i8_gemm_kt(A: torch.Tensor, B: torch.Tensor, M: int, N: int, K: int, sA: torch.Tensor | None,
+               sB: torch.Tensor | None, bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
+               C: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """phi_hip_i8_gemm_kt: A [M, K] and B [N, K] given K-tiled (pack_k_tiled)."""
+    _require_device(A, B, sA, sB, bias, C)
+    for name, t, rows in (("A", A, M), ("B", B, N)):
+        if t.numel() < rows * K:
+            raise ValueError(f"i8_gemm_kt: {name} holds {t.numel()} bytes, needs {rows * K}")
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=A.device)
+    _check(load().phi_hip_i8_gemm_kt(_stream(stream), _ptr(A), _ptr(B), _ptr(sA), _ptr(sB),
+                                     1 if sB is not None and sB.numel() == 1 else 0, _ptr(bias),
+                                     _dt(bias) if bias is not None else F32, _ptr(C), _dt(C), C.stride(0),
+                                     M, N, K))
+    return C
+
+
+def q8_linear_kt(x: torch.Tensor, Wkt: torch.Tensor, N: int, sW: torch.Tensor,
+                 bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
+                 q8: torch.Tensor | None = None, s8: torch.Tensor | None = None,
+                 C: torch.Tensor | None = None, round_mode: int = ROUND_HALF_AWAY,
+                 stream=None) -> torch.Tensor:
+    """q8_linear with the weight packed K-tiled (pack_k_tiled, N rows): q8
+    (M * K bytes) is written K-tiled; C is bit-identical to q8_linear's."""
+    _require_device(x, Wkt, sW, bias, q8, s8, C)
+    M, K = x.shape
+    if Wkt.numel() < N * K:
+        raise ValueError(f"q8_linear_kt: the packed weight holds {Wkt.numel()} bytes, needs {N * K}")
+    if q8 is None:
+        q8 = torch.empty((M * K,), dtype=torch.int8, device=x.device)
+    if s8 is None:
+        s8 = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if q8.numel() < M * K:
+        raise ValueError(f"q8_linear_kt: q8 holds {q8.numel()} bytes, needs {M * K}")
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    _check(load().phi_hip_q8_linear_kt(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(Wkt),
+                                       _ptr(sW), 1 if sW.numel() == 1 else 0, _ptr(bias),
+                                       _dt(bias) if bias is not None else F32, N, _ptr(C), _dt(C),
+                                       C.stride(0), _ptr(q8), _ptr(s8), round_mode))
+    return C

@@ -239,6 +239,33 @@ def test_any_k_gemm_contract(lib):
     assert rc == 2 and "leading dimension" in Q.last_error()
 
 
+def test_k_tiled_contracts(lib):
+    """The K-tiled entries take whole 256-deep K-steps, 16-byte aligned
+    operands and whole 16-byte output pieces, and refuse anything else before
+    any device work."""
+    odd = ctypes.c_void_p(0x10008)
+    rc = lib.phi_hip_pack_k_tiled(None, FAKE, 320, 4, 320, FAKE)
+    assert rc == 2 and "not a multiple of 256" in Q.last_error()
+    rc = lib.phi_hip_pack_k_tiled(None, odd, 512, 4, 512, FAKE)
+    assert rc == 3 and "16-byte aligned" in Q.last_error()
+    rc = lib.phi_hip_pack_k_tiled(None, FAKE, 520, 4, 512, FAKE)
+    assert rc == 3 and "multiple of 16" in Q.last_error()
+    rc = lib.phi_hip_pack_k_tiled(None, FAKE, 512, 0, 512, FAKE)
+    assert rc == 2 and "empty" in Q.last_error()
+    rc = lib.phi_hip_i8_gemm_kt(None, FAKE, FAKE, FAKE, FAKE, 1, None, Q.F32, FAKE, Q.BF16, 12, 4, 12, 512)
+    assert rc == 7 and "16-byte output pieces" in Q.last_error()
+    rc = lib.phi_hip_i8_gemm_kt(None, FAKE, odd, FAKE, FAKE, 1, None, Q.F32, FAKE, Q.BF16, 16, 4, 16, 512)
+    assert rc == 3
+    rc = lib.phi_hip_q8_linear_kt(None, FAKE, Q.BF16, 16384 + 256, 4, 16384 + 256, FAKE, FAKE, 1, None, Q.F32, 16,
+                                  FAKE, Q.BF16, 16, FAKE, FAKE, 0)
+    assert rc == 7 and "16384" in Q.last_error()
+    rc = lib.phi_hip_q8_linear_kt(None, FAKE, Q.BF16, 512, 4, 512, FAKE, FAKE, 1, None, Q.F32, 16, FAKE, Q.BF16,
+                                  16, None, FAKE, 0)
+    assert rc == 1 and "activation scratch" in Q.last_error()
+    rc = lib.phi_hip_quant_rotate_kt(None, FAKE, Q.BF16, 4, 300, 300, FAKE, FAKE, 127.0, 0)
+    assert rc == 2
+
+
 def test_workspace_queries(lib):
     assert lib.phi_hip_workspace_bytes(4352, 12288, 3072) >= 0
     assert lib.phi_hip_gemv_workspace_bytes(60) >= 0

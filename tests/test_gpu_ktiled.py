@@ -1,0 +1,112 @@
+"""GPU parity of the K-tiled operand path (phi_hip_pack_k_tiled,
+phi_hip_quant_rotate_kt, phi_hip_i8_gemm_kt, phi_hip_q8_linear_kt).
+
+The K-tiled layout is a re-arrangement of the same bytes, so the bar is
+identity with the row-major path, which the other GPU tests hold bit-exact
+against the oracle:
+* pack_k_tiled is the permutation the header documents (checked against a
+  numpy gather on small matrices, partial strips included) and loses nothing
+  (unpacking restores the matrix);
+* quant_rotate_kt writes the same codes and scales as quant_rotate, in that
+  permutation;
+* the K-tiled GEMM and linear give the row-major path's outputs bit for bit
+  (int32, fp32 and bf16), at small, ragged and the configs' full sizes, on
+  each tile plan (mixed, 256 x 256 only, 128 x 128 only).
+"""
+import numpy as np
+import pytest
+import torch
+
+import phi_qlinear as Q
+from phi_qlinear import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def kt_index(rows, K):
+    """For each (r, k) of a rows x K matrix, its byte position in the K-tiled
+    layout (the header's formula, evaluated with numpy)."""
+    r = np.arange(rows)[:, None]
+    k = np.arange(K)[None, :]
+    s, rr = r // 256, r % 256
+    h = np.minimum(256, rows - 256 * s)
+    slot = ((k // 16) % 4) ^ ((rr // 4) % 4)
+    return 256 * K * s + h * 64 * (k // 64) + 64 * rr + 16 * slot + k % 16
+
+
+@pytest.mark.parametrize("rows,K", [(1, 256), (16, 512), (100, 256), (256, 768), (300, 512), (513, 1024)])
+def test_pack_is_the_documented_permutation(dev, rows, K):
+    W = synth.int8_weight(rows, K, seed=rows + K)
+    packed = Q.pack_k_tiled(W.to(dev)).cpu().numpy()
+    idx = kt_index(rows, K)
+    assert np.array_equal(np.sort(idx.ravel()), np.arange(rows * K))  # a permutation of rows * K bytes
+    assert np.array_equal(packed[idx], W.numpy())
+
+
+def test_pack_with_row_pitch(dev):
+    """A source with row pitch > K packs only its first K columns."""
+    rows, K, ld = 300, 512, 640
+    big = synth.int8_weight(rows, ld, seed=5).to(dev)
+    packed = Q.pack_k_tiled(big[:, :K]).cpu().numpy()
+    assert np.array_equal(packed[kt_index(rows, K)], big[:, :K].cpu().numpy())
+
+
+@pytest.mark.parametrize("rows,K", [(1, 256), (77, 3072), (300, 1024), (4352, 3072), (4352, 12288)])
+def test_quant_rotate_kt_is_quant_rotate_packed(dev, rows, K):
+    x = synth.activations(rows, K, seed=rows, device=dev)
+    q, s = Q.quant_rotate(x)
+    qk, sk = Q.quant_rotate_kt(x)
+    assert torch.equal(s, sk)
+    assert torch.equal(qk, Q.pack_k_tiled(q))
+
+
+GEMM_SHAPES = [(1, 256, 256), (100, 264, 512), (300, 1000, 768), (513, 520, 1024), (4352, 12288, 3072),
+               (4352, 3072, 12288), (32760, 512, 512)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("out", ["bf16", "f32", "i32"])
+def test_gemm_kt_matches_row_major(dev, M, N, K, out):
+    A = synth.int8_weight(M, K, seed=M, device=dev)
+    B = synth.int8_weight(N, K, seed=N + 1, device=dev)
+    sA = torch.rand(M, device=dev) * 0.01 + 1e-3
+    sB = torch.rand(N, device=dev) * 0.01 + 1e-3
+    bias = synth.bias(N, seed=3, device=dev)
+    odt = {"bf16": torch.bfloat16, "f32": torch.float32, "i32": torch.int32}[out]
+    want = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=odt)
+    got = Q.i8_gemm_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, sA, sB, bias, out_dtype=odt)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16 if out == "bf16" else torch.int32),
+                       want.view(torch.int16 if out == "bf16" else torch.int32))
+
+
+@pytest.mark.parametrize("plan", ["persist256", "persist128"])
+def test_gemm_kt_each_tile_plan(dev, monkeypatch, plan):
+    """Forced single-size plans: 256 x 256 tiles over a partial last strip,
+    and 128 x 128 tiles in both halves of every strip."""
+    monkeypatch.setenv("PHI_GEMM_KERNEL", plan)
+    M, N, K = 700, 1040, 1536
+    A = synth.int8_weight(M, K, seed=11, device=dev)
+    B = synth.int8_weight(N, K, seed=12, device=dev)
+    want = Q.i8_gemm(A, B, None, None, out_dtype=torch.int32)
+    got = Q.i8_gemm_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 256, 512), (77, 3072, 1000), (4352, 3072, 12288), (4352, 12288, 3072)])
+def test_q8_linear_kt_matches_q8_linear(dev, M, K, N):
+    x = synth.activations(M, K, seed=M + 7, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    want = Q.q8_linear(x, W, sW, b, q8=q8, s8=s8)
+    qk = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    sk = torch.empty((M,), dtype=torch.float32, device=dev)
+    got = Q.q8_linear_kt(x, Q.pack_k_tiled(W), N, sW, b, q8=qk, s8=sk)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(sk, s8)
+    assert torch.equal(qk, Q.pack_k_tiled(q8))
