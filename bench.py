@@ -58,6 +58,10 @@ CONFIGS = {
     # Ceilings, not a workload: int8 MFMAs with no data movement (zero, static
     # and rotating random operands) and the operand stream into LDS alone.
     "mfma_ceiling": dict(kind="ceiling"),
+    # A reference point, not this library: the vendor int8 GEMM (hipBLASLt,
+    # through torch._int_mm) on config 1's shapes, int32 out, no epilogue.
+    "c1_up_vendor": dict(kind="vendor", M=4352, K=3072, N=12288),
+    "c1_down_vendor": dict(kind="vendor", M=4352, K=12288, N=3072),
 }
 
 
@@ -149,43 +153,58 @@ def bench_w8a8(cfg, steps, warmup, layout="kt"):
         qk = q8.view(-1)
         torch.cuda.synchronize()
 
-    def step():
+    def linear():
+        if layout == "kt":
+            Q.q8_linear_kt(x, Wk, N, sW, b, q8=qk, s8=s8, C=y)
+        else:
+            Q.q8_linear(x, W, sW, b, q8=q8, s8=s8, C=y)
+
+    def prologue():
         if layout == "kt":
             Q.quant_rotate_kt(x, q=qk, s=s8)
         else:
             Q.quant_rotate(x, q=q8, s=s8)
-        mid = torch.cuda.Event(enable_timing=True)
-        mid.record()
+
+    def gemm():
         if layout == "kt":
             Q.i8_gemm_kt(qk, Wk, M, N, K, s8, sW, b, C=y)
         else:
             Q.i8_gemm(q8, W, s8, sW, b, C=y)
-        return mid
 
     for _ in range(warmup):
-        step()
+        linear()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    mids = []
+    # The timed region: `steps` whole linears back to back, nothing recorded
+    # between them (an event record costs ~4.5 us of stream time a step).
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     start.record()
-    for a, z in ev:
-        a.record()
-        mids.append(step())
-        z.record()
+    for _ in range(steps):
+        linear()
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
-    gemm_ms = sum(m.elapsed_time(z) for m, (_, z) in zip(mids, ev)) / steps
-    pro_ms = sum(a.elapsed_time(m) for m, (a, _) in zip(mids, ev)) / steps
+    # The roofline region, right after: the same steps with an event pair
+    # around each GEMM launch, on the launch stream.  It runs later in the
+    # clock transient than the timed region, so its GEMM time is, if
+    # anything, pessimistic.
+    mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        prologue()
+        mids[i].record()
+        gemm()
+        ends[i].record()
+    torch.cuda.synchronize()
+    gemm_ms = sum(m.elapsed_time(z) for m, z in zip(mids, ends)) / steps
+    pro_ms = (sum(ends[i - 1].elapsed_time(mids[i]) for i in range(1, steps)) / (steps - 1)) if steps > 1 else None
     ops = 2.0 * M * N * K
     return {
         "value": ops / (ms * 1e-3) / 1e12, "ms": ms, "gemm_ms": gemm_ms, "prologue_ms": pro_ms,
         "roofline": {"bound": "mfma", "achieved": ops / (gemm_ms * 1e-3) / 1e12,
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "traffic": None},
-        "dtype": "int8", "extra": {"prologue_us": pro_ms * 1e3, "gemm_us": gemm_ms * 1e3,
+        "dtype": "int8", "extra": {"prologue_us": None if pro_ms is None else pro_ms * 1e3,
+                                   "gemm_us": gemm_ms * 1e3,
                                    "fused_linear_tops": ops / (ms * 1e-3) / 1e12},
     }
 
@@ -412,6 +431,34 @@ def bench_gemv(cfg, steps, warmup):
                          "frac": gbs / HBM_PEAK_GBS, "traffic": None}}
 
 
+def bench_vendor(cfg, steps, warmup):
+    """torch._int_mm (hipBLASLt's int8 GEMM) on the shape: A [M, K] row-major
+    times B [N, K] row-major (the checkpoint layout, a column-major [K, N]
+    view), int32 out.  Timed like the W8A8 bench's timed region."""
+    import torch
+
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    A = synth.int8_weight(M, K, seed=0, device=dev)
+    B = synth.int8_weight(N, K, seed=1, device=dev)
+    for _ in range(warmup):
+        torch._int_mm(A, B.t())
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        torch._int_mm(A, B.t())
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    tops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"value": tops, "ms": ms, "dtype": "int8", "unit": "TOPS",
+            "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                         "frac": tops / INT8_PEAK_TOPS, "traffic": None}}
+
+
 def bench_ceiling(steps, warmup):
     """The two ceilings the headline GEMM is argued against, from the probe
     kernels of lib/libphi_probe.so: every wave of every CU issues int8 MFMAs
@@ -514,6 +561,8 @@ def main() -> int:
         r = bench_w4a4(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "lora":
         r = bench_lora(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "vendor":
+        r = bench_vendor(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "ceiling":
         r = bench_ceiling(min(args.steps, 20), min(args.warmup, 20))
     else:

@@ -629,7 +629,20 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     if (!aligned(lut, 16)) return fail(PHI_ERR_ALIGN, "%s: lut must be 16-byte aligned", who);
     const int bk = bias_kind_of(bias, bias_dtype, &st);
     if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
-    st = phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
+    const char* e = getenv("PHI_GEMM_KERNEL");
+    const bool force_staged = e && strcmp(e, "tile128") == 0;
+    // With a workspace (phi_hip_w4a8_workspace_bytes), large M expands the
+    // codes once into it and runs the W8A8 GEMM: one table lookup per weight
+    // instead of one per weight per 256-row tile.  Both operands then take the
+    // K-tiled layout (K <= 16384; PHI_GEMM_KT=0 keeps them row-major, an A/B
+    // switch).
+    const size_t need = phi_hip_w4a8_workspace_bytes(M, N, K, group);
+    const bool expand = !force_staged && need > 0 && workspace && ws_bytes >= need && aligned(workspace, 16) &&
+                        aligned(codes, 16) && codes_row_bytes % 16 == 0 && persist_ok(C, c_dtype, N, K, K, K, ldc);
+    const char* ekt = getenv("PHI_GEMM_KT");
+    const bool kt = expand && K <= 16384 && aligned(q8, 16) && !(ekt && ekt[0] == '0');
+    st = kt ? phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode)
+            : phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
     if (st != PHI_OK) return st;
     phi_dev::GemmParams p{};
     p.A = q8;
@@ -653,20 +666,14 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     int sh = 0;
     while ((1ll << sh) < group) sh++;
     p.group_shift = sh;
-    const char* e = getenv("PHI_GEMM_KERNEL");
-    const bool force_staged = e && strcmp(e, "tile128") == 0;
-    // With a workspace (phi_hip_w4a8_workspace_bytes), large M expands the
-    // codes once into it and runs the W8A8 GEMM: one table lookup per weight
-    // instead of one per weight per 256-row tile.
-    const size_t need = phi_hip_w4a8_workspace_bytes(M, N, K, group);
-    if (!force_staged && need > 0 && workspace && ws_bytes >= need && aligned(workspace, 16) &&
-        aligned(codes, 16) && codes_row_bytes % 16 == 0 && persist_ok(C, c_dtype, N, K, K, K, ldc)) {
-        st = check_hip(phi_dev::launch_w4_lut_expand((hipStream_t)stream, p, (int8_t*)workspace), who);
+    if (expand) {
+        st = check_hip(phi_dev::launch_w4_lut_expand((hipStream_t)stream, p, (int8_t*)workspace, kt), who);
         if (st != PHI_OK) return st;
         phi_dev::GemmParams g = p;
         g.B = (const int8_t*)workspace;
         g.ldb = K;
         g.lut = nullptr;
+        g.kt = kt ? 1 : 0;
         set_vec_flags(g, c_dtype, ldc);
         GemmKernel gk = GK_PERSIST;
         if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;

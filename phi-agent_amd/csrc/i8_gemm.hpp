@@ -71,8 +71,9 @@ hipError_t launch_i8_gemm_persist_mixed(hipStream_t stream, const GemmParams& pb
 // (i8_gemm_pipe.hip).
 hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile);
 hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus);
-// The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out.
-hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out);
+// The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out,
+// row-major or (kt, K % 64 == 0) in the K-tiled layout.
+hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out, bool kt = false);
 
 // Element-wise operation applied to every input element before the rotation.
 enum QrPreOp { QR_PLAIN = 0, QR_MOD = 1, QR_GELU = 2, QR_SILU_GATE = 3 };

@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256) void i8_gemm_persist_mixed_kernel(GemmParams p
 __global__ __launch_bounds__(256) void w4_lut_expand_kernel(const uint8_t* __restrict__ codes, int64_t ldb,
                                                             const int8_t* __restrict__ lut, int64_t lut_groups,
                                                             int group_shift, int w4_signed, int64_t N, int64_t K,
-                                                            int8_t* __restrict__ out) {
+                                                            int kt, int8_t* __restrict__ out) {
     const int64_t per_row = K / 32;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= N * per_row) return;
@@ -450,19 +450,21 @@ __global__ __launch_bounds__(256) void w4_lut_expand_kernel(const uint8_t* __res
     const u32x4 c = *(const u32x4*)(codes + row * ldb + c32 * 16);
     const u32x4 t = w4_signed ? signed_nibble_table()
                               : *(const u32x4*)(lut + (row * lut_groups + ((c32 * 32) >> group_shift)) * 16);
-    int8_t* o = out + row * K + c32 * 32;
-    *(v4i*)o = expand16b(c[0], c[1], t);
-    *(v4i*)(o + 16) = expand16b(c[2], c[3], t);
+    // Row-major, or the K-tiled operand layout (k_tiled_offset).
+    int8_t* o0 = out + (kt ? k_tiled_offset(row, c32 * 32, K, N) : row * K + c32 * 32);
+    int8_t* o1 = out + (kt ? k_tiled_offset(row, c32 * 32 + 16, K, N) : row * K + c32 * 32 + 16);
+    *(v4i*)o0 = expand16b(c[0], c[1], t);
+    *(v4i*)o1 = expand16b(c[2], c[3], t);
 }
 
-hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out) {
+hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out, bool kt) {
     if (p.K % 32 != 0 || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 || ((uintptr_t)out & 15) != 0 ||
-        (!p.w4_signed && (p.group_shift < 5 || !p.lut)))
+        (!p.w4_signed && (p.group_shift < 5 || !p.lut)) || (kt && p.K % 64 != 0))
         return hipErrorInvalidValue;
     const int64_t threads = (int64_t)p.N * (p.K / 32);
     hipLaunchKernelGGL(w4_lut_expand_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
                        (const uint8_t*)p.B, p.ldb, p.lut, p.lut_groups, p.group_shift, p.w4_signed, (int64_t)p.N,
-                       (int64_t)p.K, out);
+                       (int64_t)p.K, kt ? 1 : 0, out);
     return hipGetLastError();
 }
 

@@ -138,6 +138,27 @@ def test_in_register_linear_equals_expand_then_w8a8(dev, monkeypatch, kernel, wi
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,N,K,group", [(600, 520, 3072, 128), (777, 1032, 768, 128), (4352, 2304, 512, 256)])
+def test_expand_once_row_major_switch(dev, monkeypatch, M, N, K, group):
+    """The expand-once path (512 rows and more) with its operands row-major (PHI_GEMM_KT=0)
+    gives the bits of its K-tiled default and of expand-then-W8A8."""
+    codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=M + N + 1)
+    cd, rd, sd, kd = codes.to(dev), s_rel.to(dev), sch.to(dev), corr.to(dev)
+    x = synth.activations(M, K, seed=M + 1, device=dev)
+    q, s = Q.w4a8_expand(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    lut, s2 = Q.w4a8_prepare(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    ws = Q.w4a8_workspace(M, N, K, group, dev)
+    assert ws is not None
+    y_kt = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
+    monkeypatch.setenv("PHI_GEMM_KT", "0")
+    y_row = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
+    monkeypatch.delenv("PHI_GEMM_KT")
+    y_ref = Q.q8_linear(x, q, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y_kt.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(y_row.view(torch.int16), y_ref.view(torch.int16))
+
+
 @pytest.mark.slow
 def test_config2_full_size(dev, orc):
     """M=4352, K=3072, N=9216, group 128: in-register path vs expand + W8A8,
@@ -149,8 +170,10 @@ def test_config2_full_size(dev, orc):
     lut, s2 = Q.w4a8_prepare(codes, s_rel, Q.F16, sch, k=K, group=group, correction=corr)
     y_ref = Q.q8_linear(x, q, s)
     y = Q.w4a8_linear(x, codes, lut, s2, group=group)
+    y_ws = Q.w4a8_linear(x, codes, lut, s2, group=group, workspace=Q.w4a8_workspace(M, N, K, group, dev))
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(y_ws.view(torch.int16), y_ref.view(torch.int16))
     rows = torch.arange(0, N, 577)
     qo, so = orc.w4a8_expand(np_of(codes[rows]), np_of(s_rel[rows]), Q.F16, np_of(sch[rows]),
                              k=K, group=group, correction=np_of(corr[:, rows]))
