@@ -61,7 +61,14 @@ CONFIGS = {
     # A reference point, not this library: the vendor int8 GEMM (hipBLASLt,
     # through torch._int_mm) on config 1's shapes, int32 out, no epilogue.
     "c1_up_vendor": dict(kind="vendor", M=4352, K=3072, N=12288),
+    # The headline step with the GEMM's per-tile timeline recorded (the
+    # pipeline rebuilt with its trace hooks in lib/libphi_probe.so).
+    "c1_up_tiles": dict(kind="tiletrace", M=4352, K=3072, N=12288),
+    "c1_down_tiles": dict(kind="tiletrace", M=4352, K=12288, N=3072),
     "c1_down_vendor": dict(kind="vendor", M=4352, K=12288, N=3072),
+    # A reference point for the prologue: torch's bf16 -> int8 conversion of
+    # the same activation tensor moves the prologue's bytes (2K in, K out a row).
+    "c1_prologue_vendor": dict(kind="convref", M=4352, K=3072),
 }
 
 
@@ -459,6 +466,137 @@ def bench_vendor(cfg, steps, warmup):
                          "frac": tops / INT8_PEAK_TOPS, "traffic": None}}
 
 
+def bench_tiletrace(cfg, steps, warmup):
+    """The headline step (K-tiled quantiser, then the GEMM) with the GEMM
+    launched from the traced build of the pipeline (phi_probe_tile_trace):
+    the same kernel code plus one real-time stamp per workgroup at each
+    tile's start, K-loop end and epilogue end.  The record of the last timed
+    launch gives where a workgroup's time goes, averaged over workgroups."""
+    import ctypes
+
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    lib = ctypes.CDLL(os.path.join(PKG, "lib", "libphi_probe.so"))
+    P, I = ctypes.c_void_p, ctypes.c_int
+    lib.phi_probe_tile_trace.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, P, ctypes.c_longlong]
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    Wk = Q.pack_k_tiled(W)
+    q8 = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    slots = 1024 * 64
+    rec = torch.zeros(slots, dtype=torch.int64, device=dev)
+    # The library's plan: whole rounds of 256 x 256 tiles, the rest 128 x 128.
+    big_rows = Q.big_tile_rows(M, N)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        Q.quant_rotate_kt(x, q=q8, s=s8)
+        rc = lib.phi_probe_tile_trace(stream, q8.data_ptr(), Wk.data_ptr(), s8.data_ptr(), sW.data_ptr(),
+                                      b.data_ptr(), y.data_ptr(), M, N, K, big_rows, 1, rec.data_ptr(), slots)
+        if rc != 0:
+            raise RuntimeError(f"phi_probe_tile_trace failed ({rc})")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    r = rec.view(-1, 64).cpu().tolist()
+    used = [w for w in r if w[24] != 0]
+    t0 = min(w[24] for w in used)
+    us = lambda t: (t - t0) / 100.0  # 100 MHz real-time clock
+
+    def tiles(w, base):
+        out = []
+        for i in range(8):
+            a, k, e = w[base + 3 * i], w[base + 3 * i + 1], w[base + 3 * i + 2]
+            if a == 0:
+                break
+            out.append(((k - a) / 100.0, (e - k) / 100.0))
+        return out
+
+    big = [t for w in used for t in tiles(w, 0)]
+    small = [t for w in used for t in tiles(w, 26)]
+    mean = lambda v: sum(v) / len(v) if v else None
+    first = [us(w[0] if w[0] else w[26]) for w in used if w[0] or w[26]]
+    bigdone = [us(w[25]) for w in used if w[25]]
+    ends = [us(w[50]) for w in used]
+    per_xcd = {}
+    for w in used:
+        d = per_xcd.setdefault(int(w[60]), [])
+        d.append(us(w[25]) if w[25] else us(w[50]))
+    ops = 2.0 * M * N * K
+    extra = {
+        "big_rows": big_rows, "workgroups": len(used),
+        "big_tiles": len(big), "big_kloop_us": mean([t[0] for t in big]), "big_epilogue_us": mean([t[1] for t in big]),
+        "small_tiles": len(small), "small_kloop_us": mean([t[0] for t in small]),
+        "small_epilogue_us": mean([t[1] for t in small]),
+        "first_tile_start_us": mean(first),
+        "big_phase_end_us": {"min": min(bigdone), "mean": mean(bigdone), "max": max(bigdone)} if bigdone else None,
+        "kernel_end_us": {"min": min(ends), "mean": mean(ends), "max": max(ends)},
+        "big_phase_end_by_xcd_us": {str(k): round(mean(v), 2) for k, v in sorted(per_xcd.items())},
+    }
+    log("bench: tile trace " + json.dumps(extra))
+    return {"value": ops / (ms * 1e-3) / 1e12, "ms": ms, "dtype": "int8", "unit": "TOPS",
+            "roofline": {"bound": "mfma", "achieved": ops / (ms * 1e-3) / 1e12, "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "traffic": None},
+            "extra": extra}
+
+
+def bench_convref(cfg, steps, warmup):
+    """torch's elementwise bf16 -> int8 conversion over the prologue's
+    activation tensor: the prologue's HBM bytes with none of its work."""
+    import torch
+
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K = cfg["M"], cfg["K"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    for _ in range(warmup):
+        q.copy_(x)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        q.copy_(x)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gbs = 3.0 * M * K / (ms * 1e-3) / 1e9
+    # A plain bf16 copy of the same tensor (4K bytes a row moved).
+    x2 = torch.empty_like(x)
+    for _ in range(warmup):
+        x2.copy_(x)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        x2.copy_(x)
+    end.record()
+    torch.cuda.synchronize()
+    ms_copy = start.elapsed_time(end) / steps
+    return {"value": gbs, "ms": ms, "dtype": "bf16", "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "extra": {"convert_us": ms * 1e3, "copy_us": ms_copy * 1e3,
+                      "copy_gbs": 4.0 * M * K / (ms_copy * 1e-3) / 1e9}}
+
+
 def bench_ceiling(steps, warmup):
     """The two ceilings the headline GEMM is argued against, from the probe
     kernels of lib/libphi_probe.so: every wave of every CU issues int8 MFMAs
@@ -561,6 +699,10 @@ def main() -> int:
         r = bench_w4a4(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "lora":
         r = bench_lora(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "tiletrace":
+        r = bench_tiletrace(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "convref":
+        r = bench_convref(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "vendor":
         r = bench_vendor(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "ceiling":

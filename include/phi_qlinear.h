@@ -210,6 +210,12 @@ phi_status phi_hip_i8_gemm_kt(phi_stream_t stream, const int8_t* A, const int8_t
                               int sb_scalar, const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
                               int64_t M, int64_t N, int64_t K);
 
+/* The rows of an M x N persistent GEMM on the current device that run as
+ * 256 x 256 tiles (a multiple of 256, or M); the rest run as 128 x 128 tiles
+ * in the same launch.  The plan minimises the rounds of tiles over the
+ * device's compute units.  0 for an empty problem. */
+int64_t phi_hip_big_tile_rows(int64_t M, int64_t N);
+
 /* phi_hip_q8_linear with the weight W K-tiled (phi_hip_pack_k_tiled at load
  * time): the prologue writes q8 (M x K bytes) K-tiled, then phi_hip_i8_gemm_kt.
  * C is bit-identical to phi_hip_q8_linear's; s8 is the same; q8 holds the same

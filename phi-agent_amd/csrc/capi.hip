@@ -495,6 +495,11 @@ static phi_status i8_gemm_kt_impl(const char* who, phi_stream_t stream, const in
     return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, false, c_dtype, ldc), who);
 }
 
+int64_t phi_hip_big_tile_rows(int64_t M, int64_t N) {
+    if (M <= 0 || N <= 0 || M > INT32_MAX || N > INT32_MAX) return 0;
+    return big_tile_rows(M, N, num_cus());
+}
+
 phi_status phi_hip_pack_k_tiled(phi_stream_t stream, const int8_t* src, int64_t ld, int64_t rows, int64_t K,
                                 int8_t* dst) {
     static const char* who = "pack_k_tiled";

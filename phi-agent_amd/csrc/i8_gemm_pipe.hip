@@ -43,6 +43,16 @@
 #include "i8_gemm.hpp"
 #include "persist_common.hpp"
 
+// Tile-timeline hooks.  The library defines them empty.  The tracing build
+// in probe.hip defines them to record the real-time clock per workgroup: at
+// the kernel's start, at each tile's start, K-loop end and epilogue end, and
+// between the two tile sizes.
+#ifndef PHI_PIPE_STAMP
+#define PHI_PIPE_STAMP(phase, tile, point)
+#define PHI_PIPE_TRACE_BEGIN
+#define PHI_PIPE_TRACE_END
+#endif
+
 namespace phi_dev {
 
 namespace {
@@ -369,6 +379,7 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
         int8_t* ln = w.le + ((i + 1) & 1) * EBYTES;
         const NextTile nt = next_tile<WT>(s, p, t + s.G, i + 1 < ntile);
         constexpr int VWR = C::VWR, VWN = C::VWN;
+        PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 0);
         if (s.KT == 4) {
             pstep<WT, 0, true, VWR, true, false, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 1, false, VWR, false, true, G, KT>(f0, acc, w, p, nt, ln);
@@ -390,7 +401,9 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
             pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
         }
+        PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 1);
         epilogue<WT, G>(acc, p, s, t, w, le);
+        PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 2);
         if (++i == ntile) break;
     }
     // Loads past the last K-step (into released stages) and the epilogue's
@@ -404,7 +417,9 @@ __global__ __launch_bounds__(256) void i8_gemm_pipe_kernel(GemmParams p) {
     __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    PHI_PIPE_TRACE_BEGIN
     pipe_tiles<WT, G, KT>(p, la, lb, eall, cbuf);
+    PHI_PIPE_TRACE_END
 }
 
 // Both tile sizes in one launch: the workgroup's 256 x 256 tiles of pb, then
@@ -416,9 +431,12 @@ __global__ __launch_bounds__(256) void i8_gemm_pipe_mixed_kernel(GemmParams pb, 
     __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
+    PHI_PIPE_TRACE_BEGIN
     pipe_tiles<128, G, KT>(pb, la, lb, eall, cbuf);
     __syncthreads();  // every wave is done with the big tiles' LDS
+    PHI_PIPE_STAMP(2, 0, 0);
     pipe_tiles<64, G, KT>(ps, la, lb, eall, cbuf);
+    PHI_PIPE_TRACE_END
 }
 
 }  // namespace

@@ -15,8 +15,46 @@
 //   phi_probe_lds_dma  every wave streams 16 rows x 64 bytes per instruction
 //                   from a window of global memory into LDS, 4 K-steps of the
 //                   headline tile's A and B in flight, with no MFMAs.
+//   phi_probe_tile_trace  the persistent pipeline (i8_gemm_pipe.hip, compiled
+//                   here a second time into namespace phi_dev_trace with its
+//                   timeline hooks defined) with one record of real-time clock
+//                   stamps per workgroup: kernel start, each tile's start,
+//                   K-loop end and epilogue end, the switch between tile
+//                   sizes, and the end.  The stamps go to LDS during the run
+//                   and out to memory once, at the end.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+// The per-workgroup record (64 words of the 100 MHz real-time clock):
+//   [3 i + p]       256 x 256 tile i < 8, point p (0 start, 1 K-loop end, 2 epilogue end)
+//   [24] kernel start, [25] switch to 128 x 128 tiles, [50] kernel end
+//   [26 + 3 i + p]  128 x 128 tile i < 8, point p
+//   [60] the XCD the workgroup ran on
+__shared__ unsigned long long phi_trace_lds[64];
+__device__ unsigned long long* phi_trace_out;
+
+#define PHI_PIPE_STAMP(phase, tile, point)                                                              \
+    if (threadIdx.x == 0 && (tile) < 8)                                                                 \
+        phi_trace_lds[(phase) == 0 ? (tile) * 3 + (point) : (phase) == 1 ? 26 + (tile) * 3 + (point) : 25] = \
+            __builtin_amdgcn_s_memrealtime();
+#define PHI_PIPE_TRACE_BEGIN                                                   \
+    if (threadIdx.x < 64) phi_trace_lds[threadIdx.x] = 0;                     \
+    __syncthreads();                                                           \
+    if (threadIdx.x == 0) phi_trace_lds[24] = __builtin_amdgcn_s_memrealtime();
+#define PHI_PIPE_TRACE_END                                                            \
+    __syncthreads();                                                                  \
+    if (threadIdx.x == 0) {                                                           \
+        phi_trace_lds[50] = __builtin_amdgcn_s_memrealtime();                         \
+        unsigned int xcc_;                                                            \
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_));           \
+        phi_trace_lds[60] = xcc_ & 15;                                                \
+    }                                                                                 \
+    __syncthreads();                                                                  \
+    if (threadIdx.x < 64) phi_trace_out[blockIdx.x * 64 + threadIdx.x] = phi_trace_lds[threadIdx.x];
+
+#define phi_dev phi_dev_trace
+#include "i8_gemm_pipe.hip"
+#undef phi_dev
 
 namespace {
 
@@ -112,6 +150,59 @@ int phi_probe_lds_dma(void* stream, const int8_t* src, long long window, int ite
     if (window < (1 << 20) || window > (1ll << 31) - 1) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(lds_dma_probe, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, (int)window, iters, sink);
     return (int)hipGetLastError();
+}
+
+// The K-tiled (kt) or row-major pipeline over A [M, K], B [N, K] (bf16 out,
+// fp32 row scales sA, one fp32 scale sB, bf16 bias): 256 x 256 tiles for the
+// first big_rows rows (a multiple of 256), 128 x 128 tiles for the rest, in
+// one launch, as the library's plan runs it.  out holds slots >= grid x 64
+// words.
+int phi_probe_tile_trace(void* stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
+                         const void* bias, void* C, int M, int N, int K, int big_rows, int kt,
+                         unsigned long long* out, long long slots) {
+    if (M <= 0 || N <= 0 || K % 256 != 0 || K <= 0 || big_rows < 0 || big_rows > M ||
+        (big_rows % 256 != 0 && big_rows != M) || N % 8 != 0)
+        return (int)hipErrorInvalidValue;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return (int)hipErrorInvalidDevice;
+    const long long big = (long long)((big_rows + 255) / 256) * ((N + 255) / 256);
+    const long long small = (long long)((M - big_rows + 127) / 128) * ((N + 127) / 128);
+    const long long most = big > small ? big : small;
+    if ((most < cus ? most : cus) * 64 > slots) return (int)hipErrorInvalidValue;
+    hipError_t e = hipMemcpyToSymbolAsync(HIP_SYMBOL(phi_trace_out), &out, sizeof(out), 0, hipMemcpyHostToDevice,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) return (int)e;
+    phi_dev_trace::GemmParams p{};
+    p.A = A;
+    p.B = B;
+    p.sA = sA;
+    p.sB = sB;
+    p.bias = bias;
+    p.C = C;
+    p.lda = K;
+    p.ldb = K;
+    p.ldc = N;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.sb_scalar = 1;
+    p.bias_kind = bias ? phi_dev_trace::BIAS_BF16 : phi_dev_trace::BIAS_NONE;
+    p.c_kind = phi_dev_trace::C_BF16;
+    p.group_m = 4;
+    p.c_vec = 1;
+    p.c_vec16 = 1;
+    p.s_vec = 1;
+    p.kt = kt ? 1 : 0;
+    phi_dev_trace::GemmParams pb = p, ps = p;
+    pb.M = big_rows;
+    ps.M = M - big_rows;
+    ps.A = A + (size_t)big_rows * K;
+    ps.sA = sA + big_rows;
+    ps.C = (int8_t*)C + (size_t)big_rows * N * 2;
+    if (big_rows == M) return (int)phi_dev_trace::launch_i8_gemm_pipe((hipStream_t)stream, pb, cus, 128);
+    if (big_rows == 0) return (int)phi_dev_trace::launch_i8_gemm_pipe((hipStream_t)stream, ps, cus, 64);
+    return (int)phi_dev_trace::launch_i8_gemm_pipe_mixed((hipStream_t)stream, pb, ps, cus);
 }
 
 }  // extern "C"

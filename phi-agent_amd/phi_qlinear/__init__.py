@@ -66,7 +66,7 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
            "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
            "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes",
-           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt"]
+           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows"]
 
 _lib = None
 
@@ -117,6 +117,8 @@ def load() -> ctypes.CDLL:
     L.phi_hip_noalloc_scratch_bytes.restype = SZ
     L.phi_hip_pack_k_tiled.argtypes = [P, P, I64, I64, I64, P]
     L.phi_hip_quant_rotate_kt.argtypes = [P, P, I, I64, I64, I64, P, P, F, I]
+    L.phi_hip_big_tile_rows.argtypes = [I64, I64]
+    L.phi_hip_big_tile_rows.restype = I64
     L.phi_hip_i8_gemm_kt.argtypes = [P, P, P, P, P, I, P, I, P, I, I64, I64, I64, I64]
     L.phi_hip_q8_linear_kt.argtypes = [P, P, I, I64, I64, I64, P, P, I, P, I, I64, P, I, I64, P, P, I]
     for name in EXPORTS:
@@ -479,6 +481,12 @@ def pack_k_tiled(W: torch.Tensor, out: torch.Tensor | None = None, stream=None) 
         raise ValueError(f"pack_k_tiled: out holds {out.numel()} bytes, needs {rows * K}")
     _check(load().phi_hip_pack_k_tiled(_stream(stream), _ptr(W), W.stride(0), rows, K, _ptr(out)))
     return out
+
+
+def big_tile_rows(M: int, N: int) -> int:
+    """Rows of an M x N GEMM the persistent plan runs as 256 x 256 tiles on
+    the current device (phi_hip_big_tile_rows)."""
+    return int(load().phi_hip_big_tile_rows(M, N))
 
 
 def quant_rotate_kt(x: torch.Tensor, q: torch.Tensor | None = None, s: torch.Tensor | None = None,

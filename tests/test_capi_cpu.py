@@ -266,6 +266,17 @@ def test_k_tiled_contracts(lib):
     assert rc == 2
 
 
+def test_tile_plan(lib):
+    """The persistent plan on 256 compute units (the CPU fallback): config 1
+    up runs 16 tile-rows of 256 x 256 (three whole rounds) and the last 256
+    rows as 128 x 128 tiles; config 1 down, one round of 204 256 x 256 tiles;
+    config 0, 128 x 128 tiles only."""
+    assert lib.phi_hip_big_tile_rows(4352, 12288) == 4096
+    assert lib.phi_hip_big_tile_rows(4352, 3072) == 4352
+    assert lib.phi_hip_big_tile_rows(256, 3072) == 0
+    assert lib.phi_hip_big_tile_rows(0, 3072) == 0
+
+
 def test_workspace_queries(lib):
     assert lib.phi_hip_workspace_bytes(4352, 12288, 3072) >= 0
     assert lib.phi_hip_gemv_workspace_bytes(60) >= 0
