@@ -531,6 +531,14 @@ def bench_tiletrace(cfg, steps, warmup):
 
     big = [t for w in used for t in tiles(w, 0)]
     small = [t for w in used for t in tiles(w, 26)]
+    by_round = {}
+    for w in used:
+        for i, t in enumerate(tiles(w, 0)):
+            by_round.setdefault(i, []).append(t[0])
+    per_wg = {}
+    for w in used:
+        n = len(tiles(w, 0))
+        per_wg[n] = per_wg.get(n, 0) + 1
     mean = lambda v: sum(v) / len(v) if v else None
     first = [us(w[0] if w[0] else w[26]) for w in used if w[0] or w[26]]
     bigdone = [us(w[25]) for w in used if w[25]]
@@ -549,6 +557,8 @@ def bench_tiletrace(cfg, steps, warmup):
         "big_phase_end_us": {"min": min(bigdone), "mean": mean(bigdone), "max": max(bigdone)} if bigdone else None,
         "kernel_end_us": {"min": min(ends), "mean": mean(ends), "max": max(ends)},
         "big_phase_end_by_xcd_us": {str(k): round(mean(v), 2) for k, v in sorted(per_xcd.items())},
+        "big_kloop_by_tile_us": {str(k): round(mean(v), 2) for k, v in sorted(by_round.items())},
+        "workgroups_by_big_tiles": {str(k): v for k, v in sorted(per_wg.items())},
     }
     log("bench: tile trace " + json.dumps(extra))
     return {"value": ops / (ms * 1e-3) / 1e12, "ms": ms, "dtype": "int8", "unit": "TOPS",
@@ -657,11 +667,25 @@ def bench_ceiling(steps, warmup):
         dma[label] = cus * 4 * dma_iters * 8 * 1024 / secs / 1e9
         log(f"bench: LDS DMA stream ({label} window) {dma[label]:.0f} GB/s")
         del buf
+    # VALU work beside the MFMAs: V v_perm_b32 after every MFMA (the W4 table
+    # lookup's instruction), the rotating operands of mode 2.
+    lib.phi_probe_mfma_valu.argtypes = lib.phi_probe_mfma.argtypes
+    beside = {}
+    for v in (0, 1, 2, 3, 4, 6, 8):
+        def launch(v=v):
+            rc = lib.phi_probe_mfma_valu(stream, ctypes.c_void_p(ops.data_ptr()), v, iters,
+                                         ctypes.c_void_p(sink.data_ptr()), cus)
+            if rc != 0:
+                raise RuntimeError(f"mfma+valu probe launch failed ({rc})")
+        secs = timed(launch)
+        beside[str(v)] = cus * 4 * iters * 32 * 65536 / secs / 1e12
+        log(f"bench: mfma with {v} VALU ops beside each: {beside[str(v)]:.0f} TOPS")
     value = tops["rotating"]
     return {"value": value, "ms": None, "dtype": "int8", "unit": "TOPS",
             "roofline": {"bound": "mfma", "achieved": value, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                          "frac": value / INT8_PEAK_TOPS, "traffic": None},
-            "extra": {"mfma_tops": tops, "lds_dma_gbs": dma, "cus": cus, "mfma_per_wave_per_launch": iters * 32}}
+            "extra": {"mfma_tops": tops, "lds_dma_gbs": dma, "mfma_tops_with_valu_per_mfma": beside,
+                      "cus": cus, "mfma_per_wave_per_launch": iters * 32}}
 
 
 def main() -> int:

@@ -15,6 +15,9 @@
 //   phi_probe_lds_dma  every wave streams 16 rows x 64 bytes per instruction
 //                   from a window of global memory into LDS, 4 K-steps of the
 //                   headline tile's A and B in flight, with no MFMAs.
+//   phi_probe_mfma_valu  the mode-2 MFMA loop with V v_perm_b32 operations
+//                   after every MFMA: the VALU work a wave can issue beside
+//                   its MFMAs before they slow down.
 //   phi_probe_tile_trace  the persistent pipeline (i8_gemm_pipe.hip, compiled
 //                   here a second time into namespace phi_dev_trace with its
 //                   timeline hooks defined) with one record of real-time clock
@@ -104,6 +107,50 @@ __global__ __launch_bounds__(256) void mfma_probe(const int8_t* ops, int iters, 
     if (t == 0x7fffffff) sink[blockIdx.x * 4 + wave] = t;  // keeps the MFMAs live
 }
 
+// The GEMM's MFMA loop (mode 2 operands) with V independent VALU operations
+// (v_perm_b32, the W4 table lookup's instruction) placed after every MFMA, in
+// four chains: how much VALU work a wave can issue beside its MFMAs before
+// they slow down.
+template <int V>
+__global__ __launch_bounds__(256) void mfma_valu_probe(const int8_t* ops, int iters, int* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v4i a[8], b[8];
+#pragma unroll
+    for (int f = 0; f < 8; f++) {
+        a[f] = *(const v4i*)(ops + ((wave * 16 + f) * 64 + lane) * 16);
+        b[f] = *(const v4i*)(ops + ((wave * 16 + 8 + f) * 64 + lane) * 16);
+    }
+    v16i acc[16];
+#pragma unroll
+    for (int q = 0; q < 16; q++) acc[q] = v16i{};
+    uint32_t c[4] = {(uint32_t)lane, (uint32_t)lane * 3u, (uint32_t)lane * 5u, (uint32_t)lane * 7u};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int s = 0; s < 2; s++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                acc[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[(q >> 2) + 4 * s], a[(q & 3) + 4 * s], acc[q], 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < V; v++)
+                    c[v & 3] = __builtin_amdgcn_perm(c[v & 3], (uint32_t)b[(q + v) & 7][v & 3], 0x05010400u + v);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+            }
+        const int x = 0x5a3c96e1 * (it + 1) + lane;
+#pragma unroll
+        for (int f = 0; f < 8; f++) {
+            a[f] ^= v4i{x, x >> 3, x >> 5, x >> 7};
+            b[f] ^= v4i{x >> 1, x >> 2, x >> 4, x >> 6};
+        }
+    }
+    int t = (int)(c[0] ^ c[1] ^ c[2] ^ c[3]);
+#pragma unroll
+    for (int q = 0; q < 16; q++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) t += acc[q][r];
+    if (t == 0x7fffffff) sink[blockIdx.x * 4 + wave] = t;
+}
+
 __global__ __launch_bounds__(256) void lds_dma_probe(const int8_t* src, int window, int iters, int* sink) {
     __shared__ __align__(16) int8_t st[4][4][8192];  // wave, stage, 8 loads of 1 KB
     const int lane = threadIdx.x & 63;
@@ -142,6 +189,22 @@ int phi_probe_mfma(void* stream, const int8_t* ops, int mode, int iters, int* si
         case 0: hipLaunchKernelGGL(mfma_probe<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         case 1: hipLaunchKernelGGL(mfma_probe<1>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         default: hipLaunchKernelGGL(mfma_probe<2>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
+    }
+    return (int)hipGetLastError();
+}
+
+// V VALU operations after every MFMA (V in 0, 1, 2, 3, 4, 6, 8).
+int phi_probe_mfma_valu(void* stream, const int8_t* ops, int v, int iters, int* sink, int grid) {
+    hipStream_t st = (hipStream_t)stream;
+    switch (v) {
+        case 0: hipLaunchKernelGGL(mfma_valu_probe<0>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        case 1: hipLaunchKernelGGL(mfma_valu_probe<1>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        case 2: hipLaunchKernelGGL(mfma_valu_probe<2>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        case 3: hipLaunchKernelGGL(mfma_valu_probe<3>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        case 4: hipLaunchKernelGGL(mfma_valu_probe<4>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        case 6: hipLaunchKernelGGL(mfma_valu_probe<6>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        case 8: hipLaunchKernelGGL(mfma_valu_probe<8>, dim3(grid), dim3(256), 0, st, ops, iters, sink); break;
+        default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
 }
