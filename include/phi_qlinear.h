@@ -202,6 +202,15 @@ phi_status phi_hip_pack_k_tiled(phi_stream_t stream, const int8_t* src, int64_t 
 phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
                                   int64_t ldx, int8_t* q, float* s, float qmax, int round_mode);
 
+/* phi_hip_quant_rotate_mod and phi_hip_quant_rotate_act (rotation on) writing
+ * q (rows x K bytes) K-tiled: the DiT block's modulation or the MLP's
+ * activation fused in front of a K-tiled linear.  K % 256 == 0, K <= 16384. */
+phi_status phi_hip_quant_rotate_mod_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                      int64_t ldx, const float* mod_scale, const float* mod_shift, int8_t* q,
+                                      float* s, float qmax, int round_mode);
+phi_status phi_hip_quant_rotate_act_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                      int64_t ldx, int act, int8_t* q, float* s, float qmax, int round_mode);
+
 /* phi_hip_i8_gemm with A [M, K] and B [N, K] both K-tiled: the same result,
  * bit for bit, as phi_hip_i8_gemm on the row-major operands.  Needs
  * K % 256 == 0, whole 16-byte output pieces (N % 8 for bf16, N % 4 else) on
@@ -209,6 +218,13 @@ phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dty
 phi_status phi_hip_i8_gemm_kt(phi_stream_t stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
                               int sb_scalar, const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
                               int64_t M, int64_t N, int64_t K);
+
+/* phi_hip_i8_gemm_residual with A and B K-tiled: H = fma(linear, gate[n], H)
+ * in place on the fp32 residual stream H [M, ldh].  Same contract as
+ * phi_hip_i8_gemm_kt (N % 4 == 0). */
+phi_status phi_hip_i8_gemm_residual_kt(phi_stream_t stream, const int8_t* A, const int8_t* B, const float* sA,
+                                       const float* sB, int sb_scalar, const void* bias, int bias_dtype,
+                                       const float* gate, float* H, int64_t ldh, int64_t M, int64_t N, int64_t K);
 
 /* The rows of an M x N persistent GEMM on the current device that run as
  * 256 x 256 tiles (a multiple of 256, or M); the rest run as 128 x 128 tiles

@@ -460,7 +460,8 @@ static phi_status check_kt(const char* who, const void* A, const void* B, int64_
 
 static phi_status i8_gemm_kt_impl(const char* who, phi_stream_t stream, const int8_t* A, const int8_t* B,
                                   const float* sA, const float* sB, int sb_scalar, const void* bias, int bias_dtype,
-                                  void* C, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K) {
+                                  void* C, int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                  const float* gate = nullptr) {
     phi_status st = check_gemm(who, A, K, B, K, M, N, K, sA, sB, C, c_dtype, ldc, false);
     if (st != PHI_OK) return st;
     if ((st = check_kt(who, A, B, K)) != PHI_OK) return st;
@@ -487,6 +488,7 @@ static phi_status i8_gemm_kt_impl(const char* who, phi_stream_t stream, const in
     p.c_kind = c_kind_of(c_dtype);
     p.group_m = 4;
     p.kt = 1;
+    p.gate = gate;
     set_vec_flags(p, c_dtype, ldc);
     GemmKernel gk = GK_PERSIST;
     const char* e = getenv("PHI_GEMM_KERNEL");
@@ -513,12 +515,11 @@ phi_status phi_hip_pack_k_tiled(phi_stream_t stream, const int8_t* src, int64_t 
     return check_hip(phi_dev::launch_pack_k_tiled((hipStream_t)stream, src, ld, rows, K, dst), who);
 }
 
-phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
-                                  int64_t ldx, int8_t* q, float* s, float qmax, int round_mode) {
-    static const char* who = "quant_convrot_kt";
+static phi_status quant_rotate_kt_impl(const char* who, phi_stream_t stream, const void* x, int x_dtype, int64_t rows,
+                                       int64_t K, int64_t ldx, const phi_dev::QrPre& pre, int8_t* q, float* s,
+                                       float qmax, int round_mode) {
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     if (rows <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem (rows=%lld)", who, (long long)rows);
-    phi_dev::QrPre pre{};
     phi_status st = quant_rotate_check(who, x, x_dtype, rows, K, ldx, pre, q, K, s, qmax, round_mode);
     if (st != PHI_OK) return st;
     if (K > 16384) return fail(PHI_ERR_UNSUPPORTED, "%s: K=%lld exceeds 16384 (K-tiled activations)", who, (long long)K);
@@ -527,12 +528,43 @@ phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dty
                      who);
 }
 
+phi_status phi_hip_quant_rotate_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                  int64_t ldx, int8_t* q, float* s, float qmax, int round_mode) {
+    const phi_dev::QrPre pre{};
+    return quant_rotate_kt_impl("quant_convrot_kt", stream, x, x_dtype, rows, K, ldx, pre, q, s, qmax, round_mode);
+}
+
+phi_status phi_hip_quant_rotate_mod_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                      int64_t ldx, const float* mod_scale, const float* mod_shift, int8_t* q,
+                                      float* s, float qmax, int round_mode) {
+    const phi_dev::QrPre pre = {mod_scale || mod_shift ? phi_dev::QR_MOD : phi_dev::QR_PLAIN, mod_scale, mod_shift, 0};
+    return quant_rotate_kt_impl("quant_rotate_mod_kt", stream, x, x_dtype, rows, K, ldx, pre, q, s, qmax, round_mode);
+}
+
+phi_status phi_hip_quant_rotate_act_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t rows, int64_t K,
+                                      int64_t ldx, int act, int8_t* q, float* s, float qmax, int round_mode) {
+    if (act != PHI_ACT_GELU_TANH && act != PHI_ACT_SILU_GATE)
+        return fail(PHI_ERR_ARG, "quant_rotate_act_kt: act must be PHI_ACT_GELU_TANH or PHI_ACT_SILU_GATE");
+    const phi_dev::QrPre pre = {act == PHI_ACT_GELU_TANH ? phi_dev::QR_GELU : phi_dev::QR_SILU_GATE, nullptr, nullptr, K};
+    return quant_rotate_kt_impl("quant_rotate_act_kt", stream, x, x_dtype, rows, K, ldx, pre, q, s, qmax, round_mode);
+}
+
 phi_status phi_hip_i8_gemm_kt(phi_stream_t stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
                               int sb_scalar, const void* bias, int bias_dtype, void* C, int c_dtype, int64_t ldc,
                               int64_t M, int64_t N, int64_t K) {
     static const char* who = "int8_gemm_kt";
     if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
     return i8_gemm_kt_impl(who, stream, A, B, sA, sB, sb_scalar, bias, bias_dtype, C, c_dtype, ldc, M, N, K);
+}
+
+phi_status phi_hip_i8_gemm_residual_kt(phi_stream_t stream, const int8_t* A, const int8_t* B, const float* sA,
+                                       const float* sB, int sb_scalar, const void* bias, int bias_dtype,
+                                       const float* gate, float* H, int64_t ldh, int64_t M, int64_t N, int64_t K) {
+    static const char* who = "int8_gemm_residual_kt";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!gate) return fail(PHI_ERR_ARG, "%s: null gate", who);
+    if (!aligned(gate, 4)) return fail(PHI_ERR_ALIGN, "%s: gate must be 4-byte aligned", who);
+    return i8_gemm_kt_impl(who, stream, A, B, sA, sB, sb_scalar, bias, bias_dtype, H, PHI_F32, ldh, M, N, K, gate);
 }
 
 phi_status phi_hip_q8_linear_kt(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,

@@ -447,15 +447,17 @@ hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_
     const int bm = 2 * wave_tile;
     const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
     const int grid = tiles < num_cus ? tiles : num_cus;
-    if (p.kt && p.gate) return hipErrorInvalidValue;  // the gated residual reads row-major operands only
+    const dim3 g3(grid), b3(256);
     if (wave_tile == 128) {
-        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true, false>), dim3(grid), dim3(256), 0, stream, p);
-        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, true>), dim3(grid), dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, false>), dim3(grid), dim3(256), 0, stream, p);
+        if (p.gate && p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true, true>), g3, b3, 0, stream, p);
+        else if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true, false>), g3, b3, 0, stream, p);
+        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, true>), g3, b3, 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, false>), g3, b3, 0, stream, p);
     } else {
-        if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true, false>), dim3(grid), dim3(256), 0, stream, p);
-        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, true>), dim3(grid), dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, false>), dim3(grid), dim3(256), 0, stream, p);
+        if (p.gate && p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true, true>), g3, b3, 0, stream, p);
+        else if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true, false>), g3, b3, 0, stream, p);
+        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, true>), g3, b3, 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, false>), g3, b3, 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -465,8 +467,9 @@ hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, c
     const int big = ((pb.M + 255) / 256) * ((pb.N + 255) / 256), small = ((ps.M + 127) / 128) * ((ps.N + 127) / 128);
     const int most = big > small ? big : small;
     const int grid = most < num_cus ? most : num_cus;
-    if (pb.kt != ps.kt || (pb.kt && pb.gate)) return hipErrorInvalidValue;
-    if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    if (pb.kt != ps.kt || (pb.gate != nullptr) != (ps.gate != nullptr)) return hipErrorInvalidValue;
+    if (pb.gate && pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, true>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    else if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
     else if (pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, true>), dim3(grid), dim3(256), 0, stream, pb, ps);
     else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
     return hipGetLastError();

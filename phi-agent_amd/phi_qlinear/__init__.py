@@ -66,7 +66,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
            "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
            "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes",
-           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows"]
+           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows",
+           "phi_hip_quant_rotate_mod_kt", "phi_hip_quant_rotate_act_kt", "phi_hip_i8_gemm_residual_kt"]
 
 _lib = None
 
@@ -117,6 +118,9 @@ def load() -> ctypes.CDLL:
     L.phi_hip_noalloc_scratch_bytes.restype = SZ
     L.phi_hip_pack_k_tiled.argtypes = [P, P, I64, I64, I64, P]
     L.phi_hip_quant_rotate_kt.argtypes = [P, P, I, I64, I64, I64, P, P, F, I]
+    L.phi_hip_quant_rotate_mod_kt.argtypes = [P, P, I, I64, I64, I64, P, P, P, P, F, I]
+    L.phi_hip_quant_rotate_act_kt.argtypes = [P, P, I, I64, I64, I64, I, P, P, F, I]
+    L.phi_hip_i8_gemm_residual_kt.argtypes = [P, P, P, P, P, I, P, I, P, P, I64, I64, I64, I64]
     L.phi_hip_big_tile_rows.argtypes = [I64, I64]
     L.phi_hip_big_tile_rows.restype = I64
     L.phi_hip_i8_gemm_kt.argtypes = [P, P, P, P, P, I, P, I, P, I, I64, I64, I64, I64]
@@ -490,19 +494,47 @@ def big_tile_rows(M: int, N: int) -> int:
 
 
 def quant_rotate_kt(x: torch.Tensor, q: torch.Tensor | None = None, s: torch.Tensor | None = None,
-                    qmax: float = 127.0, round_mode: int = ROUND_HALF_AWAY, stream=None):
-    """quant_rotate with q (rows * K bytes) written K-tiled (phi_hip_quant_rotate_kt)."""
-    _require_device(x, q, s)
-    rows, K = x.shape
+                    qmax: float = 127.0, round_mode: int = ROUND_HALF_AWAY, *, mod_scale=None, mod_shift=None,
+                    act: str | None = None, stream=None):
+    """quant_rotate with q (rows * K bytes) written K-tiled
+    (phi_hip_quant_rotate_kt / _mod_kt / _act_kt).  For act="silu_gate" x is
+    [rows, 2K] (gate then value halves)."""
+    _require_device(x, q, s, mod_scale, mod_shift)
+    rows = x.shape[0]
+    K = x.shape[1] // 2 if act == "silu_gate" else x.shape[1]
     if q is None:
         q = torch.empty((rows * K,), dtype=torch.int8, device=x.device)
     if s is None:
         s = torch.empty((rows,), dtype=torch.float32, device=x.device)
     if q.numel() < rows * K:
         raise ValueError(f"quant_rotate_kt: q holds {q.numel()} bytes, needs {rows * K}")
-    _check(load().phi_hip_quant_rotate_kt(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0), _ptr(q),
-                                          _ptr(s), qmax, round_mode))
+    L = load()
+    if act is not None:
+        code = {"gelu_tanh": ACT_GELU_TANH, "silu_gate": ACT_SILU_GATE}[act]
+        _check(L.phi_hip_quant_rotate_act_kt(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0), code,
+                                             _ptr(q), _ptr(s), qmax, round_mode))
+    elif mod_scale is not None or mod_shift is not None:
+        _check(L.phi_hip_quant_rotate_mod_kt(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0),
+                                             _ptr(mod_scale), _ptr(mod_shift), _ptr(q), _ptr(s), qmax, round_mode))
+    else:
+        _check(L.phi_hip_quant_rotate_kt(_stream(stream), _ptr(x), _dt(x), rows, K, x.stride(0), _ptr(q),
+                                         _ptr(s), qmax, round_mode))
     return q, s
+
+
+def i8_gemm_residual_kt(A: torch.Tensor, B: torch.Tensor, M: int, N: int, K: int, sA: torch.Tensor,
+                        sB: torch.Tensor, bias: torch.Tensor | None, gate: torch.Tensor, H: torch.Tensor,
+                        stream=None) -> torch.Tensor:
+    """phi_hip_i8_gemm_residual_kt: H = fma(linear, gate, H) in place, A and B K-tiled."""
+    _require_device(A, B, sA, sB, bias, gate, H)
+    for name, t, rows in (("A", A, M), ("B", B, N)):
+        if t.numel() < rows * K:
+            raise ValueError(f"i8_gemm_residual_kt: {name} holds {t.numel()} bytes, needs {rows * K}")
+    _check(load().phi_hip_i8_gemm_residual_kt(_stream(stream), _ptr(A), _ptr(B), _ptr(sA), _ptr(sB),
+                                              1 if sB.numel() == 1 else 0, _ptr(bias),
+                                              _dt(bias) if bias is not None else F32, _ptr(gate), _ptr(H),
+                                              H.stride(0), M, N, K))
+    return H
 
 
 def i8_gemm_kt(A: torch.Tensor, B: torch.Tensor, M: int, N: int, K: int, sA: torch.Tensor | None,

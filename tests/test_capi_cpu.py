@@ -264,6 +264,12 @@ def test_k_tiled_contracts(lib):
     assert rc == 1 and "activation scratch" in Q.last_error()
     rc = lib.phi_hip_quant_rotate_kt(None, FAKE, Q.BF16, 4, 300, 300, FAKE, FAKE, 127.0, 0)
     assert rc == 2
+    rc = lib.phi_hip_quant_rotate_act_kt(None, FAKE, Q.BF16, 4, 512, 512, 9, FAKE, FAKE, 127.0, 0)
+    assert rc == 1 and "act" in Q.last_error()
+    rc = lib.phi_hip_quant_rotate_mod_kt(None, FAKE, Q.BF16, 4, 16640, 16640, FAKE, FAKE, FAKE, FAKE, 127.0, 0)
+    assert rc == 7 and "16384" in Q.last_error()
+    rc = lib.phi_hip_i8_gemm_residual_kt(None, FAKE, FAKE, FAKE, FAKE, 1, None, Q.F32, None, FAKE, 16, 4, 16, 512)
+    assert rc == 1 and "gate" in Q.last_error()
 
 
 def test_tile_plan(lib):

@@ -1,5 +1,6 @@
 """GPU parity of the K-tiled operand path (phi_hip_pack_k_tiled,
-phi_hip_quant_rotate_kt, phi_hip_i8_gemm_kt, phi_hip_q8_linear_kt).
+phi_hip_quant_rotate_kt / _mod_kt / _act_kt, phi_hip_i8_gemm_kt,
+phi_hip_i8_gemm_residual_kt, phi_hip_q8_linear_kt).
 
 The K-tiled layout is a re-arrangement of the same bytes, so the bar is
 identity with the row-major path, which the other GPU tests hold bit-exact
@@ -8,10 +9,11 @@ against the oracle:
   numpy gather on small matrices, partial strips included) and loses nothing
   (unpacking restores the matrix);
 * quant_rotate_kt writes the same codes and scales as quant_rotate, in that
-  permutation;
+  permutation, with and without the modulation or an activation in front;
 * the K-tiled GEMM and linear give the row-major path's outputs bit for bit
   (int32, fp32 and bf16), at small, ragged and the configs' full sizes, on
-  each tile plan (mixed, 256 x 256 only, 128 x 128 only).
+  each tile plan (mixed, 256 x 256 only, 128 x 128 only), and so does the
+  gated residual update.
 """
 import numpy as np
 import pytest
@@ -110,3 +112,39 @@ def test_q8_linear_kt_matches_q8_linear(dev, M, K, N):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert torch.equal(sk, s8)
     assert torch.equal(qk, Q.pack_k_tiled(q8))
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (77, 3072), (300, 1024), (4352, 3072)])
+def test_fused_prologues_kt(dev, M, K):
+    """The modulation and the activations in front of the K-tiled quantiser
+    give the row-major codes, packed, and the same scales."""
+    g = torch.Generator(device=dev).manual_seed(M + K)
+    x = synth.activations(M, K, seed=M, device=dev)
+    sc = torch.randn(K, generator=g, device=dev) * 0.1
+    sh = torch.randn(K, generator=g, device=dev) * 0.1
+    q, s = Q.quant_rotate(x, mod_scale=sc, mod_shift=sh)
+    qk, sk = Q.quant_rotate_kt(x, mod_scale=sc, mod_shift=sh)
+    assert torch.equal(sk, s) and torch.equal(qk, Q.pack_k_tiled(q))
+    q, s = Q.quant_rotate(x, act="gelu_tanh")
+    qk, sk = Q.quant_rotate_kt(x, act="gelu_tanh")
+    assert torch.equal(sk, s) and torch.equal(qk, Q.pack_k_tiled(q))
+    gx = synth.activations(M, 2 * K, seed=M + 1, device=dev)
+    q, s = Q.quant_rotate(gx, act="silu_gate")
+    qk, sk = Q.quant_rotate_kt(gx, act="silu_gate")
+    assert torch.equal(sk, s) and torch.equal(qk, Q.pack_k_tiled(q))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 768), (4352, 3072, 12288), (700, 1040, 1536)])
+def test_gemm_residual_kt_matches_row_major(dev, M, N, K):
+    A = synth.int8_weight(M, K, seed=M, device=dev)
+    B = synth.int8_weight(N, K, seed=N, device=dev)
+    sA = torch.rand(M, device=dev) * 0.01 + 1e-3
+    sB = synth.weight_scale(0.002, device=dev)
+    bias = synth.bias(N, seed=3, device=dev)
+    gate = torch.randn(N, device=dev) * 0.1
+    H0 = torch.randn(M, N, device=dev)
+    H_row, H_kt = H0.clone(), H0.clone()
+    Q.i8_gemm_residual(A, B, sA, sB, bias, gate, H_row)
+    Q.i8_gemm_residual_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, sA, sB, bias, gate, H_kt)
+    torch.cuda.synchronize()
+    assert torch.equal(H_kt.view(torch.int32), H_row.view(torch.int32))
