@@ -23,7 +23,7 @@ constexpr int kRsrcWord3 = 0x00020000;
 
 
 constexpr int EBYTES = 4 * 1024;  // per parity: sa | sb | bias | gate (4 waves x 256 B each)
-constexpr int CHUNK = 4096;       // per-wave epilogue staging
+constexpr int CHUNK = 4096 + 512;  // per-wave epilogue staging: 32 rows x 128 bytes, then fp32 bias
 
 constexpr int SG_VALU = 0x002, SG_MFMA = 0x008, SG_VMEM_R = 0x020, SG_DSR = 0x100, SG_DSW = 0x200;
 
@@ -72,7 +72,7 @@ __device__ __forceinline__ int xcd_remap(int pid, int nblocks) {
 // The lane and wave indices the epilogue and its operand loads use, the
 // wave's epilogue staging area, and the load cursor's tile origin.
 struct EpiWave {
-    int8_t* lc;  // this wave's CHUNK bytes of epilogue staging
+    int8_t* lc;  // this wave's CHUNK bytes of epilogue staging (the bias copy at lc + 4096)
     int wave, wm, wn, lane, lrow, lhalf;
     int cm0, cn0;
 };
@@ -127,20 +127,28 @@ __device__ __forceinline__ void issue_epi(const EpiWave& w, const GemmParams& p,
 }
 
 
-// Scaled epilogue operands of this lane's four columns starting at tile
-// column ct.  The column-scale area holds one float per column: a scalar
-// scale was loaded into every slot.  The bias area holds bf16 pairs or fp32
-// words, which are zeros when there is no bias (its loads fell outside a
-// zero-length range).  Both views are read, at immediate offsets from two
-// per-lane bases, and the uniform format selects: no branch (branches here
-// split the epilogue into small blocks with waits of their own) and no
-// per-call offset for the compiler to keep live through the main loop.
-__device__ __forceinline__ void col_operands(bool bf, const int8_t* e, int ct, v4f& sb, v4f& bz) {
+// The bias of the wave's WT columns as fp32, written after the wave's
+// staging rows: converted once a tile, one value a lane per 64 columns,
+// instead of by each of the 32 lanes that use a column.  The bias area holds
+// bf16 pairs or fp32 words, zeros without a bias (its loads fell outside a
+// zero-length range); both views are read and the uniform format selects.
+template <int WT>
+__device__ __forceinline__ void bias_to_f32(const EpiWave& w, bool bf, const int8_t* e) {
+#pragma unroll
+    for (int c0 = 0; c0 < WT; c0 += 64) {
+        const int c = c0 + w.lane, col = w.wn * WT + c;
+        const float f = *(const float*)(e + 2048 + col * 4);
+        const uint32_t h = *(const unsigned short*)(e + 2048 + col * 2);
+        *(float*)(w.lc + 4096 + c * 4) = bf ? __uint_as_float(h << 16) : f;
+    }
+}
+
+// Epilogue operands of this lane's four columns starting at wave column cw
+// (tile column ct = the wave's first column + cw).  The column-scale area
+// holds one float per column: a scalar scale was loaded into every slot.
+__device__ __forceinline__ void col_operands(const EpiWave& w, const int8_t* e, int ct, int cw, v4f& sb, v4f& bz) {
     sb = *(const v4f*)(e + 1024 + ct * 4);
-    const v4f f = *(const v4f*)(e + 2048 + ct * 4);
-    const u32x2 h = *(const u32x2*)(e + 2048 + ct * 2);
-    bz = v4f{bf ? __uint_as_float(h[0] << 16) : f[0], bf ? __uint_as_float(h[0] & 0xffff0000u) : f[1],
-             bf ? __uint_as_float(h[1] << 16) : f[2], bf ? __uint_as_float(h[1] & 0xffff0000u) : f[3]};
+    bz = *(const v4f*)(w.lc + 4096 + cw * 4);
 }
 
 // Epilogue of logical tile t (operands in the LDS area e).  Lane l holds row
@@ -161,7 +169,6 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
     tile_mn(s, t, tm, tn);
     const int m0 = tm * BM, n0 = tn * BM;
     const int esz = p.c_kind == C_BF16 ? 2 : 4;
-    const bool bf = p.bias_kind == BIAS_BF16;
     const int pitch = (int)p.ldc * esz;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (int8_t*)p.C + (int64_t)m0 * pitch, (short)0, min(BM, p.M - m0) * pitch, kRsrcWord3);
@@ -170,6 +177,9 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
     float sa[NB];
 #pragma unroll
     for (int i = 0; i < NB; i++) sa[i] = *(const float*)(e + (w.wm * WT + i * 32 + w.lrow) * 4);
+    // A wave's LDS accesses complete in order: the operand reads below see
+    // this copy.
+    bias_to_f32<WT>(w, p.bias_kind == BIAS_BF16, e);
     if (p.c_kind == C_BF16) {
 #pragma unroll
         for (int jp = 0; jp < NB / 2; jp++) {
@@ -178,7 +188,8 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
             for (int jj = 0; jj < 2; jj++)
 #pragma unroll
                 for (int g = 0; g < 4; g++)
-                    col_operands(bf, e, w.wn * WT + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
+                    col_operands(w, e, w.wn * WT + (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf,
+                                 (2 * jp + jj) * 32 + 8 * g + 4 * w.lhalf, sb[jj][g], bz[jj][g]);
 #pragma unroll
             for (int i = 0; i < NB; i++) {
 #pragma unroll
@@ -221,7 +232,8 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
         v4f sb[4], bz[4];
         if (p.c_kind == C_F32) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) col_operands(bf, e, w.wn * WT + j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
+            for (int g = 0; g < 4; g++)
+                col_operands(w, e, w.wn * WT + j * 32 + 8 * g + 4 * w.lhalf, j * 32 + 8 * g + 4 * w.lhalf, sb[g], bz[g]);
         }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
