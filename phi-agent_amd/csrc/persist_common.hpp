@@ -154,9 +154,18 @@ __device__ __forceinline__ void col_operands(const EpiWave& w, const int8_t* e, 
 // Epilogue of logical tile t (operands in the LDS area e).  Lane l holds row
 // l % 32 of each A block and, in registers 4g..4g+3, columns 8g + 4(l/32) +
 // 0..3 of each B block.  Each 32-row strip goes through the wave's LDS area
-// (16-byte slots swizzled by row) and is stored as whole rows: bf16 in
-// 32 x 64-column pieces (128 bytes a row), fp32 / int32 in 32 x 32-column
-// pieces.
+// and is stored as whole rows: bf16 in 32 x 64-column pieces (128 bytes a
+// row), fp32 / int32 in 32 x 32-column pieces.
+//
+// Staging layout: row r at r * 128; 16-byte chunk c of the row in slot
+// c ^ ((r >> 1) & 7).  The 128-byte pitch puts even rows in banks 0-31 and
+// odd rows in banks 32-63, and the slot swizzle spreads rows 2s and 2s + 1
+// over the eight slots: a write of one chunk by 16 rows (fp32, 16 bytes a
+// lane) touches every bank once.  The bf16 writes are 8 bytes a lane, 32
+// rows at a time: their half of the slot is flipped for rows 16-31
+// (lane half h goes to half h ^ (r >> 4)), so these too touch every bank
+// once, and the reads of rows 16-31 swap the halves back.  The read-back (16
+// lanes a clock: two rows, eight chunks each) is conflict-free as well.
 template <int WT, bool G>
 __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const GemmParams& p, const Shape& s, int t,
                                          const EpiWave& w, const int8_t* e) {
@@ -202,8 +211,8 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
 #pragma unroll
                         for (int q = 0; q < 4; q++)
                             v[q] = fmaf((float)blk[4 * g + q] * sa[i], sb[jj][g][q], bz[jj][g][q]);
-                        const int slot = (jj * 4 + g) ^ (w.lrow & 7);
-                        *(u32x2*)(lc + w.lrow * 128 + slot * 16 + w.lhalf * 8) =
+                        const int slot = (jj * 4 + g) ^ ((w.lrow >> 1) & 7);
+                        *(u32x2*)(lc + w.lrow * 128 + slot * 16 + (w.lhalf ^ (w.lrow >> 4)) * 8) =
                             u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
                     }
                 }
@@ -211,7 +220,8 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++) {
                     const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
-                    const u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
+                    const u32x4 h = *(const u32x4*)(lc + r * 128 + ((sl ^ ((r >> 1) & 7)) * 16));
+                    const u32x4 v = tt < 2 ? h : u32x4{h[2], h[3], h[0], h[1]};  // rows 16-31: halves flipped
                     const int col = colw + jp * 64 + sl * 8;
                     const int off = col < p.N ? (w.wm * WT + i * 32 + r) * pitch + col * 2 : kDropOffset;
                     __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
@@ -260,13 +270,13 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
 #pragma unroll
                     for (int q = 0; q < 4; q++) o[q] = (unsigned)blk[4 * g + q];
                 }
-                const int slot = (2 * g + w.lhalf) ^ (w.lrow & 7);
+                const int slot = (2 * g + w.lhalf) ^ ((w.lrow >> 1) & 7);
                 *(u32x4*)(lc + w.lrow * 128 + slot * 16) = o;
             }
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
                 const int r = tt * 8 + (w.lane >> 3), sl = w.lane & 7;
-                u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ (r & 7)) * 16));
+                u32x4 v = *(const u32x4*)(lc + r * 128 + ((sl ^ ((r >> 1) & 7)) * 16));
                 const int col = colw + j * 32 + sl * 4;
                 if (gated) {
                     const v4f gt = *(const v4f*)(e + 3072 + (w.wn * WT + j * 32 + sl * 4) * 4);
