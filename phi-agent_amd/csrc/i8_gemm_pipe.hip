@@ -37,6 +37,10 @@
 //   * Chunk c (16 bytes) of row r sits in slot c ^ ((r >> 2) & 3) of the
 //     row's 64 bytes: the 16-byte fragment reads of 16 consecutive rows hit
 //     16 distinct bank windows.
+//   * Fused tile transitions (bf16 output without a gate, K > 256): the
+//     first half of the next tile's K-step 0 is issued inside the epilogue,
+//     one MFMA per accumulator block as soon as the epilogue has read the
+//     block out, so those MFMAs run beside the epilogue's conversion.
 // The epilogue, the tile order and the epilogue-operand loads are those of
 // persist_common.hpp.
 #include "device_common.hpp"
@@ -279,6 +283,42 @@ __device__ __forceinline__ void pstep(Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PC
     });
 }
 
+// The epilogue of the tile in acc (bf16 output, no gate) fused with the first
+// half of the next tile's K-step 0.  f0 already holds that half's fragments
+// (read from stage 0 during the last K-step, as for any tile).  As soon as the
+// epilogue has read a block out of its accumulators, that block's first
+// K-step-0 MFMA (an inline 0 as its input) is issued, and it runs beside the
+// epilogue's conversion.  After the last tile the same code runs: stage 0
+// then holds the last tile's own K-step 0 (the cursors' loads past the last
+// K-step), and the MFMAs' results are dropped.
+template <int WT>
+__device__ __forceinline__ void epilogue_kstep0a(const Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB],
+                                                 const Pw& w, const GemmParams& p, const Shape& s, int t,
+                                                 const int8_t* le) {
+    epilogue<WT, false>(acc, p, s, t, w, le, [&](int j, int i) {
+        acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f0.b[j], f0.a[i], v16i{}, 0, 0, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The rest of the next tile's K-step 0, as pstep<0> runs it: B of K-step 3
+// (stage 3 was released by the last K-step's barrier), the second-half
+// fragments, the wait and barrier, and the second quarter (A of K-step 4 into
+// stage 0, K-step 1's first fragments into f0).  The memory operations are
+// those of the epilogue followed by pstep<0>'s, in the same order, so every
+// wait counts as in the unfused loop.
+template <int WT, bool KT>
+__device__ __forceinline__ void kstep0b(Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB], Pw& w,
+                                        const GemmParams& p) {
+    load_b<WT, 3, KT>(w, p);
+    Frag<WT> f1;
+    frag<WT, 0, 1>(f1, w);
+    wait_vm_lgkm0<PCfg<WT>::VWR>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    pquarter<WT, 1, 0, PCfg<WT>::DL, false>(f1, f0, acc, w, [&] { load_a<WT, 0, KT>(w, p); });
+}
+
 template <int WT>
 __device__ __forceinline__ NextTile next_tile(const Shape& s, const GemmParams& p, int t, bool valid) {
     NextTile nt{0, 0, valid};
@@ -295,7 +335,7 @@ __device__ __forceinline__ NextTile next_tile(const Shape& s, const GemmParams& 
 // la and four B stages at lb (STG bytes each), the epilogue-operand areas
 // eall and the epilogue staging cbuf.  K % 256 == 0.  Returns at once when
 // the workgroup has no tile.
-template <int WT, bool G, bool KT>
+template <int WT, bool G, bool KT, bool F>
 __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8_t* lb, int8_t* eall, int8_t* cbuf) {
     using C = PCfg<WT>;
     constexpr int NB = C::NB, DL = C::DL, BM = C::BM;
@@ -373,20 +413,23 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
     Frag<WT> f0;
     frag<WT, 0, 0>(f0, w);
     v16i acc[NB][NB];
-    for (int i = 0;;) {
-        const int t = r + i * s.G;
-        int8_t* le = w.le + (i & 1) * EBYTES;
-        int8_t* ln = w.le + ((i + 1) & 1) * EBYTES;
-        const NextTile nt = next_tile<WT>(s, p, t + s.G, i + 1 < ntile);
-        constexpr int VWR = C::VWR, VWN = C::VWN;
-        PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 0);
-        if (s.KT == 4) {
-            pstep<WT, 0, true, VWR, true, false, G, KT>(f0, acc, w, p, nt, ln);
-            pstep<WT, 1, false, VWR, false, true, G, KT>(f0, acc, w, p, nt, ln);
-            pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
-            pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
-        } else {
-            pstep<WT, 0, true, VWR, false, false, G, KT>(f0, acc, w, p, nt, ln);
+    constexpr int VWR = C::VWR, VWN = C::VWN;
+    if constexpr (F) {
+        // Fused tile transitions (bf16 output, no gate, K > 256: the
+        // launcher's condition).  K-step 0 of the first tile runs here; that
+        // of every later tile inside the previous tile's epilogue
+        // (epilogue_kstep0).  A separate loop: the accumulators are live
+        // across its back edge, where the unfused loop's are dead.
+        {
+            const NextTile nt0 = next_tile<WT>(s, p, r + s.G, 1 < ntile);
+            pstep<WT, 0, true, VWR, false, false, G, KT>(f0, acc, w, p, nt0, w.le + EBYTES);
+        }
+        for (int i = 0;;) {
+            const int t = r + i * s.G;
+            int8_t* le = w.le + (i & 1) * EBYTES;
+            int8_t* ln = w.le + ((i + 1) & 1) * EBYTES;
+            const NextTile nt = next_tile<WT>(s, p, t + s.G, i + 1 < ntile);
+            PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 0);
             pstep<WT, 1, false, VWR, false, false, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
@@ -400,31 +443,65 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
             pstep<WT, 1, false, VWN, false, true, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 1);
+            epilogue_kstep0a<WT>(f0, acc, w, p, s, t, le);
+            PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 2);
+            if (++i == ntile) break;
+            kstep0b<WT, KT>(f0, acc, w, p);
         }
-        PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 1);
-        epilogue<WT, G>(acc, p, s, t, w, le);
-        PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 2);
-        if (++i == ntile) break;
+    } else {
+        for (int i = 0;;) {
+            const int t = r + i * s.G;
+            int8_t* le = w.le + (i & 1) * EBYTES;
+            int8_t* ln = w.le + ((i + 1) & 1) * EBYTES;
+            const NextTile nt = next_tile<WT>(s, p, t + s.G, i + 1 < ntile);
+            PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 0);
+            if (s.KT == 4) {
+                pstep<WT, 0, true, VWR, true, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 1, false, VWR, false, true, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            } else {
+                pstep<WT, 0, true, VWR, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 1, false, VWR, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                for (int k = 4; k < s.KT - 4; k += 4) {
+                    pstep<WT, 0, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                    pstep<WT, 1, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                    pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                    pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                }
+                pstep<WT, 0, false, VWN, true, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 1, false, VWN, false, true, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+                pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
+            }
+            PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 1);
+            epilogue<WT, G>(acc, p, s, t, w, le);
+            PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 2);
+            if (++i == ntile) break;
+        }
     }
     // Loads past the last K-step (into released stages) and the epilogue's
     // stores are still in flight: let them land before the LDS is released.
     wait_all();
 }
 
-template <int WT, bool G, bool KT>
+template <int WT, bool G, bool KT, bool F>
 __global__ __launch_bounds__(256) void i8_gemm_pipe_kernel(GemmParams p) {
     constexpr int STG = PCfg<WT>::STG;
     __shared__ __align__(16) int8_t la[NSTG * STG], lb[NSTG * STG];
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
     PHI_PIPE_TRACE_BEGIN
-    pipe_tiles<WT, G, KT>(p, la, lb, eall, cbuf);
+    pipe_tiles<WT, G, KT, F>(p, la, lb, eall, cbuf);
     PHI_PIPE_TRACE_END
 }
 
 // Both tile sizes in one launch: the workgroup's 256 x 256 tiles of pb, then
 // its 128 x 128 tiles of ps (the rows below pb's), in the same LDS.
-template <bool G, bool KT>
+template <bool G, bool KT, bool F>
 __global__ __launch_bounds__(256) void i8_gemm_pipe_mixed_kernel(GemmParams pb, GemmParams ps) {
     constexpr int STG = PCfg<128>::STG;
     static_assert(PCfg<64>::STG <= STG, "the small tiles' stages fit in the big tiles' ones");
@@ -432,14 +509,29 @@ __global__ __launch_bounds__(256) void i8_gemm_pipe_mixed_kernel(GemmParams pb, 
     __shared__ __align__(16) int8_t eall[2 * EBYTES];
     __shared__ __align__(16) int8_t cbuf[4 * CHUNK];
     PHI_PIPE_TRACE_BEGIN
-    pipe_tiles<128, G, KT>(pb, la, lb, eall, cbuf);
+    pipe_tiles<128, G, KT, F>(pb, la, lb, eall, cbuf);
     __syncthreads();  // every wave is done with the big tiles' LDS
     PHI_PIPE_STAMP(2, 0, 0);
-    pipe_tiles<64, G, KT>(ps, la, lb, eall, cbuf);
+    pipe_tiles<64, G, KT, F>(ps, la, lb, eall, cbuf);
     PHI_PIPE_TRACE_END
 }
 
 }  // namespace
+
+// The fused tile transitions serve the bf16 output without a gate at K > 256.
+static bool fuse_transitions(const GemmParams& p) { return !p.gate && p.c_kind == C_BF16 && p.K > NSTG * PK; }
+
+template <int WT>
+static void launch_pipe_wt(hipStream_t stream, const GemmParams& p, dim3 g3) {
+    const dim3 b3(256);
+    if (p.gate && p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<WT, true, true, false>), g3, b3, 0, stream, p);
+    else if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<WT, true, false, false>), g3, b3, 0, stream, p);
+    else if (fuse_transitions(p)) {
+        if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<WT, false, true, true>), g3, b3, 0, stream, p);
+        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<WT, false, false, true>), g3, b3, 0, stream, p);
+    } else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<WT, false, true, false>), g3, b3, 0, stream, p);
+    else hipLaunchKernelGGL((i8_gemm_pipe_kernel<WT, false, false, false>), g3, b3, 0, stream, p);
+}
 
 hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile) {
     if (p.K % (NSTG * PK) != 0 || p.K < NSTG * PK) return hipErrorInvalidValue;
@@ -447,18 +539,8 @@ hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_
     const int bm = 2 * wave_tile;
     const int tiles = ((p.M + bm - 1) / bm) * ((p.N + bm - 1) / bm);
     const int grid = tiles < num_cus ? tiles : num_cus;
-    const dim3 g3(grid), b3(256);
-    if (wave_tile == 128) {
-        if (p.gate && p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true, true>), g3, b3, 0, stream, p);
-        else if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, true, false>), g3, b3, 0, stream, p);
-        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, true>), g3, b3, 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<128, false, false>), g3, b3, 0, stream, p);
-    } else {
-        if (p.gate && p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true, true>), g3, b3, 0, stream, p);
-        else if (p.gate) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, true, false>), g3, b3, 0, stream, p);
-        else if (p.kt) hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, true>), g3, b3, 0, stream, p);
-        else hipLaunchKernelGGL((i8_gemm_pipe_kernel<64, false, false>), g3, b3, 0, stream, p);
-    }
+    if (wave_tile == 128) launch_pipe_wt<128>(stream, p, dim3(grid));
+    else launch_pipe_wt<64>(stream, p, dim3(grid));
     return hipGetLastError();
 }
 
@@ -467,11 +549,16 @@ hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, c
     const int big = ((pb.M + 255) / 256) * ((pb.N + 255) / 256), small = ((ps.M + 127) / 128) * ((ps.N + 127) / 128);
     const int most = big > small ? big : small;
     const int grid = most < num_cus ? most : num_cus;
-    if (pb.kt != ps.kt || (pb.gate != nullptr) != (ps.gate != nullptr)) return hipErrorInvalidValue;
-    if (pb.gate && pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, true>), dim3(grid), dim3(256), 0, stream, pb, ps);
-    else if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
-    else if (pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, true>), dim3(grid), dim3(256), 0, stream, pb, ps);
-    else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, false>), dim3(grid), dim3(256), 0, stream, pb, ps);
+    if (pb.kt != ps.kt || (pb.gate != nullptr) != (ps.gate != nullptr) || pb.c_kind != ps.c_kind)
+        return hipErrorInvalidValue;
+    const dim3 g3(grid), b3(256);
+    if (pb.gate && pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, true, false>), g3, b3, 0, stream, pb, ps);
+    else if (pb.gate) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<true, false, false>), g3, b3, 0, stream, pb, ps);
+    else if (fuse_transitions(pb)) {
+        if (pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, true, true>), g3, b3, 0, stream, pb, ps);
+        else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, false, true>), g3, b3, 0, stream, pb, ps);
+    } else if (pb.kt) hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, true, false>), g3, b3, 0, stream, pb, ps);
+    else hipLaunchKernelGGL((i8_gemm_pipe_mixed_kernel<false, false, false>), g3, b3, 0, stream, pb, ps);
     return hipGetLastError();
 }
 

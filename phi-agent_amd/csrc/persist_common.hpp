@@ -166,9 +166,17 @@ __device__ __forceinline__ void col_operands(const EpiWave& w, const int8_t* e, 
 // (lane half h goes to half h ^ (r >> 4)), so these too touch every bank
 // once, and the reads of rows 16-31 swap the halves back.  The read-back (16
 // lanes a clock: two rows, eight chunks each) is conflict-free as well.
-template <int WT, bool G>
+//
+// hook(j, i) runs on the bf16 path right after block (j, i) has been read
+// out of its accumulators (the pipelined kernel issues the next tile's first
+// MFMAs on that block there); the other paths never call it.
+struct NoHook {
+    __device__ __forceinline__ void operator()(int, int) const {}
+};
+
+template <int WT, bool G, typename Hook = NoHook>
 __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const GemmParams& p, const Shape& s, int t,
-                                         const EpiWave& w, const int8_t* e) {
+                                         const EpiWave& w, const int8_t* e, Hook&& hook = Hook{}) {
     constexpr int NB = WT / 32, BM = 2 * WT;
 #pragma unroll
     for (int j = 0; j < NB; j++)
@@ -205,6 +213,7 @@ __device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const Ge
                 for (int jj = 0; jj < 2; jj++) {
                     v16i blk = acc[2 * jp + jj][i];
                     asm volatile("" : "+v"(blk));
+                    hook(2 * jp + jj, i);
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         float v[4];
