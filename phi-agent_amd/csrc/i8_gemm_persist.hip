@@ -324,6 +324,7 @@ __device__ __forceinline__ void persist_tiles(const GemmParams& p, int8_t* a0, i
     s.KT = p.K / BK;
     s.group_m = p.group_m;
     s.G = gridDim.x;
+    init_div(s);
     // Tiles r, r + G, ... of this workgroup (r after the XCD remap).
     const int r = xcd_remap(blockIdx.x, s.G);
     if (r >= s.ntiles) return;
@@ -402,7 +403,11 @@ __device__ __forceinline__ void persist_tiles(const GemmParams& p, int8_t* a0, i
         }
         step<WT, 0, true, W4, G>(f0, acc, w, p, kn, ln, w4r);
         step<WT, 1, false, W4, G>(f0, acc, w, p, kn + 1, ln, w4r);
-        epilogue<WT, G>(acc, p, s, t, w, le);
+        {
+            int tm, tn;
+            tile_mn(s, t, tm, tn);
+            epilogue<WT, G>(acc, p, tm * C::BM, tn * C::BM, w, le);
+        }
         if (++i == ntile) break;
     }
     // The reloads past the last K-step still write LDS: let them land.

@@ -293,9 +293,9 @@ __device__ __forceinline__ void pstep(Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PC
 // K-step), and the MFMAs' results are dropped.
 template <int WT>
 __device__ __forceinline__ void epilogue_kstep0a(const Frag<WT>& f0, v16i (&acc)[PCfg<WT>::NB][PCfg<WT>::NB],
-                                                 const Pw& w, const GemmParams& p, const Shape& s, int t,
+                                                 const Pw& w, const GemmParams& p, const NextTile& cur,
                                                  const int8_t* le) {
-    epilogue<WT, false>(acc, p, s, t, w, le, [&](int j, int i) {
+    epilogue<WT, false>(acc, p, cur.m0, cur.n0, w, le, [&](int j, int i) {
         acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f0.b[j], f0.a[i], v16i{}, 0, 0, 0);
     });
     __builtin_amdgcn_sched_barrier(0);
@@ -353,6 +353,7 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
     s.KT = p.K / PK;
     s.group_m = p.group_m;
     s.G = gridDim.x;
+    init_div(s);
     const int r = xcd_remap(blockIdx.x, s.G);
     if (r >= s.ntiles) return;
     const int ntile = (s.ntiles - r - 1) / s.G + 1;
@@ -424,6 +425,7 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
             const NextTile nt0 = next_tile<WT>(s, p, r + s.G, 1 < ntile);
             pstep<WT, 0, true, VWR, false, false, G, KT>(f0, acc, w, p, nt0, w.le + EBYTES);
         }
+        NextTile cur = first;
         for (int i = 0;;) {
             const int t = r + i * s.G;
             int8_t* le = w.le + (i & 1) * EBYTES;
@@ -444,12 +446,14 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
             pstep<WT, 2, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 1);
-            epilogue_kstep0a<WT>(f0, acc, w, p, s, t, le);
+            epilogue_kstep0a<WT>(f0, acc, w, p, cur, le);
             PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 2);
             if (++i == ntile) break;
             kstep0b<WT, KT>(f0, acc, w, p);
+            cur = nt;
         }
     } else {
+        NextTile cur = first;
         for (int i = 0;;) {
             const int t = r + i * s.G;
             int8_t* le = w.le + (i & 1) * EBYTES;
@@ -478,9 +482,10 @@ __device__ __forceinline__ void pipe_tiles(const GemmParams& p, int8_t* la, int8
                 pstep<WT, 3, false, VWN, false, false, G, KT>(f0, acc, w, p, nt, ln);
             }
             PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 1);
-            epilogue<WT, G>(acc, p, s, t, w, le);
+            epilogue<WT, G>(acc, p, cur.m0, cur.n0, w, le);
             PHI_PIPE_STAMP(WT == 128 ? 0 : 1, i, 2);
             if (++i == ntile) break;
+            cur = nt;
         }
     }
     // Loads past the last K-step (into released stages) and the epilogue's

@@ -79,16 +79,42 @@ struct EpiWave {
 
 struct Shape {
     int tiles_m, tiles_n, ntiles, KT, group_m, G;
+    // Tile order divisors (group_m * tiles_n and group_m) and their
+    // multipliers for udiv_inv, set by init_div.
+    unsigned per_group, pg_mul, gm_mul;
 };
 
+// Multiplier for dividing by a loop-invariant d >= 1: ceil(2^32 / d), which
+// is (2^32 - 1) / d + 1 for every d (0 for d = 1, handled in udiv_inv).
+__device__ __forceinline__ unsigned inv_mul(unsigned d) { return 0xffffffffu / d + 1u; }
+
+// n / d for n < 2^32 with m = inv_mul(d): the high word of n * m is n / d or
+// one more (m exceeds 2^32 / d by less than 1, so n * m / 2^32 exceeds n / d
+// by less than n / 2^32 < 1), and one comparison corrects it.  A handful of
+// scalar instructions instead of the reciprocal sequence of a general
+// division, which sits between every two tiles of the persistent loops.
+__device__ __forceinline__ unsigned udiv_inv(unsigned n, unsigned d, unsigned m) {
+    unsigned q = d == 1u ? n : __umulhi(n, m);
+    return q * d > n ? q - 1u : q;
+}
+
+__device__ __forceinline__ void init_div(Shape& s) {
+    s.per_group = (unsigned)(s.group_m * s.tiles_n);
+    s.pg_mul = inv_mul(s.per_group);
+    s.gm_mul = inv_mul((unsigned)s.group_m);
+}
+
+// Logical tile -> (tile row, tile column): groups of group_m tile rows, each
+// walked down its rows first.
 __device__ __forceinline__ void tile_mn(const Shape& s, int logical, int& tm, int& tn) {
-    const int per_group = s.group_m * s.tiles_n;
-    const int gid = logical / per_group;
+    const int gid = (int)udiv_inv((unsigned)logical, s.per_group, s.pg_mul);
     const int first_m = gid * s.group_m;
     const int gsz = min(s.tiles_m - first_m, s.group_m);
-    const int in_group = logical - gid * per_group;
-    tm = first_m + in_group % gsz;
-    tn = in_group / gsz;
+    const int in_group = logical - gid * (int)s.per_group;
+    // gsz is group_m except in a last, shorter group.
+    const int q = gsz == s.group_m ? (int)udiv_inv((unsigned)in_group, (unsigned)gsz, s.gm_mul) : in_group / gsz;
+    tm = first_m + (in_group - q * gsz);
+    tn = q;
 }
 
 
@@ -151,7 +177,7 @@ __device__ __forceinline__ void col_operands(const EpiWave& w, const int8_t* e, 
     bz = *(const v4f*)(w.lc + 4096 + cw * 4);
 }
 
-// Epilogue of logical tile t (operands in the LDS area e).  Lane l holds row
+// Epilogue of the tile at (m0, n0) (operands in the LDS area e).  Lane l holds row
 // l % 32 of each A block and, in registers 4g..4g+3, columns 8g + 4(l/32) +
 // 0..3 of each B block.  Each 32-row strip goes through the wave's LDS area
 // and is stored as whole rows: bf16 in 32 x 64-column pieces (128 bytes a
@@ -175,16 +201,13 @@ struct NoHook {
 };
 
 template <int WT, bool G, typename Hook = NoHook>
-__device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const GemmParams& p, const Shape& s, int t,
+__device__ __forceinline__ void epilogue(v16i (&acc)[WT / 32][WT / 32], const GemmParams& p, int m0, int n0,
                                          const EpiWave& w, const int8_t* e, Hook&& hook = Hook{}) {
     constexpr int NB = WT / 32, BM = 2 * WT;
 #pragma unroll
     for (int j = 0; j < NB; j++)
 #pragma unroll
         for (int i = 0; i < NB; i++) asm volatile("" : "+a"(acc[j][i]));
-    int tm, tn;
-    tile_mn(s, t, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BM;
     const int esz = p.c_kind == C_BF16 ? 2 : 4;
     const int pitch = (int)p.ldc * esz;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
