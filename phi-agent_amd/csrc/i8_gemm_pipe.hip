@@ -222,21 +222,23 @@ __device__ __forceinline__ void mma(const Frag<WT>& f, v16i (&acc)[PCfg<WT>::NB]
 }
 
 // Places a quarter's R fragment reads and V loads between the NB^2 - 1
-// MFMAs after its first (slots 0 .. NB^2 - 2).  Slot T takes the loads that
-// bring the running total to (T + 1) / (NB^2 - 1) of V.  The reads are spread
-// the same way over all slots but the last, so the next quarter's first
-// MFMAs, which need them, have one MFMA of slack.  Spreading the reads keeps
-// the four waves' fragment reads from meeting the stages' incoming DMA in
-// bursts: with the 256 x 256 tile's eight reads in the first eight slots the
-// K-step took 1206 clocks at 4352 x 12288 x 3072, spread 1092 (1024 of
-// MFMA issue).  Twelve other placements measured 1092-1228.
+// MFMAs after its first (slots 0 .. NB^2 - 2).  The reads are spread over all
+// slots but the last, slot T taking those that bring the running total to
+// (T + 1) / (NB^2 - 2) of R, so the next quarter's first MFMAs, which need
+// them, have one MFMA of slack.  The loads are spread the same way over all
+// slots; a 128 x 128 tile's two loads go to the first and the last slot.
+// Spreading the reads keeps the four waves' fragment reads from meeting the
+// stages' incoming DMA in bursts.  Measured at 4352 x 12288 x 3072 (clocks a
+// K-step): the 256 x 256 tile's eight reads in the first eight slots 1206,
+// spread as here 1092 (1024 of MFMA issue; twelve other placements
+// 1092-1228); the 128 x 128 tile's four reads one, one and two a slot 392,
+// two, two, none 382, with the loads moved as here 368 (256 of MFMA issue).
 template <int NB, int R, int V, int T = 0>
 __device__ __forceinline__ void sched_quarter() {
     constexpr int SLOTS = NB * NB - 1;
     if constexpr (T < SLOTS) {
-        constexpr int r = R <= SLOTS - 1 ? (T < SLOTS - 1 ? (T + 1) * R / (SLOTS - 1) - T * R / (SLOTS - 1) : 0)
-                                         : (T + 1) * R / SLOTS - T * R / SLOTS;
-        constexpr int v = (T + 1) * V / SLOTS - T * V / SLOTS;
+        constexpr int r = T < SLOTS - 1 ? (T + 1) * R / (SLOTS - 1) - T * R / (SLOTS - 1) : 0;
+        constexpr int v = NB == 2 && V == 2 ? (T == 0 || T == SLOTS - 1 ? 1 : 0) : (T + 1) * V / SLOTS - T * V / SLOTS;
         if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(SG_DSR, r, 0);
         if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, v, 0);
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
