@@ -482,9 +482,13 @@ def bench_vendor(cfg, steps, warmup):
 def bench_tiletrace(cfg, steps, warmup):
     """The headline step (K-tiled quantiser, then the GEMM) with the GEMM
     launched from the traced build of the pipeline (phi_probe_tile_trace):
-    the same kernel code plus one real-time stamp per workgroup at each
-    tile's start, K-loop end and epilogue end.  The record of the last timed
-    launch gives where a workgroup's time goes, averaged over workgroups."""
+    the same kernel code plus stamps per workgroup at each tile's start,
+    K-loop end and epilogue end, in the 100 MHz real-time clock and in shader
+    clock cycles.  The record of the last timed launch gives where a
+    workgroup's time goes, averaged over workgroups.  With the bf16 output the
+    tiles' transitions are fused: a tile's first K-step runs inside the
+    previous tile's epilogue (the first tile's before its start stamp), so a
+    K-loop span holds K/64 - 1 K-steps."""
     import ctypes
 
     import torch
@@ -505,7 +509,7 @@ def bench_tiletrace(cfg, steps, warmup):
     q8 = torch.empty((M * K,), dtype=torch.int8, device=dev)
     s8 = torch.empty((M,), dtype=torch.float32, device=dev)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    slots = 1024 * 64
+    slots = 1024 * 128
     rec = torch.zeros(slots, dtype=torch.int64, device=dev)
     # The library's plan: whole rounds of 256 x 256 tiles, the rest 128 x 128.
     big_rows = Q.big_tile_rows(M, N)
@@ -528,22 +532,26 @@ def bench_tiletrace(cfg, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
-    r = rec.view(-1, 64).cpu().tolist()
+    r = rec.view(-1, 128).cpu().tolist()
     used = [w for w in r if w[24] != 0]
     t0 = min(w[24] for w in used)
     us = lambda t: (t - t0) / 100.0  # 100 MHz real-time clock
+    fused = K > 256  # the bf16 output without a gate at K > 256
+    ksteps = K // 64 - (1 if fused else 0)
 
-    def tiles(w, base):
+    def tiles(w, base, c=0):
         out = []
         for i in range(8):
-            a, k, e = w[base + 3 * i], w[base + 3 * i + 1], w[base + 3 * i + 2]
-            if a == 0:
+            a, k, e = w[c + base + 3 * i], w[c + base + 3 * i + 1], w[c + base + 3 * i + 2]
+            if w[base + 3 * i] == 0:
                 break
-            out.append(((k - a) / 100.0, (e - k) / 100.0))
+            out.append(((k - a) / (100.0 if c == 0 else 1.0), (e - k) / (100.0 if c == 0 else 1.0)))
         return out
 
     big = [t for w in used for t in tiles(w, 0)]
     small = [t for w in used for t in tiles(w, 26)]
+    big_c = [t for w in used for t in tiles(w, 0, 64)]
+    small_c = [t for w in used for t in tiles(w, 26, 64)]
     by_round = {}
     for w in used:
         for i, t in enumerate(tiles(w, 0)):
@@ -556,16 +564,24 @@ def bench_tiletrace(cfg, steps, warmup):
     first = [us(w[0] if w[0] else w[26]) for w in used if w[0] or w[26]]
     bigdone = [us(w[25]) for w in used if w[25]]
     ends = [us(w[50]) for w in used]
+    cycles = [w[64 + 50] - w[64 + 24] for w in used]
+    clock = [(w[64 + 50] - w[64 + 24]) / ((w[50] - w[24]) * 10.0) for w in used if w[50] > w[24]]  # GHz
     per_xcd = {}
     for w in used:
         d = per_xcd.setdefault(int(w[60]), [])
         d.append(us(w[25]) if w[25] else us(w[50]))
     ops = 2.0 * M * N * K
     extra = {
-        "big_rows": big_rows, "workgroups": len(used),
+        "big_rows": big_rows, "workgroups": len(used), "ksteps_per_kloop": ksteps,
         "big_tiles": len(big), "big_kloop_us": mean([t[0] for t in big]), "big_epilogue_us": mean([t[1] for t in big]),
+        "big_kloop_cycles_per_kstep": mean([t[0] / ksteps for t in big_c]) if big_c else None,
+        "big_epilogue_cycles": mean([t[1] for t in big_c]),
         "small_tiles": len(small), "small_kloop_us": mean([t[0] for t in small]),
         "small_epilogue_us": mean([t[1] for t in small]),
+        "small_kloop_cycles_per_kstep": mean([t[0] / ksteps for t in small_c]) if small_c else None,
+        "small_epilogue_cycles": mean([t[1] for t in small_c]),
+        "workgroup_cycles": {"mean": mean(cycles), "max": max(cycles)},
+        "shader_clock_ghz": mean(clock),
         "first_tile_start_us": mean(first),
         "big_phase_end_us": {"min": min(bigdone), "mean": mean(bigdone), "max": max(bigdone)} if bigdone else None,
         "kernel_end_us": {"min": min(ends), "mean": mean(ends), "max": max(ends)},

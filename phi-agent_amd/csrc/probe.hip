@@ -20,40 +20,46 @@
 //                   its MFMAs before they slow down.
 //   phi_probe_tile_trace  the persistent pipeline (i8_gemm_pipe.hip, compiled
 //                   here a second time into namespace phi_dev_trace with its
-//                   timeline hooks defined) with one record of real-time clock
-//                   stamps per workgroup: kernel start, each tile's start,
-//                   K-loop end and epilogue end, the switch between tile
-//                   sizes, and the end.  The stamps go to LDS during the run
-//                   and out to memory once, at the end.
+//                   timeline hooks defined) with one record of stamps per
+//                   workgroup, each point in both the real-time clock and
+//                   the shader clock: kernel start, each tile's start, K-loop
+//                   end and epilogue end, the switch between tile sizes, and
+//                   the end.  The stamps go to LDS during the run and out to
+//                   memory once, at the end.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// The per-workgroup record (64 words of the 100 MHz real-time clock):
+// The per-workgroup record: words 0-63 hold the 100 MHz real-time clock,
+// words 64-127 the shader clock (s_memtime, cycles) at the same points:
 //   [3 i + p]       256 x 256 tile i < 8, point p (0 start, 1 K-loop end, 2 epilogue end)
 //   [24] kernel start, [25] switch to 128 x 128 tiles, [50] kernel end
 //   [26 + 3 i + p]  128 x 128 tile i < 8, point p
 //   [60] the XCD the workgroup ran on
-__shared__ unsigned long long phi_trace_lds[64];
+__shared__ unsigned long long phi_trace_lds[128];
 __device__ unsigned long long* phi_trace_out;
 
-#define PHI_PIPE_STAMP(phase, tile, point)                                                              \
-    if (threadIdx.x == 0 && (tile) < 8)                                                                 \
-        phi_trace_lds[(phase) == 0 ? (tile) * 3 + (point) : (phase) == 1 ? 26 + (tile) * 3 + (point) : 25] = \
-            __builtin_amdgcn_s_memrealtime();
+#define PHI_TRACE_SLOT(k)                                               \
+    do {                                                                \
+        phi_trace_lds[k] = __builtin_amdgcn_s_memrealtime();             \
+        phi_trace_lds[64 + (k)] = __builtin_amdgcn_s_memtime();          \
+    } while (0)
+#define PHI_PIPE_STAMP(phase, tile, point)                                                                  \
+    if (threadIdx.x == 0 && (tile) < 8)                                                                     \
+        PHI_TRACE_SLOT((phase) == 0 ? (tile) * 3 + (point) : (phase) == 1 ? 26 + (tile) * 3 + (point) : 25);
 #define PHI_PIPE_TRACE_BEGIN                                                   \
-    if (threadIdx.x < 64) phi_trace_lds[threadIdx.x] = 0;                     \
+    if (threadIdx.x < 128) phi_trace_lds[threadIdx.x] = 0;                    \
     __syncthreads();                                                           \
-    if (threadIdx.x == 0) phi_trace_lds[24] = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) PHI_TRACE_SLOT(24);
 #define PHI_PIPE_TRACE_END                                                            \
     __syncthreads();                                                                  \
     if (threadIdx.x == 0) {                                                           \
-        phi_trace_lds[50] = __builtin_amdgcn_s_memrealtime();                         \
+        PHI_TRACE_SLOT(50);                                                           \
         unsigned int xcc_;                                                            \
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_));           \
         phi_trace_lds[60] = xcc_ & 15;                                                \
     }                                                                                 \
     __syncthreads();                                                                  \
-    if (threadIdx.x < 64) phi_trace_out[blockIdx.x * 64 + threadIdx.x] = phi_trace_lds[threadIdx.x];
+    if (threadIdx.x < 128) phi_trace_out[blockIdx.x * 128 + threadIdx.x] = phi_trace_lds[threadIdx.x];
 
 #define phi_dev phi_dev_trace
 #include "i8_gemm_pipe.hip"
@@ -218,7 +224,7 @@ int phi_probe_lds_dma(void* stream, const int8_t* src, long long window, int ite
 // The K-tiled (kt) or row-major pipeline over A [M, K], B [N, K] (bf16 out,
 // fp32 row scales sA, one fp32 scale sB, bf16 bias): 256 x 256 tiles for the
 // first big_rows rows (a multiple of 256), 128 x 128 tiles for the rest, in
-// one launch, as the library's plan runs it.  out holds slots >= grid x 64
+// one launch, as the library's plan runs it.  out holds slots >= grid x 128
 // words.
 int phi_probe_tile_trace(void* stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
                          const void* bias, void* C, int M, int N, int K, int big_rows, int kt,
@@ -232,7 +238,7 @@ int phi_probe_tile_trace(void* stream, const int8_t* A, const int8_t* B, const f
     const long long big = (long long)((big_rows + 255) / 256) * ((N + 255) / 256);
     const long long small = (long long)((M - big_rows + 127) / 128) * ((N + 127) / 128);
     const long long most = big > small ? big : small;
-    if ((most < cus ? most : cus) * 64 > slots) return (int)hipErrorInvalidValue;
+    if ((most < cus ? most : cus) * 128 > slots) return (int)hipErrorInvalidValue;
     hipError_t e = hipMemcpyToSymbolAsync(HIP_SYMBOL(phi_trace_out), &out, sizeof(out), 0, hipMemcpyHostToDevice,
                                           (hipStream_t)stream);
     if (e != hipSuccess) return (int)e;
