@@ -53,3 +53,26 @@ def test_bench_refuses_more_than_one_gpu():
     out = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                          capture_output=True, text=True, timeout=60)
     assert out.returncode == 2 and "one GPU" in out.stderr
+
+
+def test_tile_order_division_by_multiplier():
+    """The persistent GEMMs divide tile indices by loop-invariant d with the
+    multiplier m = (2^32 - 1) / d + 1 (mod 2^32): q = hi32(n * m), minus one
+    where q * d > n (persist_common.hpp, udiv_inv; d = 1 takes q = n).  The
+    claim is exactness for every n < 2^32; checked here by brute force over
+    every divisor up to 2^13 and spread-out larger ones, at the n where an
+    error would first show (multiples of d and their neighbours) and across
+    the range."""
+    rng = np.random.default_rng(7)
+    ds = list(range(1, 1 << 13)) + [int(v) for v in rng.integers(1 << 13, 1 << 31, 200)] + [(1 << 31) - 1, 1 << 31, (1 << 32) - 1]
+    for d in ds:
+        d = np.uint64(d)
+        m = (np.uint64(0xFFFFFFFF) // d + np.uint64(1)) & np.uint64(0xFFFFFFFF)
+        k = rng.integers(0, (1 << 32) // int(d) + 1, 64, dtype=np.uint64)
+        n = np.concatenate([k * d, k * d + d - np.uint64(1), k * d - np.uint64(1),
+                            rng.integers(0, 1 << 32, 64, dtype=np.uint64),
+                            np.array([0, 1, (1 << 32) - 1], dtype=np.uint64)])
+        n = n[n < np.uint64(1 << 32)]
+        q = n if d == 1 else (n * m) >> np.uint64(32)
+        q = np.where(q * d > n, q - np.uint64(1), q)
+        assert np.array_equal(q, n // d), int(d)
