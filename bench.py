@@ -69,6 +69,9 @@ CONFIGS = {
     # A reference point for the prologue: torch's bf16 -> int8 conversion of
     # the same activation tensor moves the prologue's bytes (2K in, K out a row).
     "c1_prologue_vendor": dict(kind="convref", M=4352, K=3072),
+    # The prologue against the floor of its memory pattern (probe kernels).
+    "c1_prologue_floor": dict(kind="qrfloor", M=4352, K=3072),
+    "c1_down_prologue_floor": dict(kind="qrfloor", M=4352, K=12288),
 }
 
 
@@ -636,6 +639,84 @@ def bench_convref(cfg, steps, warmup):
                       "copy_gbs": 4.0 * M * K / (ms_copy * 1e-3) / 1e9}}
 
 
+def bench_prologue_floor(cfg, steps, warmup):
+    """The rotate+quantise prologue (quant_rotate_kt, K-tiled codes) against
+    what its memory pattern alone costs: phi_probe_prologue_stream loads the
+    same bf16 rows and stores the same 16-byte code chunks on the same launch
+    shape, without the rotation and quantisation (mode 0, K-tiled and
+    row-major stores), and with the LDS round trips and barrier added (mode
+    1); and torch's bf16 -> int8 conversion of the tensor.  Interleaved
+    rounds in one process, median per variant."""
+    import ctypes
+    import statistics
+
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    dev = torch.device("cuda:0")
+    M, K = cfg["M"], cfg["K"]
+    G = K // 256
+    x = synth.activations(M, K, seed=0, device=dev)
+    q = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    s = torch.empty((M,), dtype=torch.float32, device=dev)
+    q2 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    lib = ctypes.CDLL(os.path.join(PKG, "lib", "libphi_probe.so"))
+    lib.phi_probe_prologue_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def probe(mode, kt, run=0):
+        def go():
+            rc = lib.phi_probe_prologue_stream(stream, x.data_ptr(), M, G, q.data_ptr(), s.data_ptr(), mode, kt, run)
+            if rc != 0:
+                raise RuntimeError(f"prologue stream probe failed ({rc})")
+        return go
+
+    def prologue(lg_run):
+        def go():
+            os.environ["PHI_QR_RUN"] = str(lg_run)
+            Q.quant_rotate_kt(x, q=q, s=s)
+        return go
+
+    variants = {
+        "prologue": prologue(3),
+        "prologue_run1": prologue(0),
+        "prologue_run2": prologue(1),
+        "prologue_run4": prologue(2),
+        "stream_kt": probe(0, 1),
+        "stream_kt_run2": probe(0, 1, 2),
+        "stream_kt_run4": probe(0, 1, 4),
+        "stream_kt_run8": probe(0, 1, 8),
+        "stream_row_major": probe(0, 0),
+        "stream_lds_kt": probe(1, 1),
+        "torch_convert": lambda: q2.copy_(x),
+    }
+    times = {k: [] for k in variants}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for rnd in range(3):
+        for name, fn in variants.items():
+            for _ in range(warmup):
+                fn()
+            start.record()
+            for _ in range(steps):
+                fn()
+            end.record()
+            torch.cuda.synchronize()
+            times[name].append(start.elapsed_time(end) / steps * 1e3)
+    us = {k: statistics.median(v) for k, v in times.items()}
+    nbytes = 3.0 * M * K + 4.0 * M
+    gbs = nbytes / (us["prologue"] * 1e-6) / 1e9
+    return {"value": gbs, "ms": us["prologue"] * 1e-3, "dtype": "bf16", "unit": "GB/s",
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+            "extra": {"us": {k: round(v, 2) for k, v in us.items()},
+                      "gbs": {k: round(nbytes / (v * 1e-6) / 1e9, 1) for k, v in us.items()},
+                      "rounds_us": {k: [round(t, 2) for t in v] for k, v in times.items()}}}
+
+
 def bench_ceiling(steps, warmup):
     """The two ceilings the headline GEMM is argued against, from the probe
     kernels of lib/libphi_probe.so: every wave of every CU issues int8 MFMAs
@@ -756,6 +837,8 @@ def main() -> int:
         r = bench_tiletrace(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "convref":
         r = bench_convref(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "qrfloor":
+        r = bench_prologue_floor(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "vendor":
         r = bench_vendor(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "ceiling":

@@ -9,6 +9,7 @@
  */
 #include "oracle.h"
 
+#include <limits.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -135,8 +136,15 @@ void orc_convrot_rows(const float* x, float* out, int64_t rows, int64_t cols) {
 
 /* The host rule: the fp32 product widened to double, pushed half a unit away
  * from zero and truncated (core/host/quant.cpp:163-166); or, with
- * ORC_ROUND_HALF_EVEN, the nearest integer with ties to even. */
+ * ORC_ROUND_HALF_EVEN, the nearest integer with ties to even.  A NaN product
+ * (a NaN element, or inf * 0 when the row's amax is inf) becomes the most
+ * negative code: the device form clamps with fminf(fmaxf(d, -qmax), qmax),
+ * which maps NaN to -qmax (core/kernels/int8_gemm.cpp:779), and the host
+ * form's (long) cast of a NaN gives LONG_MIN on x86-64, clamped to -127
+ * (core/host/quant.cpp:164-165).  Written out here instead of left to the
+ * cast. */
 static long round_code(float prod, int round_mode) {
+    if (isnan(prod)) return LONG_MIN;
     const double d = (double)prod;
     if (round_mode == ORC_ROUND_HALF_EVEN) return (long)nearbyint(d);
     return (long)(d >= 0 ? d + 0.5 : d - 0.5);

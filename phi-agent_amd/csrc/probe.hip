@@ -18,6 +18,10 @@
 //   phi_probe_mfma_valu  the mode-2 MFMA loop with V v_perm_b32 operations
 //                   after every MFMA: the VALU work a wave can issue beside
 //                   its MFMAs before they slow down.
+//   phi_probe_prologue_stream  the rotate+quantise prologue's loads, stores
+//                   and launch shape without its arithmetic (and, in mode 1,
+//                   with its LDS round trips and barrier): the floor the
+//                   prologue is measured against.
 //   phi_probe_tile_trace  the persistent pipeline (i8_gemm_pipe.hip, compiled
 //                   here a second time into namespace phi_dev_trace with its
 //                   timeline hooks defined) with one record of stamps per
@@ -186,9 +190,105 @@ __global__ __launch_bounds__(256) void lds_dma_probe(const int8_t* src, int wind
     if (st[wave][0][lane] == 127 && st[wave][1][lane] == -128 && lane == 0) sink[blockIdx.x] = 1;
 }
 
+// The rotate+quantise prologue's memory pattern without its arithmetic, on
+// quant_rotate_tiles' launch shape at one round a wave: one row a block of
+// ceil(G / 4) waves, a 16-lane team a 256-group.  Each lane loads its 16
+// bf16 inputs (32 bytes), keeps their high bytes, and stores those 16 bytes
+// where the codes go (K-tiled when kt, else row-major); lane 0 of the row's
+// first wave stores one float.  MODE 1 adds the kernel's LDS traffic: the
+// values as fp32 through the team's 16 x 16 tile and back (row write, column
+// read, column write, row read) and the cross-wave exchange of one word a
+// wave with its barrier.
+// run > 0 remaps blocks so each XCD (blocks are dealt to the 8 XCDs in
+// turn) takes runs of that many consecutive rows.
+template <int MODE>
+__global__ __launch_bounds__(1024) void prologue_stream_probe(const uint16_t* x, int rows, int G, int8_t* q,
+                                                              float* s, int kt, int run) {
+    extern __shared__ __align__(16) float plds[];
+    const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
+    int row = blockIdx.x;
+    if (run > 0 && (int)blockIdx.x < (int)gridDim.x / (8 * run) * (8 * run)) {
+        const int b = blockIdx.x, c = b % (8 * run);
+        row = b - c + (c % 8) * run + c / 8;
+    }
+    const int team = lane >> 4, tl = lane & 15, sw = tl >> 2;
+    const int g = wr * 4 + team;
+    const uint4* src = (const uint4*)(x + (int64_t)row * G * 256 + (int64_t)min(g, G - 1) * 256 + tl * 16);
+    const uint4 a = src[0], b = src[1];
+    uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t packed[4];
+    uint32_t word = w[0];
+    if (MODE == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) packed[i] = __builtin_amdgcn_perm(w[2 * i + 1], w[2 * i], 0x07050301u);
+    } else {
+        float* T = plds + wr * 1088 + team * 272;
+        float* trow = T + tl * 16;
+        uint32_t* red = (uint32_t*)(plds + wpr * 1088);
+        float v[16], c[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = __uint_as_float(i & 1 ? w[i >> 1] & 0xffff0000u : w[i >> 1] << 16);
+#pragma unroll
+        for (int k = 0; k < 4; k++) *(float4*)(trow + 4 * (k ^ sw)) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) c[4 * k + i] = T[64 * k + 4 * (sw ^ k) + (tl & 3) + 16 * i];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (lane == 0) red[wr] = __float_as_uint(c[0]);
+        __syncthreads();
+        for (int i = 0; i < wpr; i++) word ^= red[i];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) T[64 * k + 4 * (sw ^ k) + (tl & 3) + 16 * i] = c[4 * k + i];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 u = *(const float4*)(trow + 4 * (k ^ sw));
+            packed[k] = __builtin_amdgcn_perm(__float_as_uint(u.y), __float_as_uint(u.x), 0x07030703u) ^
+                        __builtin_amdgcn_perm(__float_as_uint(u.w), __float_as_uint(u.z), 0x03070307u);
+        }
+    }
+    int8_t* dst;
+    if (kt) {
+        const int64_t st = row >> 8, rr = row & 255, h = min(256, rows - (int)(st << 8));
+        dst = q + st * 256 * (int64_t)G * 256 + (int64_t)g * 4 * h * 64 + (tl >> 2) * h * 64 + rr * 64 +
+              (((tl & 3) ^ ((rr >> 2) & 3)) * 16);
+    } else {
+        dst = q + (int64_t)row * G * 256 + (int64_t)g * 256 + tl * 16;
+    }
+    if (g < G) *(uint4*)dst = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    if (wr == 0 && lane == 0) s[row] = __uint_as_float(word);
+}
+
 }  // namespace
 
 extern "C" {
+
+// The prologue stream probe over x [rows, 256 G] bf16 into q (rows x 256 G
+// bytes) and s [rows]; G <= 64; run as in prologue_stream_probe.
+int phi_probe_prologue_stream(void* stream, const uint16_t* x, int rows, int G, int8_t* q, float* s, int mode, int kt,
+                              int run) {
+    if (rows <= 0 || G <= 0 || G > 64) return (int)hipErrorInvalidValue;
+    const int wpr = (G + 3) / 4;
+    const size_t lds = ((size_t)wpr * 1088 + 16) * sizeof(float);
+    static bool lds_set = false;
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)prologue_stream_probe<1>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)((16 * 1088 + 16) * sizeof(float)));
+        if (e != hipSuccess) return (int)e;
+        lds_set = true;
+    }
+    if (mode == 0)
+        hipLaunchKernelGGL(prologue_stream_probe<0>, dim3(rows), dim3(64 * wpr), 0, (hipStream_t)stream, x, rows, G, q,
+                           s, kt, run);
+    else
+        hipLaunchKernelGGL(prologue_stream_probe<1>, dim3(rows), dim3(64 * wpr), lds, (hipStream_t)stream, x, rows, G,
+                           q, s, kt, run);
+    return (int)hipGetLastError();
+}
 
 int phi_probe_mfma(void* stream, const int8_t* ops, int mode, int iters, int* sink, int grid) {
     switch (mode) {

@@ -196,14 +196,18 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
 // tiles of a wave are 272 floats apart, so the teams' column accesses use
 // different banks.
 //
-// The kernel issues about fifteen VALU instructions per element against four
-// bytes of HBM traffic (bf16 in, int8 out), so VALU issue bounds it next to
-// HBM.  Hence: one fma per butterfly output (sum - 2x is exact as
-// fma(-2, x, sum), the product being exact), the final 1/16 folded into the
-// scale, the amax as v_max3 over |.|, and half-away rounding as add +
-// truncate (pre_half_away) with the truncation done by the int conversion.
-// R > 1 spreads the per-wave costs (addresses, scale division, reductions)
-// over more elements.
+// About fifteen VALU instructions an element against four bytes of HBM
+// traffic (bf16 in, int8 out).  The arithmetic does not overlap the memory
+// traffic well: every wave loads at its start and stores at its end, so the
+// chip runs a load phase, an arithmetic phase and a store phase about 1.6
+// times over (at 4352 x 3072: 10.3 us against 5.7 us for the same loads and
+// stores alone, the prologue stream probe).  Hence few instructions: one
+// fma per butterfly output (exact as sum - 2x while 2x does not overflow),
+// the final 1/16 folded into the scale, the amax as v_max3 over |.|,
+// half-away rounding as add + truncate (pre_half_away) without the clamp on
+// rows that cannot need it, and the bytes packed by the conversions
+// themselves (cvt_pack4).  R > 1 spreads the per-wave costs (addresses,
+// scale division, reductions) over more elements.
 constexpr int QT_TILE = 272;
 constexpr int QT_WAVE = 4 * QT_TILE;
 constexpr int QT_MAX_ROUNDS = 5;
@@ -228,6 +232,24 @@ __device__ __forceinline__ void bfly16f(float (&v)[16]) {
         v[b + 2 * ST] = fmaf(-2.0f, x1, sum);
         v[b + 3 * ST] = fmaf(-2.0f, x0, sum);
     }
+}
+
+// bfly16f<4> that also returns (s0 + s1) + (s2 + s3) over its four quadruple
+// sums.  That value is finite only if all 16 inputs are: an inf or NaN input
+// makes its quadruple's sum inf or NaN (never finite).  With finite inputs the
+// outputs fma(-2, x, sum) are finite or +-inf, never NaN.
+__device__ __forceinline__ float bfly16f_last(float (&v)[16]) {
+    float s[4];
+#pragma unroll
+    for (int o = 0; o < 4; o++) {
+        const float x0 = v[o], x1 = v[o + 4], x2 = v[o + 8], x3 = v[o + 12];
+        s[o] = ((x0 + x1) + x2) + x3;
+        v[o] = fmaf(-2.0f, x3, s[o]);
+        v[o + 4] = fmaf(-2.0f, x2, s[o]);
+        v[o + 8] = fmaf(-2.0f, x1, s[o]);
+        v[o + 12] = fmaf(-2.0f, x0, s[o]);
+    }
+    return (s[0] + s[1]) + (s[2] + s[3]);
 }
 
 // max(m, |a|, |b|) in one instruction (fmaxf would first canonicalise each
@@ -256,126 +278,250 @@ __device__ __forceinline__ uint32_t wave_max_bits(uint32_t u) {
 // floor(fl(d + (0.5 - 2^-25))) is d rounded half away from zero (checked over
 // all fp32 d < 2^25; above that d is an integer and the addition returns d),
 // and |v| * inv is |v * inv| exactly.  The clamp commutes with the truncation
-// because qmax is an integer.
+// because qmax is an integer.  A NaN product (a NaN value, or inf * 0 in a
+// row whose amax is inf) gives -qmax, as the reference's clamp
+// fminf(fmaxf(d, -qmax), qmax) does (core/kernels/int8_gemm.cpp:779).
 __device__ __forceinline__ float pre_half_away(float v, float inv, float qmax) {
-    return copysignf(fminf(fabsf(v) * inv + 0.49999997f, qmax), v);
+    const float p = fabsf(v) * inv;
+    return p != p ? -qmax : copysignf(fminf(p + 0.49999997f, qmax), v);
 }
 
+// fmaxf returns -qmax for a NaN product here.
 __device__ __forceinline__ float pre_half_even(float v, float inv, float qmax) {
     return fminf(fmaxf(rintf(v * inv), -qmax), qmax);
 }
 
-// Four fp32 values truncated to int and packed little-endian into one dword.
-// Callers pass values whose truncations fit int8.
+// The fast path's codes: pre_half_away and pre_half_even without the clamp.
+// They give the clamped codes whenever |v| inv < qmax + 1/2 and v inv is not
+// NaN, which holds on every element of a row whose rotated values are all
+// finite: there |v| <= amax, so |v| inv <= qmax (1 + 3 2^-24), and qmax is an
+// integer in [1, 127] (checked by the C ABI).
+__device__ __forceinline__ float pre_half_away_nc(float v, float inv) {
+    return copysignf(fabsf(v) * inv + 0.49999997f, v);
+}
+__device__ __forceinline__ float pre_half_even_nc(float v, float inv) { return rintf(v * inv); }
+
+// Four fp32 values truncated to int and packed little-endian into one dword:
+// each conversion writes the low byte of its int32 result into its byte of
+// the dword (SDWA dst_sel), the first clearing the others.  Callers pass
+// values whose truncations fit int8.
 __device__ __forceinline__ uint32_t cvt_pack4(float a, float b, float c, float d) {
-    return pack4((int)a, (int)b, (int)c, (int)d);
+    uint32_t r;
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_0 dst_unused:UNUSED_PAD src0_sel:DWORD" : "=v"(r) : "v"(a));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(r) : "v"(b));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(r) : "v"(c));
+    asm("v_cvt_i32_f32_sdwa %0, %1 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:DWORD" : "+v"(r) : "v"(d));
+    return r;
+}
+
+template <int OP> constexpr int qt_ns = OP == QR_SILU_GATE ? 2 : 1;  // input sets (the SiLU gate has two)
+template <bool BF16_IN> constexpr int qt_nw = BF16_IN ? 8 : 16;        // input dwords per lane and set
+
+// One round's inputs: the lane's 16 elements of a group at element offset
+// off, and for the SiLU gate the value operand's 16 at off + off2.
+template <bool BF16_IN, int OP>
+__device__ __forceinline__ void qt_load(const void* __restrict__ x, int64_t off, const QrPre& pre_op,
+                                        uint32_t (&raw)[qt_ns<OP>][qt_nw<BF16_IN>]) {
+#pragma unroll
+    for (int h = 0; h < qt_ns<OP>; h++) {
+        const int64_t o = off + (h ? pre_op.off2 : 0);
+        const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)x + o) : (const uint4*)((const float*)x + o);
+#pragma unroll
+        for (int i = 0; i < qt_nw<BF16_IN> / 4; i++) {
+            const uint4 t = src[i];
+            raw[h][4 * i] = t.x;
+            raw[h][4 * i + 1] = t.y;
+            raw[h][4 * i + 2] = t.z;
+            raw[h][4 * i + 3] = t.w;
+        }
+    }
+}
+
+// One round's rotation: the pre-op on the raw inputs, passes 1 and 4 in
+// registers, the transpose through the team's tile, passes 16 and 64.  w[j]
+// receives element 16 j + tl of the group (before the final 1/16).  SUB =
+// false forms each butterfly output as fma(-2, x, sum), one rounding; SUB =
+// true as sum - 2 x, the reference's mul and subtract.  The product 2x is
+// exact unless it overflows (|x| >= 2^127), so the two agree on every group
+// whose rotated values stay below 2^126: one radix-4 pass applied twice is
+// 4 I, so each value inside the rotation is bounded by about the largest
+// output of the pass after it.  For SUB = false the result is the last pass's
+// check sum (bfly16f_last): finite only if every value entering that pass is.
+template <bool BF16_IN, int OP, bool SUB>
+__device__ __forceinline__ float qt_round(const uint32_t (&raw)[qt_ns<OP>][qt_nw<BF16_IN>], int64_t col0, int rotate,
+                                          const QrPre& pre_op, float* T, float* trow, int tl, int sw,
+                                          float (&w)[16]) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        if (BF16_IN) v[i] = __uint_as_float(i & 1 ? raw[0][i >> 1] & 0xffff0000u : raw[0][i >> 1] << 16);
+        else v[i] = __uint_as_float(raw[0][i]);
+    }
+    if (OP == QR_MOD) modulate16(v, pre_op.sc, pre_op.sh, col0);
+    if (OP == QR_GELU) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = gelu_tanh(v[i]);
+    }
+    if (OP == QR_SILU_GATE) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t u = raw[qt_ns<OP> - 1][BF16_IN ? i >> 1 : i];
+            v[i] = silu_mul(v[i], __uint_as_float(BF16_IN ? (i & 1 ? u & 0xffff0000u : u << 16) : u));
+        }
+    }
+    if (rotate) {
+        if (SUB) {
+            bfly16<1>(v);
+            bfly16<4>(v);
+        } else {
+            bfly16f<1>(v);
+            bfly16f<4>(v);
+        }
+    }
+    // Row tl of the tile, then column tl: w[j] = element 16 j + tl.
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+        *(float4*)(trow + 4 * (c ^ sw)) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+    wave_lds_fence();
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float* col = T + 64 * k + 4 * (sw ^ k) + (tl & 3);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[4 * k + i] = col[16 * i];
+    }
+    wave_lds_fence();
+    float f = 0.0f;
+    if (rotate) {
+        if (SUB) {
+            bfly16<1>(w);
+            bfly16<4>(w);
+        } else {
+            bfly16f<1>(w);
+            f = bfly16f_last(w);
+        }
+    }
+    return f;
+}
+
+// max |w[j]| over a round, as bits (NaN values are passed over, as the
+// reference's `if (a > amax)` and fmaxf pass them over).
+__device__ __forceinline__ uint32_t qt_amax16(const float (&w)[16]) {
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) m = max3_abs(m, w[j], w[j + 1]);
+    return __float_as_uint(m);
+}
+
+// The row scale and the factors the codes use.  The rotation's final 1/16 is
+// applied to the amax and to inv instead of to every element.  max |w|/16
+// rounds to the max of the rounded |w|/16, so the amax and scale are exact.
+// When inv/16 is exact (inv >= 2^-122, i.e. amax below ~2^122 qmax),
+// round(w * (inv/16)) = round((w/16) * inv) wherever w/16 is exact, and where
+// it is not (|w| < 2^-122) the code is 0 either way (|w| inv/16 < 1e-5).
+// Otherwise (fold false) each element is scaled by pre = 1/16 first.
+struct QtScale {
+    float scale, pre, post;
+    bool fold;
+};
+__device__ __forceinline__ QtScale qt_scale(uint32_t amax, float qmax, int rotate) {
+    const float sixteenth = rotate ? 1.0f / 16.0f : 1.0f;
+    const float rmax = __uint_as_float(amax) * sixteenth;
+    QtScale c;
+    c.scale = rmax > 1e-30f ? rmax / qmax : 1.0f;
+    const float inv = 1.0f / c.scale;
+    c.fold = !rotate || inv >= 0x1p-122f;
+    c.pre = c.fold ? 1.0f : sixteenth;
+    c.post = c.fold ? inv * sixteenth : inv;
+    return c;
+}
+
+// One round's codes: column tl back into the tile, row tl out (16 contiguous
+// elements), quantised and stored as one 16-byte write when live.  FAST
+// leaves out the clamp (pre_half_away_nc).
+template <bool HALF_EVEN, bool FAST>
+__device__ __forceinline__ void qt_store(const float (&w)[16], float* T, float* trow, int tl, int sw,
+                                         const QtScale& c, float qmax, int8_t* dst, bool live) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float* col = T + 64 * k + 4 * (sw ^ k) + (tl & 3);
+#pragma unroll
+        for (int i = 0; i < 4; i++) col[16 * i] = w[4 * k + i];
+    }
+    wave_lds_fence();
+    uint32_t packed[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float4 u = *(const float4*)(trow + 4 * (k ^ sw));
+        if (!c.fold) u = make_float4(u.x * c.pre, u.y * c.pre, u.z * c.pre, u.w * c.pre);  // wave-uniform, rare
+        if (FAST) {
+            if (HALF_EVEN)
+                packed[k] = cvt_pack4(pre_half_even_nc(u.x, c.post), pre_half_even_nc(u.y, c.post),
+                                      pre_half_even_nc(u.z, c.post), pre_half_even_nc(u.w, c.post));
+            else
+                packed[k] = cvt_pack4(pre_half_away_nc(u.x, c.post), pre_half_away_nc(u.y, c.post),
+                                      pre_half_away_nc(u.z, c.post), pre_half_away_nc(u.w, c.post));
+        } else {
+            if (HALF_EVEN)
+                packed[k] = cvt_pack4(pre_half_even(u.x, c.post, qmax), pre_half_even(u.y, c.post, qmax),
+                                      pre_half_even(u.z, c.post, qmax), pre_half_even(u.w, c.post, qmax));
+            else
+                packed[k] = cvt_pack4(pre_half_away(u.x, c.post, qmax), pre_half_away(u.y, c.post, qmax),
+                                      pre_half_away(u.z, c.post, qmax), pre_half_away(u.w, c.post, qmax));
+        }
+    }
+    wave_lds_fence();
+    if (live) *(uint4*)dst = make_uint4(packed[0], packed[1], packed[2], packed[3]);
 }
 
 template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
                                                            int G, int8_t* __restrict__ q, int64_t ldq,
                                                            float* __restrict__ s, float qmax, int rotate,
-                                                           QrPre pre_op, int qkt) {
+                                                           QrPre pre_op, int qkt, int lg_run) {
     extern __shared__ __align__(16) float lds[];
-    constexpr int NW = BF16_IN ? 8 : 16;  // input dwords per lane per round
     const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
     const int wave = threadIdx.y * wpr + wr;
-    const int row = blockIdx.x * blockDim.y + threadIdx.y;
+    // Blocks are dealt to the 8 XCDs in turn.  Each XCD takes runs of
+    // 2^lg_run consecutive blocks' rows, so the rows that share the 128-byte
+    // lines of the K-tiled codes (two rows a line) are written through one
+    // L2.  The last partial set of runs keeps its order.
+    int blk = blockIdx.x;
+    {
+        const int span = 8 << lg_run;
+        if (blk < (int)(gridDim.x & ~(unsigned)(span - 1))) {
+            const int c = blk & (span - 1);
+            blk += ((c & 7) << lg_run) + (c >> 3) - c;
+        }
+    }
+    const int row = blk * blockDim.y + threadIdx.y;
     const int team = lane >> 4, tl = lane & 15, sw = tl >> 2;
     const int g0 = wr * 4 * R + team;  // round r works on group g0 + 4 r
     float* T = lds + wave * QT_WAVE + team * QT_TILE;
     float* trow = T + tl * 16;
     uint32_t* red = (uint32_t*)(lds + blockDim.y * wpr * QT_WAVE);
 
-    // Every round's loads first.  Lanes past the row's last group, or in a
-    // row past the last, read valid data of another group and discard it.
+    // Lanes past the row's last group, or in a row past the last, read valid
+    // data of another group and discard it.
     const int64_t xrow = (int64_t)min(row, rows - 1) * ldx + tl * 16;
-    // The SiLU gate's value operand is a second set of the same loads.
-    constexpr int NS = OP == QR_SILU_GATE ? 2 : 1;
-    uint32_t raw[NS][R][NW];
-#pragma unroll
-    for (int h = 0; h < NS; h++)
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int64_t off = xrow + (int64_t)min(g0 + 4 * r, G - 1) * 256 + (h ? pre_op.off2 : 0);
-            const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)x + off) : (const uint4*)((const float*)x + off);
-#pragma unroll
-            for (int i = 0; i < NW / 4; i++) {
-                const uint4 t = src[i];
-                raw[h][r][4 * i] = t.x;
-                raw[h][r][4 * i + 1] = t.y;
-                raw[h][r][4 * i + 2] = t.z;
-                raw[h][r][4 * i + 3] = t.w;
-            }
-        }
+    auto gcol = [&](int r) { return (int64_t)min(g0 + 4 * r, G - 1) * 256; };
 
+    // First pass, every round's loads first.
     float rot[R][16];
     uint32_t amax = 0;
+    bool nonfinite = false;  // an inf or NaN among a live round's values
+    {
+        uint32_t raw[R][qt_ns<OP>][qt_nw<BF16_IN>];
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        float v[16];
+        for (int r = 0; r < R; r++) qt_load<BF16_IN, OP>(x, xrow + gcol(r), pre_op, raw[r]);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            if (BF16_IN) v[i] = __uint_as_float(i & 1 ? raw[0][r][i >> 1] & 0xffff0000u : raw[0][r][i >> 1] << 16);
-            else v[i] = __uint_as_float(raw[0][r][i]);
-        }
-        if (OP == QR_MOD) modulate16(v, pre_op.sc, pre_op.sh, (int64_t)min(g0 + 4 * r, G - 1) * 256 + tl * 16);
-        if (OP == QR_GELU) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) v[i] = gelu_tanh(v[i]);
-        }
-        if (OP == QR_SILU_GATE) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t u = raw[NS - 1][r][BF16_IN ? i >> 1 : i];
-                v[i] = silu_mul(v[i], __uint_as_float(BF16_IN ? (i & 1 ? u & 0xffff0000u : u << 16) : u));
+        for (int r = 0; r < R; r++) {
+            const float f = qt_round<BF16_IN, OP, false>(raw[r], gcol(r) + tl * 16, rotate, pre_op, T, trow, tl, sw, rot[r]);
+            if (g0 + 4 * r < G) {
+                amax = max(amax, qt_amax16(rot[r]));
+                nonfinite |= !__builtin_isfinite(f);
             }
         }
-        if (rotate) {
-            bfly16f<1>(v);
-            bfly16f<4>(v);
-        }
-        // Row tl of the tile, then column tl: w[j] = element 16 j + tl.
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            *(float4*)(trow + 4 * (c ^ sw)) = make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
-        wave_lds_fence();
-        float(&w)[16] = rot[r];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float* col = T + 64 * k + 4 * (sw ^ k) + (tl & 3);
-#pragma unroll
-            for (int i = 0; i < 4; i++) w[4 * k + i] = col[16 * i];
-        }
-        wave_lds_fence();
-        if (rotate) {
-            bfly16f<1>(w);
-            bfly16f<4>(w);
-        }
-        float m = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) m = max3_abs(m, w[j], w[j + 1]);
-        if (g0 + 4 * r < G) amax = max(amax, __float_as_uint(m));
     }
-
-    amax = wave_max_bits(amax);
-    if (wpr > 1) {
-        if (lane == 0) red[wave] = amax;
-        __syncthreads();
-        for (int i = 0; i < wpr; i++) amax = max(amax, red[threadIdx.y * wpr + i]);
-    }
-    // The rotation's final 1/16 is applied to the amax and to inv instead of
-    // to every element.  max |w|/16 rounds to the max of the rounded |w|/16,
-    // so the amax and scale are exact.  When inv/16 is exact (inv >= 2^-122,
-    // i.e. amax below ~2^122 qmax), round(w * (inv/16)) = round((w/16) * inv)
-    // wherever w/16 is exact, and where it is not (|w| < 2^-122) the code is 0
-    // either way (|w| inv/16 < 1e-5).  Otherwise each element is scaled first.
-    const float sixteenth = rotate ? 1.0f / 16.0f : 1.0f;
-    const float rmax = __uint_as_float(amax) * sixteenth;
-    const float scale = rmax > 1e-30f ? rmax / qmax : 1.0f;
-    const float inv = 1.0f / scale;
-    const bool fold = !rotate || inv >= 0x1p-122f;
-    const float pre = fold ? 1.0f : sixteenth, post = fold ? inv * sixteenth : inv;
 
     // The lane's 16 bytes of group g land at qrow + g * gstep: row-major, or
     // K-tiled (256-row strips of h rows; the group's four 64-byte K-steps are
@@ -391,38 +537,91 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
         qrow = q + (int64_t)row * ldq + tl * 16;
         gstep = 256;
     }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        // Column tl back into the tile, row tl out: 16 contiguous elements.
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float* col = T + 64 * k + 4 * (sw ^ k) + (tl & 3);
-#pragma unroll
-            for (int i = 0; i < 4; i++) col[16 * i] = rot[r][4 * k + i];
+
+    // The row's amax (non-negative, so bit 31 is free) travels with a flag
+    // for a non-finite value in bit 31.  A row is fast when its rotated
+    // values are finite and below 2^126: the fma butterflies then give the
+    // reference's values, and the codes need no clamp (pre_half_away_nc).
+    // Other rows are rotated again in the reference's form, one round at a
+    // time, and quantised with the clamp.  Where waves share barriers
+    // (several waves a row), the whole block does so when any of its rows
+    // needs it; a fast row gets the same values and codes that way.
+    amax = wave_max_bits(amax);
+    uint32_t flag = __builtin_amdgcn_ballot_w64(nonfinite) ? 0x80000000u : 0u;
+    bool redo;
+    if (wpr > 1) {
+        if (lane == 0) red[wave] = amax | flag;
+        __syncthreads();
+        for (int i = 0; i < wpr; i++) {
+            const uint32_t e = red[threadIdx.y * wpr + i];
+            amax = max(amax, e & 0x7fffffffu);
+            flag |= e;
         }
-        wave_lds_fence();
-        uint32_t packed[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float4 t = *(const float4*)(trow + 4 * (c ^ sw));
-            float4 u = t;
-            if (!fold) u = make_float4(t.x * pre, t.y * pre, t.z * pre, t.w * pre);  // wave-uniform, rare
-            if (HALF_EVEN)
-                packed[c] = cvt_pack4(pre_half_even(u.x, post, qmax), pre_half_even(u.y, post, qmax),
-                                      pre_half_even(u.z, post, qmax), pre_half_even(u.w, post, qmax));
-            else
-                packed[c] = cvt_pack4(pre_half_away(u.x, post, qmax), pre_half_away(u.y, post, qmax),
-                                      pre_half_away(u.z, post, qmax), pre_half_away(u.w, post, qmax));
+        uint32_t slow = 0;
+        for (int i = 0; i < (int)blockDim.y * wpr; i++) {
+            const uint32_t e = red[i];
+            slow |= (e >> 31) | ((e & 0x7fffffffu) >= 0x7e800000u ? 1u : 0u);
         }
-        wave_lds_fence();
-        if (row < rows && g0 + 4 * r < G)
-            *(uint4*)(qrow + (int64_t)(g0 + 4 * r) * gstep) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        redo = slow != 0;
+    } else {
+        redo = (flag >> 31) != 0 || amax >= 0x7e800000u;
     }
-    if (wr == 0 && lane == 0 && row < rows) s[row] = scale;
+
+    if (__builtin_amdgcn_readfirstlane(rotate && redo)) {
+        // The inputs are loaded again each time: the opaque base keeps the
+        // compiler from holding earlier loads live across the passes.
+        uint32_t a2 = 0;
+#pragma unroll 1
+        for (int r = 0; r < R; r++) {
+            const void* xr = x;
+            asm volatile("" : "+s"(xr));
+            uint32_t raw[qt_ns<OP>][qt_nw<BF16_IN>];
+            qt_load<BF16_IN, OP>(xr, xrow + gcol(r), pre_op, raw);
+            float w[16];
+            qt_round<BF16_IN, OP, true>(raw, gcol(r) + tl * 16, rotate, pre_op, T, trow, tl, sw, w);
+            if (g0 + 4 * r < G) a2 = max(a2, qt_amax16(w));
+        }
+        amax = wave_max_bits(a2);
+        if (wpr > 1) {
+            __syncthreads();  // every wave has read the first pass's entries
+            if (lane == 0) red[wave] = amax;
+            __syncthreads();
+            for (int i = 0; i < wpr; i++) amax = max(amax, red[threadIdx.y * wpr + i]);
+        }
+        const QtScale c = qt_scale(amax, qmax, rotate);
+#pragma unroll 1
+        for (int r = 0; r < R; r++) {
+            const void* xr = x;
+            asm volatile("" : "+s"(xr));
+            uint32_t raw[qt_ns<OP>][qt_nw<BF16_IN>];
+            qt_load<BF16_IN, OP>(xr, xrow + gcol(r), pre_op, raw);
+            float w[16];
+            qt_round<BF16_IN, OP, true>(raw, gcol(r) + tl * 16, rotate, pre_op, T, trow, tl, sw, w);
+            qt_store<HALF_EVEN, false>(w, T, trow, tl, sw, c, qmax, qrow + (int64_t)(g0 + 4 * r) * gstep,
+                                       row < rows && g0 + 4 * r < G);
+        }
+        if (wr == 0 && lane == 0 && row < rows) s[row] = c.scale;
+    } else {
+        // Here every row of the block is fast, or there is no rotation (then
+        // nothing was checked, and the codes are clamped).
+        const QtScale c = qt_scale(amax, qmax, rotate);
+        if (__builtin_amdgcn_readfirstlane(rotate)) {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                qt_store<HALF_EVEN, true>(rot[r], T, trow, tl, sw, c, qmax, qrow + (int64_t)(g0 + 4 * r) * gstep,
+                                          row < rows && g0 + 4 * r < G);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                qt_store<HALF_EVEN, false>(rot[r], T, trow, tl, sw, c, qmax, qrow + (int64_t)(g0 + 4 * r) * gstep,
+                                           row < rows && g0 + 4 * r < G);
+        }
+        if (wr == 0 && lane == 0 && row < rows) s[row] = c.scale;
+    }
 }
 
-// Rounds per wave for G groups.  A large problem is bound by VALU issue, so R
-// minimises instructions per element: ~14.3 per element plus ~90 per wave and
+// Rounds per wave for G groups.  For a large problem R minimises the
+// instructions per element: ~14.3 per element plus ~90 per wave and
 // round-set spread over the 16 R elements a lane holds, times the share of
 // lanes doing live work, with 10 % more for R >= 4 (at most five waves per
 // SIMD).  A small one (under 2^17 groups, about two waves of waves on the
@@ -461,8 +660,12 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
         lds_set = true;
     }
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
+    // Runs of 8 blocks a XCD: config 1's prologue 11.0 -> 10.4 us, config 1
+    // down's 32.3 -> 29.0 us (K-tiled codes; runs of 2 and 4 measured too).
+    const char* env = getenv("PHI_QR_RUN");  // A/B switch: log2 of the run length
+    const int lg_run = env ? atoi(env) : 3;
     hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows, G,
-                       q, ldq, s, qmax, rotate, pre, qkt);
+                       q, ldq, s, qmax, rotate, pre, qkt, lg_run);
     return hipGetLastError();
 }
 

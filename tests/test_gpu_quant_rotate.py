@@ -193,6 +193,45 @@ def test_huge_rows(dev, orc):
             assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
 
 
+def nonfinite_rows(K):
+    """Finite rows beside rows with a NaN, an inf of either sign, both infs,
+    and values that overflow inside the rotation (to inf, or to +inf and -inf
+    that meet as NaN)."""
+    rng = np.random.default_rng(K)
+    x = rng.standard_normal((9, K)).astype(np.float32)
+    x[1, 300] = np.nan
+    x[2, 5] = np.inf
+    x[3, K - 68] = -np.inf
+    x[4, 10], x[4, K - 1] = np.inf, -np.inf
+    x[5, 256:260] = 3e38
+    x[6, 0], x[6, 1] = 3e38, -3e38
+    x[7, :] = np.nan
+    return torch.from_numpy(x)
+
+
+@pytest.mark.parametrize("rounds", [0, 1, 3, 5])
+@pytest.mark.parametrize("K", [768, 3072, 16640])
+def test_nonfinite_rows(dev, orc, monkeypatch, rounds, K):
+    """Rows holding inf or NaN take the clamped path and give the reference's
+    codes (a NaN product is -qmax); the finite rows of the same launch take
+    the unclamped one.  Every rounds-per-wave instance (0: the library's
+    choice), the row kernel past 64 groups, both rounding modes, bf16 and
+    fp32 input, row-major and K-tiled output."""
+    if rounds:
+        monkeypatch.setenv("PHI_QR_ROUNDS", str(rounds))
+    x32 = nonfinite_rows(K)
+    for dtype in (torch.float32, torch.bfloat16):
+        x = x32.to(dtype)
+        for mode in (Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN):
+            q, s, qo, so = run(dev, orc, x, round_mode=mode)
+            assert np.array_equal(q, qo), (dtype, mode, np.argwhere(q != qo)[:5])
+            assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+            if K <= 16384:
+                qk, sk = Q.quant_rotate_kt(x.to(dev), round_mode=mode)
+                assert torch.equal(qk.cpu(), Q.pack_k_tiled(torch.from_numpy(qo).to(dev)).cpu())
+                assert np.array_equal(sk.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
 def test_zero_rows_and_tiny_rows(dev, orc):
     x = torch.zeros((4, 512), dtype=torch.float32)
     x[1, 7] = 1e-31  # amax below 1e-30 -> scale 1

@@ -197,3 +197,40 @@ def test_bf16_activations_match_reference_on_their_fp32_values():
     q, s = O.quantize_rows(b)
     qr, sr = O.ref_quantize(O.bf16_to_f32(b))
     assert np.array_equal(q, qr) and np.array_equal(s.view(np.uint32), sr.view(np.uint32))
+
+
+def nonfinite_rows():
+    """Rows with a NaN, an inf of either sign, both infs, and values that
+    overflow inside the rotation, beside finite rows."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((8, 768)).astype(np.float32)
+    x[1, 300] = np.nan
+    x[2, 5] = np.inf
+    x[3, 700] = -np.inf
+    x[4, 10], x[4, 600] = np.inf, -np.inf
+    x[5, 256:260] = 3e38           # the group's first pass overflows to inf
+    x[6, 0], x[6, 1] = 3e38, -3e38  # +inf and -inf meet in a later pass: NaN, no inf
+    return x
+
+
+def test_nan_products_give_the_most_negative_code():
+    """A NaN product becomes -qmax (the device form's fminf(fmaxf(d, -qmax),
+    qmax)); an inf amax makes every finite value's code 0."""
+    x = nonfinite_rows()
+    for mode in (O.ROUND_HALF_AWAY, O.ROUND_HALF_EVEN):
+        q, s = O.quantize_rows(x, round_mode=mode)
+        y = O.convrot(x)
+        assert np.all(q[1, 256:512] == -127) and np.isfinite(s[1])
+        assert np.isinf(s[2]) and np.isinf(s[3]) and np.isinf(s[4])
+        for r in (2, 3, 4):
+            assert np.array_equal(q[r] == -127, ~np.isfinite(y[r])) and np.all(q[r][np.isfinite(y[r])] == 0)
+        assert np.array_equal(q[0], O.quantize_rows(x[:1], round_mode=mode)[0][0])
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference build (oracle/_ref) absent")
+def test_nonfinite_rows_match_reference_build():
+    x = nonfinite_rows()
+    q, s = O.quantize_rows(x)
+    qr, sr = O.ref_quantize(x)
+    assert np.array_equal(q, qr)
+    assert np.array_equal(s.view(np.uint32), sr.view(np.uint32))
