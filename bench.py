@@ -675,17 +675,17 @@ def bench_prologue_floor(cfg, steps, warmup):
                 raise RuntimeError(f"prologue stream probe failed ({rc})")
         return go
 
-    def prologue(lg_run):
+    def prologue(lg_run=3, rounds=0):
         def go():
             os.environ["PHI_QR_RUN"] = str(lg_run)
+            os.environ["PHI_QR_ROUNDS"] = str(rounds)
             Q.quant_rotate_kt(x, q=q, s=s)
         return go
 
     variants = {
-        "prologue": prologue(3),
+        "prologue": prologue(),
         "prologue_run1": prologue(0),
-        "prologue_run2": prologue(1),
-        "prologue_run4": prologue(2),
+        **{f"prologue_r{r}": prologue(3, r) for r in range(1, 6)},
         "stream_kt": probe(0, 1),
         "stream_kt_run2": probe(0, 1, 2),
         "stream_kt_run4": probe(0, 1, 4),
@@ -695,9 +695,16 @@ def bench_prologue_floor(cfg, steps, warmup):
         "torch_convert": lambda: q2.copy_(x),
     }
     times = {k: [] for k in variants}
+    same = {}
+    variants["prologue"]()
+    torch.cuda.synchronize()
+    q_ref, s_ref = q.clone(), s.clone()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for rnd in range(3):
         for name, fn in variants.items():
+            if name.startswith("prologue"):
+                q.zero_()
+                s.zero_()
             for _ in range(warmup):
                 fn()
             start.record()
@@ -706,13 +713,17 @@ def bench_prologue_floor(cfg, steps, warmup):
             end.record()
             torch.cuda.synchronize()
             times[name].append(start.elapsed_time(end) / steps * 1e3)
+            if name.startswith("prologue"):
+                same[name] = bool(torch.equal(q, q_ref) and torch.equal(s, s_ref)) and same.get(name, True)
+    os.environ.pop("PHI_QR_RUN", None)
+    os.environ.pop("PHI_QR_ROUNDS", None)
     us = {k: statistics.median(v) for k, v in times.items()}
     nbytes = 3.0 * M * K + 4.0 * M
     gbs = nbytes / (us["prologue"] * 1e-6) / 1e9
     return {"value": gbs, "ms": us["prologue"] * 1e-3, "dtype": "bf16", "unit": "GB/s",
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": None},
-            "extra": {"us": {k: round(v, 2) for k, v in us.items()},
+            "extra": {"us": {k: round(v, 2) for k, v in us.items()}, "codes_equal": same,
                       "gbs": {k: round(nbytes / (v * 1e-6) / 1e9, 1) for k, v in us.items()},
                       "rounds_us": {k: [round(t, 2) for t in v] for k, v in times.items()}}}
 

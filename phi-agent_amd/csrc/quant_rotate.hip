@@ -452,7 +452,9 @@ __device__ __forceinline__ void qt_store(const float (&w)[16], float* T, float* 
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         float4 u = *(const float4*)(trow + 4 * (k ^ sw));
-        if (!c.fold) u = make_float4(u.x * c.pre, u.y * c.pre, u.z * c.pre, u.w * c.pre);  // wave-uniform, rare
+        // Wave-uniform and rare; never on a fast row (amax < 2^126 makes
+        // inv >= 2^-122, so the 1/16 is folded).
+        if (!FAST && !c.fold) u = make_float4(u.x * c.pre, u.y * c.pre, u.z * c.pre, u.w * c.pre);
         if (FAST) {
             if (HALF_EVEN)
                 packed[k] = cvt_pack4(pre_half_even_nc(u.x, c.post), pre_half_even_nc(u.y, c.post),
@@ -473,46 +475,22 @@ __device__ __forceinline__ void qt_store(const float (&w)[16], float* T, float* 
     if (live) *(uint4*)dst = make_uint4(packed[0], packed[1], packed[2], packed[3]);
 }
 
+// One row's work after its loads: the rotation of the wave's R rounds, the
+// row amax across the row's waves (red: one word a wave of the block), the
+// reference-form second pass for rows that need it, and the codes and scale.
 template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
-__global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
-                                                           int G, int8_t* __restrict__ q, int64_t ldq,
-                                                           float* __restrict__ s, float qmax, int rotate,
-                                                           QrPre pre_op, int qkt, int lg_run) {
-    extern __shared__ __align__(16) float lds[];
-    const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
-    const int wave = threadIdx.y * wpr + wr;
-    // Blocks are dealt to the 8 XCDs in turn.  Each XCD takes runs of
-    // 2^lg_run consecutive blocks' rows, so the rows that share the 128-byte
-    // lines of the K-tiled codes (two rows a line) are written through one
-    // L2.  The last partial set of runs keeps its order.
-    int blk = blockIdx.x;
-    {
-        const int span = 8 << lg_run;
-        if (blk < (int)(gridDim.x & ~(unsigned)(span - 1))) {
-            const int c = blk & (span - 1);
-            blk += ((c & 7) << lg_run) + (c >> 3) - c;
-        }
-    }
-    const int row = blk * blockDim.y + threadIdx.y;
-    const int team = lane >> 4, tl = lane & 15, sw = tl >> 2;
-    const int g0 = wr * 4 * R + team;  // round r works on group g0 + 4 r
-    float* T = lds + wave * QT_WAVE + team * QT_TILE;
-    float* trow = T + tl * 16;
-    uint32_t* red = (uint32_t*)(lds + blockDim.y * wpr * QT_WAVE);
-
-    // Lanes past the row's last group, or in a row past the last, read valid
-    // data of another group and discard it.
-    const int64_t xrow = (int64_t)min(row, rows - 1) * ldx + tl * 16;
+__device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw<BF16_IN>],
+                                       const void* __restrict__ x, int64_t xrow, int row, int rows, int G,
+                                       int8_t* __restrict__ q, int64_t ldq, float* __restrict__ s, float qmax,
+                                       int rotate, const QrPre& pre_op, int qkt, uint32_t* red, float* T, float* trow,
+                                       int lane, int wr, int wpr, int wave, int g0, int tl, int sw) {
     auto gcol = [&](int r) { return (int64_t)min(g0 + 4 * r, G - 1) * 256; };
 
-    // First pass, every round's loads first.
+    // First pass, on the inputs the caller loaded.
     float rot[R][16];
     uint32_t amax = 0;
     bool nonfinite = false;  // an inf or NaN among a live round's values
     {
-        uint32_t raw[R][qt_ns<OP>][qt_nw<BF16_IN>];
-#pragma unroll
-        for (int r = 0; r < R; r++) qt_load<BF16_IN, OP>(x, xrow + gcol(r), pre_op, raw[r]);
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float f = qt_round<BF16_IN, OP, false>(raw[r], gcol(r) + tl * 16, rotate, pre_op, T, trow, tl, sw, rot[r]);
@@ -550,19 +528,17 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
     uint32_t flag = __builtin_amdgcn_ballot_w64(nonfinite) ? 0x80000000u : 0u;
     bool redo;
     if (wpr > 1) {
+        // Lane l reads wave l's word (at most 16 waves a block; the lanes
+        // past them repeat the last), then one reduction gives the row's
+        // amax and flag, and one ballot whether any row of the block is slow.
         if (lane == 0) red[wave] = amax | flag;
         __syncthreads();
-        for (int i = 0; i < wpr; i++) {
-            const uint32_t e = red[threadIdx.y * wpr + i];
-            amax = max(amax, e & 0x7fffffffu);
-            flag |= e;
-        }
-        uint32_t slow = 0;
-        for (int i = 0; i < (int)blockDim.y * wpr; i++) {
-            const uint32_t e = red[i];
-            slow |= (e >> 31) | ((e & 0x7fffffffu) >= 0x7e800000u ? 1u : 0u);
-        }
-        redo = slow != 0;
+        const int nw = blockDim.y * wpr, first = threadIdx.y * wpr;
+        const uint32_t e = red[min(lane, nw - 1)];
+        const bool mine = lane >= first && lane < first + wpr;
+        amax = wave_max_bits(mine ? e & 0x7fffffffu : 0u);
+        flag = __builtin_amdgcn_ballot_w64(mine && (e >> 31) != 0) ? 0x80000000u : 0u;
+        redo = __builtin_amdgcn_ballot_w64((e >> 31) != 0 || (e & 0x7fffffffu) >= 0x7e800000u) != 0;
     } else {
         redo = (flag >> 31) != 0 || amax >= 0x7e800000u;
     }
@@ -620,6 +596,44 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
     }
 }
 
+template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
+__global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
+                                                           int G, int8_t* __restrict__ q, int64_t ldq,
+                                                           float* __restrict__ s, float qmax, int rotate,
+                                                           QrPre pre_op, int qkt, int lg_run) {
+    extern __shared__ __align__(16) float lds[];
+    const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
+    const int wave = threadIdx.y * wpr + wr;
+    // Blocks are dealt to the 8 XCDs in turn.  Each XCD takes runs of
+    // 2^lg_run consecutive blocks' rows, so the rows that share the 128-byte
+    // lines of the K-tiled codes (two rows a line) are written through one
+    // L2.  The last partial set of runs keeps its order.
+    int blk = blockIdx.x;
+    {
+        const int span = 8 << lg_run;
+        if (blk < (int)(gridDim.x & ~(unsigned)(span - 1))) {
+            const int c = blk & (span - 1);
+            blk += ((c & 7) << lg_run) + (c >> 3) - c;
+        }
+    }
+    const int team = lane >> 4, tl = lane & 15, sw = tl >> 2;
+    const int g0 = wr * 4 * R + team;  // round r works on group g0 + 4 r
+    float* T = lds + wave * QT_WAVE + team * QT_TILE;
+    float* trow = T + tl * 16;
+    uint32_t* red = (uint32_t*)(lds + blockDim.y * wpr * QT_WAVE);
+
+    // Lanes past the row's last group, or in a row past the last, read valid
+    // data of another group and discard it.
+    const int row = blk * blockDim.y + threadIdx.y;
+    const int64_t xr = (int64_t)min(row, rows - 1) * ldx + tl * 16;
+    uint32_t raw[R][qt_ns<OP>][qt_nw<BF16_IN>];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        qt_load<BF16_IN, OP>(x, xr + (int64_t)min(g0 + 4 * r, G - 1) * 256, pre_op, raw[r]);
+    qt_row<BF16_IN, HALF_EVEN, R, OP>(raw, x, xr, row, rows, G, q, ldq, s, qmax, rotate, pre_op, qkt, red, T, trow,
+                                      lane, wr, wpr, wave, g0, tl, sw);
+}
+
 // Rounds per wave for G groups.  For a large problem R minimises the
 // instructions per element: ~14.3 per element plus ~90 per wave and
 // round-set spread over the 16 R elements a lane holds, times the share of
@@ -664,8 +678,8 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
     // down's 32.3 -> 29.0 us (K-tiled codes; runs of 2 and 4 measured too).
     const char* env = getenv("PHI_QR_RUN");  // A/B switch: log2 of the run length
     const int lg_run = env ? atoi(env) : 3;
-    hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows, G,
-                       q, ldq, s, qmax, rotate, pre, qkt, lg_run);
+    hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows,
+                       G, q, ldq, s, qmax, rotate, pre, qkt, lg_run);
     return hipGetLastError();
 }
 
