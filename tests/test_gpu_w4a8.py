@@ -116,7 +116,7 @@ def test_prepare_table_reproduces_expand(dev, orc):
 @pytest.mark.parametrize("kernel", ["auto", "persist256", "persist128", "tile128"])
 @pytest.mark.parametrize("M,N,K,group", [(64, 256, 1024, 128), (300, 520, 3072, 128),
                                          (1, 64, 512, 64), (130, 128, 2048, 256),
-                                         (777, 1032, 768, 128), (4352, 2304, 512, 256)])
+                                         (777, 1032, 768, 128), (4352, 2304, 512, 256), (640, 264, 1280, 128)])
 def test_in_register_linear_equals_expand_then_w8a8(dev, monkeypatch, kernel, with_ws, M, N, K, group):
     """Every W4A8 GEMM (persistent in both tile sizes and their mix, the
     register-staged kernel, and with a workspace the expand-once path for
@@ -138,7 +138,8 @@ def test_in_register_linear_equals_expand_then_w8a8(dev, monkeypatch, kernel, wi
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("M,N,K,group", [(600, 520, 3072, 128), (777, 1032, 768, 128), (4352, 2304, 512, 256)])
+@pytest.mark.parametrize("M,N,K,group", [(600, 520, 3072, 128), (777, 1032, 768, 128), (4352, 2304, 512, 256),
+                                         (640, 264, 1280, 128)])
 def test_expand_once_row_major_switch(dev, monkeypatch, M, N, K, group):
     """The expand-once path (512 rows and more) with its operands row-major (PHI_GEMM_KT=0)
     gives the bits of its K-tiled default and of expand-then-W8A8."""
