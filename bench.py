@@ -138,12 +138,16 @@ def cpu_baseline(cfg) -> dict | None:
     return out
 
 
-def bench_w8a8(cfg, steps, warmup, layout="kt"):
+def bench_w8a8(cfg, steps, warmup, layout="kt", weights="uniform"):
     """One step: rotate + quantise the activations, then the GEMM with the
     dequant + bias epilogue to bf16.  layout "kt": the weight is packed into
     the K-tiled operand layout once, before timing (a load-time step, like
     the checkpoint's quantisation), and the prologue writes q8 K-tiled;
-    "row": row-major operands (the reference's layout)."""
+    "row": row-major operands (the reference's layout).  weights "uniform":
+    int8 codes uniform on [-127, 127] with one scale; "gaussian": the
+    reference benchmark's weights (core/bench/media_bench.cpp:224-231),
+    N(0, 1) values rotated and quantised per row (this library's quantiser,
+    the reference's quantize_weight), with the per-row scales."""
     import torch
 
     import phi_qlinear as Q
@@ -152,8 +156,12 @@ def bench_w8a8(cfg, steps, warmup, layout="kt"):
     dev = torch.device("cuda:0")
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
     x = synth.activations(M, K, seed=0, device=dev)
-    W = synth.int8_weight(N, K, seed=1, device=dev)
-    sW = synth.weight_scale(0.002, device=dev)
+    if weights == "gaussian":
+        g = torch.Generator(device=dev).manual_seed(11)
+        W, sW = Q.quant_rotate(torch.randn((N, K), generator=g, device=dev))
+    else:
+        W = synth.int8_weight(N, K, seed=1, device=dev)
+        sW = synth.weight_scale(0.002, device=dev)
     b = synth.bias(N, seed=2, device=dev)
     q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
     s8 = torch.empty((M,), dtype=torch.float32, device=dev)
@@ -819,6 +827,9 @@ def main() -> int:
     ap.add_argument("--config", default="c1_up", choices=sorted(CONFIGS))
     ap.add_argument("--layout", default="kt", choices=["kt", "row"],
                     help="W8A8 operands: K-tiled (weight packed before timing) or row-major")
+    ap.add_argument("--weights", default="uniform", choices=["uniform", "gaussian"],
+                    help="W8A8 weight codes: uniform int8, or the reference benchmark's rotated, "
+                         "per-row quantised N(0, 1) weights")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
@@ -835,7 +846,7 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     log(f"bench: config {args.config} {cfg}, warmup {args.warmup}, steps {args.steps}")
     if cfg["kind"] == "w8a8":
-        r = bench_w8a8(cfg, args.steps, args.warmup, args.layout)
+        r = bench_w8a8(cfg, args.steps, args.warmup, args.layout, args.weights)
     elif cfg["kind"] == "block":
         r = bench_block(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "w4a8":
@@ -875,10 +886,12 @@ def main() -> int:
         "warmup": args.warmup, "ms_per_step": r["ms"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": r["dtype"],
         "data": "synthetic (seeded: bf16 N(0,1) activations with 0.1% x20 outlier channels, "
-                "int8 U[-127,127] weights, scale 0.002, bf16 N(0,0.02) bias)",
+                + ("N(0,1) weights rotated and quantised per row to int8 with per-row scales "
+                   "(the reference benchmark's weights)" if args.weights == "gaussian"
+                   else "int8 U[-127,127] weights, scale 0.002") + ", bf16 N(0,0.02) bias)",
         "config": {"workload": workload, **{k: v for k, v in cfg.items() if k != "kind"},
-                   **({"operand_layout": "k-tiled" if args.layout == "kt" else "row-major"}
-                      if cfg["kind"] == "w8a8" else {}),
+                   **({"operand_layout": "k-tiled" if args.layout == "kt" else "row-major",
+                       "weights": args.weights} if cfg["kind"] == "w8a8" else {}),
                    "parallelism": "single GPU"},
         "roofline": r["roofline"], "cpu_baseline": cpu,
     }
