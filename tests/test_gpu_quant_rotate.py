@@ -1,7 +1,7 @@
 """GPU parity: rotate + per-token quantise (phi_hip_quant_rotate) vs the oracle.
 
-Bar: int8 codes and fp32 scales bit-exact (reference
-core/host/quant.cpp:109-169)."""
+Bar: int8 codes and fp32 scales bit-exact (reference core/host/quant.cpp:109-169),
+for finite and non-finite rows alike."""
 import numpy as np
 import pytest
 import torch
