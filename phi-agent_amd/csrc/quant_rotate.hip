@@ -197,11 +197,11 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
 // different banks.
 //
 // About fifteen VALU instructions an element against four bytes of HBM
-// traffic (bf16 in, int8 out).  The arithmetic does not overlap the memory
-// traffic well: every wave loads at its start and stores at its end, so the
-// chip runs a load phase, an arithmetic phase and a store phase about 1.6
-// times over (at 4352 x 3072: 10.3 us against 5.7 us for the same loads and
-// stores alone, the prologue stream probe).  Hence few instructions: one
+// traffic (bf16 in, int8 out).  At one round a wave the prologue is bound by
+// VALU issue (at 4352 x 3072 the VALU instructions fill the busy clocks, and
+// the same loads and stores alone take 5.7 us against its 9.7 us); with more
+// rounds a wave there are fewer waves, and it waits on memory instead.
+// Hence few instructions: one
 // fma per butterfly output (exact as sum - 2x while 2x does not overflow),
 // the final 1/16 folded into the scale, the amax as v_max3 over |.|,
 // half-away rounding as add + truncate (pre_half_away) without the clamp on
