@@ -318,14 +318,15 @@ template <int OP> constexpr int qt_ns = OP == QR_SILU_GATE ? 2 : 1;  // input se
 template <bool BF16_IN> constexpr int qt_nw = BF16_IN ? 8 : 16;        // input dwords per lane and set
 
 // One round's inputs: the lane's 16 elements of a group at element offset
-// off, and for the SiLU gate the value operand's 16 at off + off2.
+// off of the row at xr, and for the SiLU gate the value operand's 16 at
+// off + off2.
 template <bool BF16_IN, int OP>
-__device__ __forceinline__ void qt_load(const void* __restrict__ x, int64_t off, const QrPre& pre_op,
+__device__ __forceinline__ void qt_load(const void* __restrict__ xr, int off, const QrPre& pre_op,
                                         uint32_t (&raw)[qt_ns<OP>][qt_nw<BF16_IN>]) {
 #pragma unroll
     for (int h = 0; h < qt_ns<OP>; h++) {
-        const int64_t o = off + (h ? pre_op.off2 : 0);
-        const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)x + o) : (const uint4*)((const float*)x + o);
+        const int o = off + (h ? (int)pre_op.off2 : 0);
+        const uint4* src = BF16_IN ? (const uint4*)((const uint16_t*)xr + o) : (const uint4*)((const float*)xr + o);
 #pragma unroll
         for (int i = 0; i < qt_nw<BF16_IN> / 4; i++) {
             const uint4 t = src[i];
@@ -480,11 +481,11 @@ __device__ __forceinline__ void qt_store(const float (&w)[16], float* T, float* 
 // reference-form second pass for rows that need it, and the codes and scale.
 template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw<BF16_IN>],
-                                       const void* __restrict__ x, int64_t xrow, int row, int rows, int G,
+                                       const void* __restrict__ xr, int row, int rows, int G,
                                        int8_t* __restrict__ q, int64_t ldq, float* __restrict__ s, float qmax,
                                        int rotate, const QrPre& pre_op, int qkt, uint32_t* red, float* T, float* trow,
                                        int lane, int wr, int wpr, int wave, int g0, int tl, int sw) {
-    auto gcol = [&](int r) { return (int64_t)min(g0 + 4 * r, G - 1) * 256; };
+    auto gcol = [&](int r) { return min(g0 + 4 * r, G - 1) * 256; };
 
     // First pass, on the inputs the caller loaded.
     float rot[R][16];
@@ -533,7 +534,7 @@ __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw
         // amax and flag, and one ballot whether any row of the block is slow.
         if (lane == 0) red[wave] = amax | flag;
         __syncthreads();
-        const int nw = blockDim.y * wpr, first = threadIdx.y * wpr;
+        const int nw = blockDim.y * wpr, first = __builtin_amdgcn_readfirstlane(threadIdx.y) * wpr;
         const uint32_t e = red[min(lane, nw - 1)];
         const bool mine = lane >= first && lane < first + wpr;
         amax = wave_max_bits(mine ? e & 0x7fffffffu : 0u);
@@ -549,10 +550,10 @@ __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw
         uint32_t a2 = 0;
 #pragma unroll 1
         for (int r = 0; r < R; r++) {
-            const void* xr = x;
-            asm volatile("" : "+s"(xr));
+            const void* xo = xr;
+            asm volatile("" : "+s"(xo));
             uint32_t raw[qt_ns<OP>][qt_nw<BF16_IN>];
-            qt_load<BF16_IN, OP>(xr, xrow + gcol(r), pre_op, raw);
+            qt_load<BF16_IN, OP>(xo, tl * 16 + gcol(r), pre_op, raw);
             float w[16];
             qt_round<BF16_IN, OP, true>(raw, gcol(r) + tl * 16, rotate, pre_op, T, trow, tl, sw, w);
             if (g0 + 4 * r < G) a2 = max(a2, qt_amax16(w));
@@ -562,15 +563,15 @@ __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw
             __syncthreads();  // every wave has read the first pass's entries
             if (lane == 0) red[wave] = amax;
             __syncthreads();
-            for (int i = 0; i < wpr; i++) amax = max(amax, red[threadIdx.y * wpr + i]);
+            for (int i = 0; i < wpr; i++) amax = max(amax, red[__builtin_amdgcn_readfirstlane(threadIdx.y) * wpr + i]);
         }
         const QtScale c = qt_scale(amax, qmax, rotate);
 #pragma unroll 1
         for (int r = 0; r < R; r++) {
-            const void* xr = x;
-            asm volatile("" : "+s"(xr));
+            const void* xo = xr;
+            asm volatile("" : "+s"(xo));
             uint32_t raw[qt_ns<OP>][qt_nw<BF16_IN>];
-            qt_load<BF16_IN, OP>(xr, xrow + gcol(r), pre_op, raw);
+            qt_load<BF16_IN, OP>(xo, tl * 16 + gcol(r), pre_op, raw);
             float w[16];
             qt_round<BF16_IN, OP, true>(raw, gcol(r) + tl * 16, rotate, pre_op, T, trow, tl, sw, w);
             qt_store<HALF_EVEN, false>(w, T, trow, tl, sw, c, qmax, qrow + (int64_t)(g0 + 4 * r) * gstep,
@@ -602,8 +603,12 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
                                                            float* __restrict__ s, float qmax, int rotate,
                                                            QrPre pre_op, int qkt, int lg_run) {
     extern __shared__ __align__(16) float lds[];
-    const int lane = threadIdx.x & 63, wr = threadIdx.x >> 6, wpr = blockDim.x >> 6;
-    const int wave = threadIdx.y * wpr + wr;
+    // The wave's index in its row and its row within the block are the same
+    // for all its lanes; read as such, the row's address arithmetic runs on
+    // the scalar unit instead of as 64-bit VALU work in every wave.
+    const int lane = threadIdx.x & 63, wpr = blockDim.x >> 6;
+    const int wr = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), ty = __builtin_amdgcn_readfirstlane(threadIdx.y);
+    const int wave = ty * wpr + wr;
     // Blocks are dealt to the 8 XCDs in turn.  Each XCD takes runs of
     // 2^lg_run consecutive blocks' rows, so the rows that share the 128-byte
     // lines of the K-tiled codes (two rows a line) are written through one
@@ -624,14 +629,14 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
 
     // Lanes past the row's last group, or in a row past the last, read valid
     // data of another group and discard it.
-    const int row = blk * blockDim.y + threadIdx.y;
-    const int64_t xr = (int64_t)min(row, rows - 1) * ldx + tl * 16;
+    const int row = blk * blockDim.y + ty;
+    const int64_t roff = (int64_t)min(row, rows - 1) * ldx;
+    const void* xr = BF16_IN ? (const void*)((const uint16_t*)x + roff) : (const void*)((const float*)x + roff);
     uint32_t raw[R][qt_ns<OP>][qt_nw<BF16_IN>];
 #pragma unroll
-    for (int r = 0; r < R; r++)
-        qt_load<BF16_IN, OP>(x, xr + (int64_t)min(g0 + 4 * r, G - 1) * 256, pre_op, raw[r]);
-    qt_row<BF16_IN, HALF_EVEN, R, OP>(raw, x, xr, row, rows, G, q, ldq, s, qmax, rotate, pre_op, qkt, red, T, trow,
-                                      lane, wr, wpr, wave, g0, tl, sw);
+    for (int r = 0; r < R; r++) qt_load<BF16_IN, OP>(xr, tl * 16 + min(g0 + 4 * r, G - 1) * 256, pre_op, raw[r]);
+    qt_row<BF16_IN, HALF_EVEN, R, OP>(raw, xr, row, rows, G, q, ldq, s, qmax, rotate, pre_op, qkt, red, T, trow, lane,
+                                      wr, wpr, wave, g0, tl, sw);
 }
 
 // Rounds per wave for G groups.  For a large problem R minimises the
