@@ -22,6 +22,9 @@
 //                   and launch shape without its arithmetic (and, in mode 1,
 //                   with its LDS round trips and barrier): the floor the
 //                   prologue is measured against.
+//   phi_probe_qt_scale  the prologue's exact scale divisions (qt_scale.hpp:
+//                   rmax / qmax, and 1 / scale from v_rcp_f32) on each lane's
+//                   own value, for the tests that hold them to IEEE division.
 //   phi_probe_tile_trace  the persistent pipeline (i8_gemm_pipe.hip, compiled
 //                   here a second time into namespace phi_dev_trace with its
 //                   timeline hooks defined) with one record of stamps per
@@ -68,6 +71,7 @@ __device__ unsigned long long* phi_trace_out;
 #define phi_dev phi_dev_trace
 #include "i8_gemm_pipe.hip"
 #undef phi_dev
+#include "qt_scale.hpp"
 
 namespace {
 
@@ -265,7 +269,26 @@ __global__ __launch_bounds__(1024) void prologue_stream_probe(const uint16_t* x,
 
 }  // namespace
 
+// Mode 0: out = rmax / qmax by qt_div_qmax; mode 1: out = 1 / b by
+// qt_rcp_bits, each lane on its own value.
+__global__ __launch_bounds__(256) void qt_scale_probe(const float* in, int n, int mode, float qmax, float qrcp,
+                                                      float* out) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float v = in[i];
+    out[i] = mode == 0 ? phi_dev::qt_div_qmax(v, qmax, qrcp) : phi_dev::qt_rcp_bits(v, __float_as_uint(v));
+}
+
 extern "C" {
+
+// The prologue's scale divisions over in[0, n) into out (see qt_scale_probe);
+// qmax an integer in [1, 127] for mode 0.
+int phi_probe_qt_scale(void* stream, const float* in, int n, int mode, float qmax, float* out) {
+    if (n <= 0 || !in || !out || (mode != 0 && mode != 1)) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(qt_scale_probe, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, in, n,
+                       mode, qmax, 1.0f / qmax, out);
+    return (int)hipGetLastError();
+}
 
 // The prologue stream probe over x [rows, 256 G] bf16 into q (rows x 256 G
 // bytes) and s [rows]; G <= 64; run as in prologue_stream_probe.

@@ -32,6 +32,7 @@
 
 #include "device_common.hpp"
 #include "i8_gemm.hpp"
+#include "qt_scale.hpp"
 
 namespace phi_dev {
 
@@ -413,29 +414,6 @@ __device__ __forceinline__ uint32_t qt_amax16(const float (&w)[16]) {
     return __float_as_uint(m);
 }
 
-// The row scale and the factors the codes use.  The rotation's final 1/16 is
-// applied to the amax and to inv instead of to every element.  max |w|/16
-// rounds to the max of the rounded |w|/16, so the amax and scale are exact.
-// When inv/16 is exact (inv >= 2^-122, i.e. amax below ~2^122 qmax),
-// round(w * (inv/16)) = round((w/16) * inv) wherever w/16 is exact, and where
-// it is not (|w| < 2^-122) the code is 0 either way (|w| inv/16 < 1e-5).
-// Otherwise (fold false) each element is scaled by pre = 1/16 first.
-struct QtScale {
-    float scale, pre, post;
-    bool fold;
-};
-__device__ __forceinline__ QtScale qt_scale(uint32_t amax, float qmax, int rotate) {
-    const float sixteenth = rotate ? 1.0f / 16.0f : 1.0f;
-    const float rmax = __uint_as_float(amax) * sixteenth;
-    QtScale c;
-    c.scale = rmax > 1e-30f ? rmax / qmax : 1.0f;
-    const float inv = 1.0f / c.scale;
-    c.fold = !rotate || inv >= 0x1p-122f;
-    c.pre = c.fold ? 1.0f : sixteenth;
-    c.post = c.fold ? inv * sixteenth : inv;
-    return c;
-}
-
 // One round's codes: column tl back into the tile, row tl out (16 contiguous
 // elements), quantised and stored as one 16-byte write when live.  FAST
 // leaves out the clamp (pre_half_away_nc).
@@ -483,7 +461,8 @@ template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw<BF16_IN>],
                                        const void* __restrict__ xr, int row, int rows, int G,
                                        int8_t* __restrict__ q, int64_t ldq, float* __restrict__ s, float qmax,
-                                       int rotate, const QrPre& pre_op, int qkt, uint32_t* red, float* T, float* trow,
+                                       float qrcp, int rotate, const QrPre& pre_op, int qkt, uint32_t* red, float* T,
+                                       float* trow,
                                        int lane, int wr, int wpr, int wave, int g0, int tl, int sw) {
     auto gcol = [&](int r) { return min(g0 + 4 * r, G - 1) * 256; };
 
@@ -581,27 +560,29 @@ __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw
     } else {
         // Here every row of the block is fast, or there is no rotation (then
         // nothing was checked, and the codes are clamped).
-        const QtScale c = qt_scale(amax, qmax, rotate);
         if (__builtin_amdgcn_readfirstlane(rotate)) {
+            const QtScale c = qt_scale_fast(amax, qmax, qrcp);
 #pragma unroll
             for (int r = 0; r < R; r++)
                 qt_store<HALF_EVEN, true>(rot[r], T, trow, tl, sw, c, qmax, qrow + (int64_t)(g0 + 4 * r) * gstep,
                                           row < rows && g0 + 4 * r < G);
+            if (wr == 0 && lane == 0 && row < rows) s[row] = c.scale;
         } else {
+            const QtScale c = qt_scale(amax, qmax, rotate);
 #pragma unroll
             for (int r = 0; r < R; r++)
                 qt_store<HALF_EVEN, false>(rot[r], T, trow, tl, sw, c, qmax, qrow + (int64_t)(g0 + 4 * r) * gstep,
                                            row < rows && g0 + 4 * r < G);
+            if (wr == 0 && lane == 0 && row < rows) s[row] = c.scale;
         }
-        if (wr == 0 && lane == 0 && row < rows) s[row] = c.scale;
     }
 }
 
 template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
                                                            int G, int8_t* __restrict__ q, int64_t ldq,
-                                                           float* __restrict__ s, float qmax, int rotate,
-                                                           QrPre pre_op, int qkt, int lg_run) {
+                                                           float* __restrict__ s, float qmax, float qrcp,
+                                                           int rotate, QrPre pre_op, int qkt, int lg_run) {
     extern __shared__ __align__(16) float lds[];
     // The wave's index in its row and its row within the block are the same
     // for all its lanes; read as such, the row's address arithmetic runs on
@@ -635,8 +616,8 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
     uint32_t raw[R][qt_ns<OP>][qt_nw<BF16_IN>];
 #pragma unroll
     for (int r = 0; r < R; r++) qt_load<BF16_IN, OP>(xr, tl * 16 + min(g0 + 4 * r, G - 1) * 256, pre_op, raw[r]);
-    qt_row<BF16_IN, HALF_EVEN, R, OP>(raw, xr, row, rows, G, q, ldq, s, qmax, rotate, pre_op, qkt, red, T, trow, lane,
-                                      wr, wpr, wave, g0, tl, sw);
+    qt_row<BF16_IN, HALF_EVEN, R, OP>(raw, xr, row, rows, G, q, ldq, s, qmax, qrcp, rotate, pre_op, qkt, red, T, trow,
+                                      lane, wr, wpr, wave, g0, tl, sw);
 }
 
 // Rounds per wave for G groups.  For a large problem R minimises the
@@ -684,7 +665,7 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
     const char* env = getenv("PHI_QR_RUN");  // A/B switch: log2 of the run length
     const int lg_run = env ? atoi(env) : 3;
     hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows,
-                       G, q, ldq, s, qmax, rotate, pre, qkt, lg_run);
+                       G, q, ldq, s, qmax, 1.0f / qmax, rotate, pre, qkt, lg_run);
     return hipGetLastError();
 }
 

@@ -2,6 +2,8 @@
 
 Bar: int8 codes and fp32 scales bit-exact (reference core/host/quant.cpp:109-169),
 for finite and non-finite rows alike."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -261,3 +263,52 @@ def test_contract_errors(dev):
         Q.quant_rotate(torch.zeros((2, 300), device=dev))
     with pytest.raises(Q.QLinearError, match="exceeds"):
         Q.quant_rotate(torch.zeros((1, 24576 + 256), device=dev))
+
+
+def _all_significands(exp: int) -> np.ndarray:
+    return ((np.arange(1 << 23, dtype=np.uint32)) | np.uint32((127 + exp) << 23)).view(np.float32)
+
+
+def test_scale_divisions_on_device(dev):
+    """The fast row-scale divisions (csrc/qt_scale.hpp) on the GPU, every
+    significand at the ends of their ranges and at 1, against IEEE division
+    (numpy's float32 divide): rmax / qmax from the rounded 1/qmax with one fma
+    correction, and 1 / scale from v_rcp_f32's estimate with two Newton steps
+    (the all-ones significand fixed).  The estimate is the hardware's own; the
+    CPU check (test_host_logic.py) covers any estimate within 2 ulps."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(Q.LIB_PATH), "libphi_probe.so"))
+    f = lib.phi_probe_qt_scale
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
+    st = torch.cuda.current_stream().cuda_stream
+    for mode, exps, qmaxes in ((0, (-90, 0, 121), (127.0, 7.0, 1.0, 100.0)), (1, (-97, 0, 121), (127.0,))):
+        for e in exps:
+            a = _all_significands(e)
+            x = torch.from_numpy(a).to(dev)
+            out = torch.empty_like(x)
+            for qm in qmaxes:
+                assert f(st, x.data_ptr(), a.size, mode, qm, out.data_ptr()) == 0
+                torch.cuda.synchronize()
+                want = a / np.float32(qm) if mode == 0 else np.float32(1.0) / a
+                got = out.cpu().numpy()
+                bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+                assert bad.size == 0, f"mode {mode} exp {e} qmax {qm}: {bad.size} mismatches, first b={a[bad[0]]!r}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("round_mode", [Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN])
+def test_row_scales_across_the_division_ranges(dev, orc, dtype, round_mode):
+    """Rows whose amax spans the fast divisions' range and its edges: rotated
+    amax around 2^-86 (below it the kernel divides as IEEE does), near the
+    1e-30 scale floor, ordinary, and up to just under 2^126 (the fast-row
+    limit).  Codes and scales bit-exact against the oracle."""
+    x = synth.activations(24, 3072, seed=7, dtype=torch.float32)
+    exps = [-120, -100, -90, -88, -87, -86, -85, -84, -80, -40, -5, 0, 3, 20, 60, 100, 110, 118, 119, 120, 121, 122,
+            -99, -98]
+    for i, e in enumerate(exps):
+        x[i] *= float(2.0 ** e)
+    x = x.to(dtype)
+    q, s, qo, so = run(dev, orc, x, round_mode=round_mode)
+    assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"

@@ -76,3 +76,17 @@ def test_tile_order_division_by_multiplier():
         q = n if d == 1 else (n * m) >> np.uint64(32)
         q = np.where(q * d > n, q - np.uint64(1), q)
         assert np.array_equal(q, n // d), int(d)
+
+
+def test_prologue_scale_divisions_equal_ieee_division():
+    """The prologue's fast scale divisions (phi-agent_amd/csrc/qt_scale.hpp):
+    rmax / qmax from the rounded 1/qmax with one fma correction, and 1 / scale
+    by two Newton steps from an estimate, equal IEEE division for every
+    significand and every integer qmax in [1, 127] (tests/cpp/scale_exact.c,
+    checked against C's own division).  The GPU side, with v_rcp_f32 as the
+    estimate, is test_gpu_quant_rotate.py::test_scale_divisions_on_device."""
+    cdir = os.path.join(ROOT, "tests", "cpp")
+    subprocess.run(["make", "-C", cdir, "scale_exact"], check=True, capture_output=True)
+    out = subprocess.run([os.path.join(cdir, "scale_exact")], capture_output=True, text=True, timeout=600)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "div_qmax_mismatches 0 rcp_mismatches 0 all_ones_mismatches 0" in out.stdout
