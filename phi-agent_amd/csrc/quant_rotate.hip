@@ -199,16 +199,17 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
 //
 // About fifteen VALU instructions an element against four bytes of HBM
 // traffic (bf16 in, int8 out).  At one round a wave the prologue is bound by
-// VALU issue (at 4352 x 3072 the VALU instructions fill the busy clocks, and
-// the same loads and stores alone take 5.7 us against its 9.7 us); with more
-// rounds a wave there are fewer waves, and it waits on memory instead.
-// Hence few instructions: one
-// fma per butterfly output (exact as sum - 2x while 2x does not overflow),
-// the final 1/16 folded into the scale, the amax as v_max3 over |.|,
-// half-away rounding as add + truncate (pre_half_away) without the clamp on
-// rows that cannot need it, and the bytes packed by the conversions
-// themselves (cvt_pack4).  R > 1 spreads the per-wave costs (addresses,
-// scale division, reductions) over more elements.
+// VALU issue (at 4352 x 3072 the VALU instructions fill 0.9 of the busy
+// clocks, and the same loads and stores alone take 5.7 us against its
+// 9.6 us); with more rounds a wave there are fewer waves, and it waits on
+// memory instead.  Hence few instructions: one fma per butterfly output
+// (exact as sum - 2x while 2x does not overflow), the final 1/16 folded into
+// the scale, the amax as v_max3 over |.|, half-away rounding as add +
+// truncate (pre_half_away) without the clamp on rows that cannot need it,
+// the bytes packed by the conversions themselves (cvt_pack4), the row's
+// address arithmetic on the scalar unit, and the scale's two divisions in
+// nine instructions (qt_scale_fast).  R > 1 spreads the per-wave costs
+// (addresses, scale divisions, reductions) over more elements.
 constexpr int QT_TILE = 272;
 constexpr int QT_WAVE = 4 * QT_TILE;
 constexpr int QT_MAX_ROUNDS = 5;
