@@ -5,6 +5,7 @@ files are written with the safetensors library (independent of this code)."""
 import json
 import os
 import struct
+import subprocess
 
 import numpy as np
 import pytest
@@ -222,3 +223,54 @@ def test_lora_key_conventions(tmp_path):
     empty = C.lora_file(str(tmp_path / "none.safetensors"), {"x.weight": torch.zeros(2)})
     out = C.run("lora_probe", "t", 1, 1, "lora", empty, 1.0, check=False)
     assert out.returncode == 3 and "holds no A/B factor pairs" in out.stdout
+
+
+def test_mutated_headers_under_sanitizers(tmp_path):
+    """Bounded mutation fuzz of the header parser and layout rules: 300
+    seeded corruptions of a valid two-family checkpoint (bytes flipped,
+    JSON tokens and huge or negative numbers spliced in, spans deleted, the
+    length field and the data section cut or overstated), each probed with
+    st_tool built under AddressSanitizer and UndefinedBehaviorSanitizer.
+    Every run ends with a result or a refusal (exit 0 or 3), and the
+    sanitizers report nothing."""
+    cdir = os.path.join(C.ROOT, "tests", "cpp")
+    mk = subprocess.run(["make", "-C", cdir, "st_tool_asan"], capture_output=True, text=True)
+    if mk.returncode != 0:
+        pytest.skip("sanitizer build unavailable: " + mk.stderr[-200:])
+    exe = os.path.join(cdir, "st_tool_asan")
+    g = torch.Generator().manual_seed(9)
+    base = C.write(str(tmp_path / "base.safetensors"), {
+        "a.weight": torch.randint(-127, 128, (64, 256), generator=g, dtype=torch.int8),
+        "a.weight_scale": torch.rand(64, generator=g),
+        "a.comfy_quant": C.comfy_blob({"format": "int8_tensorwise"}),
+        "b.weight": torch.randint(0, 255, (64, 128), generator=g, dtype=torch.uint8),
+        "b.weight_scale": torch.rand(64, 2, generator=g).half(),
+        "b.comfy_quant": C.comfy_blob({"format": "asym_w4a8_int8", "group_size": 128}),
+    })
+    raw = open(base, "rb").read()
+    hlen = struct.unpack("<Q", raw[:8])[0]
+    hdr, body = raw[8:8 + hlen], raw[8 + hlen:]
+    tokens = [b'"', b"{", b"}", b"[", b"]", b",", b":", b"-1", b"99999999999999999999", b"18446744073709551615",
+              b'"I4"', b'"F8_E4M3"', b'"float8_e4m3fn"', b"null", b"\\u0000", b"1e999", b'"data_offsets"',
+              b'"shape"', b'"dtype"', b"0", b"4294967296"]
+    rng = np.random.default_rng(17)
+    logs = str(tmp_path / "san")
+    env = dict(os.environ, ASAN_OPTIONS=f"detect_leaks=0:log_path={logs}",
+               UBSAN_OPTIONS=f"print_stacktrace=1:log_path={logs}")
+    p = tmp_path / "m.safetensors"
+    for it in range(300):
+        h = bytearray(hdr)
+        for _ in range(int(rng.integers(1, 7))):
+            pos, op = int(rng.integers(len(h))), rng.random()
+            if op < 0.4:
+                h[pos] = int(rng.integers(256))
+            elif op < 0.8:
+                h[pos:pos] = tokens[int(rng.integers(len(tokens)))]
+            else:
+                del h[pos:pos + int(rng.integers(1, 9))]
+        b = body if rng.random() < 0.8 else body[:int(rng.integers(len(body) + 1))]
+        n = len(h) if rng.random() < 0.9 else [0, 1, len(h) + 5, 2 ** 40, 2 ** 64 - 1][int(rng.integers(5))]
+        p.write_bytes(struct.pack("<Q", n) + bytes(h) + b)
+        out = subprocess.run([exe, "probe", str(p), "ab"[it % 2]], capture_output=True, env=env, timeout=60)
+        reports = [f for f in os.listdir(tmp_path) if f.startswith("san")]
+        assert out.returncode in (0, 3) and not reports, (it, out.returncode, out.stdout[-300:], reports)
