@@ -12,6 +12,9 @@
 //                             wave uses a K-step's fragments (each 4 times),
 //                             rotated by a cheap XOR every K-step so the
 //                             operands change as they do when read from LDS
+//                     mode 3  mode 2 with the A fragments walked in snake
+//                             order (one operand changes between MFMAs)
+//                     mode 4  mode 2 with the two operands' roles swapped
 //   phi_probe_lds_dma  every wave streams 16 rows x 64 bytes per instruction
 //                   from a window of global memory into LDS, 4 K-steps of the
 //                   headline tile's A and B in flight, with no MFMAs.
@@ -102,9 +105,14 @@ __global__ __launch_bounds__(256) void mfma_probe(const int8_t* ops, int iters, 
 #pragma unroll
         for (int s = 0; s < 2; s++)
 #pragma unroll
-            for (int q = 0; q < 16; q++)
-                acc[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[(q >> 2) + 4 * s], a[(q & 3) + 4 * s], acc[q], 0, 0, 0);
-        if (MODE == 2) {
+            for (int q = 0; q < 16; q++) {
+                const int jb = q >> 2, ia = MODE == 3 && (jb & 1) ? 3 - (q & 3) : q & 3;
+                if (MODE == 4)
+                    acc[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ia + 4 * s], b[jb + 4 * s], acc[q], 0, 0, 0);
+                else
+                    acc[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[jb + 4 * s], a[ia + 4 * s], acc[q], 0, 0, 0);
+            }
+        if (MODE >= 2) {
             const int x = 0x5a3c96e1 * (it + 1) + lane;
 #pragma unroll
             for (int f = 0; f < 8; f++) {
@@ -317,6 +325,8 @@ int phi_probe_mfma(void* stream, const int8_t* ops, int mode, int iters, int* si
     switch (mode) {
         case 0: hipLaunchKernelGGL(mfma_probe<0>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         case 1: hipLaunchKernelGGL(mfma_probe<1>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
+        case 3: hipLaunchKernelGGL(mfma_probe<3>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
+        case 4: hipLaunchKernelGGL(mfma_probe<4>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         default: hipLaunchKernelGGL(mfma_probe<2>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
     }
     return (int)hipGetLastError();
