@@ -683,11 +683,23 @@ def bench_prologue_floor(cfg, steps, warmup):
                 raise RuntimeError(f"prologue stream probe failed ({rc})")
         return go
 
+    # The prologue variants call the C ABI directly, with the A/B switches set
+    # once per variant (setup), so that the host keeps ahead of ~10 us
+    # launches: under a kernel tracer, where host calls are slower, the launches
+    # sit ~20 us apart while each runs ~10 us.
+    qlib = Q.load()
+
     def prologue(lg_run=3, rounds=0):
         def go():
+            rc = qlib.phi_hip_quant_rotate_kt(stream, x.data_ptr(), Q.BF16, M, K, K, q.data_ptr(), s.data_ptr(),
+                                              127.0, Q.ROUND_HALF_AWAY)
+            if rc != 0:
+                raise RuntimeError(f"quant_rotate_kt failed ({rc})")
+
+        def setup():
             os.environ["PHI_QR_RUN"] = str(lg_run)
             os.environ["PHI_QR_ROUNDS"] = str(rounds)
-            Q.quant_rotate_kt(x, q=q, s=s)
+        go.setup = setup
         return go
 
     variants = {
@@ -704,6 +716,7 @@ def bench_prologue_floor(cfg, steps, warmup):
     }
     times = {k: [] for k in variants}
     same = {}
+    variants["prologue"].setup()
     variants["prologue"]()
     torch.cuda.synchronize()
     q_ref, s_ref = q.clone(), s.clone()
@@ -713,6 +726,16 @@ def bench_prologue_floor(cfg, steps, warmup):
             if name.startswith("prologue"):
                 q.zero_()
                 s.zero_()
+                fn.setup()
+            if name == "prologue":
+                # The round's first prologue variant follows lighter kernels
+                # (the stream probes, torch's copy).  A kernel trace shows the
+                # board's clock transient there: launches 1-50 fast, then
+                # 25 % slower, recovering over some hundreds of launches.
+                # Without 1000 untimed launches first, this variant measured
+                # 6-8 % slower than the identical forced-R variant after it.
+                for _ in range(max(3 * warmup, 1000)):
+                    fn()
             for _ in range(warmup):
                 fn()
             start.record()
