@@ -594,6 +594,9 @@ def bench_tiletrace(cfg, steps, warmup):
         "workgroup_cycles": {"mean": mean(cycles), "max": max(cycles)},
         "shader_clock_ghz": mean(clock),
         "first_tile_start_us": mean(first),
+        "workgroup_start_us": {"min": min(us(w[24]) for w in used), "mean": mean([us(w[24]) for w in used]),
+                               "max": max(us(w[24]) for w in used)},
+        "workgroup_setup_us": mean([(w[0] if w[0] else w[26]) / 100.0 - w[24] / 100.0 for w in used if w[0] or w[26]]),
         "big_phase_end_us": {"min": min(bigdone), "mean": mean(bigdone), "max": max(bigdone)} if bigdone else None,
         "kernel_end_us": {"min": min(ends), "mean": mean(ends), "max": max(ends)},
         "big_phase_end_by_xcd_us": {str(k): round(mean(v), 2) for k, v in sorted(per_xcd.items())},
