@@ -150,30 +150,34 @@ def test_every_near_tie_unrotated(dev, orc, round_mode, inv_pow):
 
 
 @pytest.mark.parametrize("round_mode", [Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN])
-def test_every_near_tie_through_the_rotation(dev, orc, round_mode):
+@pytest.mark.parametrize("groups", [96, 64, 12])
+def test_every_near_tie_through_the_rotation(dev, orc, round_mode, groups):
     """The near-tie set through the rotation and the folded inv/16.  A 256-group
     holding one non-zero c at position p rotates to +-c in every element, times
     1/16, with no rounding; with c = 16 t the group's values are exactly +-t.
     One group per row holds 16 * 127, so amax = 127, scale = 1 and the kernel's
-    folded multiplier is 1/16: every code is the rounding of +-t."""
+    folded multiplier is 1/16: every code is the rounding of +-t.  96 groups a
+    row run the row kernel; 64 and 12 the register-resident kernel's fast rows
+    (its exact scale divisions and unclamped codes), with 16 and 3 waves
+    sharing a row (12 groups is config 1's K)."""
     v = near_ties()
-    per_row = 95  # groups left in a 96-group (K = 24576) row after the amax group
+    per_row = groups - 1  # groups left in a row after the amax group
     rows = (v.size + per_row - 1) // per_row
-    K = 96 * 256
+    K = groups * 256
     x = np.zeros((rows, K), np.float32)
     want = np.zeros((rows, per_row), np.float32)
     for i, t in enumerate(v):
         r, g = divmod(i, per_row)
         x[r, g * 256 + (i * 37) % 256] = np.float32(16.0) * t
         want[r, g] = t
-    x[:, 95 * 256 + 5] = np.float32(16.0 * 127.0)
+    x[:, per_row * 256 + 5] = np.float32(16.0 * 127.0)
     q, s, qo, so = run(dev, orc, torch.from_numpy(x), round_mode=round_mode)
     assert np.array_equal(s.view(np.uint32), so.view(np.uint32))
     assert np.all(s == 1.0)
     assert np.array_equal(q, qo), f"{(q != qo).sum()} code mismatches"
     if round_mode == Q.ROUND_HALF_AWAY:
         # Each group's codes are +-round(t); the sign pattern is the column's.
-        mag = np.abs(q[:, :95 * 256].reshape(rows, 95, 256).astype(np.int16))
+        mag = np.abs(q[:, :per_row * 256].reshape(rows, per_row, 256).astype(np.int16))
         n = v.size
         got = mag.max(axis=2).reshape(-1)[:n]
         assert np.array_equal(got, np.abs(half_away(want.reshape(-1)[:n])).astype(np.int16))
