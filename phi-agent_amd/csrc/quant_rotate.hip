@@ -201,7 +201,7 @@ __global__ __launch_bounds__(1024) void quant_rotate_rows(const void* __restrict
 // traffic (bf16 in, int8 out).  At one round a wave the prologue is bound by
 // VALU issue (at 4352 x 3072 the VALU instructions fill 0.9 of the busy
 // clocks, and the same loads and stores alone take 5.7 us against its
-// 9.6 us); with more rounds a wave there are fewer waves, and it waits on
+// 9.2 us); with more rounds a wave there are fewer waves, and it waits on
 // memory instead.  Hence few instructions: one fma per butterfly output
 // (exact as sum - 2x while 2x does not overflow), the final 1/16 folded into
 // the scale, the amax as v_max3 over |.|, half-away rounding as add +
