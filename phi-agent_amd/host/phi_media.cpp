@@ -9,6 +9,10 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <mutex>
+#include <optional>
+#include <string_view>
+#include <unordered_map>
 #include <vector>
 
 namespace phi::media {
@@ -211,19 +215,125 @@ void GpuCtx::new_step() {
     if (aa) aa->reset();
 }
 
+// ---------------------------------------------------------------- VRAM accountant
+
+struct VramBudget::State {
+    mutable std::mutex m;
+    u64 local = 0, peak = 0;
+    u64 forced = 0;  // set_limit()
+    mutable u64 derived = 0;
+};
+
+VramBudget& VramBudget::instance() {
+    static VramBudget b;
+    return b;
+}
+
+VramBudget::State& VramBudget::state() const {
+    static State s;
+    return s;
+}
+
+static std::string mib_text(u64 bytes) { return std::to_string((bytes + (1ull << 19)) >> 20) + " MiB"; }
+
+u64 VramBudget::derived_limit() const {
+    constexpr u64 kMiB = 1ull << 20, kMinReserve = 384 * kMiB, kMaxReserve = 2048 * kMiB, kEnvReserve = 256 * kMiB;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) total_b = 0;
+    const u64 total = total_b;
+    if (const char* e = std::getenv("PHI_VRAM_BUDGET_MB")) {
+        const long long mb = std::atoll(e);
+        if (mb >= 256) {
+            u64 want = (u64)mb * kMiB;
+            if (total) want = std::min(want, total > kEnvReserve ? total - kEnvReserve : 0);
+            return want;
+        }
+    }
+    if (!total) return 0;  // no device answer: no ceiling of our own
+    const u64 reserve = std::clamp(total / 16, kMinReserve, kMaxReserve);
+    return total > reserve ? total - reserve : 0;
+}
+
+u64 VramBudget::limit() const {
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    if (s.forced) return s.forced;
+    if (!s.derived) s.derived = derived_limit();
+    return s.derived;
+}
+
+void VramBudget::set_limit(u64 bytes) {
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    s.forced = bytes;
+    s.derived = 0;
+}
+
+bool VramBudget::would_exceed(u64 bytes) const {
+    const u64 lim = limit();
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    return lim != 0 && (bytes > lim || s.local > lim - bytes);
+}
+
+void VramBudget::charge(u64 bytes, const char* tag) {
+    if (bytes == 0) return;
+    const u64 lim = limit();
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    if (lim != 0 && (bytes > lim || s.local > lim - bytes))
+        throw MediaError("VRAM budget exceeded: requesting " + mib_text(bytes) + " for " + (tag ? tag : "allocation") +
+                         " would take resident " + mib_text(s.local + bytes) + " past the limit " + mib_text(lim));
+    s.local += bytes;
+    s.peak = std::max(s.peak, s.local);
+}
+
+void VramBudget::release(u64 bytes) {
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    s.local = s.local > bytes ? s.local - bytes : 0;
+}
+
+u64 VramBudget::local() const {
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    return s.local;
+}
+
+u64 VramBudget::peak() const {
+    State& s = state();
+    std::lock_guard<std::mutex> lk(s.m);
+    return s.peak;
+}
+
 // ---------------------------------------------------------------- GpuArena
 
 GpuArena::GpuArena(ComputeContext& ctx, u64 bytes) {
     init(&ctx, bytes);
-    chunks_.push_back(ctx.create_device_buffer(bytes));
-    capacity_ = bytes;
+    chunks_.push_back(grow(bytes));
 }
 
 GpuArena::~GpuArena() { release_chunks(); }
 
-void GpuArena::init(ComputeContext* ctx, u64 chunk_bytes) {
+void GpuArena::init(ComputeContext* ctx, u64 chunk_bytes, const char* tag) {
     ctx_ = ctx;
     if (chunk_bytes) chunk_bytes_ = chunk_bytes;
+    if (tag) tag_ = tag;
+}
+
+// A new chunk, charged to the accountant before the device allocation; a
+// refused charge allocates nothing.
+GpuBuffer* GpuArena::grow(u64 bytes) {
+    vram_budget().charge(bytes, tag_);
+    GpuBuffer* b = nullptr;
+    try {
+        b = ctx_->create_device_buffer(bytes);
+    } catch (...) {
+        vram_budget().release(bytes);
+        throw;
+    }
+    capacity_ += bytes;
+    return b;
 }
 
 void GpuArena::release_chunks() {
@@ -232,6 +342,7 @@ void GpuArena::release_chunks() {
         (void)hipStreamSynchronize(ctx_->stream());
         for (GpuBuffer* b : chunks_) ctx_->release_buffer(b);
     }
+    vram_budget().release(capacity_);
     chunks_.clear();
     cur_ = 0;
     cur_off_ = 0;
@@ -240,29 +351,29 @@ void GpuArena::release_chunks() {
 }
 
 GpuAlloc GpuArena::alloc(u64 bytes, u64 align) {
+    if (bytes == 0) return GpuAlloc{};
     if (!ctx_) throw MediaError("arena: not initialised");
     if (align == 0 || (align & (align - 1)) != 0) throw MediaError("arena: alignment must be a power of two");
-    const u64 need = bytes ? bytes : 1;
     // The current chunk, then any later chunk (kept from before a reset) that
     // fits, then a new chunk.
     for (size_t c = cur_; c < chunks_.size(); c++) {
         const u64 start = c == cur_ ? cur_off_ : 0;
         const u64 off = (start + align - 1) & ~(align - 1);
-        if (off + need <= chunks_[c]->bytes) {
-            used_ += (off - (c == cur_ ? cur_off_ : 0)) + need;
+        if (off + bytes <= chunks_[c]->bytes) {
+            used_ += (off - (c == cur_ ? cur_off_ : 0)) + bytes;
             cur_ = c;
-            cur_off_ = off + need;
+            cur_off_ = off + bytes;
             return GpuAlloc{chunks_[c], off, bytes};
         }
     }
-    const u64 size = need > chunk_bytes_ ? need : chunk_bytes_;
-    GpuBuffer* b = ctx_->create_device_buffer(size);
-    chunks_.push_back(b);
-    capacity_ += size;
+    // Nothing live at a fully rewound arena: its chunks, each sized for some
+    // earlier need, give way to one that fits this one.
+    if (cur_ == 0 && cur_off_ == 0 && !chunks_.empty()) release_chunks();
+    chunks_.push_back(grow(std::max(bytes, chunk_bytes_)));
     cur_ = chunks_.size() - 1;
-    cur_off_ = need;
-    used_ += need;
-    return GpuAlloc{b, 0, bytes};
+    cur_off_ = bytes;
+    used_ += bytes;
+    return GpuAlloc{chunks_.back(), 0, bytes};
 }
 
 void GpuArena::reset() {
@@ -280,185 +391,209 @@ void GpuArena::rewind_to(const Mark& m) {
 }
 
 // ---------------------------------------------------------------- LoRA factor files
+//
+// Key grammar (the format notes of core/models/lora.hpp:1-45): a key names a
+// module's down factor ("<module>.lora_A…" or "<module>.lora_down…"), its up
+// factor (".lora_B…" / ".lora_up…") or its alpha ("<module>.alpha").  The module
+// part then loses, in this order: every display prefix ComfyUI or kohya put in
+// front of it, kohya's "lora_unet_" / "lora_te_" head (whose '_' stand for '.'),
+// and a trailing ".weight".  Those spellings, the alpha defaults and the error
+// texts are the file format's and the reference's (core/models/lora.cpp:20-84).
 
 namespace {
 
-bool ends_with_s(const std::string& s, const std::string& suf) {
-    return s.size() >= suf.size() && s.compare(s.size() - suf.size(), suf.size(), suf) == 0;
+enum class LoraRole { None, Down, Up, Alpha };
+
+bool has_suffix(std::string_view s, std::string_view tail) {
+    return s.size() >= tail.size() && s.substr(s.size() - tail.size()) == tail;
 }
 
-// The display-name prefixes ComfyUI and kohya put before the module path, and
-// kohya's lora_unet_ / lora_te_ forms where '_' stands for '.'.
-std::string strip_display_prefix(std::string s) {
-    static const char* prefixes[] = {"model.diffusion_model.", "diffusion_model.", "model.", "unet.", "transformer."};
-    for (bool again = true; again;) {
-        again = false;
-        for (const char* p : prefixes) {
-            const size_t n = strlen(p);
-            if (s.size() > n && s.compare(0, n, p) == 0) {
-                s.erase(0, n);
-                again = true;
-                break;
-            }
-        }
-    }
-    for (const char* p : {"lora_unet_", "lora_te_"}) {
-        const size_t n = strlen(p);
-        if (s.compare(0, n, p) == 0) {
-            s.erase(0, n);
-            for (char& c : s)
-                if (c == '_') c = '.';
-            break;
-        }
-    }
-    if (ends_with_s(s, ".weight")) s.erase(s.size() - 7);
-    return s;
+// True when `tail` is the last dotted components of `whole`
+// ("attn.to_q" of "blocks.0.attn.to_q").
+bool is_dotted_tail(std::string_view tail, std::string_view whole) {
+    return whole.size() > tail.size() && whole[whole.size() - tail.size() - 1] == '.' && has_suffix(whole, tail);
 }
 
 // A factor names its module with or without the checkpoint's container prefix.
-bool target_matches(const std::string& factor, const std::string& want) {
-    return factor == want || ends_with_s(want, "." + factor) || ends_with_s(factor, "." + want);
+bool same_module(std::string_view factor, std::string_view weight) {
+    return factor == weight || is_dotted_tail(factor, weight) || is_dotted_tail(weight, factor);
+}
+
+std::string canonical_module(std::string_view s) {
+    static constexpr std::string_view kDisplay[] = {"model.diffusion_model.", "diffusion_model.", "model.", "unet.",
+                                                    "transformer."};
+    // A display prefix is peeled only when something follows it; the list is
+    // searched afresh after every peel.
+    for (;;) {
+        const auto hit = std::find_if(std::begin(kDisplay), std::end(kDisplay), [&](std::string_view p) {
+            return s.size() > p.size() && s.substr(0, p.size()) == p;
+        });
+        if (hit == std::end(kDisplay)) break;
+        s.remove_prefix(hit->size());
+    }
+    std::string name(s);
+    for (std::string_view head : {std::string_view("lora_unet_"), std::string_view("lora_te_")}) {
+        if (name.compare(0, head.size(), head) != 0) continue;
+        name.erase(0, head.size());
+        std::replace(name.begin(), name.end(), '_', '.');
+        break;
+    }
+    if (has_suffix(name, ".weight")) name.resize(name.size() - 7);
+    return name;
+}
+
+// The role of a LoRA file's key and the module it belongs to ("" with None).
+LoraRole classify_lora_key(const std::string& key, std::string* module) {
+    module->clear();
+    if (has_suffix(key, ".alpha")) {
+        *module = canonical_module(std::string_view(key).substr(0, key.size() - 6));
+        return LoraRole::Alpha;
+    }
+    static const struct {
+        const char* tag;
+        LoraRole role;
+    } kTags[] = {{".lora_A", LoraRole::Down}, {".lora_down", LoraRole::Down}, {".lora_B", LoraRole::Up},
+                 {".lora_up", LoraRole::Up}};
+    for (const auto& tag : kTags) {
+        const size_t at = key.find(tag.tag);
+        if (at == std::string::npos) continue;
+        *module = canonical_module(std::string_view(key).substr(0, at));
+        return tag.role;
+    }
+    return LoraRole::None;
+}
+
+// The file-wide alpha: the first of the metadata spellings kohya and ComfyUI
+// write ("ss_network_alpha", "lora_alpha", "network_alpha") that holds a
+// positive number; 0 when none does.
+float metadata_alpha(const std::map<std::string, std::string>& meta) {
+    for (const char* key : {"ss_network_alpha", "lora_alpha", "network_alpha"}) {
+        const auto it = meta.find(key);
+        if (it == meta.end()) continue;
+        const float v = (float)std::atof(it->second.c_str());
+        if (v > 0) return v;
+    }
+    return 0.0f;
+}
+
+std::string file_name_of(const std::string& path) {
+    const size_t cut = path.find_last_of("/\\");
+    return cut == std::string::npos ? path : path.substr(cut + 1);
 }
 
 }  // namespace
 
 std::string lora_normalize_target(const std::string& key, bool* is_a, bool* is_b) {
-    if (is_a) *is_a = false;
-    if (is_b) *is_b = false;
-    if (ends_with_s(key, ".alpha")) return strip_display_prefix(key.substr(0, key.size() - 6));
-    for (const char* m : {".lora_A", ".lora_down"}) {
-        const size_t p = key.find(m);
-        if (p != std::string::npos) {
-            if (is_a) *is_a = true;
-            return strip_display_prefix(key.substr(0, p));
-        }
-    }
-    for (const char* m : {".lora_B", ".lora_up"}) {
-        const size_t p = key.find(m);
-        if (p != std::string::npos) {
-            if (is_b) *is_b = true;
-            return strip_display_prefix(key.substr(0, p));
-        }
-    }
-    return "";
+    std::string module;
+    const LoraRole role = classify_lora_key(key, &module);
+    if (is_a) *is_a = role == LoraRole::Down;
+    if (is_b) *is_b = role == LoraRole::Up;
+    return module;
 }
 
-// core/models/lora.cpp:86-181
+// The semantics of core/models/lora.cpp:87-165: modules in the order of their
+// first key; a module needs both factors, 2-D, with agreeing rank; its alpha is
+// its own ".alpha" (the last one read), else the file's, else its rank; the
+// file's strength multiplies the delta.
 void LoraSet::add(const std::string& path, float strength) {
-    if ((int)files_.size() >= kMaxLoras)
+    if ((int)paths_.size() >= kMaxLoras)
         throw MediaError("LoRA: at most " + std::to_string(kMaxLoras) + " files may be chained");
-    SafeTensors st(path);
-    File file;
-    file.path = path;
-    file.strength = strength;
-    // A file-wide alpha from the metadata; a per-module "<base>.alpha" overrides it.
-    float file_alpha = 0.0f;
-    for (const char* key : {"ss_network_alpha", "lora_alpha", "network_alpha"}) {
-        const auto it = st.metadata().find(key);
-        if (it == st.metadata().end()) continue;
-        file_alpha = (float)std::atof(it->second.c_str());
-        if (file_alpha > 0) break;
-    }
-    struct Pending {
-        const StTensor* a = nullptr;
-        const StTensor* b = nullptr;
-        float alpha = 0.0f;
-        bool has_alpha = false;
+    const SafeTensors st(path);
+    const float file_alpha = metadata_alpha(st.metadata());
+
+    struct ModuleKeys {
+        std::string module;
+        const StTensor* down = nullptr;
+        const StTensor* up = nullptr;
+        std::optional<float> alpha;
     };
-    std::map<std::string, Pending> pending;
-    std::vector<std::string> order;
-    for (const std::string& name : st.names()) {
-        const StTensor& t = st.require(name);
-        bool is_a = false, is_b = false;
-        const std::string target = lora_normalize_target(name, &is_a, &is_b);
-        if (target.empty()) continue;
-        auto it = pending.find(target);
-        if (it == pending.end()) {
-            order.push_back(target);
-            it = pending.emplace(target, Pending{}).first;
-        }
-        Pending& p = it->second;
-        if (is_a) {
-            p.a = &t;
-        } else if (is_b) {
-            p.b = &t;
-        } else if (ends_with_s(name, ".alpha")) {
-            const std::vector<float> v = st.to_f32(t);
-            if (!v.empty()) {
-                p.alpha = v[0];
-                p.has_alpha = true;
-            }
+    std::vector<ModuleKeys> modules;
+    std::unordered_map<std::string, size_t> slot_of;
+    std::string module;
+    for (const std::string& key : st.names()) {
+        const LoraRole role = classify_lora_key(key, &module);
+        if (role == LoraRole::None || module.empty()) continue;
+        const auto [slot, fresh] = slot_of.try_emplace(module, modules.size());
+        if (fresh) modules.push_back(ModuleKeys{module, nullptr, nullptr, std::nullopt});
+        ModuleKeys& keys = modules[slot->second];
+        const StTensor& t = st.require(key);
+        switch (role) {
+            case LoraRole::Down: keys.down = &t; break;
+            case LoraRole::Up: keys.up = &t; break;
+            default:
+                if (const std::vector<float> v = st.to_f32(t); !v.empty()) keys.alpha = v.front();
+                break;
         }
     }
-    for (const std::string& target : order) {
-        const Pending& p = pending[target];
-        if (!p.a || !p.b || p.a->shape.size() != 2 || p.b->shape.size() != 2) continue;
-        Factor f;
-        f.target = target;
-        f.rank = p.a->shape[0];
-        f.k = p.a->shape[1];
-        f.n = p.b->shape[0];
-        if (p.b->shape[1] != f.rank || f.rank <= 0 || f.n <= 0 || f.k <= 0) continue;
-        const float alpha = p.has_alpha ? p.alpha : (file_alpha > 0 ? file_alpha : (float)f.rank);
-        f.scale = strength * alpha / (float)f.rank;
-        f.A = st.to_f32(*p.a);
-        f.B = st.to_f32(*p.b);
-        if ((i64)f.A.size() != f.rank * f.k || (i64)f.B.size() != f.n * f.rank) continue;
-        file.factors.push_back(std::move(f));
+
+    const size_t before = adapters_.size();
+    for (const ModuleKeys& keys : modules) {
+        if (!keys.down || !keys.up || keys.down->shape.size() != 2 || keys.up->shape.size() != 2) continue;
+        Adapter ad;
+        ad.module = keys.module;
+        ad.rank = keys.down->shape[0];
+        ad.cols = keys.down->shape[1];
+        ad.rows = keys.up->shape[0];
+        if (keys.up->shape[1] != ad.rank || ad.rank <= 0 || ad.rows <= 0 || ad.cols <= 0) continue;
+        const float alpha = keys.alpha ? *keys.alpha : file_alpha > 0 ? file_alpha : (float)ad.rank;
+        ad.scale = strength * alpha / (float)ad.rank;
+        std::vector<float> down = st.to_f32(*keys.down);
+        const std::vector<float> up = st.to_f32(*keys.up);
+        if ((i64)down.size() != ad.rank * ad.cols || (i64)up.size() != ad.rows * ad.rank) continue;
+        ad.f32 = std::move(down);
+        ad.f32.insert(ad.f32.end(), up.begin(), up.end());
+        adapters_.push_back(std::move(ad));
     }
-    if (file.factors.empty()) {
-        const size_t slash = path.find_last_of("/\\");
-        throw MediaError("LoRA: " + (slash == std::string::npos ? path : path.substr(slash + 1)) +
-                         " holds no A/B factor pairs this engine can map");
-    }
-    files_.push_back(std::move(file));
+    if (adapters_.size() == before)
+        throw MediaError("LoRA: " + file_name_of(path) + " holds no A/B factor pairs this engine can map");
     paths_.push_back(path);
 }
 
+std::vector<const LoraSet::Adapter*> LoraSet::matching(const std::string& target) const {
+    std::vector<const Adapter*> hits;
+    for (const Adapter& ad : adapters_)
+        if (same_module(ad.module, target)) hits.push_back(&ad);
+    return hits;
+}
+
 int LoraSet::deltas_for(const std::string& target, i64 n, i64 k, std::vector<Delta>* out) const {
-    int found = 0;
-    for (const File& file : files_)
-        for (const Factor& f : file.factors) {
-            if (!target_matches(f.target, target) || f.n != n || f.k != k) continue;
-            if (out) out->push_back(Delta{f.n, f.k, f.rank, f.scale, f.A.data(), f.B.data()});
-            found++;
-        }
-    return found;
+    int count = 0;
+    for (const Adapter* ad : matching(target)) {
+        if (ad->rows != n || ad->cols != k) continue;  // a delta of another shape is never guessed onto this one
+        if (out) out->push_back(ad->delta());
+        count++;
+    }
+    return count;
 }
 
 int LoraSet::deltas_for_rows(const std::string& target, i64 row0, i64 rows, i64 k, std::vector<Delta>* out) const {
-    int found = 0;
     if (rows <= 0 || k <= 0 || row0 < 0) return 0;
-    for (const File& file : files_)
-        for (const Factor& f : file.factors) {
-            if (!target_matches(f.target, target) || f.k != k || row0 + rows > f.n) continue;
-            if (out) out->push_back(Delta{f.n, f.k, f.rank, f.scale, f.A.data(), f.B.data()});
-            found++;
-        }
-    return found;
+    int count = 0;
+    for (const Adapter* ad : matching(target)) {
+        if (ad->cols != k || row0 + rows > ad->rows) continue;  // the slice lies outside the delta
+        if (out) out->push_back(ad->delta());
+        count++;
+    }
+    return count;
 }
 
-bool LoraSet::touches(const std::string& target) const {
-    for (const File& file : files_)
-        for (const Factor& f : file.factors)
-            if (target_matches(f.target, target)) return true;
-    return false;
-}
+bool LoraSet::touches(const std::string& target) const { return !matching(target).empty(); }
 
 namespace {
 
-// w[o][i] += (scale * B[row0 + o][r]) * A[r][i], r ascending, 0 entries of B skipped
+// w[o][:] += (scale * up[row0 + o][r]) * down[r][:] as rank-one updates for
+// r = 0, 1, …, rank-1, skipping the 0 entries of up.  Every element of w sees
+// its terms in ascending r, the order that fixes the fp32 result
 // (core/models/lora.cpp:182-201).
-void fold_rows_host(const LoraSet::Delta& d, float* w, i64 row0, i64 rows, i64 k) {
-    for (i64 o = 0; o < rows; o++) {
-        float* wrow = w + o * k;
-        const float* brow = d.b + (row0 + o) * d.rank;
-        for (i64 r = 0; r < d.rank; r++) {
-            const float br = brow[r];
-            if (br == 0.0f) continue;
-            const float s = d.scale * br;
-            const float* arow = d.a + r * k;
-            for (i64 i = 0; i < k; i++) wrow[i] += s * arow[i];
+void rank1_updates(const LoraSet::Delta& d, float* w, i64 row0, i64 rows, i64 k) {
+    for (i64 r = 0; r < d.rank; r++) {
+        const float* down = d.a + r * k;
+        for (i64 o = 0; o < rows; o++) {
+            const float u = d.b[(row0 + o) * d.rank + r];
+            if (u == 0.0f) continue;
+            const float s = d.scale * u;
+            float* wrow = w + o * k;
+            for (i64 i = 0; i < k; i++) wrow[i] += s * down[i];
         }
     }
 }
@@ -469,7 +604,7 @@ int LoraSet::apply(const std::string& target, float* w, i64 n, i64 k) const {
     if (!w || n <= 0 || k <= 0) return 0;
     std::vector<Delta> ds;
     deltas_for(target, n, k, &ds);
-    for (const Delta& d : ds) fold_rows_host(d, w, 0, n, k);
+    for (const Delta& d : ds) rank1_updates(d, w, 0, n, k);
     return (int)ds.size();
 }
 
@@ -477,56 +612,63 @@ int LoraSet::apply_rows(const std::string& target, float* w, i64 row0, i64 rows,
     if (!w) return 0;
     std::vector<Delta> ds;
     deltas_for_rows(target, row0, rows, k, &ds);
-    for (const Delta& d : ds) fold_rows_host(d, w, row0, rows, k);
+    for (const Delta& d : ds) rank1_updates(d, w, row0, rows, k);
     return (int)ds.size();
 }
 
-// core/models/model_common.cpp:1587-1652
+// The operands of core/models/model_common.cpp:1587-1652.  The matching factors
+// sit side by side along the rank axis, module by module and in file order
+// within a module; that order decides the correction's fp32 sums.
 LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::vector<LoraModule>& mods, i64 n, i64 k) {
-    LoraTail t;
-    if (mods.empty() || n <= 0 || k <= 0) return t;
-    std::vector<std::pair<const LoraModule*, LoraSet::Delta>> found;
-    i64 rank = 0;
+    if (mods.empty() || n <= 0 || k <= 0) return LoraTail{};
+    struct Slice {
+        i64 out_row0;  // the module's first output row
+        i64 col0;      // the factor's first rank column
+        LoraSet::Delta d;
+    };
+    std::vector<Slice> slices;
+    i64 width = 0;
     for (const LoraModule& m : mods) {
         if (!m.lora || m.n <= 0) continue;
         if (m.row0 < 0 || m.row0 + m.n > n)
             throw MediaError("LoRA correction: module " + m.base + " covers rows [" + std::to_string(m.row0) + ", " +
                              std::to_string(m.row0 + m.n) + ") of a " + std::to_string(n) + "-row weight");
-        std::vector<LoraSet::Delta> d;
-        m.lora->deltas_for(m.base, m.n, k, &d);
-        for (const LoraSet::Delta& f : d) {
-            found.push_back({&m, f});
-            rank += f.rank;
+        std::vector<LoraSet::Delta> ds;
+        m.lora->deltas_for(m.base, m.n, k, &ds);
+        for (const LoraSet::Delta& d : ds) {
+            slices.push_back(Slice{m.row0, width, d});
+            width += d.rank;
         }
     }
-    if (rank <= 0) return t;
-    if (rank > kLoraRankBound)
-        throw MediaError("LoRA correction: the factors matching this module need a " + std::to_string(rank) +
+    if (width == 0) return LoraTail{};
+    if (width > kLoraRankBound)
+        throw MediaError("LoRA correction: the factors matching this module need a " + std::to_string(width) +
                          "-wide correction, past the " + std::to_string(kLoraRankBound) +
                          " the activation plans reserve (kLoraRankBound)");
     if (!g.ctx) throw MediaError("load_lora_tail: no compute context");
-    // A stacked along the rank axis; B likewise, each factor's scale folded into
-    // its own columns and its rows placed at its module's output rows.
-    std::vector<float> a((size_t)rank * (size_t)k, 0.0f), b((size_t)n * (size_t)rank, 0.0f);
-    i64 r0 = 0;
-    for (const auto& [mod, f] : found) {
-        memcpy(&a[(size_t)r0 * (size_t)k], f.a, (size_t)f.rank * (size_t)k * 4);
-        for (i64 o = 0; o < f.n; o++) {
-            float* brow = &b[(size_t)(mod->row0 + o) * (size_t)rank + (size_t)r0];
-            const float* src = f.b + o * f.rank;
-            for (i64 r = 0; r < f.rank; r++) brow[r] = f.scale * src[r];
+
+    // at [width, k]: each slice's down rows.  bt [n, width]: output row o of a
+    // slice's module holds scale * up[o - out_row0][:] in the slice's columns and
+    // zeros elsewhere, so bt . (at . x) is the sum of every factor's product.
+    std::vector<float> at((size_t)(width * k)), bt((size_t)(n * width), 0.0f);
+    for (const Slice& s : slices) {
+        std::copy_n(s.d.a, (size_t)(s.d.rank * k), at.begin() + (std::ptrdiff_t)(s.col0 * k));
+        for (i64 o = 0; o < s.d.n; o++) {
+            const float* up = s.d.b + o * s.d.rank;
+            std::transform(up, up + s.d.rank, bt.begin() + (std::ptrdiff_t)((s.out_row0 + o) * width + s.col0),
+                           [scale = s.d.scale](float u) { return scale * u; });
         }
-        r0 += f.rank;
     }
-    t.at = arena.alloc((u64)a.size() * 4);
-    t.bt = arena.alloc((u64)b.size() * 4);
-    g.ctx->upload(t.at.res, a.data(), a.size() * 4, t.at.off);
-    g.ctx->upload(t.bt.res, b.data(), b.size() * 4, t.bt.off);
-    t.rank = rank;
-    t.n = n;
-    t.k = k;
-    t.active = true;
-    return t;
+    LoraTail tail;
+    tail.at = arena.alloc((u64)at.size() * 4);
+    tail.bt = arena.alloc((u64)bt.size() * 4);
+    g.ctx->upload(tail.at.res, at.data(), at.size() * 4, tail.at.off);
+    g.ctx->upload(tail.bt.res, bt.data(), bt.size() * 4, tail.bt.off);
+    tail.rank = width;
+    tail.n = n;
+    tail.k = k;
+    tail.active = true;
+    return tail;
 }
 
 LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::string& base, const LoraSet* lora, i64 n, i64 k) {
@@ -536,9 +678,11 @@ LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::string& base, con
 
 namespace {
 
-// The conditions of the reference's device-expand path (w4a8_plan_of,
-// core/models/model_common.cpp:605-680), each checked rather than trusted.
-struct W4a8Plan {
+// Where the parts of a grouped weight (asym_w4a8_int8, w6a8_int8) live, for the
+// device expand.  The family's rules are core/host/st.cpp:839-925 and the
+// device path's own conditions core/models/model_common.cpp:605-680; unlike
+// that path, a weight_correction plane is carried to the expand here.
+struct GroupedParts {
     CodeLayout layout = CodeLayout::Nibble4;
     const StTensor* codes = nullptr;
     const StTensor* srel = nullptr;
@@ -549,52 +693,64 @@ struct W4a8Plan {
     RelDType rel_dtype = RelDType::F32;
 };
 
-std::string w4a8_plan_of(const SafeTensors& st, const StTensor& t, W4a8Plan* out) {
+std::optional<RelDType> rel_dtype_of(StDType d) {
+    switch (d) {
+        case StDType::F32: return RelDType::F32;
+        case StDType::F16: return RelDType::F16;
+        case StDType::BF16: return RelDType::BF16;
+        case StDType::F8_E4M3: return RelDType::F8_E4M3;
+        case StDType::F8_E5M2: return RelDType::F8_E5M2;
+        case StDType::U8: return RelDType::U8_E4M3;  // an fp8 table in a byte container
+        default: return std::nullopt;
+    }
+}
+
+// Empty when `t` can be expanded on the device, with `out` filled; otherwise why not.
+std::string grouped_parts_of(const SafeTensors& st, const StTensor& t, GroupedParts* out) {
     const SafeTensors::WeightLayout L = st.weight_layout(t.name);
-    const std::string& f = L.spec.format;
-    const bool six = f == "w6a8_int8" || f == "w6a8";
-    if (t.shape.size() != 2 || (t.dtype != StDType::I8 && t.dtype != StDType::U8)) return "codes are not a 2-D byte tensor";
+    const bool six = L.spec.format == "w6a8_int8" || L.spec.format == "w6a8";
+    // Codes: a 2-D byte plane already in the rotated basis.
+    if (t.shape.size() != 2 || (t.dtype != StDType::I8 && t.dtype != StDType::U8))
+        return "codes are not a 2-D byte tensor";
     if (!L.spec.convrot) return "the weight is not convrot-rotated";
+    // The relative-scale table and its element type.
     if (!L.rel_scale || L.rel_scale->shape.size() != 2) return "no 2-D weight_s_rel table";
-    RelDType rdt;
-    switch (L.rel_scale->dtype) {
-        case StDType::F32: rdt = RelDType::F32; break;
-        case StDType::F16: rdt = RelDType::F16; break;
-        case StDType::BF16: rdt = RelDType::BF16; break;
-        case StDType::F8_E4M3: rdt = RelDType::F8_E4M3; break;
-        case StDType::F8_E5M2: rdt = RelDType::F8_E5M2; break;
-        case StDType::U8: rdt = RelDType::U8_E4M3; break;
-        default: return std::string("weight_s_rel dtype ") + st_dtype_name(L.rel_scale->dtype) + " is not decodable";
-    }
-    const i64 n = t.shape[0], k = st.logical_cols(t);
-    const i64 group = L.group;
-    const i64 per = six ? 4 : 2;
-    if (group <= 0 || group % per != 0 || k % group != 0) return "group " + std::to_string(group) + " does not divide K";
-    const i64 need = six ? (k / 2 + k / 4) : k / 2;
-    if ((i64)t.row_bytes() < need) return "code rows are shorter than K needs";
-    if (L.rel_scale->shape[0] != n || L.rel_scale->shape[1] != k / group) return "weight_s_rel is not [N, K/group]";
+    const std::optional<RelDType> rel = rel_dtype_of(L.rel_scale->dtype);
+    if (!rel) return std::string("weight_s_rel dtype ") + st_dtype_name(L.rel_scale->dtype) + " is not decodable";
+    // Geometry: whole groups of whole code bytes, and rows wide enough for K.
+    GroupedParts p;
+    p.n = t.shape[0];
+    p.k = st.logical_cols(t);
+    p.group = L.group;
+    const i64 codes_per_unit = six ? 4 : 2;  // codes that fill whole bytes
+    if (p.group <= 0 || p.group % codes_per_unit != 0 || p.k % p.group != 0)
+        return "group " + std::to_string(p.group) + " does not divide K";
+    const i64 row_need = six ? p.k / 2 + p.k / 4 : p.k / 2;  // six bits: a nibble plane, then a 2-bit plane
+    if ((i64)t.row_bytes() < row_need) return "code rows are shorter than K needs";
+    if (L.rel_scale->shape[0] != p.n || L.rel_scale->shape[1] != p.k / p.group)
+        return "weight_s_rel is not [N, K/group]";
+    // The optional tables.
     if (six && L.codebook) return "a six-bit weight with a codebook";
-    if (!six && L.codebook && (L.codebook->dtype != StDType::F32 || L.codebook->numel != 16))
+    if (L.codebook && !six && (L.codebook->dtype != StDType::F32 || L.codebook->numel != 16))
         return "the codebook is not 16 fp32 levels";
-    if (L.row_scale && (L.row_scale->dtype != StDType::F32 || (L.row_scale->numel != 1 && L.row_scale->numel != n)))
-        return "the channel scale is not fp32 [N] or [1]";
-    if (L.correction) {
-        const i64 cg = L.correction->shape.empty() ? 0 : L.correction->shape[0];
-        const i64 cn = L.correction->shape.size() > 1 ? L.correction->shape[1] : 0;
-        if (L.correction->dtype != StDType::F32 || cg != k / group || cn != n)
-            return "weight_correction is not fp32 [K/group, N]";
+    if (L.row_scale) {
+        const bool per_row_or_one = L.row_scale->numel == 1 || L.row_scale->numel == p.n;
+        if (L.row_scale->dtype != StDType::F32 || !per_row_or_one) return "the channel scale is not fp32 [N] or [1]";
     }
-    out->layout = six ? CodeLayout::Packed6 : CodeLayout::Nibble4;
-    out->codes = &t;
-    out->srel = L.rel_scale;
-    out->sch = L.row_scale;
-    out->codebook = six ? nullptr : L.codebook;
-    out->correction = L.correction;
-    out->n = n;
-    out->k = k;
-    out->group = group;
-    out->srel_row_bytes = (i64)L.rel_scale->row_bytes();
-    out->rel_dtype = rdt;
+    if (const StTensor* c = L.correction) {
+        const bool fits = c->dtype == StDType::F32 && c->shape.size() == 2 && c->shape[0] == p.k / p.group &&
+                          c->shape[1] == p.n;
+        if (!fits) return "weight_correction is not fp32 [K/group, N]";
+    }
+    p.layout = six ? CodeLayout::Packed6 : CodeLayout::Nibble4;
+    p.codes = &t;
+    p.srel = L.rel_scale;
+    p.sch = L.row_scale;
+    p.codebook = six ? nullptr : L.codebook;
+    p.correction = L.correction;
+    p.srel_row_bytes = (i64)L.rel_scale->row_bytes();
+    p.rel_dtype = *rel;
+    *out = p;
     return "";
 }
 
@@ -614,10 +770,20 @@ u64 checked_mul(u64 a, u64 b, const std::string& what) {
 struct Scratch {
     ComputeContext& ctx;
     GpuBuffer* b;
-    Scratch(ComputeContext& c, u64 bytes) : ctx(c), b(c.create_device_buffer(bytes)) {}
+    u64 charged;
+    Scratch(ComputeContext& c, u64 bytes) : ctx(c), b(nullptr), charged(bytes) {
+        vram_budget().charge(bytes, "load scratch");
+        try {
+            b = c.create_device_buffer(bytes);
+        } catch (...) {
+            vram_budget().release(bytes);
+            throw;
+        }
+    }
     ~Scratch() {
         (void)hipStreamSynchronize(ctx.stream());
         ctx.release_buffer(b);
+        vram_budget().release(charged);
     }
     Scratch(const Scratch&) = delete;
     Scratch& operator=(const Scratch&) = delete;
@@ -751,36 +917,36 @@ void requant_rows_device(GpuCtx& g, const SafeTensors& st, const StTensor& t, i6
 
 // The stored parts of a grouped weight staged on the device and expanded into
 // q [n, k] / s [n] (w4a8_pack_rows, core/models/model_common.cpp:680-748).
-void expand_grouped(GpuCtx& g, const StTensor& t, const W4a8Plan& pl, int8_t* q, float* s, const SafeTensors& st) {
+void expand_grouped(GpuCtx& g, const StTensor& t, const GroupedParts& parts, int8_t* q, float* s, const SafeTensors& st) {
     ComputeContext& ctx = *g.ctx;
-    const i64 n = pl.n;
-    const u64 cb = checked_mul((u64)n, t.row_bytes(), "w4a8 codes"), sb = pl.srel->nbytes, hb = pl.sch ? (u64)n * 4 : 0,
-              kb = pl.codebook ? 64 : 0, rb = pl.correction ? pl.correction->nbytes : 0;
+    const i64 n = parts.n;
+    const u64 cb = checked_mul((u64)n, t.row_bytes(), "w4a8 codes"), sb = parts.srel->nbytes, hb = parts.sch ? (u64)n * 4 : 0,
+              kb = parts.codebook ? 64 : 0, rb = parts.correction ? parts.correction->nbytes : 0;
     const u64 o_codes = 0, o_srel = up256(cb), o_sch = o_srel + up256(sb), o_cb = o_sch + up256(hb),
               o_corr = o_cb + up256(kb), total = o_corr + up256(rb);
     Scratch stage(ctx, total);
     ctx.upload(stage.b, t.data, cb, o_codes);
-    ctx.upload(stage.b, pl.srel->data, sb, o_srel);
-    if (pl.sch) {
+    ctx.upload(stage.b, parts.srel->data, sb, o_srel);
+    if (parts.sch) {
         std::vector<float> v((size_t)n);
-        for (i64 r = 0; r < n; r++) v[(size_t)r] = st.row_scale_value(*pl.sch, r);  // a [1] table broadcasts
+        for (i64 r = 0; r < n; r++) v[(size_t)r] = st.row_scale_value(*parts.sch, r);  // a [1] table broadcasts
         ctx.upload(stage.b, v.data(), hb, o_sch);
     }
-    if (pl.codebook) ctx.upload(stage.b, pl.codebook->data, kb, o_cb);
-    if (pl.correction) ctx.upload(stage.b, pl.correction->data, rb, o_corr);
+    if (parts.codebook) ctx.upload(stage.b, parts.codebook->data, kb, o_cb);
+    if (parts.correction) ctx.upload(stage.b, parts.correction->data, rb, o_corr);
     phi_w4a8_weight w{};
     w.codes = (const uint8_t*)stage.at(o_codes);
     w.codes_row_bytes = (int64_t)t.row_bytes();
     w.s_rel = (const void*)stage.at(o_srel);
-    w.s_rel_dtype = phi_rel_dtype(pl.rel_dtype);
-    w.srel_row_bytes = pl.srel_row_bytes;
-    w.s_channel = pl.sch ? (const float*)stage.at(o_sch) : nullptr;
-    w.codebook = pl.codebook ? (const float*)stage.at(o_cb) : nullptr;
-    w.correction = pl.correction ? (const float*)stage.at(o_corr) : nullptr;
+    w.s_rel_dtype = phi_rel_dtype(parts.rel_dtype);
+    w.srel_row_bytes = parts.srel_row_bytes;
+    w.s_channel = parts.sch ? (const float*)stage.at(o_sch) : nullptr;
+    w.codebook = parts.codebook ? (const float*)stage.at(o_cb) : nullptr;
+    w.correction = parts.correction ? (const float*)stage.at(o_corr) : nullptr;
     w.rows = n;
-    w.k = pl.k;
-    w.group = pl.group;
-    w.layout = pl.layout == CodeLayout::Nibble4 ? 0 : 1;
+    w.k = parts.k;
+    w.group = parts.group;
+    w.layout = parts.layout == CodeLayout::Nibble4 ? 0 : 1;
     ctx.check(phi_hip_w4a8_expand(ctx.stream(), &w, q, s), "w4a8_expand");
     ctx.submit();
 }
@@ -832,12 +998,12 @@ QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::strin
             throw MediaError("load_quant_linear: '" + base + "' (" + L.spec.format +
                              "): a LoRA is not folded into a grouped weight here; load the tail with load_lora_tail "
                              "and apply it with apply_lora_tail");
-        W4a8Plan pl;
-        const std::string why = w4a8_plan_of(st, t, &pl);
+        GroupedParts parts;
+        const std::string why = grouped_parts_of(st, t, &parts);
         if (!why.empty()) throw MediaError("load_quant_linear: '" + base + "' (" + L.spec.format + "): " + why);
         q.w = alloc(nk);
         q.scale = alloc((u64)n * 4);
-        expand_grouped(g, t, pl, dev_i8(q.w), dev_f32(q.scale), st);
+        expand_grouped(g, t, parts, dev_i8(q.w), dev_f32(q.scale), st);
         return q;
     }
     if (L.spec.valid && L.spec.format == "convrot_w4a4")
@@ -957,10 +1123,10 @@ QuantLinear load_quant3_linear(GpuCtx& g, const SafeTensors& st, const std::stri
             if (rotate)
                 throw MediaError("load_quant3_linear: '" + bases[i] + "' (" + L.spec.format +
                                  ") is stored rotated, but " + base_q + "'s spec asks for a rotation");
-            W4a8Plan pl;
-            const std::string why = w4a8_plan_of(st, t, &pl);
+            GroupedParts parts;
+            const std::string why = grouped_parts_of(st, t, &parts);
             if (!why.empty()) throw MediaError("load_quant3_linear: '" + bases[i] + "' (" + L.spec.format + "): " + why);
-            expand_grouped(g, t, pl, qi, si, st);
+            expand_grouped(g, t, parts, qi, si, st);
             continue;
         }
         requant_rows_device(g, st, t, rows_of[i], k, plan, qi, si);
@@ -982,11 +1148,11 @@ I8Upload upload_quant_linear_i8(GpuCtx& g, const SafeTensors& st, const std::str
     // A grouped weight is expanded on the device whatever `lora` holds (the
     // reference never folds into a streamed weight: the tail corrects it).
     if (L.packed) {
-        W4a8Plan pl;
-        if (w4a8_plan_of(st, t, &pl).empty()) {
+        GroupedParts parts;
+        if (grouped_parts_of(st, t, &parts).empty()) {
             out.w = arena.alloc(nk);
             out.s = arena.alloc((u64)out.n * 4);
-            expand_grouped(g, t, pl, dev_i8(out.w), dev_f32(out.s), st);
+            expand_grouped(g, t, parts, dev_i8(out.w), dev_f32(out.s), st);
             return out;
         }
     }

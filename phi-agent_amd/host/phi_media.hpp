@@ -238,11 +238,42 @@ void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 
 
 // ---- loading weights from checkpoints (safetensors.hpp reads the files) ----
 
+// The process-wide VRAM accountant (core/runtime/vram_budget.hpp:42-264): the
+// ledger every arena charges before it grows.  charge() throws MediaError when
+// the ledger would pass the limit, before anything is allocated, so a plan that
+// does not fit fails as a plain error, never as a half-committed device.
+//   limit: PHI_VRAM_BUDGET_MB (MiB, at least 256, at most the device less a
+//   256 MiB reserve) when set, else the device's memory less a reserve of one
+//   sixteenth, kept within [384 MiB, 2 GiB].  set_limit() overrides both (0 goes
+//   back to them).
+class VramBudget {
+public:
+    static VramBudget& instance();
+    void charge(u64 bytes, const char* tag = nullptr);
+    void release(u64 bytes);
+    u64 local() const;  // bytes charged and not released
+    u64 peak() const;
+    u64 limit() const;
+    bool would_exceed(u64 bytes) const;
+    void set_limit(u64 bytes);
+
+private:
+    VramBudget() = default;
+    u64 derived_limit() const;
+    struct State;
+    State& state() const;
+};
+inline VramBudget& vram_budget() { return VramBudget::instance(); }
+
 // A bump allocator over device memory chunks, as the reference's GpuArena
-// (core/runtime/sched.hpp:40-100): alloc() hands out aligned pieces (256 bytes
-// by default) and adds a chunk when the current one is full; reset()
-// invalidates every allocation and keeps the chunks; mark() / rewind_to() give
-// back what was allocated after a mark.  Owns its chunks.
+// (core/runtime/sched.hpp:40-100, sched.cpp:65-109): alloc() hands out aligned
+// pieces (256 bytes by default) and adds a chunk when the current one is full,
+// charging the VRAM accountant for it first; alloc(0) returns an empty
+// GpuAlloc; a grow from a fully rewound arena (nothing live) first returns the
+// old chunks, so a mark/rewind caller holds one chunk of the largest size it
+// needed rather than the sum.  reset() invalidates every allocation and keeps
+// the chunks; mark() / rewind_to() give back what was allocated after a mark.
+// Owns its chunks and releases their charge with them.
 class GpuArena {
 public:
     struct Mark {
@@ -257,7 +288,7 @@ public:
     GpuArena(const GpuArena&) = delete;
     GpuArena& operator=(const GpuArena&) = delete;
 
-    void init(ComputeContext* ctx, u64 chunk_bytes = 192ull << 20);
+    void init(ComputeContext* ctx, u64 chunk_bytes = 192ull << 20, const char* tag = "arena");
     // Size of future chunks (0 is ignored).
     void set_chunk_bytes(u64 chunk_bytes) {
         if (chunk_bytes) chunk_bytes_ = chunk_bytes;
@@ -275,7 +306,9 @@ public:
     void rewind_to(const Mark& m);
 
 private:
+    GpuBuffer* grow(u64 bytes);
     ComputeContext* ctx_ = nullptr;
+    const char* tag_ = "arena";
     u64 chunk_bytes_ = 192ull << 20;
     std::vector<GpuBuffer*> chunks_;
     size_t cur_ = 0;
@@ -299,11 +332,11 @@ public:
     // factor pair this loader can map.  strength scales the file's deltas.
     void add(const std::string& path, float strength = kLoraStrengthDefault);
     void clear() {
-        files_.clear();
+        adapters_.clear();
         paths_.clear();
     }
-    bool empty() const { return files_.empty(); }
-    size_t size() const { return files_.size(); }
+    bool empty() const { return paths_.empty(); }
+    size_t size() const { return paths_.size(); }
     const std::vector<std::string>& paths() const { return paths_; }
 
     // One factor as stored: W_eff = W + scale * b @ a, a [rank, k], b [n, rank],
@@ -327,19 +360,21 @@ public:
     int apply_rows(const std::string& target, float* w, i64 row0, i64 rows, i64 k) const;
 
 private:
-    struct Factor {
-        std::string target;
-        i64 n = 0, k = 0, rank = 0;
+    // One adapted module of one file: the delta scale * up . down, with down
+    // [rank, cols] and up [rows, rank] stored back to back in f32.
+    struct Adapter {
+        std::string module;
+        i64 rows = 0, cols = 0, rank = 0;
         float scale = 1.0f;
-        std::vector<float> A;  // [rank, k]
-        std::vector<float> B;  // [n, rank]
+        std::vector<float> f32;
+        const float* down() const { return f32.data(); }
+        const float* up() const { return f32.data() + (size_t)(rank * cols); }
+        Delta delta() const { return Delta{rows, cols, rank, scale, down(), up()}; }
     };
-    struct File {
-        std::string path;
-        float strength = kLoraStrengthDefault;
-        std::vector<Factor> factors;
-    };
-    std::vector<File> files_;
+    // The adapters whose module names `target`, in chain order.
+    std::vector<const Adapter*> matching(const std::string& target) const;
+
+    std::vector<Adapter> adapters_;  // file by file; within a file, modules in order of their first key
     std::vector<std::string> paths_;
 };
 

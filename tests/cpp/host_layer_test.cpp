@@ -472,6 +472,61 @@ static void test_arena(ComputeContext& ctx) {
     printf("arena and context: %s\n", failures ? "mismatch" : "ok");
 }
 
+// The ownership contract of core/runtime/sched.cpp:65-109 and
+// core/runtime/vram_budget.cpp:345-420: alloc(0) is empty, every grow is
+// charged before it allocates and a charge past the limit throws (the arena
+// unchanged), a grow from a fully rewound arena returns the old chunks first,
+// and a released arena gives its charge back.
+static void test_arena_budget(ComputeContext& ctx) {
+    constexpr u64 MiB = 1ull << 20;
+    VramBudget& vb = vram_budget();
+    const u64 base = vb.local();
+    {
+        GpuArena a;
+        a.init(&ctx, 1 * MiB, "test arena");
+        const GpuAlloc z = a.alloc(0);
+        CHECK(!z && z.bytes == 0 && a.chunks() == 0 && vb.local() == base, "arena: alloc(0) is an empty GpuAlloc");
+        const GpuAlloc p = a.alloc(4096);
+        CHECK(p && a.chunks() == 1 && vb.local() == base + 1 * MiB, "arena: a grow charges its chunk (%llu)",
+              (unsigned long long)(vb.local() - base));
+        const GpuAlloc z2 = a.alloc(0);
+        CHECK(!z2 && a.used() == 4096, "arena: alloc(0) leaves the arena as it was");
+
+        // A limit 1.5 MiB above what is charged: the next 1 MiB chunk fits, the
+        // one after is refused before anything is allocated.
+        vb.set_limit(vb.local() + MiB + MiB / 2);
+        const GpuAlloc q = a.alloc(MiB - 4096 + 1);  // does not fit the first chunk's rest
+        CHECK(q && a.chunks() == 2, "arena: a grow within the limit");
+        bool refused = false;
+        const u64 charged = vb.local(), cap = a.capacity();
+        try {
+            (void)a.alloc(MiB);
+        } catch (const MediaError& e) {
+            refused = strstr(e.what(), "VRAM budget exceeded") && strstr(e.what(), "test arena");
+        }
+        CHECK(refused, "arena: a grow past the limit throws MediaError naming the arena");
+        CHECK(vb.local() == charged && a.capacity() == cap && a.chunks() == 2,
+              "arena: a refused grow allocates and charges nothing");
+        vb.set_limit(0);
+
+        // Fully rewound: the two chunks give way to one of the size asked for.
+        a.reset();
+        a.set_chunk_bytes(8 * MiB);
+        const GpuAlloc big = a.alloc(5 * MiB);
+        CHECK(big && a.chunks() == 1 && a.capacity() == 8 * MiB && vb.local() == base + 8 * MiB,
+              "arena: a grow from a rewound arena releases the old chunks first (chunks %d, charged %llu)",
+              a.chunks(), (unsigned long long)(vb.local() - base));
+        // Not rewound: the live chunk stays.
+        const GpuAlloc more = a.alloc(MiB);
+        CHECK(more && more.res == big.res && a.chunks() == 1, "arena: a chunk with room is used");
+        const GpuAlloc over = a.alloc(4 * MiB);
+        CHECK(over && a.chunks() == 2 && vb.local() == base + 16 * MiB, "arena: a grow with live allocations keeps them");
+    }
+    CHECK(vb.local() == base, "arena: destruction releases the charge (%llu left)",
+          (unsigned long long)(vb.local() - base));
+    printf("arena budget: %s\n", failures ? "mismatch" : "ok");
+}
+
 int main() {
     try {
         ComputeContext ctx(0);
@@ -483,6 +538,7 @@ int main() {
         test_lora_tail(ctx);
         test_any_k_gemm(ctx);
         test_arena(ctx);
+        test_arena_budget(ctx);
     } catch (const std::exception& e) {
         printf("FAIL exception: %s\n", e.what());
         return 1;
