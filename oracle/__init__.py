@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_EXE = os.path.join(HERE, "_ref", "phiref")
 
 F32, BF16, F16, I32, I8, F8_E4M3, F8_E5M2, U8_E4M3 = range(8)
-ROUND_HALF_AWAY, ROUND_HALF_EVEN = 0, 1
+ROUND_HALF_AWAY, ROUND_HALF_EVEN, ROUND_DEVICE_FLOOR = 0, 1, 2
 
 _lib = None
 
@@ -68,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.orc_f8_e5m2_to_f32.restype = ctypes.c_float
         L.orc_scale_at.argtypes = [P, I, I64]
         L.orc_scale_at.restype = ctypes.c_float
+        L.orc_round_forms_differ.argtypes = [P, I64]
+        L.orc_round_forms_differ.restype = I64
         _lib = L
     return _lib
 
@@ -130,6 +132,16 @@ def quantize_rows(x, *, rotate=True, qmax=127.0, round_mode=ROUND_HALF_AWAY, x_i
     if rc != 0:
         raise ValueError(f"quantize_rows: cols={cols} is not a multiple of 256")
     return q, s
+
+
+def round_forms_differ(cap: int = 16) -> tuple[int, np.ndarray]:
+    """Every fp32 d with |d| <= 128 where the host rule (ROUND_HALF_AWAY, double
+    arithmetic, core/host/quant.cpp:163-166) and the reference device kernel's
+    fp32 floorf(d + 0.5f) form (ROUND_DEVICE_FLOOR, core/kernels/int8_gemm.cpp:777-780)
+    give different codes: (count, the first `cap` of them)."""
+    out = np.zeros(cap, np.float32)
+    n = lib().orc_round_forms_differ(_p(out), cap)
+    return int(n), out[:min(n, cap)]
 
 
 # ---------------------------------------------------------------- A4 / A5

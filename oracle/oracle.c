@@ -150,6 +150,32 @@ static long round_code(float prod, int round_mode) {
     return (long)(d >= 0 ? d + 0.5 : d - 0.5);
 }
 
+/* The reference device kernel's form (core/kernels/int8_gemm.cpp:777-780): the
+ * clamp first, in fp32 (NaN -> -qmax), then the half-unit push as an fp32 sum,
+ * rounded to nearest even before floorf / ceilf see it. */
+static long round_code_device(float prod, float qmax) {
+    const float d = fminf(fmaxf(prod, -qmax), qmax);
+    const float pushed = d >= 0.0f ? d + 0.5f : d - 0.5f;
+    return (long)(d >= 0.0f ? floorf(pushed) : ceilf(pushed));
+}
+
+int64_t orc_round_forms_differ(float* out, int64_t cap) {
+    int64_t found = 0;
+    const uint32_t top = 0x43000000u; /* 128.0f */
+    for (uint32_t sign = 0; sign <= 1; sign++) {
+        for (uint32_t bits = 0; bits <= top; bits++) {
+            const uint32_t b = bits | (sign << 31);
+            float d;
+            memcpy(&d, &b, 4);
+            if (round_code(d, ORC_ROUND_HALF_AWAY) != round_code_device(d, 128.0f)) {
+                if (found < cap) out[found] = d;
+                found++;
+            }
+        }
+    }
+    return found;
+}
+
 int orc_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
                       int rotate, float qmax, int round_mode, int8_t* q, float* s) {
     if (rotate && cols % 256 != 0) return -1;
@@ -171,7 +197,8 @@ int orc_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, in
         const float inv = 1.0f / scale;
         s[r] = scale;
         for (int64_t c = 0; c < cols; c++) {
-            long v = round_code(row[c] * inv, round_mode);
+            long v = round_mode == ORC_ROUND_DEVICE_FLOOR ? round_code_device(row[c] * inv, qmax)
+                                                           : round_code(row[c] * inv, round_mode);
             v = v < -lim ? -lim : (v > lim ? lim : v);
             q[r * cols + c] = (int8_t)v;
         }

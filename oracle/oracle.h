@@ -31,7 +31,12 @@ enum orc_dtype {
     ORC_U8_E4M3 = 7 /* an E4M3 table stored in a byte container */
 };
 
-enum orc_round { ORC_ROUND_HALF_AWAY = 0, ORC_ROUND_HALF_EVEN = 1 };
+/* HALF_AWAY: the host rule (core/host/quant.cpp:163-166), the library's contract.
+ * HALF_EVEN: the documented alternative.
+ * DEVICE_FLOOR: the reference's device kernel (core/kernels/int8_gemm.cpp:777-780):
+ * clamp to +-qmax in fp32, then floorf(d + 0.5f) / ceilf(d - 0.5f) with fp32 sums,
+ * which differs from HALF_AWAY exactly at d = +-(0.5 - 2^-25). */
+enum orc_round { ORC_ROUND_HALF_AWAY = 0, ORC_ROUND_HALF_EVEN = 1, ORC_ROUND_DEVICE_FLOOR = 2 };
 
 /* ---- scalar conversions (core/util/media_common.cpp:62-193) ---- */
 float orc_f16_to_f32(uint16_t h);              /* media_common.cpp:62-87 */
@@ -50,6 +55,9 @@ void orc_convrot_rows(const float* x, float* out, int64_t rows, int64_t cols);
  *      core/kernels/int8_gemm.cpp:755) ----
  * x is f32 or bf16 [rows, ldx]; rotate selects the convrot pre-pass.
  * Returns 0, or -1 when cols is not a whole number of 256-groups. */
+/* Every fp32 d with |d| <= 128 whose HALF_AWAY and DEVICE_FLOOR codes differ:
+ * returns how many, and stores the first `cap` of them in `out`. */
+int64_t orc_round_forms_differ(float* out, int64_t cap);
 int orc_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
                       int rotate, float qmax, int round_mode, int8_t* q, float* s);
 

@@ -149,6 +149,35 @@ def test_every_near_tie_unrotated(dev, orc, round_mode, inv_pow):
         assert np.array_equal(q[0, :v.size], half_away(v))
 
 
+@pytest.mark.parametrize("rotate", [False, True])
+def test_rounding_contract_at_the_device_floor_edge(dev, orc, rotate):
+    """The library rounds by the reference's host rule (core/host/quant.cpp:163-166),
+    not by its device kernel's fp32 floorf(d + 0.5f) (core/kernels/int8_gemm.cpp:777-780).
+    The two differ only at d = +-(0.5 - 2^-25): 0 by the host rule, +-1 by the
+    device form.  Rows put exactly those products through both kernels, without
+    and with the rotation (one non-zero per 256-group rotates to +-c/16 in every
+    element, exactly)."""
+    edge = np.float32(0.5 - 2.0 ** -25)
+    K = 1024
+    row = np.zeros(K, np.float32)
+    if rotate:
+        row[0], row[256], row[512], row[768] = 16 * edge, -16 * edge, 16 * 127.0, 16 * 1.5
+    else:
+        row[:4] = [edge, -edge, 127.0, 1.5]
+    x = torch.from_numpy(np.stack([row, row * np.float32(0.25)]))
+    q, s, qo, so = run(dev, orc, x, rotate=rotate)
+    assert np.array_equal(q, qo) and np.array_equal(s.view(np.uint32), so.view(np.uint32))
+    qd, sd = orc.quantize_rows(x.numpy(), rotate=rotate, round_mode=orc.ROUND_DEVICE_FLOOR)
+    codes = q[0, [0, 256, 512, 768]] if rotate else q[0, :4]
+    dcodes = qd[0, [0, 256, 512, 768]] if rotate else qd[0, :4]
+    assert s[0] == 1.0
+    assert list(codes[:2].astype(int)) == [0, 0] and abs(int(codes[2])) == 127
+    assert [abs(int(c)) for c in dcodes[:2]] == [1, 1]
+    # both rows (the second scaled by 1/4, so inv = 4 and the products are the same)
+    # differ at their edge products only: two groups of 256 rotated, two elements not
+    assert (q != qd).sum() == (2 * 2 * 256 if rotate else 2 * 2), "the forms differ only at the edge products"
+
+
 @pytest.mark.parametrize("round_mode", [Q.ROUND_HALF_AWAY, Q.ROUND_HALF_EVEN])
 @pytest.mark.parametrize("groups", [96, 64, 12])
 def test_every_near_tie_through_the_rotation(dev, orc, round_mode, groups):

@@ -143,6 +143,40 @@ def test_crafted_ties_distinguish_the_modes():
     assert list(quantise_identity(v, O.ROUND_HALF_EVEN)) == [0, 2, 2, 0, -2, 126]
 
 
+def test_device_floor_form_differs_from_the_host_rule_at_exactly_two_values():
+    """The reference has two quantisers: the host rule rounds half away in
+    double (core/host/quant.cpp:163-166); its device kernel clamps, then takes
+    floorf(d + 0.5f) / ceilf(d - 0.5f) with the sum rounded to fp32
+    (core/kernels/int8_gemm.cpp:777-780).  The sum is exact for every fp32 d
+    except d = +-(0.5 - 2^-25): 1 - 2^-25 lies halfway between the fp32
+    neighbours 1 - 2^-24 and 1 and rounds to the even one, 1.  The exhaustive
+    scan over every fp32 in [-128, 128] must find exactly those two."""
+    n, vals = O.round_forms_differ()
+    edge = 0.5 - 2.0 ** -25
+    assert n == 2
+    assert sorted(float(v) for v in vals) == [-edge, edge]
+    # the mechanism: the fp32 sum at the edge is 1, at its neighbours it stays below
+    assert np.float32(edge) + np.float32(0.5) == np.float32(1.0)
+    below = np.nextafter(np.float32(edge), np.float32(0))
+    assert below + np.float32(0.5) < np.float32(1.0)
+
+
+def test_device_floor_mode_in_the_quantiser():
+    """The device-kernel mode gives +-1 at d = +-(0.5 - 2^-25) where the host
+    rule (the library's contract) gives 0, and agrees on every other near-tie,
+    the exact ties included."""
+    edge = np.float32(0.5 - 2.0 ** -25)
+    v = np.concatenate([[edge, -edge], near_ties(-127, 127)]).astype(np.float32)
+    host = quantise_identity(v, O.ROUND_HALF_AWAY).astype(np.int64)
+    dev = quantise_identity(v, O.ROUND_DEVICE_FLOOR).astype(np.int64)
+    assert list(host[:2]) == [0, 0] and list(dev[:2]) == [1, -1]
+    at_edge = np.abs(v) == edge  # the near-tie set holds them too (0.5 less one ulp)
+    assert np.array_equal(host[~at_edge], dev[~at_edge])
+    assert np.array_equal(dev[at_edge] - host[at_edge], np.sign(v[at_edge]).astype(np.int64))
+    ties = np.array([0.5, -0.5, 2.5, -2.5, 126.5, -126.5], np.float32)
+    assert list(quantise_identity(ties, O.ROUND_DEVICE_FLOOR)) == [1, -1, 3, -3, 127, -127]
+
+
 def test_row_invariants():
     rng = np.random.default_rng(4)
     x = (rng.standard_normal((64, 768)) * rng.uniform(0.01, 100, (64, 1))).astype(np.float32)
