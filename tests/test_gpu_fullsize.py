@@ -1,5 +1,7 @@
 """GPU parity at the benchmark configs' full sizes, through the C ABI.
 
+* config 1 up: the benched call (the K-tiled linear with bias) on the bench's
+  own inputs, sampled rows from every 256-row strip against oracle.q8_linear.
 * config 3: the fused W8A8 linear (bf16 x -> rotate + quantise -> int8 GEMM ->
   bf16) at M=32760, K=5120 for both of its shapes (N=5120 attention out-proj and
   N=13824 MLP up).  Sampled rows are compared bit for bit against the oracle
@@ -55,6 +57,44 @@ def test_config3_fused_linear(dev, orc, N):
     assert np.array_equal(acc[ri].cpu().numpy(), acco)
     yo = orc.epilogue(acco, so, sW.cpu().numpy(), u16(b))
     assert np.array_equal(u16(y[ri]), yo)
+
+
+def test_config1_up_benched_linear(dev, orc):
+    """The call the headline bench times, on its own inputs: phi_hip_q8_linear_kt
+    with the bf16 bias at M=4352, K=3072, N=12288 (weight packed K-tiled once).
+    Rows sampled from all 17 256-row strips (each strip's first and last rows,
+    and a stride through the rest) are compared bit for bit with oracle.q8_linear:
+    the int8 codes and fp32 scales the prologue wrote (unpacked from the K-tiled
+    layout), the int32 accumulators of the same kernel plan (i8_gemm_kt, int32
+    out, on those codes), and the bf16 outputs."""
+    M, K, N = 4352, 3072, 12288
+    print(f"config 1 up benched linear M={M} K={K} N={N}", flush=True)
+    x = synth.activations(M, K, seed=0, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    Wk = Q.pack_k_tiled(W)
+    qk = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = Q.q8_linear_kt(x, Wk, N, sW, b, q8=qk, s8=s8)
+    acc = Q.i8_gemm_kt(qk, Wk, M, N, K, None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    strips = np.arange(0, M, 256)
+    rows = np.unique(np.concatenate([strips, strips + 255, np.arange(0, M, 61), [M - 1]]))
+    assert len(np.unique(rows // 256)) == 17
+    # the K-tiled byte position of (r, k), as the layout defines it
+    r, k = rows[:, None], np.arange(K)[None, :]
+    s, rr = r // 256, r % 256
+    h = np.minimum(256, M - 256 * s)
+    pos = 256 * K * s + h * 64 * (k // 64) + 64 * rr + 16 * (((k // 16) % 4) ^ ((rr // 4) % 4)) + k % 16
+    q_rows = qk.cpu().numpy()[pos]
+    ri = torch.from_numpy(rows).to(dev)
+    yo, qo, so, acco = orc.q8_linear(u16(x[ri]), W.cpu().numpy(), sW.cpu().numpy(), u16(b))
+    assert np.array_equal(q_rows, qo), f"{(q_rows != qo).sum()} code mismatches"
+    assert np.array_equal(s8[ri].cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(acc[ri].cpu().numpy(), acco)
+    got = u16(y[ri])
+    assert np.array_equal(got, yo), f"{(got != yo).sum()} bf16 mismatches"
 
 
 @pytest.mark.parametrize("out", ["bf16", "f32"])

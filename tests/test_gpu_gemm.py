@@ -116,6 +116,31 @@ def test_epilogue_bit_exact(dev, orc, kernel, bias_kind, out, sb_scalar, M, N, K
         np.testing.assert_allclose(g32, alt, rtol=BF16_REL_TOL, atol=1e-30)
 
 
+@pytest.mark.parametrize("layout", ["row", "kt"])
+@pytest.mark.parametrize("M,N,K", [(4352, 4352, 512), (3000, 8000, 768)])
+def test_epilogue_many_tiles_per_workgroup(dev, orc, layout, M, N, K):
+    """The default plan at small K with more tiles than CUs: every workgroup
+    runs several tiles, so the next tile's first MFMAs inside the epilogue, the
+    once-a-tile bias conversion and the tile order's divisions all run between
+    tiles.  bf16 bias and bf16 output, bit for bit against the oracle."""
+    A, B = rand_i8((M, K), M + 11), rand_i8((N, K), N + 13)
+    g = torch.Generator().manual_seed(M + N)
+    sa = torch.rand(M, generator=g) * 0.05 + 0.002
+    sb = torch.rand(N, generator=g) * 0.05 + 0.002
+    bias = (torch.randn(N, generator=g) * 0.02).to(torch.bfloat16)
+    Ad, Bd = A.to(dev), B.to(dev)
+    if layout == "row":
+        C = Q.i8_gemm(Ad, Bd, sa.to(dev), sb.to(dev), bias.to(dev), out_dtype=torch.bfloat16)
+    else:
+        C = Q.i8_gemm_kt(Q.pack_k_tiled(Ad), Q.pack_k_tiled(Bd), M, N, K, sa.to(dev), sb.to(dev), bias.to(dev),
+                         out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    acc = orc.gemm_i8_i32_fast(A.numpy(), B.numpy())
+    want = orc.epilogue(acc, sa.numpy(), sb.numpy(), u16(bias), out="bf16")
+    got = u16(C)
+    assert np.array_equal(got, want), f"{(got != want).sum()} of {got.size} outputs differ"
+
+
 def test_reference_gemm_int8_equality(dev, orc):
     """No bias, fp32 out: the product equals the reference host gemm_int8's
     (float)acc * sx[m] * sw[n] (core/host/quant.cpp:223-236) bit for bit."""
