@@ -7,8 +7,21 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace phi_dev {
+
+// An integer tuning switch from the environment (the A/B switches the tests
+// and the bench set between launches): its value when set and inside
+// [lo, hi], else `dflt`.  Read at each launch, so a switch set between calls
+// takes effect; a value out of range is ignored rather than passed to a kernel.
+inline int env_switch(const char* name, int dflt, int lo, int hi) {
+    const char* e = getenv(name);
+    if (!e || !*e) return dflt;
+    char* end = nullptr;
+    const long v = strtol(e, &end, 10);
+    return (*end == '\0' && v >= lo && v <= hi) ? (int)v : dflt;
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));

@@ -348,8 +348,7 @@ hipError_t launch_lora_down(hipStream_t stream, const void* x, bool x_bf16, int6
                             int M, int K, int R) {
     const int esz = x_bf16 ? 2 : 4;
     if (K % LD_KC == 0 && (uintptr_t)x % 16 == 0 && (ldx * esz) % 16 == 0 && (uintptr_t)A % 16 == 0) {
-        const char* e = getenv("PHI_LORA_TR");  // A/B switch: ranks per wave (1, 2 or 4)
-        const int tr = e ? atoi(e) : 2;
+        const int tr = env_switch("PHI_LORA_TR", 2, 1, 4);  // A/B switch: ranks per wave (1, 2 or 4)
         if (tr == 1) return launch_down_rows<1>(stream, x, x_bf16, ldx, A, h, M, K, R);
         if (tr == 2) return launch_down_rows<2>(stream, x, x_bf16, ldx, A, h, M, K, R);
         return launch_down_rows<4>(stream, x, x_bf16, ldx, A, h, M, K, R);

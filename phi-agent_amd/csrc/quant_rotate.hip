@@ -628,9 +628,8 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
 // SIMD).  A small one (under 2^17 groups, about two waves of waves on the
 // chip) is bound by latency, and the most waves (R = 1) wins.
 static int tile_rounds(int64_t rows, int G) {
-    const char* env = getenv("PHI_QR_ROUNDS");  // A/B switch: force R where it fits
-    const int forced = env ? atoi(env) : 0;
-    if (forced >= 1 && forced <= QT_MAX_ROUNDS && (G + 4 * forced - 1) / (4 * forced) <= 16) return forced;
+    const int forced = env_switch("PHI_QR_ROUNDS", 0, 1, QT_MAX_ROUNDS);  // A/B switch: force R where it fits
+    if (forced && (G + 4 * forced - 1) / (4 * forced) <= 16) return forced;
     if (rows * G < (1 << 17) && G <= 64) return 1;
     int best = 1;
     double best_cost = 1e30;
@@ -663,8 +662,8 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
     // Runs of 8 blocks a XCD: config 1's prologue 11.0 -> 10.4 us, config 1
     // down's 32.3 -> 29.0 us (K-tiled codes; runs of 2 and 4 measured too).
-    const char* env = getenv("PHI_QR_RUN");  // A/B switch: log2 of the run length
-    const int lg_run = env ? atoi(env) : 3;
+    // A/B switch: log2 of the run length, 0..4 (the kernel shifts by it)
+    const int lg_run = env_switch("PHI_QR_RUN", 3, 0, 4);
     hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows,
                        G, q, ldq, s, qmax, 1.0f / qmax, rotate, pre, qkt, lg_run);
     return hipGetLastError();
