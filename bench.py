@@ -216,14 +216,26 @@ def bench_w8a8(cfg, steps, warmup, layout="kt", weights="uniform"):
     gemm_ms = sum(m.elapsed_time(z) for m, z in zip(mids, ends)) / steps
     pro_ms = (sum(ends[i - 1].elapsed_time(mids[i]) for i in range(1, steps)) / (steps - 1)) if steps > 1 else None
     ops = 2.0 * M * N * K
+    extra = {"prologue_us": None if pro_ms is None else pro_ms * 1e3, "gemm_us": gemm_ms * 1e3,
+             "fused_linear_tops": ops / (ms * 1e-3) / 1e12}
+    if layout == "kt":
+        # The drop-in's own path (linear_gemm without K-tiled weights): the
+        # row-major linear, `steps` of them timed like the headline region,
+        # after the other two regions.
+        start.record()
+        for _ in range(steps):
+            Q.q8_linear(x, W, sW, b, q8=q8, s8=s8, C=y)
+        end.record()
+        torch.cuda.synchronize()
+        row_ms = start.elapsed_time(end) / steps
+        extra["row_major_linear_us"] = row_ms * 1e3
+        extra["row_major_linear_tops"] = ops / (row_ms * 1e-3) / 1e12
     return {
         "value": ops / (ms * 1e-3) / 1e12, "ms": ms, "gemm_ms": gemm_ms, "prologue_ms": pro_ms,
         "roofline": {"bound": "mfma", "achieved": ops / (gemm_ms * 1e-3) / 1e12,
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": ops / (gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "traffic": None},
-        "dtype": "int8", "extra": {"prologue_us": None if pro_ms is None else pro_ms * 1e3,
-                                   "gemm_us": gemm_ms * 1e3,
-                                   "fused_linear_tops": ops / (ms * 1e-3) / 1e12},
+        "dtype": "int8", "extra": extra,
     }
 
 

@@ -954,6 +954,41 @@ void expand_grouped(GpuCtx& g, const StTensor& t, const GroupedParts& parts, int
 int8_t* dev_i8(const GpuAlloc& a, u64 off = 0) { return (int8_t*)(a.res->base + a.off + off); }
 float* dev_f32(const GpuAlloc& a, u64 off = 0) { return (float*)(a.res->base + a.off + off); }
 
+// Where a loader writes an int8 weight's rows: straight into the weight's
+// allocation, or, for a K-tiled weight, into a charged load scratch that
+// finish() packs into the allocation (phi_hip_pack_k_tiled) once every row is
+// there.
+class WeightRows {
+public:
+    WeightRows(GpuCtx& g, const GpuAlloc& w, i64 n, i64 k, bool k_tiled)
+        : g_(g), w_(w), n_(n), k_(k) {
+        if (k_tiled) staging_.emplace(*g.ctx, (u64)n * (u64)k);
+    }
+    int8_t* row(i64 r) const {
+        return staging_ ? (int8_t*)staging_->at((u64)r * (u64)k_) : dev_i8(w_, (u64)r * (u64)k_);
+    }
+    void upload(i64 r, const void* src, u64 bytes) {
+        if (staging_) g_.ctx->upload(staging_->b, src, bytes, (u64)r * (u64)k_);
+        else g_.ctx->upload(w_.res, src, bytes, w_.off + (u64)r * (u64)k_);
+    }
+    // True when the weight ended up K-tiled.
+    bool finish() {
+        if (!staging_) return false;
+        g_.ctx->check(phi_hip_pack_k_tiled(g_.ctx->stream(), row(0), k_, n_, k_, dev_i8(w_)), "pack_k_tiled");
+        g_.ctx->submit();
+        return true;
+    }
+
+private:
+    GpuCtx& g_;
+    GpuAlloc w_;
+    i64 n_, k_;
+    std::optional<Scratch> staging_;
+};
+
+// The shapes the K-tiled linear takes (phi_hip_q8_linear_kt with fp32 output).
+bool k_tiled_shape(i64 n, i64 k) { return n > 0 && k > 0 && k % 256 == 0 && k <= 16384 && n % 4 == 0; }
+
 // One plain int8 weight's scales, decoded from their table.
 std::vector<float> weight_scales(const SafeTensors& st, const std::string& base, i64 n) {
     const StTensor& sc = st.require(base + ".weight_scale");
@@ -979,6 +1014,7 @@ QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::strin
                          ": a dense float weight runs the dense GEMM, which the quantized-linear library does not "
                          "serve");
     const bool touched = lora && lora->touches(base);
+    const bool kt = g.k_tiled_weights && k_tiled_shape(n, k);
     QuantLinear q;
     q.n = n;
     q.k = k;
@@ -987,7 +1023,9 @@ QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::strin
         if (t.nbytes != nk) throw MediaError("load_quant_linear: '" + base + ".weight' is not [N, K] int8");
         const std::vector<float> s = weight_scales(st, base, n);
         q.w = alloc(nk);
-        g.ctx->upload(q.w.res, t.data, t.nbytes, q.w.off);
+        WeightRows rows(g, q.w, n, k, kt);
+        rows.upload(0, t.data, t.nbytes);
+        q.k_tiled = rows.finish();
         q.scale = alloc((u64)n * 4);
         g.ctx->upload(q.scale.res, s.data(), (u64)n * 4, q.scale.off);
         return q;
@@ -1003,7 +1041,9 @@ QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::strin
         if (!why.empty()) throw MediaError("load_quant_linear: '" + base + "' (" + L.spec.format + "): " + why);
         q.w = alloc(nk);
         q.scale = alloc((u64)n * 4);
-        expand_grouped(g, t, parts, dev_i8(q.w), dev_f32(q.scale), st);
+        WeightRows rows(g, q.w, n, k, kt);
+        expand_grouped(g, t, parts, rows.row(0), dev_f32(q.scale), st);
+        q.k_tiled = rows.finish();
         return q;
     }
     if (L.spec.valid && L.spec.format == "convrot_w4a4")
@@ -1030,7 +1070,9 @@ QuantLinear load_quant_linear(GpuCtx& g, const SafeTensors& st, const std::strin
     }
     q.w = alloc(nk);
     q.scale = alloc((u64)n * 4);
-    requant_rows_device(g, st, t, n, k, plan, dev_i8(q.w), dev_f32(q.scale));
+    WeightRows rows(g, q.w, n, k, kt);
+    requant_rows_device(g, st, t, n, k, plan, rows.row(0), dev_f32(q.scale));
+    q.k_tiled = rows.finish();
     return q;
 }
 
@@ -1070,6 +1112,7 @@ QuantLinear load_quant3_linear(GpuCtx& g, const SafeTensors& st, const std::stri
     }
     q.n = total;
     const u64 nk = checked_mul((u64)q.n, (u64)k, "load_quant3_linear");
+    const bool kt = g.k_tiled_weights && k_tiled_shape(q.n, k);
     if (raw_int8 && !touched) {
         // The raw int8 rows and scale vectors, concatenated.
         std::vector<float> scales;
@@ -1080,8 +1123,9 @@ QuantLinear load_quant3_linear(GpuCtx& g, const SafeTensors& st, const std::stri
                 throw MediaError("load_quant3_linear: '" + bases[i] + ".weight' is not [N, K] int8");
         }
         q.w = alloc(nk);
-        for (int i = 0; i < 3; i++)
-            g.ctx->upload(q.w.res, ts[i]->data, ts[i]->nbytes, q.w.off + (u64)row0[i] * (u64)k);
+        WeightRows rows(g, q.w, q.n, k, kt);
+        for (int i = 0; i < 3; i++) rows.upload(row0[i], ts[i]->data, ts[i]->nbytes);
+        q.k_tiled = rows.finish();
         q.scale = alloc((u64)scales.size() * 4);
         g.ctx->upload(q.scale.res, scales.data(), scales.size() * 4, q.scale.off);
         return q;
@@ -1092,10 +1136,11 @@ QuantLinear load_quant3_linear(GpuCtx& g, const SafeTensors& st, const std::stri
         throw MediaError("load_quant3_linear: K=" + std::to_string(k) + " is not a multiple of the convrot group 256");
     q.w = alloc(nk);
     q.scale = alloc((u64)q.n * 4);
+    WeightRows rows(g, q.w, q.n, k, kt);
     for (int i = 0; i < 3; i++) {
         const StTensor& t = *ts[i];
         const SafeTensors::WeightLayout L = st.weight_layout(t.name);
-        int8_t* qi = dev_i8(q.w, (u64)row0[i] * (u64)k);
+        int8_t* qi = rows.row(row0[i]);
         float* si = dev_f32(q.scale, (u64)row0[i] * 4);
         RequantPlan plan;
         plan.rotate = rotate;
@@ -1131,6 +1176,7 @@ QuantLinear load_quant3_linear(GpuCtx& g, const SafeTensors& st, const std::stri
         }
         requant_rows_device(g, st, t, rows_of[i], k, plan, qi, si);
     }
+    q.k_tiled = rows.finish();
     return q;
 }
 
@@ -1253,6 +1299,20 @@ void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 
     if (!w.w || !w.scale) throw MediaError("linear_gemm: the int8 weight is empty");
     if (!q8 || !s8) throw MediaError("linear_gemm: the int8 path needs activation scratch");
     if (!g.ctx) throw MediaError("linear_gemm: no compute context");
+    if (w.k_tiled) {
+        // The prologue writes q8 K-tiled and the GEMM reads both operands that
+        // way: the same fp32 output as the row-major pair below.
+        if (x.bytes < (u64)m * (u64)k * 4 || out.bytes < (u64)m * (u64)w.n * 4 || q8.bytes < (u64)m * (u64)k ||
+            s8.bytes < (u64)m * 4)
+            throw MediaError("linear_gemm: a buffer is smaller than the [" + std::to_string(m) + ", " +
+                             std::to_string(k) + "] x [" + std::to_string(w.n) + "] linear needs");
+        g.ctx->check(phi_hip_q8_linear_kt(g.ctx->stream(), cat(x.res, x.off), PHI_F32, k, m, k,
+                                          (const int8_t*)cat(w.w.res, w.w.off), (const float*)cat(w.scale.res, w.scale.off),
+                                          0, nullptr, PHI_F32, w.n, at(out.res, out.off), PHI_F32, w.n,
+                                          (int8_t*)at(q8.res, q8.off), (float*)at(s8.res, s8.off), PHI_ROUND_HALF_AWAY),
+                     "linear_gemm");
+        return;
+    }
     QuantConvrotArgs qa;
     qa.x = x.res;
     qa.x_offset = x.off;

@@ -200,6 +200,9 @@ struct QuantLinear {
     GpuAlloc d;      // dense float storage (not served by this library)
     DType dtype = DType::Unknown;
     i64 n = 0, k = 0;
+    // w holds the K-tiled operand layout (phi_hip_pack_k_tiled) rather than
+    // row-major [n, k]; only linear_gemm reads such a weight.
+    bool k_tiled = false;
     bool dense() const { return dtype == DType::F16 || dtype == DType::BF16 || dtype == DType::F32; }
 };
 
@@ -217,6 +220,12 @@ struct GpuCtx {
     GpuArena* wa = nullptr;    // weights, reset per layer
     GpuArena* aa = nullptr;    // activations, reset per step
     GpuArena* keep = nullptr;  // long-lived buffers
+    // load_quant_linear / load_quant3_linear store an int8 weight K-tiled where
+    // the shape allows it (K % 256 == 0, K <= 16384, n % 4 == 0), so
+    // linear_gemm runs the K-tiled prologue and GEMM (the same output, bit for
+    // bit, about 8 % faster at the DiT shapes).  Off by default: a caller that
+    // hands QuantLinear::w to dispatch_int8_gemm itself needs it row-major.
+    bool k_tiled_weights = false;
     bool ok() const { return ctx && wa && aa; }
 
     GpuAlloc walloc(u64 bytes);
@@ -232,7 +241,9 @@ struct GpuCtx {
     void new_step();   // activation arena reset
 };
 
-// rotate+quantise x into q8/s8, then the int8 GEMM; out is [m, n] fp32.
+// rotate+quantise x into q8/s8, then the int8 GEMM; out is [m, n] fp32.  A
+// K-tiled weight (QuantLinear::k_tiled) runs phi_hip_q8_linear_kt: q8 then
+// holds the codes K-tiled, and out's rows must be 16-byte aligned.
 void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 k,
                  const GpuAlloc& out, const GpuAlloc& q8, const GpuAlloc& s8);
 

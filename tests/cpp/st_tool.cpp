@@ -5,20 +5,23 @@
 //
 //   st_tool spec <json text>                       parse_quant_spec -> JSON line
 //   st_tool probe <file> <base>                    layout of <base>.weight -> JSON line (no GPU)
-//   st_tool linear <file> <base> <x.f32> <M> <out.f32>
+//   st_tool linear <file> <base> <x.f32> <M> <out.f32> [<lora> <strength>]...
 //        load_quant_linear, then linear_gemm of x [M, K] fp32 into out [M, N] fp32 (GPU)
+//   st_tool linear_kt ...   the same with GpuCtx::k_tiled_weights set
 //   st_tool int4 <file> <base> <x.f32> <M> <out.f32>
 //        upload_quant_linear_w4a4, quant_convrot (qmax 7), int4 GEMM into out (GPU)
 //   st_tool weights <how> <file> <out.bin> <base> [<base_k> <base_v>] [lora <path> <strength>]...
 //        how = load (load_quant_linear), load3 (load_quant3_linear) or upload_i8
 //        (upload_quant_linear_i8), with an optional LoraSet; writes n, k (int64)
-//        then the int8 weight [n, k] and its fp32 scales [n] (GPU)
+//        then the int8 weight [n, k] and its fp32 scales [n] (GPU).  load_kt and
+//        load3_kt set GpuCtx::k_tiled_weights and unpack the K-tiled weight.
 //   st_tool lora_probe <target> <n> <k> lora <path> <strength>...
 //        LoraSet::touches / deltas_for -> JSON line (no GPU)
 //   st_tool tail <out.bin> <n> <k> <base>:<row0>:<rows>... lora <path> <strength>...
 //        load_lora_tail over the modules; writes rank (int64), at [rank, k] and
 //        bt [n, rank] fp32 (GPU)
 // Exit code 0 on success; a MediaError prints "error: <message>" and exits 3.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -66,8 +69,26 @@ static int lora_args(int argc, char** argv, int from, LoraSet& lora) {
     return end;
 }
 
+// A K-tiled [rows, K] matrix back in row-major order (the layout's definition:
+// 256-row strips of h rows, each 64-byte K-step of a strip one h x 64 block, the
+// 16-byte chunk c of strip row r in slot c ^ ((r >> 2) & 3)).
+static std::vector<int8_t> unpack_k_tiled(const std::vector<int8_t>& p, i64 rows, i64 K) {
+    std::vector<int8_t> out(p.size());
+    for (i64 r = 0; r < rows; r++) {
+        const i64 strip = r / 256, rr = r % 256, h = std::min<i64>(256, rows - 256 * strip);
+        for (i64 k = 0; k < K; k++) {
+            const i64 slot = ((k / 16) % 4) ^ ((rr / 4) % 4);
+            out[(size_t)(r * K + k)] = p[(size_t)(256 * K * strip + h * 64 * (k / 64) + 64 * rr + 16 * slot + k % 16)];
+        }
+    }
+    return out;
+}
+
 static int weights(int argc, char** argv) {
-    const std::string how = argv[2];
+    std::string how = argv[2];
+    const bool want_kt = how.size() > 3 && how.compare(how.size() - 3, 3, "_kt") == 0;
+    if (want_kt) how.resize(how.size() - 3);
+    bool k_tiled = false;
     SafeTensors st(argv[3]);
     const char* out = argv[4];
     LoraSet lora;
@@ -81,14 +102,15 @@ static int weights(int argc, char** argv) {
     g.ctx = &ctx;
     g.wa = &wa;
     g.aa = &aa;
+    g.k_tiled_weights = want_kt;
     GpuAlloc w, s;
     i64 n = 0, k = 0;
     if (how == "load" && end == 6) {
         const QuantLinear q = load_quant_linear(g, st, argv[5], nullptr, lp);
-        w = q.w, s = q.scale, n = q.n, k = q.k;
+        w = q.w, s = q.scale, n = q.n, k = q.k, k_tiled = q.k_tiled;
     } else if (how == "load3" && end == 8) {
         const QuantLinear q = load_quant3_linear(g, st, argv[5], argv[6], argv[7], nullptr, lp);
-        w = q.w, s = q.scale, n = q.n, k = q.k;
+        w = q.w, s = q.scale, n = q.n, k = q.k, k_tiled = q.k_tiled;
     } else if (how == "upload_i8" && end == 6) {
         const I8Upload u = upload_quant_linear_i8(g, st, argv[5], wa, lp);
         w = u.w, s = u.s, n = u.n, k = u.k;
@@ -101,6 +123,7 @@ static int weights(int argc, char** argv) {
     std::vector<float> sc((size_t)n);
     ctx.download(w.res, wq.data(), wq.size(), w.off);
     ctx.download(s.res, sc.data(), sc.size() * 4, s.off);
+    if (k_tiled) wq = unpack_k_tiled(wq, n, k);
     FILE* f = fopen(out, "wb");
     if (!f) throw MediaError(std::string("cannot write ") + out);
     write_bytes(f, &n, 8);
@@ -108,8 +131,8 @@ static int weights(int argc, char** argv) {
     write_bytes(f, wq.data(), wq.size());
     write_bytes(f, sc.data(), sc.size() * 4);
     fclose(f);
-    printf("{\"n\": %lld, \"k\": %lld, \"arena_used\": %llu}\n", (long long)n, (long long)k,
-           (unsigned long long)wa.used());
+    printf("{\"n\": %lld, \"k\": %lld, \"arena_used\": %llu, \"k_tiled\": %s}\n", (long long)n, (long long)k,
+           (unsigned long long)wa.used(), k_tiled ? "true" : "false");
     return 0;
 }
 
@@ -196,11 +219,14 @@ int main(int argc, char** argv) {
             fflush(stdout);
             return 0;
         }
-        if ((op == "linear" && argc >= 7 && (argc - 7) % 2 == 0) || (op == "int4" && argc == 7)) {
+        const bool linear_op = op == "linear" || op == "linear_kt";
+        if ((linear_op && argc >= 7 && (argc - 7) % 2 == 0) || (op == "int4" && argc == 7)) {
             const i64 M = atoll(argv[5]);
             ComputeContext ctx(0);
             GpuCtx g;
             g.ctx = &ctx;
+            g.k_tiled_weights = op == "linear_kt";
+            bool k_tiled = false;
             const StTensor& t = st.require(base + ".weight");
             const i64 K = st.logical_cols(t), N = t.shape[0];
             std::vector<float> x = read_f32(argv[4], (size_t)(M * K)), y((size_t)(M * N));
@@ -213,10 +239,11 @@ int main(int argc, char** argv) {
             const u64 o_x = 0, o_q = (u64)M * K * 4, o_s = (o_q + M * K + 255) & ~(u64)255,
                       o_y = (o_s + M * 4 + 255) & ~(u64)255;
             ctx.upload(work, x.data(), x.size() * 4, o_x);
-            if (op == "linear") {
+            if (linear_op) {
                 LoraSet lora;
                 for (int i = 7; i + 1 < argc; i += 2) lora.add(argv[i], (float)atof(argv[i + 1]));
                 const QuantLinear ql = load_quant_linear(g, st, base, nullptr, lora.empty() ? nullptr : &lora);
+                k_tiled = ql.k_tiled;
                 linear_gemm(g, ql, GpuAlloc{work, o_x, (u64)M * K * 4}, M, K, GpuAlloc{work, o_y, (u64)M * N * 4},
                             GpuAlloc{work, o_q, (u64)M * K}, GpuAlloc{work, o_s, (u64)M * 4});
             } else {
@@ -247,8 +274,8 @@ int main(int argc, char** argv) {
             ctx.download(work, y.data(), y.size() * 4, o_y);
             ctx.release_buffer(work);
             write_f32(argv[6], y);
-            printf("{\"n\": %lld, \"k\": %lld, \"arena_used\": %llu}\n", (long long)N, (long long)K,
-                   (unsigned long long)arena.used());
+            printf("{\"n\": %lld, \"k\": %lld, \"arena_used\": %llu, \"k_tiled\": %s}\n", (long long)N,
+                   (long long)K, (unsigned long long)arena.used(), k_tiled ? "true" : "false");
             return 0;
         }
         fprintf(stderr, "st_tool: bad arguments for %s\n", op.c_str());

@@ -28,10 +28,14 @@ def _tool():
 
 
 def run_linear(dev, path, base, x, op="linear"):
+    """op "linear_kt" loads with GpuCtx::k_tiled_weights: the weight must come
+    out K-tiled and linear_gemm must give the row-major path's bits."""
     xf = os.path.join(os.path.dirname(path), "x.f32")
     of = os.path.join(os.path.dirname(path), "y.f32")
     x.numpy().astype(np.float32).tofile(xf)
-    C.run(op, path, base, xf, x.shape[0], of)
+    out = C.run(op, path, base, xf, x.shape[0], of)
+    if op == "linear_kt":
+        assert '"k_tiled": true' in out.stdout, out.stdout
     return np.fromfile(of, np.float32)
 
 
@@ -49,7 +53,8 @@ REL = {torch.float32: Q.F32, torch.float16: Q.F16, torch.bfloat16: Q.BF16,
        torch.float8_e4m3fn: Q.F8_E4M3, torch.float8_e5m2: Q.F8_E5M2, torch.uint8: Q.U8_E4M3}
 
 
-def test_int8_tensorwise_checkpoint(dev, orc, tmp_path):
+@pytest.mark.parametrize("op", ["linear", "linear_kt"])
+def test_int8_tensorwise_checkpoint(dev, orc, tmp_path, op):
     N, K, M = 200, 1024, 37
     g = torch.Generator().manual_seed(5)
     W = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
@@ -58,7 +63,7 @@ def test_int8_tensorwise_checkpoint(dev, orc, tmp_path):
         "l.weight": W, "l.weight_scale": s,
         "l.comfy_quant": C.comfy_blob({"format": "int8_tensorwise", "convrot": True, "convrot_groupsize": 256})})
     x = synth.activations(M, K, seed=6).float()
-    y = run_linear(dev, path, "l", x).reshape(M, N)
+    y = run_linear(dev, path, "l", x, op=op).reshape(M, N)
     want = orc.q8_linear(x.numpy(), W.numpy(), s.numpy(), out="f32")[0]
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
 
@@ -66,7 +71,8 @@ def test_int8_tensorwise_checkpoint(dev, orc, tmp_path):
 @pytest.mark.parametrize("fmt", ["asym_w4a8_int8", "w6a8_int8"])
 @pytest.mark.parametrize("rel", [torch.float16, torch.bfloat16, torch.float32, torch.float8_e4m3fn, torch.uint8])
 @pytest.mark.parametrize("variant", ["plain", "codebook", "scalar_channel", "correction"])
-def test_grouped_checkpoint(dev, orc, tmp_path, fmt, rel, variant):
+@pytest.mark.parametrize("op", ["linear", "linear_kt"])
+def test_grouped_checkpoint(dev, orc, tmp_path, fmt, rel, variant, op):
     six = fmt == "w6a8_int8"
     if six and variant == "codebook":
         pytest.skip("six-bit weights carry no codebook")
@@ -87,7 +93,7 @@ def test_grouped_checkpoint(dev, orc, tmp_path, fmt, rel, variant):
         t["b.weight_correction"] = corr
     path = C.write(str(tmp_path / "g.safetensors"), t)
     x = synth.activations(M, K, seed=7).float()
-    y = run_linear(dev, path, "b", x).reshape(M, N)
+    y = run_linear(dev, path, "b", x, op=op).reshape(M, N)
     q, s = orc.w4a8_expand(codes.view(torch.uint8).numpy(), np_of(srel), REL[rel], sch.numpy(), k=K, group=group,
                            codebook=None if cb is None else cb.numpy(),
                            correction=None if corr is None else corr.numpy(), layout=1 if six else 0)
@@ -176,20 +182,23 @@ def oracle_grouped(orc, t, prefix, K, group):
                            t[f"{prefix}.weight_s_channel"].numpy(), k=K, group=group)
 
 
-def test_load3_int8_concatenates(dev, tmp_path):
+@pytest.mark.parametrize("how", ["load3", "load3_kt"])
+def test_load3_int8_concatenates(dev, tmp_path, how):
     """Three int8_tensorwise weights: rows q then k then v, scales likewise,
-    verbatim (core/models/model_common.cpp:1457-1480)."""
+    verbatim (core/models/model_common.cpp:1457-1480); load3_kt stores the
+    stacked matrix K-tiled, which unpacks to the same bytes."""
     K = 512
     t = {**int8_weight_tensors("a.to_q", 96, K, 1), **int8_weight_tensors("a.to_k", 32, K, 2),
          **int8_weight_tensors("a.to_v", 64, K, 3)}
     path = C.write(str(tmp_path / "qkv.safetensors"), t)
-    q, s = loaded(tmp_path, "load3", path, "a.to_q", "a.to_k", "a.to_v")
+    q, s = loaded(tmp_path, how, path, "a.to_q", "a.to_k", "a.to_v")
     want_q = np.concatenate([t[f"a.to_{x}.weight"].numpy() for x in "qkv"])
     want_s = np.concatenate([t[f"a.to_{x}.weight_scale"].numpy() for x in "qkv"])
     assert np.array_equal(q, want_q) and np.array_equal(s.view(np.uint32), want_s.view(np.uint32))
 
 
-def test_load3_grouped_and_mixed(dev, orc, tmp_path):
+@pytest.mark.parametrize("how", ["load3", "load3_kt"])
+def test_load3_grouped_and_mixed(dev, orc, tmp_path, how):
     """Grouped q|k|v: each part's rows are its decode + row requantise; a plain
     int8 part among them is decoded and requantised without a rotation (the
     requant spec of a stored-rotated base_q), as the reference's requant path."""
@@ -197,14 +206,14 @@ def test_load3_grouped_and_mixed(dev, orc, tmp_path):
     t = {**grouped_weight_tensors("b.q", 64, K, group, 4), **grouped_weight_tensors("b.k", 32, K, group, 5),
          **grouped_weight_tensors("b.v", 48, K, group, 6)}
     path = C.write(str(tmp_path / "g.safetensors"), t)
-    q, s = loaded(tmp_path, "load3", path, "b.q", "b.k", "b.v")
+    q, s = loaded(tmp_path, how, path, "b.q", "b.k", "b.v")
     parts = [oracle_grouped(orc, t, x, K, group) for x in ("b.q", "b.k", "b.v")]
     assert np.array_equal(q, np.concatenate([p[0] for p in parts]))
     assert np.array_equal(s.view(np.uint32), np.concatenate([p[1] for p in parts]).view(np.uint32))
     t2 = {**grouped_weight_tensors("c.q", 64, K, group, 7), **int8_weight_tensors("c.k", 40, K, 8),
           **grouped_weight_tensors("c.v", 48, K, group, 9)}
     path = C.write(str(tmp_path / "m.safetensors"), t2)
-    q, s = loaded(tmp_path, "load3", path, "c.q", "c.k", "c.v")
+    q, s = loaded(tmp_path, how, path, "c.q", "c.k", "c.v")
     qk, sk = orc.quantize_rows(dequant_i8(t2, "c.k"), rotate=False)
     assert np.array_equal(q[64:104], qk) and np.array_equal(s[64:104].view(np.uint32), sk.view(np.uint32))
     qq, sq = oracle_grouped(orc, t2, "c.q", K, group)
@@ -286,11 +295,13 @@ def lora_scale(strength, alpha, rank):
     return np.float32(np.float32(np.float32(strength) * np.float32(alpha)) / np.float32(rank))
 
 
+@pytest.mark.parametrize("how", ["load", "load_kt"])
 @pytest.mark.parametrize("convrot", [True, False])
-def test_lora_fold_load_quant_linear(dev, orc, tmp_path, convrot):
+def test_lora_fold_load_quant_linear(dev, orc, tmp_path, convrot, how):
     """load_quant_linear with a LoRA that touches the module: decode, rotate
     back to the original basis, add the deltas file by file, rotate and
-    quantise (core/models/model_common.cpp:1011-1030)."""
+    quantise (core/models/model_common.cpp:1011-1030); load_kt stores the
+    result K-tiled, which unpacks to the same bytes."""
     N, K, r = 64, 512, 8
     t = int8_weight_tensors("blk.attn", N, K, 15, convrot=convrot)
     path = C.write(str(tmp_path / "w.safetensors"), t)
@@ -298,7 +309,7 @@ def test_lora_fold_load_quant_linear(dev, orc, tmp_path, convrot):
     f2, A2, B2 = lora_tensors("diffusion_model.blk.attn", N, K, 4, 17)
     l1 = C.lora_file(str(tmp_path / "l1.safetensors"), f1)
     l2 = C.lora_file(str(tmp_path / "l2.safetensors"), f2, metadata={"lora_alpha": "2"})
-    q, s = loaded(tmp_path, "load", path, "blk.attn", loras=((l1, 0.7), (l2, 1.5)))
+    q, s = loaded(tmp_path, how, path, "blk.attn", loras=((l1, 0.7), (l2, 1.5)))
     w = dequant_i8(t, "blk.attn")
     if convrot:
         w = orc.convrot(w)
@@ -310,7 +321,7 @@ def test_lora_fold_load_quant_linear(dev, orc, tmp_path, convrot):
     # A LoRA for another module leaves the weight verbatim.
     f3, _, _ = lora_tensors("blk.mlp", N, K, r, 18)
     l3 = C.lora_file(str(tmp_path / "l3.safetensors"), f3)
-    q, s = loaded(tmp_path, "load", path, "blk.attn", loras=((l3, 1.0),))
+    q, s = loaded(tmp_path, how, path, "blk.attn", loras=((l3, 1.0),))
     if convrot:
         assert np.array_equal(q, t["blk.attn.weight"].numpy())
 
