@@ -405,10 +405,27 @@ phi_status phi_hip_silu_gate(phi_stream_t stream, const void* gx, int x_dtype, i
  * computes them (core/host/st.cpp:601-700): PHI_I8 codes, or PHI_I4 signed
  * nibbles (a bare packed int4), times their row's scale ((float)q * s;
  * row_scale [rows], or [1] when scale_scalar; NULL means 1 for PHI_I4),
- * PHI_F16 / PHI_BF16 widened exactly, PHI_F32 copied.  src [rows, lds]
- * elements (bytes for PHI_I4), out [rows, ldo] fp32. */
+ * PHI_F8_E4M3 / PHI_F8_E5M2 codes decoded and times the row scale (NULL
+ * means 1; dequant_fp8_row, core/host/quant.cpp:433-439), PHI_F16 / PHI_BF16
+ * widened exactly, PHI_F32 copied.  src [rows, lds] elements (bytes for
+ * PHI_I4), out [rows, ldo] fp32. */
 phi_status phi_hip_dequant_rows(phi_stream_t stream, const void* src, int src_dtype, int64_t rows, int64_t cols,
                                 int64_t lds, const float* row_scale, int scale_scalar, float* out, int64_t ldo);
+
+/* nvfp4 / mxfp4 weight rows in fp32 (replaces the host loop of
+ * dequant_nvfp4_row, core/host/quant.cpp:390-431, as SafeTensors::dequant_rows
+ * calls it, core/host/st.cpp:465-503): for rows row0 .. row0 + rows - 1 of the
+ * weight, out[r][c] = (e2m1(code) * block_scale[i]) * global_scale[r], where
+ * code is column c's nibble of codes + r * codes_ld (even columns in the HIGH
+ * nibble) and i is (row0 + r, c / block)'s index in the cuBLAS-tiled table of
+ * scale_rows x scale_cols entries (already decoded to fp32; NULL, or fewer
+ * than 4 columns: 1).  global_scale: [rows], [1] when global_scalar, or NULL
+ * (1).  block <= 0 means 16.  PHI_ERR_SHAPE when the table does not cover a
+ * (row, block) the call reads. */
+phi_status phi_hip_dequant_fp4_rows(phi_stream_t stream, const uint8_t* codes, int64_t codes_ld, int64_t row0,
+                                    int64_t rows, int64_t k, const float* block_scale, int64_t scale_rows,
+                                    int64_t scale_cols, int64_t block, const float* global_scale, int global_scalar,
+                                    float* out, int64_t ldo);
 
 /* The 256-wide J-2R rotation of fp32 rows alone, y = H x per group with the
  * reference's butterfly order and final 1/16 (convrot_forward,

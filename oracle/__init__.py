@@ -68,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.orc_f8_e5m2_to_f32.restype = ctypes.c_float
         L.orc_scale_at.argtypes = [P, I, I64]
         L.orc_scale_at.restype = ctypes.c_float
+        L.orc_dequant_fp8_rows.argtypes = [P, I64, I64, I64, I, P, P]
+        L.orc_dequant_fp4_rows.argtypes = [P, I64, I64, I64, I64, P, I, I64, I64, I64, P, P]
         L.orc_round_forms_differ.argtypes = [P, I64]
         L.orc_round_forms_differ.restype = I64
         _lib = L
@@ -132,6 +134,40 @@ def quantize_rows(x, *, rotate=True, qmax=127.0, round_mode=ROUND_HALF_AWAY, x_i
     if rc != 0:
         raise ValueError(f"quantize_rows: cols={cols} is not a multiple of 256")
     return q, s
+
+
+def dequant_fp8_rows(codes, dtype, scale=None) -> np.ndarray:
+    """fp8 weight rows in fp32: f8(code) * scale[r] (dequant_fp8_row,
+    core/host/quant.cpp:433-439).  codes uint8 [rows, k]; dtype F8_E4M3 or
+    F8_E5M2; scale None or float32 [rows]."""
+    codes = _c(codes, np.uint8)
+    rows, k = codes.shape
+    sc = None if scale is None else _c(np.broadcast_to(np.asarray(scale, np.float32).reshape(-1), (rows,)), np.float32)
+    out = np.empty((rows, k), np.float32)
+    lib().orc_dequant_fp8_rows(_p(codes), k, rows, k, dtype, _p(sc), _p(out))
+    return out
+
+
+def dequant_fp4_rows(codes, k, table=None, table_dtype=F8_E4M3, block=16, global_scale=None, row0=0) -> np.ndarray:
+    """nvfp4 / mxfp4 weight rows row0 .. row0 + rows - 1 in fp32
+    (dequant_nvfp4_row, core/host/quant.cpp:390-431): codes uint8 [rows, >= k/2]
+    (even column in the high nibble), table the stored 2-D block-scale table
+    (cuBLAS tiled layout) as raw elements of table_dtype (uint8 for the fp8
+    spellings, uint16 bits for f16/bf16, float32), global_scale None or float32
+    [rows] / [1]."""
+    codes = _c(codes, np.uint8)
+    rows, ld = codes.shape
+    if table is not None:
+        table = np.ascontiguousarray(table)
+        t_rows, t_cols = table.shape if table.ndim == 2 else (1, table.size)
+    else:
+        t_rows = t_cols = 0
+    g = None if global_scale is None else _c(np.broadcast_to(np.asarray(global_scale, np.float32).reshape(-1),
+                                                             (rows,)), np.float32)
+    out = np.empty((rows, k), np.float32)
+    lib().orc_dequant_fp4_rows(_p(codes), ld, row0, rows, k, _p(table), table_dtype, t_rows, t_cols, block, _p(g),
+                               _p(out))
+    return out
 
 
 def round_forms_differ(cap: int = 16) -> tuple[int, np.ndarray]:

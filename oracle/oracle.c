@@ -443,3 +443,66 @@ void orc_add_mul(const float* a, const float* b, const float* c, float* y, int64
     for (int64_t r = 0; r < rows; r++)
         for (int64_t k = 0; k < cols; k++) y[r * cols + k] = fmaf(b[r * cols + k], c[k], a[r * cols + k]);
 }
+
+/* ------------------------------------------------------------------------ */
+/* fp8 and nvfp4 / mxfp4 weights                                            */
+/* ------------------------------------------------------------------------ */
+
+/* core/host/quant.cpp:433-439 */
+void orc_dequant_fp8_rows(const uint8_t* codes, int64_t ld, int64_t rows, int64_t k, int dtype, const float* scale,
+                          float* out) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float s = scale ? scale[r] : 1.0f;
+        for (int64_t c = 0; c < k; c++) {
+            const uint8_t b = codes[r * ld + c];
+            out[r * k + c] = (dtype == ORC_F8_E5M2 ? orc_f8_e5m2_to_f32(b) : orc_f8_e4m3_to_f32(b)) * s;
+        }
+    }
+}
+
+/* E2M1 (core/util/media_common.cpp:179-185): magnitudes 0, .5, 1, 1.5, 2, 3,
+ * 4, 6 by the low three bits, bit 3 the sign. */
+static float e2m1(uint8_t nib) {
+    static const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    return (nib & 8) ? -mag[nib & 7] : mag[nib & 7];
+}
+
+/* core/host/quant.cpp:390-410: (row, block) in the cuBLAS tiled table. */
+static int64_t tiled_index(int64_t row, int64_t blk, int64_t nb_c, int64_t cols) {
+    const int64_t i_r = row / 128, h = row % 128, i_c = blk / 4, w = blk % 4, a = h / 32, b = h % 32;
+    const int64_t flat = (i_r * nb_c + i_c) * 512 + b * 16 + a * 4 + w;
+    return (flat / cols) * cols + flat % cols;
+}
+
+static size_t scale_bytes(int dtype) {
+    switch (dtype) {
+        case ORC_F32: return 4;
+        case ORC_F16:
+        case ORC_BF16: return 2;
+        default: return 1;
+    }
+}
+
+/* core/host/quant.cpp:412-431, with the row's global scale as
+ * core/host/st.cpp:494-503 passes it. */
+void orc_dequant_fp4_rows(const uint8_t* codes, int64_t ld, int64_t row0, int64_t rows, int64_t k,
+                          const void* table, int table_dtype, int64_t table_rows, int64_t table_cols, int64_t block,
+                          const float* global, float* out) {
+    if (block <= 0) block = 16;
+    const int64_t nb_c = table_cols > 0 ? table_cols / 4 : 0;
+    const int have = table != NULL && nb_c > 0 && table_rows > 0;
+    for (int64_t r = 0; r < rows; r++) {
+        const uint8_t* row = codes + r * ld;
+        const float g = global ? global[r] : 1.0f;
+        for (int64_t c = 0; c < k; c++) {
+            const uint8_t b = row[c / 2];
+            const uint8_t nib = (uint8_t)((c & 1) ? (b & 0x0F) : (b >> 4));
+            float s = 1.0f;
+            if (have) {
+                const int64_t i = tiled_index(row0 + r, c / block, nb_c, table_cols);
+                s = orc_scale_at((const uint8_t*)table + (size_t)i * scale_bytes(table_dtype), table_dtype, 0);
+            }
+            out[r * k + c] = e2m1(nib) * s * g;
+        }
+    }
+}

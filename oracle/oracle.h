@@ -55,6 +55,19 @@ void orc_convrot_rows(const float* x, float* out, int64_t rows, int64_t cols);
  *      core/kernels/int8_gemm.cpp:755) ----
  * x is f32 or bf16 [rows, ldx]; rotate selects the convrot pre-pass.
  * Returns 0, or -1 when cols is not a whole number of 256-groups. */
+/* ---- fp8 and nvfp4 / mxfp4 weights (SafeTensors::dequant_rows, core/host/st.cpp:601-621, :465-503) ---- */
+/* dequant_fp8_row (core/host/quant.cpp:433-439): out = f8(code) * scale[r]
+ * (scale NULL: 1); dtype ORC_F8_E4M3 or ORC_F8_E5M2; codes [rows, ld]. */
+void orc_dequant_fp8_rows(const uint8_t* codes, int64_t ld, int64_t rows, int64_t k, int dtype, const float* scale,
+                          float* out);
+/* dequant_nvfp4_row (core/host/quant.cpp:390-431) for weight rows row0 ..
+ * row0 + rows - 1: out = e2m1(nibble) * table[tiled index of (row, c / block)]
+ * * global[r]; the even column in the high nibble; the table read through
+ * orc_scale_at with its dtype (NULL, or fewer than 4 columns: 1); global NULL: 1. */
+void orc_dequant_fp4_rows(const uint8_t* codes, int64_t ld, int64_t row0, int64_t rows, int64_t k,
+                          const void* table, int table_dtype, int64_t table_rows, int64_t table_cols, int64_t block,
+                          const float* global, float* out);
+
 /* Every fp32 d with |d| <= 128 whose HALF_AWAY and DEVICE_FLOOR codes differ:
  * returns how many, and stores the first `cap` of them in `out`. */
 int64_t orc_round_forms_differ(float* out, int64_t cap);

@@ -916,7 +916,9 @@ phi_status phi_hip_dequant_rows(phi_stream_t stream, const void* src, int src_dt
         case PHI_F16: kind = phi_dev::DQ_F16, esz = 2; break;
         case PHI_BF16: kind = phi_dev::DQ_BF16, esz = 2; break;
         case PHI_F32: kind = phi_dev::DQ_F32, esz = 4; break;
-        default: return fail(PHI_ERR_ARG, "%s: src dtype must be I8, I4, F16, BF16 or F32", who);
+        case PHI_F8_E4M3: kind = phi_dev::DQ_F8_E4M3, esz = 1; break;
+        case PHI_F8_E5M2: kind = phi_dev::DQ_F8_E5M2, esz = 1; break;
+        default: return fail(PHI_ERR_ARG, "%s: src dtype must be I8, I4, F8_E4M3, F8_E5M2, F16, BF16 or F32", who);
     }
     if (src_dtype == PHI_I8 && !row_scale) return fail(PHI_ERR_ARG, "%s: int8 codes need their row scales", who);
     const int64_t src_cols = src_dtype == PHI_I4 ? (cols + 1) / 2 : cols;
@@ -926,6 +928,35 @@ phi_status phi_hip_dequant_rows(phi_stream_t stream, const void* src, int src_dt
     return check_hip(phi_dev::launch_dequant_rows((hipStream_t)stream, src, kind, rows, cols, lds, row_scale,
                                                   scale_scalar ? 1 : 0, out, ldo),
                      who);
+}
+
+phi_status phi_hip_dequant_fp4_rows(phi_stream_t stream, const uint8_t* codes, int64_t codes_ld, int64_t row0,
+                                    int64_t rows, int64_t k, const float* block_scale, int64_t scale_rows,
+                                    int64_t scale_cols, int64_t block, const float* global_scale, int global_scalar,
+                                    float* out, int64_t ldo) {
+    static const char* who = "dequant_fp4_rows";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (rows < 0 || k < 0 || row0 < 0) return fail(PHI_ERR_SHAPE, "%s: negative size", who);
+    if (rows == 0 || k == 0) return ok();
+    if (!codes || !out) return fail(PHI_ERR_ARG, "%s: null pointer", who);
+    if (codes_ld < (k + 1) / 2 || ldo < k) return fail(PHI_ERR_SHAPE, "%s: leading dimension smaller than the row", who);
+    if (block <= 0) block = 16;
+    // The table is read only when it has a geometry; then every (row, block)
+    // this call reads must fall inside it.
+    const bool have = block_scale && scale_rows > 0 && scale_cols / 4 > 0;
+    if (have) {
+        const int64_t nb_c = scale_cols / 4, last_row = row0 + rows - 1, last_blk = (k - 1) / block;
+        const int64_t last = ((last_row >> 7) * nb_c + (last_blk >> 2)) * 512 + 511;
+        if (nb_c < (last_blk >> 2) + 1 || last >= scale_rows * scale_cols)
+            return fail(PHI_ERR_SHAPE, "%s: the %lld x %lld block-scale table does not cover rows up to %lld and %lld "
+                        "blocks of %lld", who, (long long)scale_rows, (long long)scale_cols, (long long)last_row,
+                        (long long)(last_blk + 1), (long long)block);
+    }
+    if (!aligned(out, 4) || (have && !aligned(block_scale, 4)) || (global_scale && !aligned(global_scale, 4)))
+        return fail(PHI_ERR_ALIGN, "%s: misaligned operand", who);
+    phi_dev::Fp4Rows p{codes, codes_ld, row0, rows, k, have ? block_scale : nullptr, scale_cols, block,
+                       global_scale, global_scalar ? 1 : 0};
+    return check_hip(phi_dev::launch_dequant_fp4_rows((hipStream_t)stream, p, out, ldo), who);
 }
 
 phi_status phi_hip_convrot_rows(phi_stream_t stream, const float* x, int64_t rows, int64_t K, int64_t ldx, float* y,

@@ -5,8 +5,12 @@
 //
 //   dequant_rows  a stored tensor's values in fp32 (SafeTensors::dequant_rows,
 //                 core/host/st.cpp:601-700: int8 codes or a bare int4's signed
-//                 nibbles times the row scale,
+//                 nibbles times the row scale, fp8 codes times the row scale
+//                 (dequant_fp8_row, core/host/quant.cpp:433-439),
 //                 f16 / bf16 widened, fp32 copied)
+//   dequant_fp4_rows  nvfp4 / mxfp4 rows (dequant_nvfp4_row,
+//                 core/host/quant.cpp:390-431): E2M1 codes times their block's
+//                 scale from the cuBLAS-tiled table times the global scale
 //   convrot_rows  the 256-wide J-2R rotation of fp32 rows with no quantiser
 //                 (convrot_forward, core/host/quant.cpp:66-100; its inverse is
 //                 the same map, core/host/quant.hpp:63-65)
@@ -46,11 +50,47 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const void* src, int 
                 v = (float)(nib >= 8 ? nib - 16 : nib) * sc;
                 break;
             }
+            case DQ_F8_E4M3:
+            case DQ_F8_E5M2: {
+                const uint32_t b = ((const uint8_t*)src)[at];
+                const float d = kind == DQ_F8_E4M3 ? e4m3_to_f32(b) : e5m2_to_f32(b);
+                v = d * (row_scale ? row_scale[scale_scalar ? 0 : r] : 1.0f);
+                break;
+            }
             case DQ_F16: v = f16_to_f32(((const uint16_t*)src)[at]); break;
             case DQ_BF16: v = bf16_to_f32(((const uint16_t*)src)[at]); break;
             default: v = ((const float*)src)[at]; break;
         }
         out[r * ldo + c] = v;
+    }
+}
+
+// E2M1: sign, two exponent bits (bias 1), one mantissa bit; exponent 0 is the
+// subnormal 0 / 0.5.  Magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t nib) {
+    const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
+    const float mag = e == 0u ? 0.5f * (float)m : (float)(2u + m) * __uint_as_float((e - 2u + 127u) << 23);
+    return (nib & 8u) ? -mag : mag;
+}
+
+// The flat index of (row, block) in the cuBLAS "blocked" scale table: the
+// [rows, blocks] table padded to (128 rows, 4 blocks) tiles, the tiles in
+// row-tile-major order, and each 128 x 4 tile stored as 32 x (4 x 4) with the
+// row's 32-row quarter inside the 16-byte group (core/host/quant.cpp:390-410).
+__device__ __forceinline__ int64_t blocked_index(int64_t row, int64_t blk, int64_t nb_c) {
+    const int64_t h = row & 127, chunk = (row >> 7) * nb_c + (blk >> 2);
+    return chunk * 512 + (h & 31) * 16 + (h >> 5) * 4 + (blk & 3);
+}
+
+__global__ __launch_bounds__(256) void dequant_fp4_rows_kernel(Fp4Rows p, float* out, int64_t ldo) {
+    const int64_t total = p.rows * p.k, nb_c = p.scale_cols >> 2;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i / p.k, c = i - r * p.k;
+        const uint32_t b = p.codes[r * p.codes_ld + (c >> 1)];
+        const uint32_t nib = (c & 1) ? b & 15u : b >> 4;
+        const float s = p.block_scale ? p.block_scale[blocked_index(p.row0 + r, c / p.block, nb_c)] : 1.0f;
+        const float g = p.global ? p.global[p.global_scalar ? 0 : r] : 1.0f;
+        out[r * ldo + c] = (e2m1_to_f32(nib) * s) * g;
     }
 }
 
@@ -119,6 +159,11 @@ hipError_t launch_dequant_rows(hipStream_t stream, const void* src, int kind, in
                                const float* row_scale, int scale_scalar, float* out, int64_t ldo) {
     hipLaunchKernelGGL(dequant_rows_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, stream, src, kind, rows, cols,
                        lds, row_scale, scale_scalar, out, ldo);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_fp4_rows(hipStream_t stream, const Fp4Rows& p, float* out, int64_t ldo) {
+    hipLaunchKernelGGL(dequant_fp4_rows_kernel, dim3(grid_for(p.rows * p.k)), dim3(256), 0, stream, p, out, ldo);
     return hipGetLastError();
 }
 

@@ -709,6 +709,7 @@ std::optional<RelDType> rel_dtype_of(StDType d) {
 std::string grouped_parts_of(const SafeTensors& st, const StTensor& t, GroupedParts* out) {
     const SafeTensors::WeightLayout L = st.weight_layout(t.name);
     const bool six = L.spec.format == "w6a8_int8" || L.spec.format == "w6a8";
+    if (!six && L.spec.format != "asym_w4a8_int8") return "the format is not a grouped int4 / int6 family";
     // Codes: a 2-D byte plane already in the rotated basis.
     if (t.shape.size() != 2 || (t.dtype != StDType::I8 && t.dtype != StDType::U8))
         return "codes are not a 2-D byte tensor";
@@ -818,21 +819,33 @@ bool requant_rotates(const SafeTensors& st, const std::string& base) {
     return !(L.spec.valid && L.spec.convrot);
 }
 
-// What the device decodes: int8 codes times their row scale, f16 / bf16 / f32
-// widened, or a bare packed int4 (two signed nibbles a byte) times its row scale
-// (SafeTensors::dequant_rows, core/host/st.cpp:601-700).
+// What the device decodes: int8 codes times their row scale, fp8 codes times
+// their optional row scale, f16 / bf16 / f32 widened, a bare packed int4 (two
+// signed nibbles a byte) times its row scale, or nvfp4 / mxfp4 E2M1 codes times
+// their block and global scales (SafeTensors::dequant_rows,
+// core/host/st.cpp:601-700).
+constexpr int kDecodeI4 = -2, kDecodeFp4 = -3;
 struct Decodable {
-    int dtype = -1;  // PHI_I8 / PHI_F16 / PHI_BF16 / PHI_F32, or -2 for I4
+    int dtype = -1;  // PHI_I8 / PHI_F8_E4M3 / PHI_F8_E5M2 / PHI_F16 / PHI_BF16 / PHI_F32, kDecodeI4, kDecodeFp4
     const StTensor* scale = nullptr;
 };
 
 Decodable decodable(const SafeTensors& st, const StTensor& t) {
     Decodable d;
     const SafeTensors::WeightLayout L = st.weight_layout(t.name);
+    if ((t.dtype == StDType::I8 || t.dtype == StDType::U8) && (L.spec.format == "nvfp4" || L.spec.format == "mxfp4")) {
+        d.dtype = kDecodeFp4;
+        return d;
+    }
     switch (t.dtype) {
         case StDType::F32: d.dtype = PHI_F32; break;
         case StDType::F16: d.dtype = PHI_F16; break;
         case StDType::BF16: d.dtype = PHI_BF16; break;
+        case StDType::F8_E4M3:
+        case StDType::F8_E5M2:
+            d.dtype = t.dtype == StDType::F8_E4M3 ? PHI_F8_E4M3 : PHI_F8_E5M2;
+            d.scale = L.row_scale;
+            break;
         case StDType::I8:
             if (L.packed || L.rel_scale) return d;
             if (L.spec.valid && !L.known_family)
@@ -846,7 +859,7 @@ Decodable decodable(const SafeTensors& st, const StTensor& t) {
             break;
         case StDType::I4:
             if (L.packed) return d;
-            d.dtype = -2;
+            d.dtype = kDecodeI4;
             d.scale = L.row_scale;
             break;
         default: break;
@@ -869,9 +882,10 @@ void requant_rows_device(GpuCtx& g, const SafeTensors& st, const StTensor& t, i6
     const Decodable d = decodable(st, t);
     if (d.dtype == -1)
         throw MediaError("'" + t.name + "': " + st_dtype_name(t.dtype) + " is not a weight form this loader decodes");
-    const bool i4 = d.dtype == -2;
+    const bool i4 = d.dtype == kDecodeI4, fp4 = d.dtype == kDecodeFp4;
     const u64 src_row = i4 ? (u64)((k + 1) / 2) : t.row_bytes();
     if ((u64)n * src_row > t.nbytes) throw MediaError("'" + t.name + "' holds fewer rows than its shape says");
+    if (fp4 && src_row < (u64)((k + 1) / 2)) throw MediaError("'" + t.name + "': fp4 code rows are shorter than K needs");
     const u64 slab = (u64)std::max<i64>(1, std::min<i64>(n, (64ll << 20) / std::max<i64>(k * 4, 1)));
     // Device copies: the row scales (host-decoded from their table), and every
     // LoRA factor's A and B once.
@@ -880,21 +894,49 @@ void requant_rows_device(GpuCtx& g, const SafeTensors& st, const StTensor& t, i6
         scales.resize((size_t)n);
         for (i64 r = 0; r < n; r++) scales[(size_t)r] = st.row_scale_value(*d.scale, r);
     }
+    // nvfp4 / mxfp4: the block table decoded to fp32 as stored (its tiled
+    // layout kept), its geometry, and the global scale of every row.
+    std::vector<float> blocks, globals;
+    i64 blk_rows = 0, blk_cols = 0, block = 16;
+    if (fp4) {
+        const SafeTensors::WeightLayout L = st.weight_layout(t.name);
+        block = L.group > 0 ? L.group : 16;
+        if (const StTensor* b = L.rel_scale) {
+            blk_rows = b->shape.empty() ? 1 : b->shape[0];
+            blk_cols = b->shape.size() > 1 ? b->shape[1] : 0;
+            blocks.resize((size_t)b->numel);
+            for (i64 i = 0; i < b->numel; i++) blocks[(size_t)i] = st.row_scale_value(*b, i);
+        }
+        if (const StTensor* gs = L.global_scale) {
+            globals.resize((size_t)n);
+            for (i64 r = 0; r < n; r++) globals[(size_t)r] = st.row_scale_value(*gs, r);
+        }
+    }
     const u64 o_src = 0, o_f32 = up256(slab * src_row), o_sc = o_f32 + up256(slab * (u64)k * 4),
-              total = o_sc + up256((u64)n * 4 + 4);
+              o_blk = o_sc + up256((u64)n * 4 + 4), total = o_blk + up256((u64)blocks.size() * 4 + 4);
     Scratch work(ctx, total);
     if (!scales.empty()) ctx.upload(work.b, scales.data(), scales.size() * 4, o_sc);
+    if (!globals.empty()) ctx.upload(work.b, globals.data(), globals.size() * 4, o_sc);
+    if (!blocks.empty()) ctx.upload(work.b, blocks.data(), blocks.size() * 4, o_blk);
     float* f32 = (float*)work.at(o_f32);
     for (i64 r0 = 0; r0 < n; r0 += (i64)slab) {
         const i64 rows = std::min<i64>((i64)slab, n - r0);
         ctx.upload(work.b, t.data + (u64)r0 * src_row, (u64)rows * src_row, o_src);
-        const bool sc = d.scale != nullptr;
-        const bool sc1 = sc && d.scale->numel == 1;
-        ctx.check(phi_hip_dequant_rows(ctx.stream(), (const void*)work.at(o_src), i4 ? PHI_I4 : d.dtype, rows, k,
-                                       (int64_t)(i4 ? src_row : src_row / st_dtype_bytes(t.dtype)),
-                                       sc ? (const float*)work.at(o_sc) + (sc1 ? 0 : r0) : nullptr, sc1 ? 1 : 0, f32,
-                                       k),
-                  "dequant_rows");
+        if (fp4) {
+            ctx.check(phi_hip_dequant_fp4_rows(ctx.stream(), (const uint8_t*)work.at(o_src), (int64_t)src_row, r0, rows,
+                                               k, blocks.empty() ? nullptr : (const float*)work.at(o_blk), blk_rows,
+                                               blk_cols, block,
+                                               globals.empty() ? nullptr : (const float*)work.at(o_sc) + r0, 0, f32, k),
+                      "dequant_fp4_rows");
+        } else {
+            const bool sc = d.scale != nullptr;
+            const bool sc1 = sc && d.scale->numel == 1;
+            ctx.check(phi_hip_dequant_rows(ctx.stream(), (const void*)work.at(o_src), i4 ? PHI_I4 : d.dtype, rows, k,
+                                           (int64_t)(i4 ? src_row : src_row / st_dtype_bytes(t.dtype)),
+                                           sc ? (const float*)work.at(o_sc) + (sc1 ? 0 : r0) : nullptr, sc1 ? 1 : 0,
+                                           f32, k),
+                      "dequant_rows");
+        }
         if (plan.unrotate) ctx.check(phi_hip_convrot_rows(ctx.stream(), f32, rows, k, k, f32, k), "convrot");
         if (plan.deltas) {
             for (const LoraSet::Delta& f : plan.deltas(r0, rows)) {

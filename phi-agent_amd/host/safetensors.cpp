@@ -473,8 +473,25 @@ SafeTensors::WeightLayout SafeTensors::weight_layout(const std::string& weight_n
     L.correction = find(base + ".weight_correction");
     L.row_scale = find(base + ".weight_s_channel");
     if (!L.row_scale) L.row_scale = find(base + ".weight_scale");
-    L.bits = quant_bits_per_weight(L.spec.format);
+    L.global_scale = find(base + ".weight_scale_2");
     const std::string& f = L.spec.format;
+    if (f == "nvfp4" || f == "mxfp4") {
+        // Two scales, told apart by shape (core/host/st.cpp:850-880): the block
+        // table holds one entry per block (>= 2-D, more than one value), the
+        // global scale one value.  ComfyUI writes the table as weight_scale and
+        // the global as weight_scale_2; a file with the names swapped is read
+        // the same way.  fp4 has no per-row scale.
+        const auto table = [](const StTensor* t) { return t && t->numel > 1 && t->shape.size() >= 2; };
+        if (!L.rel_scale && table(L.row_scale)) {
+            L.rel_scale = L.row_scale;
+            L.row_scale = nullptr;
+        } else if (table(L.global_scale) && !table(L.rel_scale)) {
+            L.rel_scale = L.global_scale;
+            L.global_scale = L.row_scale;
+            L.row_scale = nullptr;
+        }
+    }
+    L.bits = quant_bits_per_weight(L.spec.format);
     if (f == "asym_w4a8_int8" || f == "w6a8_int8" || f == "w6a8") {
         // Both grouped families store a convrot-rotated weight (the blob carries
         // convrot_groupsize rather than a convrot flag).
@@ -489,6 +506,12 @@ SafeTensors::WeightLayout SafeTensors::weight_layout(const std::string& weight_n
     } else if (f == "convrot_w4a4") {
         L.spec.convrot = true;
         if (L.spec.convrot_groupsize <= 0) L.spec.convrot_groupsize = 256;
+        L.known_family = true;
+    } else if (f == "nvfp4" || f == "mxfp4") {
+        L.packed = true;
+        L.group = L.spec.group_size > 0 ? L.spec.group_size : 16;
+        L.known_family = true;
+    } else if (f == "fp8" || f == "float8_e4m3fn" || f == "float8_e4m3" || f == "float8_e5m2") {
         L.known_family = true;
     }
     return L;

@@ -10,6 +10,12 @@
 //                    <base>.weight_codebook F32 [16], <base>.weight_correction
 //   w6a8_int8        as above with [N, K/2 + K/4] six-bit codes, no codebook
 //   convrot_w4a4     <base>.weight I8 [N, K/2] signed nibbles, .weight_scale F32 [N]
+//   nvfp4 / mxfp4    <base>.weight U8/I8 [N, K/2] E2M1 nibbles (even column in the
+//                    HIGH nibble), a per-block scale table in the cuBLAS tiled
+//                    layout (fp8, as .weight_scale or .weight_scale_2) and one
+//                    global scale (the other of the two)
+//   fp8              <base>.weight F8_E4M3 / F8_E5M2 [N, K], optional
+//                    .weight_scale [N] or [1]
 //   <base>.comfy_quant  U8 tensor holding a padded UTF-8 JSON blob
 //
 // The file is mapped read-only; tensors are views into the mapping.
@@ -90,6 +96,7 @@ public:
         const StTensor* rel_scale = nullptr;   // weight_s_rel
         const StTensor* codebook = nullptr;    // weight_codebook
         const StTensor* correction = nullptr;  // weight_correction
+        const StTensor* global_scale = nullptr;  // nvfp4 / mxfp4: the one per-tensor scale
         bool packed = false;                   // bits < 8: the last dim is not K
         bool known_family = false;
     };

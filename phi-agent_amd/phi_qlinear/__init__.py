@@ -67,7 +67,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
            "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes",
            "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows",
-           "phi_hip_quant_rotate_mod_kt", "phi_hip_quant_rotate_act_kt", "phi_hip_i8_gemm_residual_kt"]
+           "phi_hip_quant_rotate_mod_kt", "phi_hip_quant_rotate_act_kt", "phi_hip_i8_gemm_residual_kt",
+           "phi_hip_dequant_fp4_rows"]
 
 _lib = None
 
@@ -112,6 +113,7 @@ def load() -> ctypes.CDLL:
     L.phi_hip_i4_workspace_bytes.restype = SZ
     L.phi_hip_dequant_rows.argtypes = [P, P, I, I64, I64, I64, P, I, P, I64]
     L.phi_hip_convrot_rows.argtypes = [P, P, I64, I64, I64, P, I64]
+    L.phi_hip_dequant_fp4_rows.argtypes = [P, P, I64, I64, I64, I64, P, I64, I64, I64, P, I, P, I64]
     L.phi_hip_lora_fold.argtypes = [P, P, I64, I64, I64, P, P, I64, F]
     L.phi_hip_q8_linear_noalloc.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, I]
     L.phi_hip_noalloc_scratch_bytes.argtypes = []
@@ -470,6 +472,39 @@ def lora_tail(x: torch.Tensor, At: torch.Tensor, Bt: torch.Tensor, out: torch.Te
         h = torch.empty((M, R), dtype=torch.float32, device=x.device)
     _check(load().phi_hip_lora_tail(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(At), _ptr(Bt), R, N,
                                     _ptr(out), _dt(out), out.stride(0), _ptr(h), h.numel() * h.element_size()))
+    return out
+
+
+def dequant_rows(src: torch.Tensor, dtype: int, cols: int, row_scale: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """phi_hip_dequant_rows: a stored tensor's rows in fp32.  src holds the raw
+    elements [rows, lds] (uint8 for I4 and the fp8 codes); dtype one of I8, I4,
+    F8_E4M3, F8_E5M2, F16, BF16, F32; row_scale [rows] or [1]."""
+    _require_device(src, row_scale, out)
+    rows = src.shape[0]
+    if out is None:
+        out = torch.empty((rows, cols), dtype=torch.float32, device=src.device)
+    _check(load().phi_hip_dequant_rows(_stream(stream), _ptr(src), dtype, rows, cols, src.stride(0), _ptr(row_scale),
+                                       1 if row_scale is not None and row_scale.numel() == 1 else 0, _ptr(out),
+                                       out.stride(0)))
+    return out
+
+
+def dequant_fp4_rows(codes: torch.Tensor, k: int, block_scale: torch.Tensor | None = None, *, block: int = 16,
+                     global_scale: torch.Tensor | None = None, row0: int = 0, out: torch.Tensor | None = None,
+                     stream=None) -> torch.Tensor:
+    """phi_hip_dequant_fp4_rows: nvfp4 / mxfp4 weight rows row0 .. row0 +
+    rows - 1 in fp32.  codes uint8 [rows, >= k/2]; block_scale the 2-D tiled
+    table already in fp32; global_scale [rows] or [1]."""
+    _require_device(codes, block_scale, global_scale, out)
+    rows = codes.shape[0]
+    if out is None:
+        out = torch.empty((rows, k), dtype=torch.float32, device=codes.device)
+    tr, tc = (block_scale.shape if block_scale is not None else (0, 0))
+    _check(load().phi_hip_dequant_fp4_rows(_stream(stream), _ptr(codes), codes.stride(0), row0, rows, k,
+                                           _ptr(block_scale), tr, tc, block, _ptr(global_scale),
+                                           1 if global_scale is not None and global_scale.numel() == 1 else 0,
+                                           _ptr(out), out.stride(0)))
     return out
 
 

@@ -208,12 +208,13 @@ int main(int argc, char** argv) {
             const SafeTensors::WeightLayout L = st.weight_layout(t.name);
             printf("{\"tensors\": %zu, \"dtype\": \"%s\", \"n\": %lld, \"k\": %lld, \"bits\": %d, \"group\": %lld, "
                    "\"packed\": %s, \"known\": %s, \"plain_int8\": %s, \"row_scale\": \"%s\", \"rel_scale\": \"%s\", "
-                   "\"codebook\": %s, \"correction\": %s, \"row_scale0\": %.9g, \"spec\": ",
+                   "\"codebook\": %s, \"correction\": %s, \"global_scale\": \"%s\", \"row_scale0\": %.9g, \"spec\": ",
                    st.tensors().size(), st_dtype_name(t.dtype), (long long)(t.shape.empty() ? 0 : t.shape[0]),
                    (long long)st.logical_cols(t), L.bits, (long long)L.group, L.packed ? "true" : "false",
                    L.known_family ? "true" : "false", st.is_plain_int8(t) ? "true" : "false",
                    L.row_scale ? L.row_scale->name.c_str() : "", L.rel_scale ? L.rel_scale->name.c_str() : "",
                    L.codebook ? "true" : "false", L.correction ? "true" : "false",
+                   L.global_scale ? L.global_scale->name.c_str() : "",
                    L.row_scale ? st.row_scale_value(*L.row_scale, 0) : 1.0);
             print_spec(L.spec, "}\n");
             fflush(stdout);

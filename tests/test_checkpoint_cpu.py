@@ -118,6 +118,35 @@ def test_probe_convrot_w4a4(tmp_path):
     assert (p["n"], p["k"]) == (32, 1024) and not p["packed"] and p["spec"]["convrot"] and not p["plain_int8"]
 
 
+@pytest.mark.parametrize("swapped", [False, True])
+def test_probe_nvfp4_scale_mapping(tmp_path, swapped):
+    """nvfp4's two scales are told apart by shape, whichever name each is
+    stored under (core/host/st.cpp:850-880): the >= 2-D multi-entry one is the
+    block table, the single value the global scale; fp4 has no row scale.  K is
+    twice the stored width; the family is packed 4-bit with group 16."""
+    table = torch.randint(0x20, 0x58, (128, 8), dtype=torch.int32).to(torch.uint8)
+    glob = torch.tensor(0.5)
+    t = {"n.weight": torch.zeros(64, 32, dtype=torch.uint8),
+         "n.comfy_quant": C.comfy_blob({"format": "nvfp4"})}
+    if swapped:
+        t["n.weight_scale"], t["n.weight_scale_2"] = glob, table
+    else:
+        t["n.weight_scale"], t["n.weight_scale_2"] = table, glob
+    p = C.probe(C.write(str(tmp_path / "n.safetensors"), t), "n")
+    assert p["k"] == 64 and p["bits"] == 4 and p["group"] == 16 and p["packed"] and p["known"]
+    assert p["rel_scale"] == ("n.weight_scale_2" if swapped else "n.weight_scale")
+    assert p["global_scale"] == ("n.weight_scale" if swapped else "n.weight_scale_2")
+    assert p["row_scale"] == "" and not p["plain_int8"]
+
+
+def test_probe_fp8_family(tmp_path):
+    t = {"e.weight": torch.zeros(8, 256).to(torch.float8_e4m3fn), "e.weight_scale": torch.tensor([0.5]),
+         "e.comfy_quant": C.comfy_blob({"format": "float8_e4m3fn"})}
+    p = C.probe(C.write(str(tmp_path / "e.safetensors"), t), "e")
+    assert p["dtype"] == "F8_E4M3" and p["k"] == 256 and p["known"] and not p["packed"]
+    assert p["row_scale"] == "e.weight_scale" and p["row_scale0"] == 0.5
+
+
 def test_malformed_files(tmp_path):
     path, _ = int8_file(tmp_path)
     raw = open(path, "rb").read()

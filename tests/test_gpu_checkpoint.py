@@ -372,3 +372,122 @@ def test_load_lora_tail_layout(dev, tmp_path):
     want[:n1, :4] = lora_scale(0.5, 4, 4) * Bq
     want[2 * n1:, 4:] = lora_scale(0.5, 2, 2) * Bv
     assert np.array_equal(bt, want)
+
+
+# ---------------------------------------------------------------- fp8 and nvfp4 / mxfp4 weights
+def _to_blocked(scales: np.ndarray) -> np.ndarray:
+    """The cuBLAS tiled block-scale layout (as tests/test_oracle_fp4.py builds it)."""
+    rows, cols = scales.shape
+    R, Cc = -(-rows // 128) * 128, -(-cols // 4) * 4
+    pad = np.zeros((R, Cc), scales.dtype)
+    pad[:rows, :cols] = scales
+    t = pad.reshape(R // 128, 128, Cc // 4, 4).transpose(0, 2, 1, 3).reshape(-1, 4, 32, 4).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(t.reshape(R, Cc))
+
+
+def _e4m3_codes(g, shape, lo=0x20, hi=0x58):
+    """Positive finite E4M3 codes (scale values about 0.03 to 20)."""
+    return torch.randint(lo, hi, shape, generator=g, dtype=torch.int32).to(torch.uint8)
+
+
+@pytest.mark.parametrize("fmt,block", [("nvfp4", 16), ("mxfp4", 32)])
+def test_dequant_fp4_rows_c_abi(dev, orc, fmt, block):
+    """phi_hip_dequant_fp4_rows against the oracle bit for bit, a slice from a
+    row past the first 128-row tile included (the table is indexed by the
+    weight's own row), and a table too small for the rows asked is refused."""
+    N, K = 300, 1024
+    g = torch.Generator().manual_seed(21 + block)
+    codes = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    table8 = _to_blocked(_e4m3_codes(g, (N, K // block)).numpy())
+    table = torch.from_numpy(table8).view(torch.float8_e4m3fn).float()
+    glob = torch.rand(N, generator=g) + 0.5
+    got = Q.dequant_fp4_rows(codes.to(dev), K, table.to(dev), block=block, global_scale=glob.to(dev))
+    want = orc.dequant_fp4_rows(codes.numpy(), K, table8, orc.U8_E4M3, block, glob.numpy())
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    r0 = 130
+    part = Q.dequant_fp4_rows(codes[r0:].to(dev), K, table.to(dev), block=block, global_scale=glob[:1].to(dev),
+                              row0=r0)
+    want_p = orc.dequant_fp4_rows(codes[r0:].numpy(), K, table8, orc.U8_E4M3, block, glob.numpy()[:1], row0=r0)
+    assert np.array_equal(part.cpu().numpy().view(np.uint32), want_p.view(np.uint32))
+    with pytest.raises(RuntimeError, match="block-scale table does not cover"):
+        Q.dequant_fp4_rows(codes.to(dev), K, table[:128].contiguous().to(dev), block=block)
+
+
+@pytest.mark.parametrize("dtype", ["e4m3", "e5m2"])
+def test_dequant_fp8_rows_c_abi(dev, orc, dtype):
+    g = torch.Generator().manual_seed(31)
+    codes = torch.randint(0, 256, (64, 512), generator=g, dtype=torch.int32).to(torch.uint8)
+    sc = torch.rand(64, generator=g) * 0.01 + 0.001
+    kind = Q.F8_E4M3 if dtype == "e4m3" else Q.F8_E5M2
+    for scale in (sc, sc[:1], None):
+        got = Q.dequant_rows(codes.to(dev), kind, 512, None if scale is None else scale.to(dev)).cpu().numpy()
+        want = orc.dequant_fp8_rows(codes.numpy(), orc.F8_E4M3 if dtype == "e4m3" else orc.F8_E5M2,
+                                    None if scale is None else scale.numpy())
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+        ok = ~np.isnan(want)
+        assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+
+
+@pytest.mark.parametrize("variant", ["e4m3_rows", "e4m3_scalar", "e5m2_none", "e4m3_spec"])
+def test_upload_fp8_weight(dev, orc, tmp_path, variant):
+    """An fp8 checkpoint through the streaming int8 upload: each code decoded
+    times the optional row scale (core/host/st.cpp:610-621), then rotated and
+    quantised per row (core/models/model_common.cpp:1095-1283)."""
+    N, K = 200, 512
+    g = torch.Generator().manual_seed(41)
+    e5 = variant.startswith("e5m2")
+    tdt = torch.float8_e5m2 if e5 else torch.float8_e4m3fn
+    lo, hi = (0x20, 0x50) if e5 else (0x20, 0x58)
+    codes = torch.randint(lo, hi, (N, K), generator=g, dtype=torch.int32).to(torch.uint8)
+    codes |= (torch.randint(0, 2, (N, K), generator=g, dtype=torch.int32) << 7).to(torch.uint8)  # signs
+    t = {"f.weight": codes.view(tdt)}
+    scale = None
+    if variant == "e4m3_rows":
+        scale = torch.rand(N, generator=g) * 0.01 + 0.001
+    elif variant in ("e4m3_scalar", "e4m3_spec"):
+        scale = torch.tensor([0.004])
+    if scale is not None:
+        t["f.weight_scale"] = scale
+    if variant == "e4m3_spec":
+        t["f.comfy_quant"] = C.comfy_blob({"format": "float8_e4m3fn"})
+    path = C.write(str(tmp_path / "f8.safetensors"), t)
+    q, s = loaded(tmp_path, "upload_i8", path, "f")
+    vals = orc.dequant_fp8_rows(codes.numpy(), orc.F8_E5M2 if e5 else orc.F8_E4M3,
+                                None if scale is None else scale.numpy())
+    wq, ws = orc.quantize_rows(vals, rotate=True)
+    assert np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(q, wq), f"{(q != wq).sum()} code mismatches"
+
+
+@pytest.mark.parametrize("variant", ["nvfp4", "nvfp4_swapped", "nvfp4_f8_table", "mxfp4", "nvfp4_no_global"])
+def test_upload_fp4_weight(dev, orc, tmp_path, variant):
+    """An nvfp4 / mxfp4 checkpoint through the streaming int8 upload: E2M1
+    codes times the tiled block table and the global scale (core/host/st.cpp:
+    465-503, with the scale-name mapping of :850-880), then rotated and
+    quantised per row.  200 rows: the table's last row tile is partial."""
+    N, K = 200, 1024
+    block = 32 if variant == "mxfp4" else 16
+    g = torch.Generator().manual_seed(51 + len(variant))
+    codes = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    table8 = _to_blocked(_e4m3_codes(g, (N, K // block)).numpy())
+    table_t = torch.from_numpy(table8)
+    if variant == "nvfp4_f8_table":
+        table_t = table_t.view(torch.float8_e4m3fn)
+    glob = torch.tensor(0.37)  # a 0-dim scalar, as ComfyUI writes it
+    fmt = "mxfp4" if variant == "mxfp4" else "nvfp4"
+    t = {"p.weight": codes, "p.comfy_quant": C.comfy_blob({"format": fmt, "group_size": block})}
+    if variant == "nvfp4_swapped":
+        t["p.weight_scale_2"], t["p.weight_scale"] = table_t, glob
+    else:
+        t["p.weight_scale"] = table_t
+        if variant != "nvfp4_no_global":
+            t["p.weight_scale_2"] = glob
+    path = C.write(str(tmp_path / "fp4.safetensors"), t)
+    p = C.probe(path, "p")
+    assert p["k"] == K and p["packed"] and p["known"]
+    q, s = loaded(tmp_path, "upload_i8", path, "p")
+    gl = None if variant == "nvfp4_no_global" else np.full(1, 0.37, np.float32)
+    vals = orc.dequant_fp4_rows(codes.numpy(), K, table8, orc.U8_E4M3, block, gl)
+    wq, ws = orc.quantize_rows(vals, rotate=True)
+    assert np.array_equal(s.view(np.uint32), ws.view(np.uint32))
+    assert np.array_equal(q, wq), f"{(q != wq).sum()} code mismatches"
