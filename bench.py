@@ -811,7 +811,8 @@ def bench_ceiling(steps, warmup):
 
     iters = 2000  # 64000 MFMAs a wave, about 1 ms a launch
     tops = {}
-    for mode, name in ((0, "zero"), (1, "static"), (2, "rotating")):
+    for mode, name in ((0, "zero"), (1, "static"), (2, "rotating"), (6, "zero_16x16x64"),
+                       (5, "rotating_16x16x64")):
         def launch(mode=mode):
             rc = lib.phi_probe_mfma(stream, ctypes.c_void_p(ops.data_ptr()), mode, iters,
                                     ctypes.c_void_p(sink.data_ptr()), cus)

@@ -15,6 +15,11 @@
 //                     mode 3  mode 2 with the A fragments walked in snake
 //                             order (one operand changes between MFMAs)
 //                     mode 4  mode 2 with the two operands' roles swapped
+//                     mode 5  mode 2's operands on v_mfma_i32_16x16x64_i8: the
+//                             same 128 x 128 wave tile as 8 x 8 blocks of
+//                             16 x 16, one MFMA a block per 64 K (the same
+//                             operations per iteration)
+//                     mode 6  mode 5 on all-zero operands
 //   phi_probe_lds_dma  every wave streams 16 rows x 64 bytes per instruction
 //                   from a window of global memory into LDS, 4 K-steps of the
 //                   headline tile's A and B in flight, with no MFMAs.
@@ -82,6 +87,45 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void* lptr_t;
 constexpr int kRsrcWord3 = 0x00020000;
+
+// Modes 5 and 6: the 16 x 16 x 64 form, 64 accumulators of 4 registers.
+template <int MODE>
+__global__ __launch_bounds__(256) void mfma16_probe(const int8_t* ops, int iters, int* sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v4i a[8], b[8];
+#pragma unroll
+    for (int f = 0; f < 8; f++) {
+        if (MODE == 6) {
+            a[f] = v4i{0, 0, 0, 0};
+            b[f] = v4i{0, 0, 0, 0};
+        } else {
+            a[f] = *(const v4i*)(ops + ((wave * 16 + f) * 64 + lane) * 16);
+            b[f] = *(const v4i*)(ops + ((wave * 16 + 8 + f) * 64 + lane) * 16);
+        }
+    }
+    v4i acc[64];
+#pragma unroll
+    for (int q = 0; q < 64; q++) acc[q] = v4i{};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int q = 0; q < 64; q++)
+            acc[q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[q >> 3], a[q & 7], acc[q], 0, 0, 0);
+        if (MODE == 5) {
+            const int x = 0x5a3c96e1 * (it + 1) + lane;
+#pragma unroll
+            for (int f = 0; f < 8; f++) {
+                a[f] ^= v4i{x, x >> 3, x >> 5, x >> 7};
+                b[f] ^= v4i{x >> 1, x >> 2, x >> 4, x >> 6};
+            }
+        }
+    }
+    int t = 0;
+#pragma unroll
+    for (int q = 0; q < 64; q++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) t += acc[q][r];
+    if (t == 0x7fffffff) sink[blockIdx.x * 4 + wave] = t;  // keeps the MFMAs live
+}
 
 template <int MODE>
 __global__ __launch_bounds__(256) void mfma_probe(const int8_t* ops, int iters, int* sink) {
@@ -327,6 +371,8 @@ int phi_probe_mfma(void* stream, const int8_t* ops, int mode, int iters, int* si
         case 1: hipLaunchKernelGGL(mfma_probe<1>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         case 3: hipLaunchKernelGGL(mfma_probe<3>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         case 4: hipLaunchKernelGGL(mfma_probe<4>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
+        case 5: hipLaunchKernelGGL(mfma16_probe<5>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
+        case 6: hipLaunchKernelGGL(mfma16_probe<6>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
         default: hipLaunchKernelGGL(mfma_probe<2>, dim3(grid), dim3(256), 0, (hipStream_t)stream, ops, iters, sink); break;
     }
     return (int)hipGetLastError();
