@@ -232,6 +232,30 @@ phi_status phi_hip_i8_gemm_residual_kt(phi_stream_t stream, const int8_t* A, con
  * device's compute units.  0 for an empty problem. */
 int64_t phi_hip_big_tile_rows(int64_t M, int64_t N);
 
+/* The GEMM tuning table (replaces the reference's autotune store and tuned
+ * dispatch, core/kernels/autotune.hpp:30-88: a stored launch configuration per
+ * kernel, found by a sweep that checks every variant bit-identical).  Here a
+ * plan per problem shape and operand layout for the persistent int8 GEMM that
+ * phi_hip_i8_gemm / _kt, phi_hip_q8_linear / _kt and the gated residual run:
+ *   big_rows  rows run as 256 x 256 tiles: a multiple of 256 up to M, or M;
+ *             -1 leaves it to the library's cost model (phi_hip_big_tile_rows)
+ *   group_m   tile rows per group of the XCD-aware tile order, 1..16; 0: 4
+ *   split     1: the two tile sizes as two launches; 0: one launch
+ * Every plan gives the same bits; only the time differs.  The table is
+ * process-wide and thread-safe; the host layer's GemmTuneStore sweeps,
+ * persists and loads it.  _set with plan NULL removes the shape's entry;
+ * _get returns the plan a launch of that shape runs (tuned = 1 when it comes
+ * from the table). */
+typedef struct phi_gemm_plan {
+    int64_t big_rows;
+    int32_t group_m;
+    int32_t split;
+} phi_gemm_plan;
+phi_status phi_hip_gemm_plan_set(int64_t M, int64_t N, int64_t K, int k_tiled, const phi_gemm_plan* plan);
+phi_status phi_hip_gemm_plan_get(int64_t M, int64_t N, int64_t K, int k_tiled, phi_gemm_plan* plan, int* tuned);
+int64_t phi_hip_gemm_plan_count(void);
+void phi_hip_gemm_plan_clear(void);
+
 /* phi_hip_q8_linear with the weight W K-tiled (phi_hip_pack_k_tiled at load
  * time): the prologue writes q8 (M x K bytes) K-tiled, then phi_hip_i8_gemm_kt.
  * C is bit-identical to phi_hip_q8_linear's; s8 is the same; q8 holds the same

@@ -14,7 +14,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 
 #include "../../include/phi_qlinear.h"
 #include "gemv.hpp"
@@ -196,28 +199,57 @@ int64_t big_tile_rows(int64_t M, int64_t N, int G) {
     return best_r * 256 < M ? best_r * 256 : M;
 }
 
+// The tuning table: a plan per (M, N, K, operand layout) for the int8-B
+// persistent GEMM, set by the caller (a sweep's result, persisted by the host
+// layer's GemmTuneStore).  Read on every such launch; the count lets the
+// common case, an empty table, skip the lock.
+struct PlanKey {
+    int64_t M, N, K;
+    int kt;
+    bool operator<(const PlanKey& o) const { return std::tie(M, N, K, kt) < std::tie(o.M, o.N, o.K, o.kt); }
+};
+std::mutex g_plans_mu;
+std::map<PlanKey, phi_gemm_plan> g_plans;
+std::atomic<int64_t> g_plan_count{0};
+
+bool tuned_plan(int64_t M, int64_t N, int64_t K, int kt, phi_gemm_plan* out) {
+    if (g_plan_count.load(std::memory_order_acquire) == 0) return false;
+    std::lock_guard<std::mutex> lk(g_plans_mu);
+    const auto it = g_plans.find(PlanKey{M, N, K, kt ? 1 : 0});
+    if (it == g_plans.end()) return false;
+    *out = it->second;
+    return true;
+}
+
 // The persistent kernel over the whole problem: 256 x 256 tiles for the rows
-// big_tile_rows() gives it, then 128 x 128 tiles for the rest (A, sA, C and
-// the output rows offset; B, sB and bias are shared).
-hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p, GemmKernel gk, bool w4, int c_dtype,
+// big_tile_rows() gives it (or the tuning table's plan), then 128 x 128 tiles
+// for the rest (A, sA, C and the output rows offset; B, sB and bias are shared).
+hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p0, GemmKernel gk, bool w4, int c_dtype,
                                int64_t ldc) {
     const int G = num_cus();
     // int8 B runs on the four-stage pipeline; PHI_GEMM_PIPE=0 selects the
     // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
     // runs on the two-stage kernel.
     const char* pe = getenv("PHI_GEMM_PIPE");
-    const bool pipe = p.kt || (!w4 && !(pe && pe[0] == '0'));  // K-tiled operands: the pipeline only
-    const int64_t M = p.M;
-    const int64_t rows = gk == GK_PERSIST ? big_tile_rows(M, p.N, G) : gk == GK_PERSIST256 ? M : 0;
+    const bool pipe = p0.kt || (!w4 && !(pe && pe[0] == '0'));  // K-tiled operands: the pipeline only
+    const int64_t M = p0.M;
+    phi_gemm_plan plan{};
+    const bool tuned = gk == GK_PERSIST && !w4 && tuned_plan(M, p0.N, p0.K, p0.kt, &plan);
+    phi_dev::GemmParams p = p0;
+    if (tuned && plan.group_m > 0) p.group_m = plan.group_m;
+    const int64_t rows = gk == GK_PERSIST ? (tuned && plan.big_rows >= 0 ? plan.big_rows : big_tile_rows(M, p.N, G))
+                         : gk == GK_PERSIST256 ? M
+                                               : 0;
     phi_dev::GemmParams q = p;
     q.M = (int)(M - rows);
     q.A = p.A + rows * p.lda;
     if (q.sA) q.sA = p.sA + rows;
     q.C = (int8_t*)p.C + rows * ldc * (int64_t)c_elem_bytes(c_dtype);
     if (rows > 0 && rows < M) {
-        // Both tile sizes: one launch (PHI_GEMM_MIXED=0 splits it in two, an A/B switch).
+        // Both tile sizes: one launch (PHI_GEMM_MIXED=0 splits it in two, an
+        // A/B switch; so does a tuned plan's split).
         const char* e = getenv("PHI_GEMM_MIXED");
-        if (!(e && e[0] == '0')) {
+        if (!(e && e[0] == '0') && !(tuned && plan.split)) {
             phi_dev::GemmParams b = p;
             b.M = (int)rows;
             return pipe ? phi_dev::launch_i8_gemm_pipe_mixed(stream, b, q, G)
@@ -495,6 +527,48 @@ static phi_status i8_gemm_kt_impl(const char* who, phi_stream_t stream, const in
     if (e && strcmp(e, "persist256") == 0) gk = GK_PERSIST256;
     if (e && strcmp(e, "persist128") == 0) gk = GK_PERSIST128;
     return check_hip(launch_persist_plan((hipStream_t)stream, p, gk, false, c_dtype, ldc), who);
+}
+
+phi_status phi_hip_gemm_plan_set(int64_t M, int64_t N, int64_t K, int k_tiled, const phi_gemm_plan* plan) {
+    static const char* who = "gemm_plan_set";
+    if (M <= 0 || N <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
+    const PlanKey key{M, N, K, k_tiled ? 1 : 0};
+    std::lock_guard<std::mutex> lk(g_plans_mu);
+    if (!plan) {
+        g_plans.erase(key);
+    } else {
+        if (plan->big_rows < -1 || plan->big_rows > M || (plan->big_rows >= 0 && plan->big_rows % 256 != 0 &&
+                                                          plan->big_rows != M))
+            return fail(PHI_ERR_ARG, "%s: big_rows=%lld is not -1, a multiple of 256 up to M, or M=%lld", who,
+                        (long long)plan->big_rows, (long long)M);
+        if (plan->group_m < 0 || plan->group_m > 16)
+            return fail(PHI_ERR_ARG, "%s: group_m=%d is not 0 (the default) or 1..16", who, (int)plan->group_m);
+        if (plan->split != 0 && plan->split != 1) return fail(PHI_ERR_ARG, "%s: split must be 0 or 1", who);
+        g_plans[key] = *plan;
+    }
+    g_plan_count.store((int64_t)g_plans.size(), std::memory_order_release);
+    return ok();
+}
+
+phi_status phi_hip_gemm_plan_get(int64_t M, int64_t N, int64_t K, int k_tiled, phi_gemm_plan* plan, int* tuned) {
+    static const char* who = "gemm_plan_get";
+    if (M <= 0 || N <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
+    if (!plan) return fail(PHI_ERR_ARG, "%s: null plan", who);
+    phi_gemm_plan p{-1, 0, 0};
+    const bool t = tuned_plan(M, N, K, k_tiled, &p);
+    if (tuned) *tuned = t ? 1 : 0;
+    if (p.big_rows < 0) p.big_rows = big_tile_rows(M, N, num_cus());
+    if (p.group_m == 0) p.group_m = 4;
+    *plan = p;
+    return ok();
+}
+
+int64_t phi_hip_gemm_plan_count(void) { return g_plan_count.load(std::memory_order_acquire); }
+
+void phi_hip_gemm_plan_clear(void) {
+    std::lock_guard<std::mutex> lk(g_plans_mu);
+    g_plans.clear();
+    g_plan_count.store(0, std::memory_order_release);
 }
 
 int64_t phi_hip_big_tile_rows(int64_t M, int64_t N) {

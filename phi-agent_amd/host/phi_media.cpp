@@ -5,12 +5,14 @@
 #include "safetensors.hpp"
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <map>
 #include <mutex>
 #include <optional>
+#include <random>
 #include <string_view>
 #include <unordered_map>
 #include <vector>
@@ -1307,6 +1309,237 @@ I4Upload upload_quant_linear_w4a4(GpuCtx& g, const SafeTensors& st, const std::s
     out.s = arena.alloc((u64)out.n * 4);
     g.ctx->upload(out.s.res, s.data(), (u64)out.n * 4, out.s.off);
     return out;
+}
+
+// ---------------------------------------------------------------- GEMM tuning table
+
+std::string GemmTuneStore::default_path(const std::string& base_dir) {
+    return (base_dir.empty() ? std::string(".") : base_dir) + "/data/gemm_plans.json";
+}
+
+bool GemmTuneStore::load(const std::string& path) {
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return false;
+    std::string text;
+    char buf[4096];
+    for (size_t n; (n = fread(buf, 1, sizeof buf, f)) > 0;) text.append(buf, n);
+    fclose(f);
+    std::vector<std::map<std::string, double>> recs;
+    if (!parse_number_records(text, "plans", &recs)) return false;
+    std::vector<GemmTuneEntry> items;
+    for (const auto& r : recs) {
+        const auto num = [&](const char* k, double d) {
+            const auto it = r.find(k);
+            return it == r.end() ? d : it->second;
+        };
+        GemmTuneEntry e;
+        e.M = (i64)num("M", 0);
+        e.N = (i64)num("N", 0);
+        e.K = (i64)num("K", 0);
+        e.k_tiled = num("k_tiled", 0) != 0;
+        e.big_rows = (i64)num("big_rows", -1);
+        e.group_m = (int)num("group_m", 0);
+        e.split = num("split", 0) != 0;
+        e.measured_us = num("us", 0);
+        e.tops = num("tops", 0);
+        if (e.M <= 0 || e.N <= 0 || e.K <= 0) return false;
+        items.push_back(e);
+    }
+    items_.clear();
+    for (const GemmTuneEntry& e : items) put(e);
+    return true;
+}
+
+bool GemmTuneStore::save(const std::string& path) const {
+    const std::string tmp = path + ".tmp";
+    FILE* f = fopen(tmp.c_str(), "wb");
+    if (!f) return false;
+    bool ok = fprintf(f, "{\"version\": 1, \"plans\": [") > 0;
+    for (size_t i = 0; i < items_.size(); i++) {
+        const GemmTuneEntry& e = items_[i];
+        ok = ok && fprintf(f,
+                           "%s\n  {\"M\": %lld, \"N\": %lld, \"K\": %lld, \"k_tiled\": %d, \"big_rows\": %lld, "
+                           "\"group_m\": %d, \"split\": %d, \"us\": %.3f, \"tops\": %.1f}",
+                           i ? "," : "", (long long)e.M, (long long)e.N, (long long)e.K, e.k_tiled ? 1 : 0,
+                           (long long)e.big_rows, e.group_m, e.split ? 1 : 0, e.measured_us, e.tops) > 0;
+    }
+    ok = ok && fprintf(f, "\n]}\n") > 0;
+    ok = (fclose(f) == 0) && ok;
+    return ok && std::rename(tmp.c_str(), path.c_str()) == 0;
+}
+
+void GemmTuneStore::put(const GemmTuneEntry& e) {
+    for (GemmTuneEntry& x : items_)
+        if (x.M == e.M && x.N == e.N && x.K == e.K && x.k_tiled == e.k_tiled) {
+            x = e;
+            return;
+        }
+    items_.push_back(e);
+}
+
+const GemmTuneEntry* GemmTuneStore::get(i64 M, i64 N, i64 K, bool k_tiled) const {
+    for (const GemmTuneEntry& x : items_)
+        if (x.M == M && x.N == N && x.K == K && x.k_tiled == k_tiled) return &x;
+    return nullptr;
+}
+
+void GemmTuneStore::apply() const {
+    for (const GemmTuneEntry& e : items_) {
+        const phi_gemm_plan p{e.big_rows, e.group_m, e.split ? 1 : 0};
+        if (phi_hip_gemm_plan_set(e.M, e.N, e.K, e.k_tiled ? 1 : 0, &p) != PHI_OK)
+            throw MediaError(std::string("gemm tuning table: ") + phi_hip_last_error());
+    }
+}
+
+namespace {
+
+// A shape's table entry taken out for a sweep and put back afterwards.
+struct PlanHold {
+    i64 M, N, K;
+    int kt;
+    phi_gemm_plan saved{};
+    int had = 0;
+    PlanHold(i64 m, i64 n, i64 k, int t) : M(m), N(n), K(k), kt(t) {
+        phi_hip_gemm_plan_get(M, N, K, kt, &saved, &had);
+        phi_hip_gemm_plan_set(M, N, K, kt, nullptr);
+    }
+    ~PlanHold() { phi_hip_gemm_plan_set(M, N, K, kt, had ? &saved : nullptr); }
+};
+
+}  // namespace
+
+// The sweep of core/kernels/autotune.cpp:264-334 over this library's plans.
+GemmTuneResult autotune_int8_gemm(ComputeContext& ctx, i64 M, i64 N, i64 K, int iters, bool k_tiled) {
+    GemmTuneResult r;
+    try {
+        if (M <= 0 || N <= 0 || K <= 0) throw MediaError("autotune: empty problem");
+        if (K % 256 != 0 || N % 8 != 0)
+            throw MediaError("autotune: the persistent GEMM's plans need K % 256 == 0 and N % 8 == 0");
+        if (iters < 1) iters = 1;
+        const int kt = k_tiled ? 1 : 0;
+        PlanHold hold(M, N, K, kt);
+        // Seeded operands: uniform int8 codes, scales in [0.002, 0.05), a bf16 bias.
+        std::mt19937 rng(20261202u);
+        std::uniform_int_distribution<int> code(-127, 127);
+        std::uniform_real_distribution<float> scl(0.002f, 0.05f), bia(-0.05f, 0.05f);
+        std::vector<int8_t> a((size_t)(M * K)), b((size_t)(N * K));
+        std::vector<float> sa((size_t)M), sb((size_t)N);
+        std::vector<uint16_t> bias((size_t)N);
+        for (auto& v : a) v = (int8_t)code(rng);
+        for (auto& v : b) v = (int8_t)code(rng);
+        for (auto& v : sa) v = scl(rng);
+        for (auto& v : sb) v = scl(rng);
+        for (auto& v : bias) {
+            const float f = bia(rng);
+            uint32_t u;
+            memcpy(&u, &f, 4);
+            v = (uint16_t)(u >> 16);
+        }
+        const u64 ab = (u64)(M * K), bb = (u64)(N * K), cb = (u64)(M * N) * 2;
+        const u64 o_a = 0, o_b = up256(ab), o_akt = o_b + up256(bb), o_bkt = o_akt + (kt ? up256(ab) : 0),
+                  o_sa = o_bkt + (kt ? up256(bb) : 0), o_sb = o_sa + up256((u64)M * 4),
+                  o_bias = o_sb + up256((u64)N * 4), o_c = o_bias + up256((u64)N * 2), o_c32 = o_c + up256(cb),
+                  total = o_c32 + up256((u64)(M * N) * 4);
+        Scratch buf(ctx, total);
+        ctx.upload(buf.b, a.data(), ab, o_a);
+        ctx.upload(buf.b, b.data(), bb, o_b);
+        ctx.upload(buf.b, sa.data(), (u64)M * 4, o_sa);
+        ctx.upload(buf.b, sb.data(), (u64)N * 4, o_sb);
+        ctx.upload(buf.b, bias.data(), (u64)N * 2, o_bias);
+        const int8_t* A = (const int8_t*)buf.at(o_a);
+        const int8_t* B = (const int8_t*)buf.at(o_b);
+        if (kt) {
+            ctx.check(phi_hip_pack_k_tiled(ctx.stream(), A, K, M, K, (int8_t*)buf.at(o_akt)), "pack_k_tiled");
+            ctx.check(phi_hip_pack_k_tiled(ctx.stream(), B, K, N, K, (int8_t*)buf.at(o_bkt)), "pack_k_tiled");
+            A = (const int8_t*)buf.at(o_akt);
+            B = (const int8_t*)buf.at(o_bkt);
+        }
+        auto gemm = [&](bool raw) {
+            const float* sA = raw ? nullptr : (const float*)buf.at(o_sa);
+            const float* sB = raw ? nullptr : (const float*)buf.at(o_sb);
+            const void* bz = raw ? nullptr : (const void*)buf.at(o_bias);
+            void* C = (void*)buf.at(raw ? o_c32 : o_c);
+            const int cd = raw ? PHI_I32 : PHI_BF16;
+            ctx.check(kt ? phi_hip_i8_gemm_kt(ctx.stream(), A, B, sA, sB, 0, bz, PHI_BF16, C, cd, N, M, N, K)
+                         : phi_hip_i8_gemm(ctx.stream(), A, K, B, K, sA, sB, 0, bz, PHI_BF16, C, cd, N, M, N, K, nullptr,
+                                           0),
+                      "autotune gemm");
+        };
+        // The default plan: its accumulators on sampled rows against host
+        // integer sums, and its bf16 output as every candidate's reference.
+        gemm(true);
+        gemm(false);
+        ctx.submit();
+        const i64 samples[] = {0, M / 3, M / 2, M - 1};
+        std::vector<int32_t> row((size_t)N);
+        r.default_exact = true;
+        for (const i64 m : samples) {
+            ctx.download(buf.b, row.data(), (u64)N * 4, o_c32 + (u64)(m * N) * 4);
+            for (i64 n = 0; n < N; n++) {
+                int64_t acc = 0;
+                for (i64 k = 0; k < K; k++) acc += (int64_t)a[(size_t)(m * K + k)] * b[(size_t)(n * K + k)];
+                if (acc != row[(size_t)n]) r.default_exact = false;
+            }
+        }
+        std::vector<uint16_t> ref((size_t)(M * N)), got((size_t)(M * N));
+        ctx.download(buf.b, ref.data(), cb, o_c);
+
+        // Candidates: the cost model's 256-row count and its neighbours, all
+        // rows, group heights 2, 4, 8, and one or two launches where both
+        // tile sizes run.
+        phi_gemm_plan def{};
+        ctx.check(phi_hip_gemm_plan_get(M, N, K, kt, &def, nullptr), "gemm_plan_get");
+        std::vector<i64> rows_opts{def.big_rows};
+        for (const i64 v : {def.big_rows - 256, def.big_rows + 256, M})
+            if (v >= 0 && v <= M && (v % 256 == 0 || v == M) &&
+                std::find(rows_opts.begin(), rows_opts.end(), v) == rows_opts.end())
+                rows_opts.push_back(v);
+        hipEvent_t e0, e1;
+        if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+            throw MediaError("autotune: event creation failed");
+        struct Events {
+            hipEvent_t a, b;
+            ~Events() {
+                (void)hipEventDestroy(a);
+                (void)hipEventDestroy(b);
+            }
+        } events{e0, e1};
+        double best_us = 1e300;
+        for (const i64 big : rows_opts)
+            for (const int gm : {2, 4, 8})
+                for (const int split : {0, 1}) {
+                    if (split && !(big > 0 && big < M)) continue;
+                    const phi_gemm_plan p{big, gm, split};
+                    ctx.check(phi_hip_gemm_plan_set(M, N, K, kt, &p), "gemm_plan_set");
+                    gemm(false);  // untimed
+                    if (hipEventRecord(e0, ctx.stream()) != hipSuccess) throw MediaError("autotune: event record");
+                    for (int i = 0; i < iters; i++) gemm(false);
+                    if (hipEventRecord(e1, ctx.stream()) != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
+                        throw MediaError("autotune: event wait");
+                    float ms = 0.0f;
+                    (void)hipEventElapsedTime(&ms, e0, e1);
+                    GemmTuneEntry e;
+                    e.M = M, e.N = N, e.K = K, e.k_tiled = k_tiled;
+                    e.big_rows = big, e.group_m = gm, e.split = split != 0;
+                    e.measured_us = (double)ms * 1e3 / iters;
+                    e.tops = 2.0 * (double)M * (double)N * (double)K / (e.measured_us * 1e-6) / 1e12;
+                    ctx.download(buf.b, got.data(), cb, o_c);
+                    const bool exact = memcmp(got.data(), ref.data(), (size_t)cb) == 0;
+                    if (exact) r.exact_matches++;
+                    r.tried.push_back(e);
+                    if (exact && e.measured_us < best_us) {
+                        best_us = e.measured_us;
+                        r.best = e;
+                    }
+                }
+        if (best_us == 1e300) throw MediaError("autotune: no candidate reproduced the default plan's output");
+        r.ok = r.default_exact;
+        if (!r.default_exact) r.error = "autotune: the default plan's accumulators differ from the host integer GEMM";
+    } catch (const std::exception& e) {
+        r.ok = false;
+        r.error = e.what();
+    }
+    return r;
 }
 
 // core/kernels/w4a8_expand.cpp:263-303

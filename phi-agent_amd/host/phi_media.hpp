@@ -456,6 +456,60 @@ struct LoraModule {
 LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::vector<LoraModule>& mods, i64 n, i64 k);
 LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::string& base, const LoraSet* lora, i64 n, i64 k);
 
+// ---- the GEMM tuning table (core/kernels/autotune.hpp:30-88) ----
+//
+// One plan per (M, N, K, operand layout) for the persistent int8 GEMM:
+// big_rows (rows run as 256 x 256 tiles), group_m (tile rows per group of the
+// XCD-aware tile order) and split (the two tile sizes as two launches).  Every
+// plan gives the same bits, so a sweep is free to pick the fastest; it checks
+// that anyway.  The store persists as JSON and apply() hands its plans to the
+// library, whose every launch of such a shape then runs the stored plan.
+struct GemmTuneEntry {
+    i64 M = 0, N = 0, K = 0;
+    bool k_tiled = false;
+    i64 big_rows = -1;  // -1: the library's cost model
+    int group_m = 0;    // 0: 4
+    bool split = false;
+    double measured_us = 0.0;
+    double tops = 0.0;
+};
+
+class GemmTuneStore {
+public:
+    // The default file beside a data directory, as the reference keeps its table
+    // (core/kernels/autotune.cpp:158-160).
+    static std::string default_path(const std::string& base_dir);
+    bool load(const std::string& path);        // false: unreadable or malformed (the store is unchanged)
+    bool save(const std::string& path) const;  // written whole, then renamed into place
+    void put(const GemmTuneEntry& e);          // replaces the entry of the same shape and layout
+    const GemmTuneEntry* get(i64 M, i64 N, i64 K, bool k_tiled) const;
+    // Every entry into the library's plan table (phi_hip_gemm_plan_set).
+    void apply() const;
+    size_t size() const { return items_.size(); }
+    const std::vector<GemmTuneEntry>& items() const { return items_; }
+
+private:
+    std::vector<GemmTuneEntry> items_;
+};
+
+struct GemmTuneResult {
+    bool ok = false;
+    std::string error;
+    GemmTuneEntry best;
+    std::vector<GemmTuneEntry> tried;  // measured_us / tops filled
+    int exact_matches = 0;             // candidates bit-identical to the default plan
+    bool default_exact = false;        // the default plan's sampled rows equal a host integer GEMM
+};
+
+// Sweeps the candidate plans of an M x N x K int8 GEMM (bf16 output with a
+// bias, row-major or K-tiled operands) on seeded random operands, `iters`
+// timed launches each after one untimed, on the context's stream.  The
+// default plan's int32 accumulators are checked on sampled rows against a
+// host integer GEMM and every candidate's output against the default plan's,
+// bit for bit.  Buffers are device allocations charged to the VRAM
+// accountant, released on return.  The table is left as it was.
+GemmTuneResult autotune_int8_gemm(ComputeContext& ctx, i64 M, i64 N, i64 K, int iters = 3, bool k_tiled = false);
+
 // out [m, t.n] fp32 += (x [m, t.k] fp32 . at^T) . bt^T, with h the caller's
 // [m, rank] fp32 scratch (core/models/model_common.cpp:1667-1700).
 void apply_lora_tail(GpuCtx& g, const LoraTail& t, const GpuAlloc& x, i64 m, const GpuAlloc& out, const GpuAlloc& h);

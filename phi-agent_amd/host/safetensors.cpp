@@ -357,6 +357,23 @@ QuantSpec parse_quant_spec(const void* json_bytes, size_t len) {
     return spec;
 }
 
+bool parse_number_records(const std::string& text, const std::string& key,
+                          std::vector<std::map<std::string, double>>* out) {
+    Json doc;
+    if (!JsonReader(text.data(), text.size()).parse(doc) || doc.kind != Json::Obj) return false;
+    const Json* arr = doc.get(key);
+    if (!arr || arr->kind != Json::Arr) return false;
+    out->clear();
+    for (const Json& rec : arr->arr) {
+        if (rec.kind != Json::Obj) return false;
+        std::map<std::string, double> m;
+        for (const auto& kv : rec.obj)
+            if (kv.second.kind == Json::Num) m[kv.first] = kv.second.num;
+        out->push_back(std::move(m));
+    }
+    return true;
+}
+
 int quant_bits_per_weight(const std::string& format) {
     if (format == "asym_w4a8_int8" || format == "nvfp4" || format == "mxfp4") return 4;
     if (format == "w6a8_int8" || format == "w6a8") return 6;

@@ -65,6 +65,12 @@ QuantSpec parse_quant_spec(const void* json_bytes, size_t len);
 // Bits per weight on disk for a family (core/host/quant.cpp:40-52).
 int quant_bits_per_weight(const std::string& format);
 
+// The objects of a top-level array `key` in a JSON document, each as its
+// numeric members (other members are left out).  False when the text does not
+// parse or has no such array.
+bool parse_number_records(const std::string& text, const std::string& key,
+                          std::vector<std::map<std::string, double>>* out);
+
 class SafeTensors {
 public:
     // Maps the file and parses its header; throws MediaError on a malformed file.

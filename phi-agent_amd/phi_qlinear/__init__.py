@@ -53,6 +53,11 @@ class W4a8Weight(ctypes.Structure):
                 ("k", ctypes.c_int64), ("group", ctypes.c_int64), ("layout", ctypes.c_int)]
 
 
+class GemmPlan(ctypes.Structure):
+    """phi_gemm_plan: big_rows (-1: the cost model), group_m (0: 4), split."""
+    _fields_ = [("big_rows", ctypes.c_int64), ("group_m", ctypes.c_int32), ("split", ctypes.c_int32)]
+
+
 class GemvItem(ctypes.Structure):
     _fields_ = [("W", ctypes.c_void_p), ("sW", ctypes.c_void_p), ("sw_scalar", ctypes.c_int),
                 ("bias", ctypes.c_void_p), ("C", ctypes.c_void_p), ("ldc", ctypes.c_int64)]
@@ -68,7 +73,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes",
            "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows",
            "phi_hip_quant_rotate_mod_kt", "phi_hip_quant_rotate_act_kt", "phi_hip_i8_gemm_residual_kt",
-           "phi_hip_dequant_fp4_rows"]
+           "phi_hip_dequant_fp4_rows", "phi_hip_gemm_plan_set", "phi_hip_gemm_plan_get", "phi_hip_gemm_plan_count",
+           "phi_hip_gemm_plan_clear"]
 
 _lib = None
 
@@ -114,6 +120,10 @@ def load() -> ctypes.CDLL:
     L.phi_hip_dequant_rows.argtypes = [P, P, I, I64, I64, I64, P, I, P, I64]
     L.phi_hip_convrot_rows.argtypes = [P, P, I64, I64, I64, P, I64]
     L.phi_hip_dequant_fp4_rows.argtypes = [P, P, I64, I64, I64, I64, P, I64, I64, I64, P, I, P, I64]
+    L.phi_hip_gemm_plan_set.argtypes = [I64, I64, I64, I, ctypes.POINTER(GemmPlan)]
+    L.phi_hip_gemm_plan_get.argtypes = [I64, I64, I64, I, ctypes.POINTER(GemmPlan), ctypes.POINTER(ctypes.c_int)]
+    L.phi_hip_gemm_plan_count.restype = I64
+    L.phi_hip_gemm_plan_clear.restype = None
     L.phi_hip_lora_fold.argtypes = [P, P, I64, I64, I64, P, P, I64, F]
     L.phi_hip_q8_linear_noalloc.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, I]
     L.phi_hip_noalloc_scratch_bytes.argtypes = []
@@ -506,6 +516,29 @@ def dequant_fp4_rows(codes: torch.Tensor, k: int, block_scale: torch.Tensor | No
                                            1 if global_scale is not None and global_scale.numel() == 1 else 0,
                                            _ptr(out), out.stride(0)))
     return out
+
+
+def gemm_plan_set(M: int, N: int, K: int, *, k_tiled: bool = False, big_rows: int = -1, group_m: int = 0,
+                  split: bool = False, remove: bool = False) -> None:
+    """phi_hip_gemm_plan_set: the tuning table's plan for one GEMM shape
+    (remove=True drops the entry)."""
+    plan = None if remove else ctypes.byref(GemmPlan(big_rows, group_m, 1 if split else 0))
+    _check(load().phi_hip_gemm_plan_set(M, N, K, 1 if k_tiled else 0, plan))
+
+
+def gemm_plan_get(M: int, N: int, K: int, *, k_tiled: bool = False) -> dict:
+    """The plan a GEMM of this shape runs: {big_rows, group_m, split, tuned}."""
+    plan, tuned = GemmPlan(), ctypes.c_int(0)
+    _check(load().phi_hip_gemm_plan_get(M, N, K, 1 if k_tiled else 0, ctypes.byref(plan), ctypes.byref(tuned)))
+    return {"big_rows": plan.big_rows, "group_m": plan.group_m, "split": bool(plan.split), "tuned": bool(tuned.value)}
+
+
+def gemm_plan_clear() -> None:
+    load().phi_hip_gemm_plan_clear()
+
+
+def gemm_plan_count() -> int:
+    return int(load().phi_hip_gemm_plan_count())
 
 
 def pack_k_tiled(W: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:

@@ -15,6 +15,9 @@
 //        (upload_quant_linear_i8), with an optional LoraSet; writes n, k (int64)
 //        then the int8 weight [n, k] and its fp32 scales [n] (GPU).  load_kt and
 //        load3_kt set GpuCtx::k_tiled_weights and unpack the K-tiled weight.
+//   st_tool tune <M> <N> <K> <iters> <k_tiled> <out.json>
+//        autotune_int8_gemm, then the winner saved, loaded back and applied:
+//        a JSON line with the sweep and the plan the library then runs (GPU)
 //   st_tool lora_probe <target> <n> <k> lora <path> <strength>...
 //        LoraSet::touches / deltas_for -> JSON line (no GPU)
 //   st_tool tail <out.bin> <n> <k> <base>:<row0>:<rows>... lora <path> <strength>...
@@ -28,6 +31,7 @@
 #include <vector>
 
 #include "phi_media.hpp"
+#include "phi_qlinear.h"
 #include "safetensors.hpp"
 
 using namespace phi::media;
@@ -136,6 +140,35 @@ static int weights(int argc, char** argv) {
     return 0;
 }
 
+// autotune_int8_gemm, the winner stored and saved, the table cleared, the file
+// loaded into a new store and applied: the plan the library then runs.
+static int tune(char** argv) {
+    const i64 M = atoll(argv[2]), N = atoll(argv[3]), K = atoll(argv[4]);
+    const int iters = atoi(argv[5]);
+    const bool kt = atoi(argv[6]) != 0;
+    ComputeContext ctx(0);
+    const GemmTuneResult r = autotune_int8_gemm(ctx, M, N, K, iters, kt);
+    if (!r.ok) throw MediaError(r.error);
+    GemmTuneStore store;
+    store.put(r.best);
+    if (!store.save(argv[7])) throw MediaError(std::string("cannot write ") + argv[7]);
+    phi_hip_gemm_plan_clear();
+    GemmTuneStore back;
+    if (!back.load(argv[7])) throw MediaError(std::string("cannot read back ") + argv[7]);
+    back.apply();
+    phi_gemm_plan p{};
+    int tuned = 0;
+    if (phi_hip_gemm_plan_get(M, N, K, kt ? 1 : 0, &p, &tuned) != PHI_OK) throw MediaError(phi_hip_last_error());
+    printf("{\"ok\": true, \"default_exact\": %s, \"exact\": %d, \"tried\": %zu, \"best_us\": %.3f, "
+           "\"best\": [%lld, %d, %d], \"applied\": [%lld, %d, %d], \"tuned\": %d, \"entries\": %zu, \"us\": [",
+           r.default_exact ? "true" : "false", r.exact_matches, r.tried.size(), r.best.measured_us,
+           (long long)r.best.big_rows, r.best.group_m, r.best.split ? 1 : 0, (long long)p.big_rows, (int)p.group_m,
+           (int)p.split, tuned, back.size());
+    for (size_t i = 0; i < r.tried.size(); i++) printf("%s%.3f", i ? ", " : "", r.tried[i].measured_us);
+    printf("]}\n");
+    return 0;
+}
+
 static int tail(int argc, char** argv) {
     const char* out = argv[2];
     const i64 n = atoll(argv[3]), k = atoll(argv[4]);
@@ -185,6 +218,7 @@ int main(int argc, char** argv) {
             print_spec(parse_quant_spec(text.data(), text.size()), "\n");
             return 0;
         }
+        if (op == "tune" && argc == 8) return tune(argv);
         if (op == "weights" && argc >= 6) return weights(argc, argv);
         if (op == "tail" && argc >= 6) return tail(argc, argv);
         if (op == "lora_probe" && argc >= 8) {

@@ -216,8 +216,13 @@ def test_weight_step_contracts(lib):
     assert lib.phi_hip_convrot_rows(None, None, 0, 256, 256, None, 256) == 0
     rc = lib.phi_hip_dequant_rows(None, FAKE, Q.I8, 4, 64, 64, None, 0, FAKE, 64)
     assert rc == 1 and "row scales" in Q.last_error()
-    rc = lib.phi_hip_dequant_rows(None, FAKE, Q.F8_E4M3, 4, 64, 64, None, 0, FAKE, 64)
+    rc = lib.phi_hip_dequant_rows(None, FAKE, Q.U8_E4M3, 4, 64, 64, None, 0, FAKE, 64)
     assert rc == 1 and "src dtype" in Q.last_error()
+    # nvfp4 rows: a block table too small for the rows asked is refused before a launch
+    rc = lib.phi_hip_dequant_fp4_rows(None, FAKE, 512, 100, 100, 1024, FAKE, 128, 16, 16, None, 0, FAKE, 1024)
+    assert rc == 2 and "block-scale table does not cover" in Q.last_error()
+    rc = lib.phi_hip_dequant_fp4_rows(None, FAKE, 100, 0, 4, 1024, None, 0, 0, 16, None, 0, FAKE, 1024)
+    assert rc == 2 and "leading dimension" in Q.last_error()
     rc = lib.phi_hip_dequant_rows(None, FAKE, Q.I4, 4, 64, 31, None, 0, FAKE, 64)
     assert rc == 2 and "leading dimension" in Q.last_error()
     rc = lib.phi_hip_lora_fold(None, FAKE, 30, 4, 64, FAKE, FAKE, 2, 1.0)
@@ -307,3 +312,28 @@ def test_noalloc_contract(lib):
     rc = lib.phi_hip_q8_linear_noalloc(None, FAKE, Q.BF16, K, 0, K, FAKE, K, FAKE, 1, None, Q.F32, 64,
                                        FAKE, Q.BF16, 64, 0)
     assert rc == 2 and "empty problem" in Q.last_error()
+
+
+def test_gemm_plan_table(lib):
+    """The tuning table's C ABI without a device: entries set, read back,
+    replaced and removed; malformed plans refused with the library's message."""
+    Q.gemm_plan_clear()
+    assert Q.gemm_plan_count() == 0
+    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, big_rows=4096, group_m=8, split=True)
+    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=False, big_rows=4352, group_m=2)
+    assert Q.gemm_plan_count() == 2
+    assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True) == {"big_rows": 4096, "group_m": 8, "split": True,
+                                                                "tuned": True}
+    assert Q.gemm_plan_get(4352, 12288, 3072) == {"big_rows": 4352, "group_m": 2, "split": False, "tuned": True}
+    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, big_rows=3840, group_m=4)
+    assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True)["big_rows"] == 3840 and Q.gemm_plan_count() == 2
+    for bad, msg in ((dict(big_rows=100), "big_rows=100"), (dict(big_rows=5000), "big_rows=5000"),
+                     (dict(big_rows=-2), "big_rows=-2"), (dict(group_m=17), "group_m=17")):
+        with pytest.raises(Q.QLinearError, match=msg):
+            Q.gemm_plan_set(4352, 12288, 3072, **bad)
+    with pytest.raises(Q.QLinearError, match="empty problem"):
+        Q.gemm_plan_set(0, 1, 1)
+    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, remove=True)
+    assert Q.gemm_plan_count() == 1
+    Q.gemm_plan_clear()
+    assert Q.gemm_plan_count() == 0
