@@ -20,6 +20,7 @@
 #include <tuple>
 
 #include "../../include/phi_qlinear.h"
+#include "device_common.hpp"
 #include "gemv.hpp"
 #include "lora.hpp"
 #include "i8_gemm.hpp"
@@ -221,12 +222,37 @@ bool tuned_plan(int64_t M, int64_t N, int64_t K, int kt, phi_gemm_plan* out) {
     return true;
 }
 
+// Rounds of 256 x 256 tiles the square plan costs (big_tile_rows' measure).
+double square_plan_cost(int64_t M, int64_t N, int G) {
+    const int64_t rows = big_tile_rows(M, N, G);
+    const int64_t big = (rows / 256 + (rows % 256 ? 1 : 0)) * ((N + 255) / 256);
+    const int64_t small = ((M - rows + 127) / 128) * ((N + 127) / 128);
+    return (double)((big + G - 1) / G) + kSmallRound * (double)((small + G - 1) / G);
+}
+
+// A round of 272 x 192 tiles against a round of 256 x 256 ones at the same K:
+// the outputs' ratio, 52224 / 65536.
+constexpr double kT272Round = 52224.0 / 65536.0;
+
+// Whether the 272 x 192 kernel serves p (K-tiled operands only): when its
+// whole rounds cost less than the square plan's.  PHI_GEMM_T272=0 / 1 turns
+// it off / forces it where it applies (an A/B switch).
+bool use_t272(const phi_dev::GemmParams& p, int G) {
+    if (!phi_dev::t272_ok(p)) return false;
+    const int e = phi_dev::env_switch("PHI_GEMM_T272", -1, 0, 1);
+    if (e >= 0) return e == 1;
+    const double t = kT272Round * (double)((phi_dev::t272_tile_count(p.M, p.N) + G - 1) / G);
+    return t < square_plan_cost(p.M, p.N, G) - 1e-9;
+}
+
 // The persistent kernel over the whole problem: 256 x 256 tiles for the rows
 // big_tile_rows() gives it (or the tuning table's plan), then 128 x 128 tiles
-// for the rest (A, sA, C and the output rows offset; B, sB and bias are shared).
+// for the rest (A, sA, C and the output rows offset; B, sB and bias are shared);
+// or, K-tiled, 272 x 192 tiles where those fill whole rounds better.
 hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p0, GemmKernel gk, bool w4, int c_dtype,
                                int64_t ldc) {
     const int G = num_cus();
+    if (gk == GK_PERSIST && !w4 && p0.kt && use_t272(p0, G)) return phi_dev::launch_i8_gemm_t272(stream, p0, G);
     // int8 B runs on the four-stage pipeline; PHI_GEMM_PIPE=0 selects the
     // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
     // runs on the two-stage kernel.

@@ -71,6 +71,11 @@ hipError_t launch_i8_gemm_persist_mixed(hipStream_t stream, const GemmParams& pb
 // (i8_gemm_pipe.hip).
 hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile);
 hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus);
+// Persistent kernel on 272 x 192 tiles (i8_gemm_t272.hip): K-tiled operands,
+// K % 512 == 0, no gate, M * K and N * K below 2^31 (t272_ok).
+bool t272_ok(const GemmParams& p);
+int t272_tile_count(int64_t M, int64_t N);
+hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_cus);
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out,
 // row-major or (kt, K % 64 == 0) in the K-tiled layout.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out, bool kt = false);

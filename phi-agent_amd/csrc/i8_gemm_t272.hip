@@ -1,0 +1,594 @@
+// Persistent int8 GEMM for gfx950 on 272 x 192 output tiles (K-tiled
+// operands, four-stage 64-deep K ring):
+//
+//   acc[m,n] = sum_k A[m,k] * B[n,k]                  (exact int32)
+//   C[m,n]   = fma((float)acc * sA[m], sB[n], bias[n])  -> bf16 (RNE) / fp32 / raw int32
+//
+// The product and epilogue are those of the reference's int8_gemm_tc
+// (core/kernels/int8_gemm.cpp:466-621, epilogue :588-620) and host gemm_int8
+// (core/host/quant.cpp:223-236).
+//
+// Why this tile.  The DiT shapes have M = 4352 = 16 x 272 (4096 image + 256
+// text tokens) and N a multiple of 3 x 1024.  Square 256 x 256 tiles leave
+// the GPU's 256 CUs with partial rounds there: 204 tiles at 4352 x 3072 (52
+// CUs idle for the whole kernel), 612 at 4352 x 9216 (a third round on 100
+// CUs), and a 17th tile-row at 4352 x 12288 that needs a round of smaller,
+// slower tiles.  A 272 x 192 tile (52224 outputs, 0.8 of a 256 x 256 one)
+// gives exactly 256, 768 and 1024 tiles: whole rounds on every CU.
+//
+// Tile and waves.  The tile is 17 x 12 blocks of v_mfma_i32_16x16x64_i8
+// (16 x 16 outputs, the whole 64-deep K-step in one instruction).  Four
+// waves, one a SIMD, take 51 blocks each: wave (wm, wn) owns block columns
+// 6 wn .. 6 wn + 5 and block rows 0-7 (wm = 0) or 9-16 (wm = 1), and shares
+// block row 8 with its partner: wm = 0 takes its columns 0-2 there, wm = 1
+// columns 3-5.  Every wave then issues 51 MFMAs and reads 15 fragments (9 of
+// A, 6 of B) a K-step; a plain 2 x 2 split of the rows (144 / 128) would
+// give 54 and 48 and hold the K-step at 54.  The accumulators are 204 AGPRs.
+// The wave's half of the shared row makes wm a template parameter: each wave
+// runs the loop of its half.
+//
+// The B fragment is the MFMA's first operand, so lane l holds output row
+// l % 16 of a block and columns 4 (l / 16) .. + 3, as in the square kernels.
+// Both fragments of a lane carry the same 16 K bytes (chunk l / 16 of the
+// step's 64), so the product sums every k once whatever order the
+// instruction pairs bytes in.
+//
+// The K ring.  Stage s holds A (272 rows x 64 bytes) then B (192 rows), 29
+// KB; four stages.  K-step k runs on stage k % 4:
+//   * wait for this wave's loads of K-step k + 1, then one barrier: K-step
+//     k + 1 is in LDS for every wave, and every wave's reads of stage k % 4
+//     (done during K-step k - 1) have completed;
+//   * 51 MFMAs on the fragments read during K-step k - 1, with the 15 reads
+//     of K-step k + 1's fragments and the loads of K-step k + 4 into stage
+//     k % 4 placed between them.
+// A K-step's 29 pieces of 16 rows x 64 bytes (contiguous 1 KB blocks in the
+// K-tiled layout) are 4 whole A pieces, a quarter of the 17th and 3 B pieces
+// per wave: eight load instructions for every wave, so the waits count alike
+// on all of them.  The cursors move to the next tile for the loads of its
+// K-step 0 (issued in K-step KT - 4, with the next tile's epilogue
+// operands); after the last tile they point past the operands, whose range
+// check returns zeros without touching memory.
+//
+// The epilogue converts one block row (16 rows x 96 or 48 columns) at a
+// time, stages it in the wave's LDS area and stores whole 16-byte pieces.
+#include "device_common.hpp"
+#include "i8_gemm.hpp"
+#include "persist_common.hpp"
+
+// Tile-timeline hooks, empty in the library: a tracing build defines them to
+// stamp the clocks per workgroup at the kernel's start, at each tile's start,
+// K-loop end and epilogue end, and at the end.
+#ifndef PHI_T272_STAMP
+#define PHI_T272_STAMP(tile, point)
+#define PHI_T272_TRACE_BEGIN
+#define PHI_T272_TRACE_END
+#endif
+
+namespace phi_dev {
+
+namespace {
+
+using namespace persist;
+
+constexpr int TM = 272, TN = 192;      // output tile
+constexpr int PK = 64, NSTG = 4;       // K bytes per stage, stages
+constexpr int BOFF = TM * PK;          // B's offset within a stage
+constexpr int STG = (TM + TN) * PK;    // 29696 bytes a stage
+constexpr int NA = 5, NBL = 3;         // loads a wave issues per K-step: A (4 whole + a quarter), B
+constexpr int NLD = NA + NBL;
+constexpr int NE = 3;                  // epilogue-operand loads a wave issues per tile
+// Epilogue operands of one tile (one area per tile parity): row scales
+// (272 used of 320), column scales, bias (fp32 words or bf16 pairs), and
+// the landing place of loads that fetch nothing.
+constexpr int E_SA = 0, E_SB = 1280, E_BZ = 2048, E_PAD = 2816, EB = 3072;
+// Epilogue staging: 16 rows of up to 6 blocks x 32 bytes (bf16) or 3 blocks
+// x 64 bytes (fp32 / int32), at a pitch of 208 bytes: the rows start at 16
+// distinct multiples of four banks, so a block's 8-byte (16-byte) writes and
+// the read-back of one 16-byte piece from 16 rows touch every bank once.
+constexpr int SP = 208, SBYTES = 16 * SP;
+// Stores a wave issues in an epilogue: bf16 8 full block rows x 3 + the shared
+// one 2; fp32 / int32 8 x 6 + 3.  Every one is issued (columns past N go to
+// an offset the range check drops).
+template <int CK>
+struct Nst {
+    static constexpr int v = CK == C_BF16 ? 8 * 3 + 2 : 8 * 6 + 3;
+};
+// Waits: this wave's memory operations issued after its loads of K-step
+// k + 1 are those of K-steps k + 2 and k + 3 (2 NLD), plus the epilogue's
+// stores in a tile's first three K-steps, plus the next tile's
+// epilogue-operand loads (issued after K-step KT - 4's loads) in K-steps
+// KT - 3 .. KT - 1.
+constexpr int VW = 2 * NLD;
+
+struct Frag {
+    v4i a[9], b[6];
+};
+
+struct Acc {
+    v4i f[8][6];  // the wave's full block rows
+    v4i s[3];     // its half of the shared block row
+};
+
+struct Tw {
+    int lane, wave, wn;
+    int oF;          // this lane's byte offset within a 16-row piece (row l % 16, chunk l / 16, swizzled)
+    int8_t* lds;     // stage 0 (opaque)
+    int8_t* le;      // epilogue-operand areas
+    int8_t* lc;      // this wave's staging area
+    __amdgpu_buffer_rsrc_t rA, rB;
+    // Running source offsets (this lane's byte of the piece included) and
+    // K-step strides of the wave's pieces, in VGPRs: wave-uniform, but the
+    // SGPRs cannot hold them beside the rest (they spilled there).
+    int offA[NA], stA[NA], offB[NBL], stB[NBL];
+    int cm0, cn0;    // the cursors' tile
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t whole_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, kRsrcWord3);
+}
+
+// K-step 0 of the 16-row piece at row r of a K-tiled operand of `rows` rows:
+// its byte offset and K-step stride.  A piece wholly past the operand reads
+// from its end: the range check returns zeros (those rows only feed outputs
+// the epilogue drops).
+__device__ __forceinline__ void piece_at(int r, int rows, int K, int& off, int& st) {
+    const bool in = r < rows;
+    const int s = r >> 8, h = min(256, rows - (s << 8));
+    off = in ? s * 256 * K + (r & 255) * PK : rows * K;
+    st = in ? h * PK : 0;
+}
+
+// Cursors onto the tile at (m0, n0), K-step 0; valid = false: onto nothing.
+__device__ __forceinline__ void cursor_to(Tw& w, const GemmParams& p, int m0, int n0, bool valid) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        piece_at(valid ? m0 + 16 * (w.wave + 4 * j) : p.M, p.M, p.K, w.offA[j], w.stA[j]);
+        w.offA[j] += w.lane * 16;
+    }
+    piece_at(valid ? m0 + 256 : p.M, p.M, p.K, w.offA[4], w.stA[4]);
+    w.offA[4] += 256 * w.wave + w.lane * 4;  // this wave's quarter of the 17th piece
+#pragma unroll
+    for (int j = 0; j < NBL; j++) {
+        piece_at(valid ? n0 + 16 * (w.wave + 4 * j) : p.N, p.N, p.K, w.offB[j], w.stB[j]);
+        w.offB[j] += w.lane * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < NA; j++) asm volatile("" : "+v"(w.offA[j]), "+v"(w.stA[j]));
+#pragma unroll
+    for (int j = 0; j < NBL; j++) asm volatile("" : "+v"(w.offB[j]), "+v"(w.stB[j]));
+    if (valid) {
+        w.cm0 = m0;
+        w.cn0 = n0;
+    }
+}
+
+// Load j (0-3 whole A pieces, 4 the quarter, 5-7 B pieces) of the cursors'
+// K-step into the stage at d (this wave's first A piece) / dq (its quarter);
+// the piece's cursor advances.
+template <int J>
+__device__ __forceinline__ void load1(Tw& w, int8_t* d, int8_t* dq) {
+    if constexpr (J < 4) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)(d + 4096 * J), 16, w.offA[J], 0, 0, 0);
+        w.offA[J] += w.stA[J];
+    } else if constexpr (J == 4) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rA, (lptr_t)dq, 4, w.offA[4], 0, 0, 0);
+        w.offA[4] += w.stA[4];
+    } else {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(w.rB, (lptr_t)(d + BOFF + 4096 * (J - 5)), 16, w.offB[J - 5], 0, 0,
+                                                 0);
+        w.offB[J - 5] += w.stB[J - 5];
+    }
+}
+
+// The destinations are computed in the K-step from an opaque base: hoisted
+// out of the loop, the 32 of the four stages would sit in SGPRs and spill.
+template <int ST>
+__device__ __forceinline__ int8_t* load_base(const Tw& w) {
+    return opaque_lds(w.lds + ST * STG + 1024 * w.wave);
+}
+template <int ST>
+__device__ __forceinline__ int8_t* quarter_base(const Tw& w) {
+    return opaque_lds(w.lds + ST * STG + 16 * 1024 + 256 * w.wave);
+}
+
+// The cursors' whole K-step into stage ST (the prologue's loads).
+template <int ST>
+__device__ __forceinline__ void load_step(Tw& w) {
+    int8_t* d = load_base<ST>(w);
+    int8_t* dq = quarter_base<ST>(w);
+    load1<0>(w, d, dq);
+    load1<1>(w, d, dq);
+    load1<2>(w, d, dq);
+    load1<3>(w, d, dq);
+    load1<4>(w, d, dq);
+    load1<5>(w, d, dq);
+    load1<6>(w, d, dq);
+    load1<7>(w, d, dq);
+}
+
+// The epilogue operands of the cursors' tile into area le: twelve 256-byte
+// slots (row scales 0-4, column scales 5-7, bias 8-10, nothing 11), three a
+// wave, one dword a lane.  Past M or N, or with an operand absent (or the
+// column scale a scalar, read in the epilogue instead), a slot's source range
+// is short or empty and its words read as zero.
+__device__ __forceinline__ void issue_epi(const Tw& w, const GemmParams& p, int8_t* le) {
+    const int rows = min(TM, p.M - w.cm0), cols = min(TN, p.N - w.cn0);
+    const int bsz = p.bias_kind == BIAS_F32 ? 4 : 2;
+    const bool per_col = p.sB && !p.sb_scalar, has_bias = p.bias_kind != BIAS_NONE;
+    const int8_t* sa = p.sA ? (const int8_t*)(p.sA + w.cm0) : p.A;
+    const int8_t* sb = per_col ? (const int8_t*)(p.sB + w.cn0) : p.A;
+    const int8_t* bz = has_bias ? (const int8_t*)p.bias + (int64_t)w.cn0 * bsz : p.A;
+    const int na = p.sA ? rows * 4 : 0, nb = per_col ? cols * 4 : 0, nz = has_bias ? cols * bsz : 0;
+#pragma unroll
+    for (int q = 0; q < NE; q++) {
+        // Selects on wave-uniform values: no branch inside the K-step's
+        // scheduled block.
+        const int s = 3 * w.wave + q;
+        const bool isA = s < 5, isB = !isA && s < 8, isZ = !isA && !isB && s < 11;
+        const int8_t* base = isA ? sa : isB ? sb : isZ ? bz : p.A;
+        const int bytes = isA ? na : isB ? nb : isZ ? nz : 0;
+        const int idx = isA ? s : isB ? s - 5 : isZ ? s - 8 : 0;
+        const int dst = (isA ? E_SA : isB ? E_SB : isZ ? E_BZ : E_PAD) + 256 * idx;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(whole_rsrc(base, bytes), (lptr_t)(le + dst), 4, w.lane * 4, 256 * idx,
+                                                 0, 0);
+    }
+}
+
+// Fragments of stage ST: A block rows 8 WM .. 8 WM + 8, B block columns
+// 6 wn .. 6 wn + 5.
+// Fragment bases of stage ST for this lane: A block rows 8 WM .., B block
+// columns 6 wn ...  The wave-uniform part is laundered through an SGPR in the
+// K-step: otherwise the compiler hoists one address register per read (stage
+// offsets past 64 KB do not fit the 16-bit ds_read offset), some 40 VGPRs.
+template <int WM, int ST>
+__device__ __forceinline__ const int8_t* frag_a(const Tw& w) {
+    return opaque_lds(w.lds + ST * STG + 1024 * 8 * WM) + w.oF;
+}
+template <int WM, int ST>
+__device__ __forceinline__ const int8_t* frag_b(const Tw& w) {
+    return opaque_lds(w.lds + ST * STG + BOFF + 6144 * w.wn) + w.oF;
+}
+
+// Fragment read J: 0-8 the A block rows, 9-14 the B block columns.
+template <int J>
+__device__ __forceinline__ void read1(Frag& f, const int8_t* a, const int8_t* b) {
+    if constexpr (J < 9) f.a[J] = *(const v4i*)(a + 1024 * J);
+    else f.b[J - 9] = *(const v4i*)(b + 1024 * (J - 9));
+}
+
+template <int WM, int ST>
+__device__ __forceinline__ void frag(Frag& f, const Tw& w) {
+    const int8_t* a = frag_a<WM, ST>(w);
+    const int8_t* b = frag_b<WM, ST>(w);
+#pragma unroll
+    for (int i = 0; i < 9; i++) f.a[i] = *(const v4i*)(a + 1024 * i);
+#pragma unroll
+    for (int c = 0; c < 6; c++) f.b[c] = *(const v4i*)(b + 1024 * c);
+}
+
+// MFMA q (0 .. 50) of the wave's K-step.  wm = 0: q < 48 is full row q / 6
+// (A fragment q / 6), column q % 6; q >= 48 the shared row (A fragment 8),
+// columns 0-2.  wm = 1: q < 3 the shared row (A fragment 0), columns 3-5;
+// then full rows (A fragments 1-8).
+template <int WM, int Q, bool Z>
+__device__ __forceinline__ void mma1(const Frag& f, Acc& acc) {
+    if constexpr (WM == 0 && Q >= 48) {
+        constexpr int c = Q - 48;
+        acc.s[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[c], f.a[8], Z ? v4i{} : acc.s[c], 0, 0, 0);
+    } else if constexpr (WM == 1 && Q < 3) {
+        acc.s[Q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[3 + Q], f.a[0], Z ? v4i{} : acc.s[Q], 0, 0, 0);
+    } else {
+        constexpr int q = WM == 0 ? Q : Q - 3, r = q / 6, c = q % 6;
+        acc.f[r][c] =
+            __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[c], f.a[r + WM], Z ? v4i{} : acc.f[r][c], 0, 0, 0);
+    }
+}
+
+struct NextTile {
+    int m0, n0;
+    bool valid;
+};
+
+// The K-step's instruction order, fixed: MFMA q, then the fragment read and
+// the load that slot q carries, then a scheduling fence.  Reads of K-step
+// k + 1's fragments go to slots 2, 4, .., 30, the loads of K-step k + 4 to
+// slots 4, 10, .., 46, and (K-step KT - 4) the next tile's epilogue operands
+// to slot 48.  Left to the scheduler, an interleave of the same instructions
+// made the register allocator rotate the accumulators through spare AGPRs and
+// VGPRs, with copies and s_nop waits in every K-step.
+template <int Q>
+struct Slot {
+    static constexpr int read = Q >= 2 && Q <= 30 && Q % 2 == 0 ? (Q - 2) / 2 : -1;
+    static constexpr int load = Q >= 4 && (Q - 4) % 6 == 0 && (Q - 4) / 6 < NLD ? (Q - 4) / 6 : -1;
+};
+
+struct StepPtrs {
+    const int8_t *ra, *rb;  // fragment bases of the next K-step's stage
+    int8_t *d, *dq;         // load destinations in this K-step's stage
+    int8_t* ln;             // the next tile's epilogue-operand area
+};
+
+template <int WM, bool Z, bool SW, int Q>
+__device__ __forceinline__ void kslots(const Frag& f, Frag& g, Acc& acc, Tw& w, const GemmParams& p,
+                                       const StepPtrs& sp) {
+    if constexpr (Q < 51) {
+        mma1<WM, Q, Z>(f, acc);
+        if constexpr (Slot<Q>::read >= 0) read1<Slot<Q>::read>(g, sp.ra, sp.rb);
+        if constexpr (Slot<Q>::load >= 0) load1<Slot<Q>::load>(w, sp.d, sp.dq);
+        if constexpr (SW && Q == 48) issue_epi(w, p, sp.ln);
+        __builtin_amdgcn_sched_barrier(0);
+        kslots<WM, Z, SW, Q + 1>(f, g, acc, w, p, sp);
+    }
+}
+
+// K-step k on stage S = k % 4, on the fragments f; K-step k + 1's are read
+// into g.  VWT: the wait's allowance.  Z: the tile's first K-step.  SW: the
+// cursors move to the next tile first (K-step KT - 4), and that tile's
+// epilogue operands are loaded into area ln after the K-step's loads.
+template <int WM, int S, int VWT, bool Z, bool SW>
+__device__ __forceinline__ void kstep(const Frag& f, Frag& g, Acc& acc, Tw& w, const GemmParams& p,
+                                      const NextTile& nt, int8_t* ln) {
+    if constexpr (SW) cursor_to(w, p, nt.m0, nt.n0, nt.valid);
+    wait_vm_lgkm0<VWT>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    StepPtrs sp;
+    sp.ra = frag_a<WM, (S + 1) % NSTG>(w);
+    sp.rb = frag_b<WM, (S + 1) % NSTG>(w);
+    sp.d = load_base<S>(w);
+    sp.dq = quarter_base<S>(w);
+    sp.ln = ln;
+    kslots<WM, Z, SW, 0>(f, g, acc, w, p, sp);
+}
+
+// Column operands of this lane: columns 16 c + 4 (l / 16) .. + 3 of the
+// wave's 96 (c = 0 .. 5).  The bias area holds bf16 pairs or fp32 words (zeros
+// without a bias); both views are read and the uniform format selects.
+struct ColOps {
+    v4f sb[6], bz[6];
+};
+
+// Block row R (0 .. 8) of the wave's epilogue: tile block row 8 WM + R; the
+// shared one (R = 8 for wm = 0, R = 0 for wm = 1) holds wave column blocks
+// 3 WM .. 3 WM + 2.  Convert, write the wave's staging rows, read them back as
+// 16-byte pieces (piece x: row x % 16, piece x / 16 of the row) and store.
+template <int WM, int CK, int R>
+__device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
+                                        const int8_t* e, const __amdgpu_buffer_rsrc_t& rs, int pitch, int colw) {
+    constexpr bool shared = WM == 0 ? R == 8 : R == 0;
+    constexpr int g = 8 * WM + R;          // block row in the tile
+    constexpr int c0 = shared ? 3 * WM : 0;  // first wave column block
+    constexpr int nb = shared ? 3 : 6;
+    constexpr int fr = WM == 0 ? R : R - 1;  // full-row index (unused for the shared row)
+    const int lr = w.lane & 15, lg = w.lane >> 4;
+    int8_t* lc = w.lc;
+    const float sa = CK != C_I32 ? *(const float*)(e + E_SA + (16 * g + lr) * 4) : 0.0f;
+#pragma unroll
+    for (int c = 0; c < nb; c++) {
+        v4i blk;
+        if constexpr (shared) blk = acc.s[c];
+        else blk = acc.f[fr < 0 ? 0 : fr][c];
+        asm volatile("" : "+v"(blk));
+        if constexpr (CK == C_BF16) {
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]);
+            *(u32x2*)(lc + lr * SP + c * 32 + lg * 8) = u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+        } else {
+            u32x4 o;
+            if constexpr (CK == C_F32) {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    o[q] = __float_as_uint(fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]));
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) o[q] = (unsigned)blk[q];
+            }
+            // fp32 / int32: three blocks (192 bytes a row) a pass.
+            *(u32x4*)(lc + lr * SP + (c % 3) * 64 + lg * 16) = o;
+            if (c % 3 == 2) {
+                const int cg = c - 2;
+#pragma unroll
+                for (int t = 0; t < 3; t++) {
+                    const int x = w.lane + 64 * t, ch = x >> 4, rr = x & 15;
+                    const u32x4 v = *(const u32x4*)(lc + rr * SP + ch * 16);
+                    const int col = colw + 16 * (c0 + cg) + 4 * ch;
+                    const int off = col < p.N ? (16 * g + rr) * pitch + col * 4 : kDropOffset;
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
+                }
+            }
+        }
+    }
+    if constexpr (CK == C_BF16) {
+        // 16 rows x 2 nb pieces: three stores a lane for a full row, two (the
+        // second half empty) for the shared one.
+#pragma unroll
+        for (int t = 0; t < (shared ? 2 : 3); t++) {
+            const int x = w.lane + 64 * t, ch = x >> 4, rr = x & 15;
+            const u32x4 v = *(const u32x4*)(lc + rr * SP + ch * 16);
+            const int col = colw + 16 * c0 + 8 * ch;
+            const int off = col < p.N && ch < 2 * nb ? (16 * g + rr) * pitch + col * 2 : kDropOffset;
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int WM, int CK, int R = 0>
+__device__ __forceinline__ void epi_rows(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
+                                         const int8_t* e, const __amdgpu_buffer_rsrc_t& rs, int pitch, int colw) {
+    if constexpr (R < 9) {
+        epi_row<WM, CK, R>(acc, co, p, w, e, rs, pitch, colw);
+        epi_rows<WM, CK, R + 1>(acc, co, p, w, e, rs, pitch, colw);
+    }
+}
+
+// Epilogue of the tile at (m0, n0) with operands in area e; s0 is the column
+// scale when it is one scalar.
+template <int WM, int CK>
+__device__ __forceinline__ void epilogue(Acc& acc, const GemmParams& p, int m0, int n0, const Tw& w, const int8_t* e,
+                                         float s0) {
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int c = 0; c < 6; c++) asm volatile("" : "+a"(acc.f[r][c]));
+#pragma unroll
+    for (int c = 0; c < 3; c++) asm volatile("" : "+a"(acc.s[c]));
+    constexpr int esz = CK == C_BF16 ? 2 : 4;
+    const int pitch = (int)p.ldc * esz;
+    const __amdgpu_buffer_rsrc_t rs = whole_rsrc((int8_t*)p.C + (int64_t)m0 * pitch, min(TM, p.M - m0) * pitch);
+    ColOps co;
+    if constexpr (CK != C_I32) {
+        const bool bf = p.bias_kind == BIAS_BF16, sbs = p.sb_scalar != 0;
+        const int lg = w.lane >> 4;
+#pragma unroll
+        for (int c = 0; c < 6; c++) {
+            const int col = 96 * w.wn + 16 * c + 4 * lg;
+            const v4f fz = *(const v4f*)(e + E_BZ + col * 4);
+            const u32x2 hz = *(const u32x2*)(e + E_BZ + col * 2);
+            const v4f hb = {bf16_to_f32(hz[0] & 0xffffu), bf16_to_f32(hz[0] >> 16), bf16_to_f32(hz[1] & 0xffffu),
+                            bf16_to_f32(hz[1] >> 16)};
+            co.bz[c] = bf ? hb : fz;
+            const v4f sv = *(const v4f*)(e + E_SB + col * 4);
+            co.sb[c] = sbs ? v4f{s0, s0, s0, s0} : sv;
+        }
+    }
+    epi_rows<WM, CK>(acc, co, p, w, e, rs, pitch, n0 + 96 * w.wn);
+}
+
+template <int WM>
+__device__ __forceinline__ NextTile next_tile(const Shape& s, int t, bool valid) {
+    NextTile nt{0, 0, valid};
+    if (valid) {
+        int tm, tn;
+        tile_mn(s, t, tm, tn);
+        nt.m0 = tm * TM;
+        nt.n0 = tn * TN;
+    }
+    return nt;
+}
+
+// The persistent loop of one wave (block-row half WM).  K % 512 == 0.
+template <int WM, int CK>
+__device__ __forceinline__ void t272_tiles(const GemmParams& p, int8_t* lds, int8_t* eall, int8_t* cbuf, int wave) {
+    // bf16: the epilogue's stores stay in flight into the next tile, and its
+    // first three waits count them.  fp32 / int32 issue 51 stores, more than
+    // the wait counter holds beside the loads: the epilogue drains them.
+    constexpr int NST = CK == C_BF16 ? Nst<CK>::v : 0;
+    constexpr int VWR = VW + NST, VWE = VW + NE;
+    static_assert(3 * NLD + NST < 64 && VWR < 64, "vmcnt is six bits");
+    Tw w;
+    w.lane = threadIdx.x & 63;
+    w.wave = wave;
+    w.wn = wave & 1;
+    {
+        const int lr = w.lane & 15, c = (w.lane >> 4) ^ ((lr >> 2) & 3);
+        w.oF = lr * PK + c * 16;
+    }
+    Shape s;
+    s.tiles_m = (p.M + TM - 1) / TM;
+    s.tiles_n = (p.N + TN - 1) / TN;
+    s.ntiles = s.tiles_m * s.tiles_n;
+    s.KT = p.K / PK;
+    s.group_m = p.group_m;
+    s.G = gridDim.x;
+    init_div(s);
+    const int r0 = xcd_remap(blockIdx.x, s.G);
+    if (r0 >= s.ntiles) return;
+    const int ntile = (s.ntiles - r0 - 1) / s.G + 1;
+    const float s0 = p.sb_scalar && p.sB ? p.sB[0] : 0.0f;
+    w.lds = opaque_lds(lds);
+    w.le = eall;
+    w.lc = cbuf + wave * SBYTES;
+    w.rA = whole_rsrc(p.A, p.M * p.K);
+    w.rB = whole_rsrc(p.B, p.N * p.K);
+    // Prologue: the epilogue operands and K-steps 0-3 of the first tile, then
+    // NST stores that land nowhere, standing where a previous tile's epilogue
+    // stores stand, so every tile's first waits count alike.
+    const NextTile first = next_tile<WM>(s, r0, true);
+    cursor_to(w, p, first.m0, first.n0, true);
+    issue_epi(w, p, w.le);
+    load_step<0>(w);
+    load_step<1>(w);
+    load_step<2>(w);
+    load_step<3>(w);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NST > 0) {
+        const __amdgpu_buffer_rsrc_t nowhere = whole_rsrc(p.C, 0);
+#pragma unroll
+        for (int d = 0; d < NST; d++) __builtin_amdgcn_raw_buffer_store_b32(0u, nowhere, w.lane * 4 + d * 256, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm0<3 * NLD + NST>();  // the epilogue operands and K-step 0 have landed
+    __builtin_amdgcn_s_barrier();
+    Frag f, g;
+    frag<WM, 0>(f, w);
+    Acc acc;
+    NextTile cur = first;
+    for (int i = 0;;) {
+        const int t = r0 + i * s.G;
+        int8_t* le = w.le + (i & 1) * EB;
+        int8_t* ln = w.le + ((i + 1) & 1) * EB;
+        const NextTile nt = next_tile<WM>(s, t + s.G, i + 1 < ntile);
+        PHI_T272_STAMP(i, 0);
+        kstep<WM, 0, VWR, true, false>(f, g, acc, w, p, nt, ln);
+        kstep<WM, 1, VWR, false, false>(g, f, acc, w, p, nt, ln);
+        kstep<WM, 2, VWR, false, false>(f, g, acc, w, p, nt, ln);
+        kstep<WM, 3, VW, false, false>(g, f, acc, w, p, nt, ln);
+        for (int k = 4; k < s.KT - 4; k += 4) {
+            kstep<WM, 0, VW, false, false>(f, g, acc, w, p, nt, ln);
+            kstep<WM, 1, VW, false, false>(g, f, acc, w, p, nt, ln);
+            kstep<WM, 2, VW, false, false>(f, g, acc, w, p, nt, ln);
+            kstep<WM, 3, VW, false, false>(g, f, acc, w, p, nt, ln);
+        }
+        kstep<WM, 0, VW, false, true>(f, g, acc, w, p, nt, ln);
+        kstep<WM, 1, VWE, false, false>(g, f, acc, w, p, nt, ln);
+        kstep<WM, 2, VWE, false, false>(f, g, acc, w, p, nt, ln);
+        kstep<WM, 3, VWE, false, false>(g, f, acc, w, p, nt, ln);
+        PHI_T272_STAMP(i, 1);
+        epilogue<WM, CK>(acc, p, cur.m0, cur.n0, w, le, s0);
+        PHI_T272_STAMP(i, 2);
+        if constexpr (NST == 0) wait_all();
+        if (++i == ntile) break;
+        cur = nt;
+    }
+    // Loads past the last K-step (zeros, into released stages) and the
+    // epilogue's stores are still in flight: let them land before the LDS is
+    // released.
+    wait_all();
+}
+
+template <int CK>
+__global__ __launch_bounds__(256) void i8_gemm_t272_kernel(GemmParams p) {
+    __shared__ __align__(16) int8_t lds[NSTG * STG];
+    __shared__ __align__(16) int8_t eall[2 * EB];
+    __shared__ __align__(16) int8_t cbuf[4 * SBYTES];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+    PHI_T272_TRACE_BEGIN
+    if (wave < 2) t272_tiles<0, CK>(p, lds, eall, cbuf, wave);
+    else t272_tiles<1, CK>(p, lds, eall, cbuf, wave);
+    PHI_T272_TRACE_END
+}
+
+}  // namespace
+
+int t272_tile_count(int64_t M, int64_t N) { return (int)(((M + TM - 1) / TM) * ((N + TN - 1) / TN)); }
+
+bool t272_ok(const GemmParams& p) {
+    const int64_t esz = p.c_kind == C_BF16 ? 2 : 4;
+    return p.kt && !p.gate && p.K % 512 == 0 && (int64_t)p.M * p.K < ((int64_t)1 << 31) - (1 << 20) &&
+           (int64_t)p.N * p.K < ((int64_t)1 << 31) - (1 << 20) && (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) &&
+           p.N % (16 / esz) == 0;
+}
+
+hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_cus) {
+    if (!t272_ok(p)) return hipErrorInvalidValue;
+    const int tiles = t272_tile_count(p.M, p.N);
+    const dim3 g3(tiles < num_cus ? tiles : num_cus), b3(256);
+    if (p.c_kind == C_BF16) hipLaunchKernelGGL((i8_gemm_t272_kernel<C_BF16>), g3, b3, 0, stream, p);
+    else if (p.c_kind == C_F32) hipLaunchKernelGGL((i8_gemm_t272_kernel<C_F32>), g3, b3, 0, stream, p);
+    else hipLaunchKernelGGL((i8_gemm_t272_kernel<C_I32>), g3, b3, 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace phi_dev

@@ -1,0 +1,131 @@
+"""GPU parity of the 272 x 192 persistent GEMM (i8_gemm_t272.hip).
+
+The kernel serves K-tiled problems whose rounds it fills better than the
+square plan (config 1 up and down, config 2's shape).  Its outputs must equal
+the row-major path's bit for bit (that path is held bit-exact against the
+oracle by the other GPU tests), and at config 1 down the oracle itself checks
+sampled rows of every tile row:
+* forced on (PHI_GEMM_T272=1) over ragged shapes: M and N not multiples of
+  the tile, partial 256-row strips of the K-tiled layout, fewer tiles than
+  CUs, several tiles a workgroup, K from 512 up;
+* every output kind (bf16, fp32, int32), per-column or scalar column scales,
+  no / fp32 / bf16 bias;
+* the shapes the plan picks it for by itself, against the square plan
+  (PHI_GEMM_T272=0) in the same process.
+"""
+import numpy as np
+import pytest
+import torch
+
+import phi_qlinear as Q
+from phi_qlinear import synth
+
+pytestmark = pytest.mark.gpu
+
+ODT = {"bf16": torch.bfloat16, "f32": torch.float32, "i32": torch.int32}
+
+
+def _bits(t):
+    return t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
+
+
+def _operands(dev, M, N, K, seed):
+    A = synth.int8_weight(M, K, seed=seed, device=dev)
+    B = synth.int8_weight(N, K, seed=seed + 1, device=dev)
+    sA = torch.rand(M, device=dev) * 0.01 + 1e-3
+    sB = torch.rand(N, device=dev) * 0.01 + 1e-3
+    return A, B, sA, sB
+
+
+SHAPES = [
+    (272, 192, 512),      # one tile
+    (300, 200, 512),      # ragged in both, four tiles
+    (100, 8, 1024),       # a partial tile, N = one 16-byte piece
+    (4352, 3072, 512),    # config 1 down's tile grid at small K
+    (1000, 4000, 1024),   # several tiles a workgroup, partial strips
+    (4352, 12288, 512),   # config 1 up's grid, four tiles a workgroup
+    (555, 9216, 3072),
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("out", ["bf16", "f32", "i32"])
+def test_forced_matches_row_major(dev, monkeypatch, M, N, K, out):
+    A, B, sA, sB = _operands(dev, M, N, K, seed=M + N)
+    bias = synth.bias(N, seed=3, device=dev)
+    want = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=ODT[out])
+    monkeypatch.setenv("PHI_GEMM_T272", "1")
+    got = Q.i8_gemm_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, sA, sB, bias, out_dtype=ODT[out])
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("bias_kind", ["none", "f32", "bf16"])
+@pytest.mark.parametrize("scalar_sb", [False, True])
+def test_epilogue_operands(dev, monkeypatch, bias_kind, scalar_sb):
+    M, N, K = 600, 1000, 1024
+    A, B, sA, sB = _operands(dev, M, N, K, seed=21)
+    if scalar_sb:
+        sB = synth.weight_scale(0.002, device=dev)
+    bias = {"none": None, "f32": torch.randn(N, device=dev) * 0.02,
+            "bf16": synth.bias(N, seed=4, device=dev)}[bias_kind]
+    want = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=torch.bfloat16)
+    monkeypatch.setenv("PHI_GEMM_T272", "1")
+    got = Q.i8_gemm_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, sA, sB, bias, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4352, 3072, 12288), (4352, 9216, 3072)])
+def test_chosen_plan_matches_square_plan(dev, monkeypatch, M, N, K):
+    """At the DiT shapes the plan takes 272 x 192 tiles by itself; the result
+    equals the square plan's."""
+    A, B, sA, sB = _operands(dev, M, N, K, seed=7)
+    sB = synth.weight_scale(0.002, device=dev)
+    bias = synth.bias(N, seed=5, device=dev)
+    Ak, Bk = Q.pack_k_tiled(A), Q.pack_k_tiled(B)
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
+    want = Q.i8_gemm_kt(Ak, Bk, M, N, K, sA, sB, bias, out_dtype=torch.bfloat16)
+    monkeypatch.delenv("PHI_GEMM_T272")
+    got = Q.i8_gemm_kt(Ak, Bk, M, N, K, sA, sB, bias, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
+
+
+def test_config1_down_rows_against_oracle(dev, orc):
+    """The linear at config 1 down's shape (K = 12288 -> N = 3072, bf16 bias,
+    bf16 out) on the plan's own choice, with the first and last row of each of
+    the 16 tile rows of 272 and a stride through the rest compared bit for bit
+    with the oracle: the int8 codes (unpacked from the K-tiled layout), the
+    fp32 scales, the int32 accumulators of the same plan and the outputs."""
+    M, K, N = 4352, 12288, 3072
+    print(f"t272 config 1 down M={M} K={K} N={N}", flush=True)
+    x = synth.activations(M, K, seed=31, device=dev)
+    W = synth.int8_weight(N, K, seed=32, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=33, device=dev)
+    Wk = Q.pack_k_tiled(W)
+    qk = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = Q.q8_linear_kt(x, Wk, N, sW, b, q8=qk, s8=s8)
+    acc = Q.i8_gemm_kt(qk, Wk, M, N, K, None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    tiles = np.arange(0, M, 272)
+    rows = np.unique(np.concatenate([tiles, tiles + 271, np.arange(5, M, 97)]))
+    assert len(np.unique(rows // 272)) == 16
+    r, k = rows[:, None], np.arange(K)[None, :]
+    s, rr = r // 256, r % 256
+    h = np.minimum(256, M - 256 * s)
+    pos = 256 * K * s + h * 64 * (k // 64) + 64 * rr + 16 * (((k // 16) % 4) ^ ((rr // 4) % 4)) + k % 16
+    q_rows = qk.cpu().numpy()[pos]
+
+    def u16(t):
+        return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+    ri = torch.from_numpy(rows).to(dev)
+    yo, qo, so, acco = orc.q8_linear(u16(x[ri]), W.cpu().numpy(), sW.cpu().numpy(), u16(b))
+    assert np.array_equal(q_rows, qo), f"{(q_rows != qo).sum()} code mismatches"
+    assert np.array_equal(s8[ri].cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(acc[ri].cpu().numpy(), acco)
+    got = u16(y[ri])
+    assert np.array_equal(got, yo), f"{(got != yo).sum()} bf16 mismatches"
