@@ -81,11 +81,18 @@ constexpr int NE = 3;                  // epilogue-operand loads a wave issues p
 // (272 used of 320), column scales, bias (fp32 words or bf16 pairs), and
 // the landing place of loads that fetch nothing.
 constexpr int E_SA = 0, E_SB = 1280, E_BZ = 2048, E_PAD = 2816, EB = 3072;
-// Epilogue staging: 16 rows of up to 6 blocks x 32 bytes (bf16) or 3 blocks
-// x 64 bytes (fp32 / int32), at a pitch of 208 bytes: the rows start at 16
-// distinct multiples of four banks, so a block's 8-byte (16-byte) writes and
-// the read-back of one 16-byte piece from 16 rows touch every bank once.
-constexpr int SP = 208, SBYTES = 16 * SP;
+// Epilogue staging: 16 rows of 12 16-byte pieces (6 blocks x 32 bytes of
+// bf16, or 3 blocks x 64 bytes of fp32 / int32) at a pitch of 192 bytes, piece
+// c of row r in slot (c + r / 4) % 12.  The read-back takes the pieces in row
+// order, so 16 consecutive lanes read 16 consecutive slots of the 192-byte
+// rows (distinct bank windows), and each store instruction writes rows of 192
+// contiguous bytes; the rotation spreads a block's writes from 16 rows (whose
+// pitch alone repeats every four rows) over every bank once.
+constexpr int SP = 192, SBYTES = 16 * SP;
+__device__ __forceinline__ int stage_slot(int r, int c) {
+    const int x = c + (r >> 2);
+    return x >= 12 ? x - 12 : x;
+}
 // Stores a wave issues in an epilogue: bf16 8 full block rows x 3 + the shared
 // one 2; fp32 / int32 8 x 6 + 3.  Every one is issued (columns past N go to
 // an offset the range check drops).
@@ -373,7 +380,8 @@ __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmPa
             float v[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) v[q] = fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]);
-            *(u32x2*)(lc + lr * SP + c * 32 + lg * 8) = u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+            *(u32x2*)(lc + lr * SP + stage_slot(lr, 2 * c + (lg >> 1)) * 16 + (lg & 1) * 8) =
+                u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
         } else {
             u32x4 o;
             if constexpr (CK == C_F32) {
@@ -385,13 +393,13 @@ __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmPa
                 for (int q = 0; q < 4; q++) o[q] = (unsigned)blk[q];
             }
             // fp32 / int32: three blocks (192 bytes a row) a pass.
-            *(u32x4*)(lc + lr * SP + (c % 3) * 64 + lg * 16) = o;
+            *(u32x4*)(lc + lr * SP + stage_slot(lr, 4 * (c % 3) + lg) * 16) = o;
             if (c % 3 == 2) {
                 const int cg = c - 2;
 #pragma unroll
                 for (int t = 0; t < 3; t++) {
-                    const int x = w.lane + 64 * t, ch = x >> 4, rr = x & 15;
-                    const u32x4 v = *(const u32x4*)(lc + rr * SP + ch * 16);
+                    const int x = w.lane + 64 * t, rr = x / 12, ch = x - 12 * rr;
+                    const u32x4 v = *(const u32x4*)(lc + rr * SP + stage_slot(rr, ch) * 16);
                     const int col = colw + 16 * (c0 + cg) + 4 * ch;
                     const int off = col < p.N ? (16 * g + rr) * pitch + col * 4 : kDropOffset;
                     __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
@@ -400,14 +408,15 @@ __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmPa
         }
     }
     if constexpr (CK == C_BF16) {
-        // 16 rows x 2 nb pieces: three stores a lane for a full row, two (the
-        // second half empty) for the shared one.
+        // 16 rows x 2 nb pieces in row order (piece x: row x / (2 nb), piece
+        // x % (2 nb) of the row): three stores a lane for a full row, two
+        // (the second half empty) for the shared one.
 #pragma unroll
         for (int t = 0; t < (shared ? 2 : 3); t++) {
-            const int x = w.lane + 64 * t, ch = x >> 4, rr = x & 15;
-            const u32x4 v = *(const u32x4*)(lc + rr * SP + ch * 16);
+            const int x = w.lane + 64 * t, rr = x / (2 * nb), ch = x - 2 * nb * rr;
+            const u32x4 v = *(const u32x4*)(lc + (rr & 15) * SP + stage_slot(rr & 15, ch) * 16);
             const int col = colw + 16 * c0 + 8 * ch;
-            const int off = col < p.N && ch < 2 * nb ? (16 * g + rr) * pitch + col * 2 : kDropOffset;
+            const int off = col < p.N && rr < 16 ? (16 * g + rr) * pitch + col * 2 : kDropOffset;
             __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
         }
     }
