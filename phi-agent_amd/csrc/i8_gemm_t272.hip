@@ -130,6 +130,21 @@ struct Tw {
     int cm0, cn0;    // the cursors' tile
 };
 
+// LDS slot of 16-byte chunk c of row r (r within a 16-row piece):
+// c ^ ((r >> 1) & 3).  The fragment reads (row l % 16, chunk l / 16) of every
+// 16-lane group then meet no bank conflict on gfx950, as measured; the K-tiled
+// layout's own swizzle (c ^ ((r >> 2) & 3), the square kernels' LDS layout)
+// costs two extra clocks on every one of these reads.  The DMA keeps its
+// contiguous 1 KB sources: each lane fetches, from within the same 64-byte
+// row, the chunk its LDS slot holds.
+__device__ __forceinline__ int lds_slot(int r, int c) { return c ^ ((r >> 1) & 3); }
+// Byte offset, within a 16-row piece of the K-tiled layout, of the bytes the
+// DMA lane writing LDS piece byte q (a multiple of 4) fetches.
+__device__ __forceinline__ int dma_src(int q) {
+    const int r = q >> 6, slot = (q >> 4) & 3, c = slot ^ ((r >> 1) & 3);
+    return r * 64 + 16 * (c ^ ((r >> 2) & 3)) + (q & 15);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t whole_rsrc(const void* base, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, kRsrcWord3);
 }
@@ -150,14 +165,14 @@ __device__ __forceinline__ void cursor_to(Tw& w, const GemmParams& p, int m0, in
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         piece_at(valid ? m0 + 16 * (w.wave + 4 * j) : p.M, p.M, p.K, w.offA[j], w.stA[j]);
-        w.offA[j] += w.lane * 16;
+        w.offA[j] += dma_src(w.lane * 16);
     }
     piece_at(valid ? m0 + 256 : p.M, p.M, p.K, w.offA[4], w.stA[4]);
-    w.offA[4] += 256 * w.wave + w.lane * 4;  // this wave's quarter of the 17th piece
+    w.offA[4] += dma_src(256 * w.wave + w.lane * 4);  // this wave's quarter of the 17th piece
 #pragma unroll
     for (int j = 0; j < NBL; j++) {
         piece_at(valid ? n0 + 16 * (w.wave + 4 * j) : p.N, p.N, p.K, w.offB[j], w.stB[j]);
-        w.offB[j] += w.lane * 16;
+        w.offB[j] += dma_src(w.lane * 16);
     }
 #pragma unroll
     for (int j = 0; j < NA; j++) asm volatile("" : "+v"(w.offA[j]), "+v"(w.stA[j]));
@@ -491,8 +506,8 @@ __device__ __forceinline__ void t272_tiles(const GemmParams& p, int8_t* lds, int
     w.wave = wave;
     w.wn = wave & 1;
     {
-        const int lr = w.lane & 15, c = (w.lane >> 4) ^ ((lr >> 2) & 3);
-        w.oF = lr * PK + c * 16;
+        const int lr = w.lane & 15;
+        w.oF = lr * PK + lds_slot(lr, w.lane >> 4) * 16;
     }
     Shape s;
     s.tiles_m = (p.M + TM - 1) / TM;
