@@ -65,6 +65,10 @@ CONFIGS = {
     # pipeline rebuilt with its trace hooks in lib/libphi_probe.so).
     "c1_up_tiles": dict(kind="tiletrace", M=4352, K=3072, N=12288),
     "c1_down_tiles": dict(kind="tiletrace", M=4352, K=12288, N=3072),
+    # The same for the 272 x 192 kernel the plan picks at these shapes
+    # (i8_gemm_t272.hip rebuilt with its trace hooks in lib/libphi_probe.so).
+    "c1_up_t272_tiles": dict(kind="t272trace", M=4352, K=3072, N=12288),
+    "c1_down_t272_tiles": dict(kind="t272trace", M=4352, K=12288, N=3072),
     "c1_down_vendor": dict(kind="vendor", M=4352, K=12288, N=3072),
     # A reference point for the prologue: torch's bf16 -> int8 conversion of
     # the same activation tensor moves the prologue's bytes (2K in, K out a row).
@@ -622,6 +626,90 @@ def bench_tiletrace(cfg, steps, warmup):
             "extra": extra}
 
 
+def bench_t272trace(cfg, steps, warmup):
+    """The headline step (K-tiled quantiser, then the GEMM) with the GEMM
+    launched from the traced build of the 272 x 192 kernel
+    (phi_probe_t272_trace): the same kernel code plus shader-clock stamps per
+    workgroup at each tile's start, K-loop end and epilogue end.  The record
+    of the last timed launch gives where a workgroup's time goes: clocks a
+    K-step against the 816 of MFMA issue (51 MFMAs of 16 clocks), the
+    epilogue, and the set-up before the first tile."""
+    import ctypes
+
+    import torch
+
+    import phi_qlinear as Q
+    from phi_qlinear import synth
+
+    lib = ctypes.CDLL(os.path.join(PKG, "lib", "libphi_probe.so"))
+    P, I = ctypes.c_void_p, ctypes.c_int
+    lib.phi_probe_t272_trace.argtypes = [P, P, P, P, P, P, P, I, I, I, P, ctypes.c_longlong]
+    dev = torch.device("cuda:0")
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    x = synth.activations(M, K, seed=0, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    Wk = Q.pack_k_tiled(W)
+    q8 = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    slots = 1024 * 64
+    rec = torch.zeros(slots, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        Q.quant_rotate_kt(x, q=q8, s=s8)
+        rc = lib.phi_probe_t272_trace(stream, q8.data_ptr(), Wk.data_ptr(), s8.data_ptr(), sW.data_ptr(),
+                                      b.data_ptr(), y.data_ptr(), M, N, K, rec.data_ptr(), slots)
+        if rc != 0:
+            raise RuntimeError(f"phi_probe_t272_trace failed ({rc})")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    used = [w for w in rec.view(-1, 64).cpu().tolist() if w[0] != 0]
+    ksteps = K // 64
+    kl, ep, setup = [], [], []
+    for w in used:
+        setup.append(w[1] - w[0])
+        for i in range(16):
+            a, k, e = w[1 + 3 * i], w[2 + 3 * i], w[3 + 3 * i]
+            if a == 0:
+                break
+            kl.append(k - a)
+            ep.append(e - k)
+    cycles = [w[49] - w[0] for w in used]
+    clock = [(w[49] - w[0]) / ((w[52] - w[51]) * 10.0) for w in used if w[52] > w[51]]  # GHz
+    t0 = min(w[51] for w in used)
+    per_xcd = {}
+    for w in used:
+        per_xcd.setdefault(int(w[50]), []).append((w[52] - t0) / 100.0)
+    mean = lambda v: sum(v) / len(v) if v else None
+    extra = {
+        "workgroups": len(used), "tiles": len(kl), "ksteps_per_tile": ksteps,
+        "kloop_cycles_per_kstep": mean(kl) / ksteps, "mfma_issue_cycles_per_kstep": 51 * 16,
+        "epilogue_cycles": mean(ep), "setup_cycles": mean(setup),
+        "workgroup_cycles": {"mean": mean(cycles), "max": max(cycles)},
+        "mfma_issue_share": 51 * 16 * ksteps * len(kl) / len(used) / mean(cycles),
+        "shader_clock_ghz": mean(clock),
+        "kernel_end_by_xcd_us": {str(k): round(mean(v), 2) for k, v in sorted(per_xcd.items())},
+    }
+    log("bench: t272 tile trace " + json.dumps(extra))
+    ops = 2.0 * M * N * K
+    return {"value": ops / (ms * 1e-3) / 1e12, "ms": ms, "dtype": "int8", "unit": "TOPS",
+            "roofline": {"bound": "mfma", "achieved": ops / (ms * 1e-3) / 1e12, "peak": INT8_PEAK_TOPS,
+                         "unit": "TFLOP/s", "frac": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, "traffic": None},
+            "extra": extra}
+
+
 def bench_convref(cfg, steps, warmup):
     """torch's elementwise bf16 -> int8 conversion over the prologue's
     activation tensor: the prologue's HBM bytes with none of its work."""
@@ -896,6 +984,8 @@ def main() -> int:
         r = bench_lora(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "tiletrace":
         r = bench_tiletrace(cfg, args.steps, args.warmup)
+    elif cfg["kind"] == "t272trace":
+        r = bench_t272trace(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "convref":
         r = bench_convref(cfg, args.steps, args.warmup)
     elif cfg["kind"] == "qrfloor":
