@@ -774,6 +774,45 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     // K-tiled layout (K <= 16384; PHI_GEMM_KT=0 keeps them row-major, an A/B
     // switch).
     const size_t need = phi_hip_w4a8_workspace_bytes(M, N, K, group);
+    // The 272 x 192 pipeline expands the codes in LDS, with no workspace: on
+    // K-tiled activations, K % 1024 == 0 (t272w4_ok).  PHI_W4_T272=1 / 0
+    // prefers it to / keeps it from the expand-once path (an A/B switch);
+    // without a workspace it is the in-register path wherever it applies.
+    // A kernel forced by PHI_GEMM_KERNEL keeps its own path.
+    const int w4t = phi_dev::env_switch("PHI_W4_T272", -1, 0, 1);
+    if (!e && w4t != 0 && (w4t == 1 || !(need > 0 && workspace && ws_bytes >= need)) && K <= 16384 &&
+        aligned(q8, 16) && aligned(codes, 16) && codes_row_bytes % 16 == 0 &&
+        persist_ok(C, c_dtype, N, K, K, codes_row_bytes, ldc)) {
+        phi_dev::GemmParams q{};
+        q.A = q8;
+        q.B = (const int8_t*)codes;
+        q.sA = s8;
+        q.sB = s_w;
+        q.bias = bias;
+        q.C = C;
+        q.lda = K;
+        q.ldb = codes_row_bytes;
+        q.ldc = ldc;
+        q.M = (int)M;
+        q.N = (int)N;
+        q.K = (int)K;
+        q.sb_scalar = 0;
+        q.bias_kind = bk;
+        q.c_kind = c_kind_of(c_dtype);
+        q.group_m = 4;
+        q.lut = lut;
+        q.lut_groups = K / group;
+        int gs = 0;
+        while ((1ll << gs) < group) gs++;
+        q.group_shift = gs;
+        q.kt = 1;
+        set_vec_flags(q, c_dtype, ldc);
+        if (phi_dev::t272w4_ok(q)) {
+            st = phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode);
+            if (st != PHI_OK) return st;
+            return check_hip(phi_dev::launch_i8_gemm_t272w4((hipStream_t)stream, q, num_cus()), who);
+        }
+    }
     const bool expand = !force_staged && need > 0 && workspace && ws_bytes >= need && aligned(workspace, 16) &&
                         aligned(codes, 16) && codes_row_bytes % 16 == 0 && persist_ok(C, c_dtype, N, K, K, K, ldc);
     const char* ekt = getenv("PHI_GEMM_KT");

@@ -76,6 +76,10 @@ hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, c
 bool t272_ok(const GemmParams& p);
 int t272_tile_count(int64_t M, int64_t N);
 hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_cus);
+// The same tiles with B as W4 codes (p.B [N, ldb], p.lut, p.group_shift)
+// expanded in LDS; K-tiled A, K % 1024 == 0 (t272w4_ok).
+bool t272w4_ok(const GemmParams& p);
+hipError_t launch_i8_gemm_t272w4(hipStream_t stream, const GemmParams& p, int num_cus);
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out,
 // row-major or (kt, K % 64 == 0) in the K-tiled layout.
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out, bool kt = false);

@@ -292,6 +292,37 @@ __device__ __forceinline__ void frag(Frag& f, const Tw& w) {
 // (A fragment q / 6), column q % 6; q >= 48 the shared row (A fragment 8),
 // columns 0-2.  wm = 1: q < 3 the shared row (A fragment 0), columns 3-5;
 // then full rows (A fragments 1-8).
+// One MFMA with its accumulator tied in AGPRs (inline asm): the register
+// allocator can then neither rotate the accumulators through spare AGPRs nor
+// move them between iterations.  The compiler does not see the instruction,
+// so its hazard tracking does not cover the accumulator's first VALU read
+// after the last MFMA: mfma_drain() gives those wait states explicitly.
+__device__ __forceinline__ void mfma_tied(v4i& acc, const v4i& b, const v4i& a) {
+    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(b), "v"(a));
+}
+__device__ __forceinline__ void mfma_first(v4i& acc, const v4i& b, const v4i& a) {
+    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, 0" : "=a"(acc) : "v"(b), "v"(a));
+}
+// Wait states after the last MFMA before any VALU instruction reads its
+// accumulators: 18, more than the four-pass instruction's requirement.
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory"); }
+
+template <int WM, int Q, bool Z>
+__device__ __forceinline__ void mma1t(const Frag& f, Acc& acc) {
+    if constexpr (WM == 0 && Q >= 48) {
+        constexpr int c = Q - 48;
+        if constexpr (Z) mfma_first(acc.s[c], f.b[c], f.a[8]);
+        else mfma_tied(acc.s[c], f.b[c], f.a[8]);
+    } else if constexpr (WM == 1 && Q < 3) {
+        if constexpr (Z) mfma_first(acc.s[Q], f.b[3 + Q], f.a[0]);
+        else mfma_tied(acc.s[Q], f.b[3 + Q], f.a[0]);
+    } else {
+        constexpr int q = WM == 0 ? Q : Q - 3, r = q / 6, c = q % 6;
+        if constexpr (Z) mfma_first(acc.f[r][c], f.b[c], f.a[r + WM]);
+        else mfma_tied(acc.f[r][c], f.b[c], f.a[r + WM]);
+    }
+}
+
 template <int WM, int Q, bool Z>
 __device__ __forceinline__ void mma1(const Frag& f, Acc& acc) {
     if constexpr (WM == 0 && Q >= 48) {
@@ -361,6 +392,241 @@ __device__ __forceinline__ void kstep(const Frag& f, Frag& g, Acc& acc, Tw& w, c
     sp.dq = quarter_base<S>(w);
     sp.ln = ln;
     kslots<WM, Z, SW, 0>(f, g, acc, w, p, sp);
+}
+
+// ---------------------------------------------------------------------------
+// The W4 operand (asym_w4a8_int8): B is packed 4-bit codes [N, ldb] (low
+// nibble = even column, as the checkpoint stores them) with the per-(row,
+// group) 16-entry int8 table [N, K / group, 16] of the load-time prepare
+// (w4a8.hip).  The int32 accumulators are those of expand-then-W8A8 exactly:
+// every code becomes the int8 the expansion writes (the reference's
+// w4a8_to_i8 then int8 GEMM, core/kernels/w4a8_expand.cpp:151-258).
+//
+// The codes and tables are DMA'd into LDS rings and expanded there, once per
+// workgroup, into an int8 B area the MFMA fragments are read from:
+//   * LDS: A stages 4 x 17 KB | code stages 4 x 6 KB (192 rows x 32 bytes) |
+//     table stages 4 x 3 KB (192 rows x 16 bytes) | int8 B areas 2 x 12 KB,
+//     128 KB.  A K-step's B bytes in LDS are half the int8 kernel's.
+//   * K-step k: the loads of A of K-step k + 4 and of the codes and tables of
+//     K-step k + 5; the expansion of K-step k + 2's codes (thread t: rows
+//     t / 4 + 64 i, i < 3, 16 columns 16 (t % 4) ..; three 8-byte code reads,
+//     three table reads, 12 v_perm-based lookups, six 8-byte writes) into
+//     area k % 2; the fragment reads of K-step k + 1 (A from its stage, B
+//     from area (k + 1) % 2, expanded during K-step k - 1).  The K-step's one
+//     barrier orders all of it: its wait covers the loads of K-step k - 3
+//     (A of k + 1, codes and tables of k + 2), and every wave's reads of the
+//     stages and area it overwrites finished before it.
+//   * Each wave issues 11 loads a K-step: its 5 A pieces, one whole 1 KB code
+//     piece (32 rows) and two 256-byte quarters, and three 256-byte table
+//     quarters (16 rows each).  The code pieces are gathered row by row from
+//     the row-major codes (32 bytes a row and K-step); rows past N read past
+//     the resource and come back zero.
+// Expanding once per workgroup instead of once per wave that reads a B
+// fragment halves the lookups (each B fragment is read by two waves), and the
+// lookups are ~110 VALU instructions a wave a K-step beside its 51 MFMAs.
+constexpr int W4_CS = TN * 32, W4_LS = TN * 16, W4_BS = TN * PK;  // code, table, int8 B stage bytes
+constexpr int W4_C = NSTG * BOFF, W4_L = W4_C + NSTG * W4_CS, W4_B = W4_L + NSTG * W4_LS;
+constexpr int W4_LDS = W4_B + 2 * W4_BS;  // 131072
+constexpr int NC = 3, NTB = 3, NLD4 = NA + NC + NTB;  // loads a wave issues per K-step
+constexpr int VW4 = 2 * NLD4;
+
+// The code and table cursors: this lane's source byte of each of the wave's
+// code and table pieces at K-step 0 (codes advance 32 bytes a K-step, tables
+// 16 bytes a group, both through the scalar offset), and the cursors' K-step.
+struct W4c {
+    __amdgpu_buffer_rsrc_t rC, rL;
+    int offC[NC], offL[NTB];
+    int kc;
+};
+
+// Code and table cursors onto the tile with B rows n0 .., K-step 0; valid =
+// false: onto nothing (every source past the resources).
+__device__ __forceinline__ void w4_cursor_to(W4c& c, const Tw& w, const GemmParams& p, int n0, bool valid) {
+    const int N = p.N, ldb = (int)p.ldb, g16 = (int)p.lut_groups * 16;
+    const int base = valid ? n0 : N;
+    {
+        const int n = base + 32 * w.wave + (w.lane >> 1);  // whole piece w: rows 32 w .., 16 bytes a lane
+        c.offC[0] = n < N ? n * ldb + 16 * (w.lane & 1) : N * ldb;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int qi = 2 * w.wave + i;  // quarter qi of pieces 4-5: 8 rows, 4 bytes a lane
+        const int n = base + 128 + 32 * (qi >> 2) + 8 * (qi & 3) + (w.lane >> 3);
+        c.offC[1 + i] = n < N ? n * ldb + 4 * (w.lane & 7) : N * ldb;
+    }
+#pragma unroll
+    for (int i = 0; i < NTB; i++) {
+        const int n = base + 16 * (3 * w.wave + i) + (w.lane >> 2);  // table quarter: 16 rows, 4 bytes a lane
+        c.offL[i] = n < N ? n * g16 + 4 * (w.lane & 3) : N * g16;
+    }
+#pragma unroll
+    for (int i = 0; i < NC; i++) asm volatile("" : "+v"(c.offC[i]));
+#pragma unroll
+    for (int i = 0; i < NTB; i++) asm volatile("" : "+v"(c.offL[i]));
+    c.kc = 0;
+}
+
+// W4 stage bases (opaque, computed in the K-step like the int8 ones).
+template <int ST>
+__device__ __forceinline__ int8_t* w4_a_base(const Tw& w) {
+    return opaque_lds(w.lds + ST * BOFF + 1024 * w.wave);
+}
+template <int ST>
+__device__ __forceinline__ int8_t* w4_a_quarter(const Tw& w) {
+    return opaque_lds(w.lds + ST * BOFF + 16 * 1024 + 256 * w.wave);
+}
+
+// Load J of the code and table cursors' K-step: 0 the whole code piece, 1-2
+// the code quarters, 3-5 the table quarters, into code stage CS / table
+// stage CS.  The K-step advance rides in the scalar offset.
+template <int CS, int J>
+__device__ __forceinline__ void w4_load1(const W4c& c, const Tw& w, const GemmParams& p) {
+    if constexpr (J == 0) {
+        int8_t* d = opaque_lds(w.lds + W4_C + CS * W4_CS + 1024 * w.wave);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rC, (lptr_t)d, 16, c.offC[0], 32 * c.kc, 0, 0);
+    } else if constexpr (J < 3) {
+        const int qi = 2 * w.wave + (J - 1);
+        int8_t* d = opaque_lds(w.lds + W4_C + CS * W4_CS + 4096 + 1024 * (qi >> 2) + 256 * (qi & 3));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rC, (lptr_t)d, 4, c.offC[J], 32 * c.kc, 0, 0);
+    } else {
+        int8_t* d = opaque_lds(w.lds + W4_L + CS * W4_LS + 256 * (3 * w.wave + (J - 3)));
+        const int goff = ((c.kc * PK) >> p.group_shift) * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rL, (lptr_t)d, 4, c.offL[J - 3], goff, 0, 0);
+    }
+}
+
+// One expansion unit's state: 16 codes of one row, its table, a lookup's
+// selection mask, and the even and odd columns' words of the current 8 codes.
+struct W4u {
+    u32x2 code;
+    u32x4 tab;
+    uint32_t m, ev, od;
+};
+
+// Piece P (0 .. 10) of expansion unit U (thread t: row t / 4 + 64 U, columns
+// 16 (t % 4) ..).  0: the reads.  Then for each code word h (8 codes): the
+// even columns' lookup (mask, then the v_perm pair and select: lut4b split in
+// two), the odd columns' (the same on the high nibbles), and the interleave
+// of the two into 8 output bytes, written into int8 area bo.  No MFMA slot
+// carries more than five VALU instructions, and a unit keeps nine registers.
+// This thread's byte offsets of unit 0 in a code stage, a table stage and an
+// int8 B area (row t / 4, 16-byte chunk t % 4); unit u adds 64 u rows, an
+// immediate offset.
+struct W4o {
+    int c, t, b;
+};
+
+__device__ __forceinline__ W4o w4_lane_offsets(const Tw& w) {
+    const int t = 64 * w.wave + w.lane, r = t >> 2, ch = t & 3;
+    W4o o;
+    o.c = r * 32 + 8 * ch;
+    o.t = r * 16;
+    o.b = r * 64 + 16 * lds_slot(r & 15, ch);
+    asm volatile("" : "+v"(o.c), "+v"(o.t), "+v"(o.b));
+    return o;
+}
+
+template <int P>
+__device__ __forceinline__ void w4_piece(W4u& u, int U, const W4o& lo4, const int8_t* cs, const int8_t* ls,
+                                         int8_t* bo) {
+    if constexpr (P == 0) {
+        u.code = *(const u32x2*)(cs + lo4.c + 64 * 32 * U);
+        u.tab = *(const u32x4*)(ls + lo4.t + 64 * 16 * U);
+    } else {
+        constexpr int h = (P - 1) / 5, k = (P - 1) % 5;  // code word, step within it
+        const uint32_t x = u.code[h];
+        if constexpr (k == 0 || k == 2) {
+            // bit 3 of each code (bit 7 of the byte for the odd columns) picks
+            // entries 8-15: selector 0x0d gives 0xff, 0x0c gives 0x00
+            const uint32_t b = (k == 0 ? x >> 3 : x >> 7) & 0x01010101u;
+            u.m = __builtin_amdgcn_perm(0u, 0u, b | 0x0c0c0c0cu);
+        } else if constexpr (k == 1 || k == 3) {
+            const uint32_t sel = (k == 1 ? x : x >> 4) & 0x07070707u;
+            const uint32_t lo = __builtin_amdgcn_perm(u.tab[1], u.tab[0], sel);
+            const uint32_t hi = __builtin_amdgcn_perm(u.tab[3], u.tab[2], sel);
+            const uint32_t v = (hi & u.m) | (lo & ~u.m);
+            if constexpr (k == 1) u.ev = v;
+            else u.od = v;
+        } else {
+            // ev holds columns 0, 2, 4, 6 and od columns 1, 3, 5, 7: interleave.
+            const u32x2 o = {__builtin_amdgcn_perm(u.od, u.ev, 0x05010400u),
+                             __builtin_amdgcn_perm(u.od, u.ev, 0x07030602u)};
+            *(u32x2*)(bo + lo4.b + 64 * 64 * U + 8 * h) = o;
+        }
+    }
+}
+
+// The W4 K-step's fixed order: MFMA q, then what slot q carries.
+//   slots 1-15:             the 15 fragment reads of K-step k + 1
+//   slots 2, 6, .. 42:      the 11 loads (A 0-4, then codes and tables 0-5)
+//   slots 0, 12, 24:        unit u's reads (piece 0), eight slots before
+//   slots 8 + 12 u .. + 9:  its pieces 1-10
+//   slot 48:                (K-step KT - 4) the next tile's epilogue operands
+template <int Q>
+struct Slot4 {
+    static constexpr int read = Q >= 1 && Q <= 15 ? Q - 1 : -1;
+    static constexpr int load = Q >= 2 && (Q - 2) % 4 == 0 && (Q - 2) / 4 < NLD4 ? (Q - 2) / 4 : -1;
+    static constexpr int ureads = Q <= 24 && Q % 12 == 0 ? Q / 12 : -1;
+    static constexpr int piece =  // 10 u + (p - 1)
+        Q >= 8 && (Q - 8) / 12 < 3 && (Q - 8) % 12 < 10 ? 10 * ((Q - 8) / 12) + (Q - 8) % 12 : -1;
+};
+
+struct StepPtrs4 {
+    const int8_t *ra, *rb;  // fragment bases of K-step k + 1 (A stage, int8 B area)
+    int8_t *da, *dq;        // A load destinations in this K-step's stage
+    const int8_t *cs, *ls;  // code and table stages of K-step k + 2
+    int8_t* bo;             // int8 B area being written
+    int8_t* ln;             // the next tile's epilogue-operand area
+};
+
+template <int WM, int CS, bool Z, bool SW, int Q>
+__device__ __forceinline__ void kslots4(const Frag& f, Frag& g, Acc& acc, Tw& w, W4c& c, W4u (&u)[3],
+                                        const W4o& lo4, const GemmParams& p, const StepPtrs4& sp) {
+    if constexpr (Q < 51) {
+        mma1t<WM, Q, Z>(f, acc);
+        if constexpr (Slot4<Q>::ureads >= 0) {
+            constexpr int U = Slot4<Q>::ureads;
+            w4_piece<0>(u[U], U, lo4, sp.cs, sp.ls, sp.bo);
+        }
+        if constexpr (Slot4<Q>::read >= 0) read1<Slot4<Q>::read>(g, sp.ra, sp.rb);
+        if constexpr (Slot4<Q>::load >= 0) {
+            constexpr int L = Slot4<Q>::load;
+            if constexpr (L < NA) load1<L>(w, sp.da, sp.dq);
+            else w4_load1<CS, L - NA>(c, w, p);
+        }
+        if constexpr (Slot4<Q>::piece >= 0) {
+            constexpr int U = Slot4<Q>::piece / 10, P = Slot4<Q>::piece % 10 + 1;
+            w4_piece<P>(u[U], U, lo4, sp.cs, sp.ls, sp.bo);
+        }
+        if constexpr (SW && Q == 48) issue_epi(w, p, sp.ln);
+        __builtin_amdgcn_sched_barrier(0);
+        kslots4<WM, CS, Z, SW, Q + 1>(f, g, acc, w, c, u, lo4, p, sp);
+    }
+}
+
+// W4 K-step k on A stage S = k % 4.  SWA: the A cursor moves to the next tile
+// first (K-step KT - 4), with that tile's epilogue operands after the loads;
+// SWC: the code and table cursors move to it first (K-step KT - 5).
+template <int WM, int S, int VWT, bool Z, bool SWA, bool SWC>
+__device__ __forceinline__ void kstep4(const Frag& f, Frag& g, Acc& acc, Tw& w, W4c& c, const W4o& lo4,
+                                       const GemmParams& p, const NextTile& nt, int8_t* ln) {
+    if constexpr (SWA) cursor_to(w, p, nt.m0, nt.n0, nt.valid);
+    if constexpr (SWC) w4_cursor_to(c, w, p, nt.n0, nt.valid);
+    wait_vm_lgkm0<VWT>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    StepPtrs4 sp;
+    sp.ra = opaque_lds(w.lds + ((S + 1) % NSTG) * BOFF + 1024 * 8 * WM) + w.oF;
+    sp.rb = opaque_lds(w.lds + W4_B + ((S + 1) % 2) * W4_BS + 6144 * w.wn) + w.oF;
+    sp.da = w4_a_base<S>(w);
+    sp.dq = w4_a_quarter<S>(w);
+    sp.cs = opaque_lds(w.lds + W4_C + ((S + 2) % NSTG) * W4_CS);
+    sp.ls = opaque_lds(w.lds + W4_L + ((S + 2) % NSTG) * W4_LS);
+    sp.bo = opaque_lds(w.lds + W4_B + (S % 2) * W4_BS);
+    sp.ln = ln;
+    W4u u[3];
+    kslots4<WM, (S + 1) % NSTG, Z, SWA, 0>(f, g, acc, w, c, u, lo4, p, sp);
+    c.kc++;
 }
 
 // Column operands of this lane: columns 16 c + 4 (l / 16) .. + 3 of the
@@ -582,6 +848,184 @@ __device__ __forceinline__ void t272_tiles(const GemmParams& p, int8_t* lds, int
     wait_all();
 }
 
+// The W4 persistent loop of one wave.  K % 1024 == 0 (the code cursor moves
+// to the next tile at K-step KT - 5, which must fall after the tile's first
+// four K-steps).
+template <int WM, int CK>
+__device__ __forceinline__ void t272w4_tiles(const GemmParams& p, int8_t* lds, int8_t* eall, int8_t* cbuf, int wave) {
+    constexpr int NST = CK == C_BF16 ? Nst<CK>::v : 0;
+    constexpr int VWR = VW4 + NST, VWE = VW4 + NE;
+    static_assert(NST + 27 < 64 && VWR < 64, "vmcnt is six bits");
+    Tw w;
+    W4c c;
+    w.lane = threadIdx.x & 63;
+    w.wave = wave;
+    w.wn = wave & 1;
+    {
+        const int lr = w.lane & 15;
+        w.oF = lr * PK + lds_slot(lr, w.lane >> 4) * 16;
+    }
+    Shape s;
+    s.tiles_m = (p.M + TM - 1) / TM;
+    s.tiles_n = (p.N + TN - 1) / TN;
+    s.ntiles = s.tiles_m * s.tiles_n;
+    s.KT = p.K / PK;
+    s.group_m = p.group_m;
+    s.G = gridDim.x;
+    init_div(s);
+    const int r0 = xcd_remap(blockIdx.x, s.G);
+    if (r0 >= s.ntiles) return;
+    const int ntile = (s.ntiles - r0 - 1) / s.G + 1;
+    const float s0 = p.sb_scalar && p.sB ? p.sB[0] : 0.0f;
+    w.lds = opaque_lds(lds);
+    w.le = eall;
+    w.lc = cbuf + wave * SBYTES;
+    w.rA = whole_rsrc(p.A, p.M * p.K);
+    c.rC = whole_rsrc(p.B, p.N * (int)p.ldb);
+    c.rL = whole_rsrc(p.lut, p.N * (int)p.lut_groups * 16);
+    // Prologue: the epilogue operands; codes and tables of K-steps 0-3 and A
+    // of K-steps 0-3 (in the order the K-steps would issue them); the
+    // expansion of K-steps 0 and 1 once their codes have landed; then codes
+    // and tables of K-step 4 into the stage K-step 0's codes left, and NST
+    // stores that land nowhere, standing where a previous tile's epilogue
+    // stores stand.  From there every K-step's wait counts as in the loop.
+    const NextTile first = next_tile<WM>(s, r0, true);
+    cursor_to(w, p, first.m0, first.n0, true);
+    w4_cursor_to(c, w, p, first.n0, true);
+    const W4o lo4 = w4_lane_offsets(w);
+    issue_epi(w, p, w.le);
+    {
+#define PHI_W4_CODES(CS)                  \
+    w4_load1<CS, 0>(c, w, p);             \
+    w4_load1<CS, 1>(c, w, p);             \
+    w4_load1<CS, 2>(c, w, p);             \
+    w4_load1<CS, 3>(c, w, p);             \
+    w4_load1<CS, 4>(c, w, p);             \
+    w4_load1<CS, 5>(c, w, p);             \
+    c.kc++;
+#define PHI_W4_A(ST)                                                  \
+    {                                                                 \
+        int8_t* da = w4_a_base<ST>(w);                                \
+        int8_t* dq = w4_a_quarter<ST>(w);                             \
+        load1<0>(w, da, dq);                                          \
+        load1<1>(w, da, dq);                                          \
+        load1<2>(w, da, dq);                                          \
+        load1<3>(w, da, dq);                                          \
+        load1<4>(w, da, dq);                                          \
+    }
+        PHI_W4_CODES(0)
+        PHI_W4_A(0)
+        PHI_W4_CODES(1)
+        PHI_W4_A(1)
+        PHI_W4_CODES(2)
+        PHI_W4_A(2)
+        PHI_W4_CODES(3)
+        PHI_W4_A(3)
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm0<2 * NLD4 + NA>();  // codes and tables of K-steps 0-1, A of K-step 0 have landed
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        W4u u[3];
+        const int8_t* cs0 = opaque_lds(w.lds + W4_C);
+        const int8_t* ls0 = opaque_lds(w.lds + W4_L);
+        int8_t* b0 = opaque_lds(w.lds + W4_B);
+        const int8_t* cs1 = opaque_lds(w.lds + W4_C + W4_CS);
+        const int8_t* ls1 = opaque_lds(w.lds + W4_L + W4_LS);
+        int8_t* b1 = opaque_lds(w.lds + W4_B + W4_BS);
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+#pragma unroll
+            for (int U = 0; U < 3; U++) {
+                const int8_t* cs = x ? cs1 : cs0;
+                const int8_t* ls = x ? ls1 : ls0;
+                int8_t* bo = x ? b1 : b0;
+                w4_piece<0>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<1>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<2>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<3>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<4>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<5>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<6>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<7>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<8>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<9>(u[U], U, lo4, cs, ls, bo);
+                w4_piece<10>(u[U], U, lo4, cs, ls, bo);
+            }
+        }
+    }
+    wait_vm_lgkm0<63>();  // this wave's expansion writes are done (lgkmcnt 0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    PHI_W4_CODES(0)
+#undef PHI_W4_CODES
+#undef PHI_W4_A
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NST > 0) {
+        const __amdgpu_buffer_rsrc_t nowhere = whole_rsrc(p.C, 0);
+#pragma unroll
+        for (int d = 0; d < NST; d++) __builtin_amdgcn_raw_buffer_store_b32(0u, nowhere, w.lane * 4 + d * 256, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Frag f, g;
+    {
+        const int8_t* a = opaque_lds(w.lds + 1024 * 8 * WM) + w.oF;
+        const int8_t* b = opaque_lds(w.lds + W4_B + 6144 * w.wn) + w.oF;
+#pragma unroll
+        for (int i = 0; i < 9; i++) f.a[i] = *(const v4i*)(a + 1024 * i);
+#pragma unroll
+        for (int j = 0; j < 6; j++) f.b[j] = *(const v4i*)(b + 1024 * j);
+    }
+    Acc acc;
+    NextTile cur = first;
+    for (int i = 0;;) {
+        const int t = r0 + i * s.G;
+        int8_t* le = w.le + (i & 1) * EB;
+        int8_t* ln = w.le + ((i + 1) & 1) * EB;
+        const NextTile nt = next_tile<WM>(s, t + s.G, i + 1 < ntile);
+        PHI_T272_STAMP(i, 0);
+        kstep4<WM, 0, VWR, true, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 1, VWR, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 2, VWR, false, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 3, VW4, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+        for (int k = 4; k < s.KT - 8; k += 4) {
+            kstep4<WM, 0, VW4, false, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+            kstep4<WM, 1, VW4, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+            kstep4<WM, 2, VW4, false, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+            kstep4<WM, 3, VW4, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+        }
+        kstep4<WM, 0, VW4, false, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 1, VW4, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 2, VW4, false, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 3, VW4, false, false, true>(g, f, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 0, VW4, false, true, false>(f, g, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 1, VWE, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 2, VWE, false, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
+        kstep4<WM, 3, VWE, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
+        PHI_T272_STAMP(i, 1);
+        mfma_drain();
+        epilogue<WM, CK>(acc, p, cur.m0, cur.n0, w, le, s0);
+        PHI_T272_STAMP(i, 2);
+        if constexpr (NST == 0) wait_all();
+        if (++i == ntile) break;
+        cur = nt;
+    }
+    wait_all();
+}
+
+template <int CK>
+__global__ __launch_bounds__(256) void i8_gemm_t272w4_kernel(GemmParams p) {
+    __shared__ __align__(16) int8_t lds[W4_LDS];
+    __shared__ __align__(16) int8_t eall[2 * EB];
+    __shared__ __align__(16) int8_t cbuf[4 * SBYTES];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+    PHI_T272_TRACE_BEGIN
+    if (wave < 2) t272w4_tiles<0, CK>(p, lds, eall, cbuf, wave);
+    else t272w4_tiles<1, CK>(p, lds, eall, cbuf, wave);
+    PHI_T272_TRACE_END
+}
+
 template <int CK>
 __global__ __launch_bounds__(256) void i8_gemm_t272_kernel(GemmParams p) {
     __shared__ __align__(16) int8_t lds[NSTG * STG];
@@ -603,6 +1047,27 @@ bool t272_ok(const GemmParams& p) {
     return p.kt && !p.gate && p.K % 512 == 0 && (int64_t)p.M * p.K < ((int64_t)1 << 31) - (1 << 20) &&
            (int64_t)p.N * p.K < ((int64_t)1 << 31) - (1 << 20) && (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) &&
            p.N % (16 / esz) == 0;
+}
+
+bool t272w4_ok(const GemmParams& p) {
+    const int64_t esz = p.c_kind == C_BF16 ? 2 : 4;
+    return p.kt && !p.gate && !p.w4_signed && p.lut && p.K % 1024 == 0 && p.group_shift >= 6 &&
+           p.group_shift < 31 && (1ll << p.group_shift) <= p.K && p.lut_groups == (p.K >> p.group_shift) &&
+           p.ldb >= p.K / 2 && p.ldb % 16 == 0 && ((uintptr_t)p.B & 15) == 0 &&
+           (int64_t)p.M * p.K < ((int64_t)1 << 31) - (1 << 20) &&
+           ((int64_t)p.N + 512) * p.ldb < ((int64_t)1 << 31) &&
+           ((int64_t)p.N + 512) * p.lut_groups * 16 < ((int64_t)1 << 31) &&
+           (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) && p.N % (16 / esz) == 0;
+}
+
+hipError_t launch_i8_gemm_t272w4(hipStream_t stream, const GemmParams& p, int num_cus) {
+    if (!t272w4_ok(p)) return hipErrorInvalidValue;
+    const int tiles = t272_tile_count(p.M, p.N);
+    const dim3 g3(tiles < num_cus ? tiles : num_cus), b3(256);
+    if (p.c_kind == C_BF16) hipLaunchKernelGGL((i8_gemm_t272w4_kernel<C_BF16>), g3, b3, 0, stream, p);
+    else if (p.c_kind == C_F32) hipLaunchKernelGGL((i8_gemm_t272w4_kernel<C_F32>), g3, b3, 0, stream, p);
+    else hipLaunchKernelGGL((i8_gemm_t272w4_kernel<C_I32>), g3, b3, 0, stream, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_cus) {

@@ -1,6 +1,7 @@
 // Pieces shared by the persistent int8 GEMM kernels (i8_gemm_persist.hip,
-// i8_gemm_pipe.hip): buffer-resource and wait helpers, the XCD-aware tile
-// order, the epilogue-operand loads and the epilogue.
+// i8_gemm_pipe.hip, i8_gemm_t272.hip): buffer-resource and wait helpers, the
+// XCD-aware tile order, the 4-bit code expansion through a per-(row, group)
+// table, the epilogue-operand loads and the epilogue.
 //
 // The product and epilogue are those of the reference's int8_gemm_tc
 // (core/kernels/int8_gemm.cpp:466-621, epilogue :588-620) and host gemm_int8
@@ -117,6 +118,33 @@ __device__ __forceinline__ void tile_mn(const Shape& s, int logical, int& tm, in
     tn = q;
 }
 
+
+// Four codes (bytes of x, each 0..15) -> four int8 through the 16-byte table
+// t: v_perm_b32 picks from entries 0..7 and 8..15 by the low three bits, and
+// bit 3 chooses (selector bytes 0x0c / 0x0d give 0x00 / 0xff).
+__device__ __forceinline__ uint32_t lut4b(uint32_t x, const u32x4& t) {
+    const uint32_t sel = x & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(t[1], t[0], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(t[3], t[2], sel);
+    const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((x >> 3) & 0x01010101u) | 0x0c0c0c0cu);
+    return (hi & m) | (lo & ~m);
+}
+
+// The table of signed nibbles (convrot_w4a4): codes 0..7 are 0..7, 8..15 are -8..-1.
+__device__ __forceinline__ u32x4 signed_nibble_table() { return u32x4{0x03020100u, 0x07060504u, 0xfbfaf9f8u, 0xfffefdfcu}; }
+
+// 16 codes (8 bytes) -> 16 int8 operand bytes in column order.
+__device__ __forceinline__ v4i expand16b(uint32_t c0, uint32_t c1, const u32x4& t) {
+    const uint32_t e0 = lut4b(c0 & 0x0f0f0f0fu, t), o0 = lut4b((c0 >> 4) & 0x0f0f0f0fu, t);
+    const uint32_t e1 = lut4b(c1 & 0x0f0f0f0fu, t), o1 = lut4b((c1 >> 4) & 0x0f0f0f0fu, t);
+    // e holds columns 0,2,4,6 and o columns 1,3,5,7: interleave.
+    v4i r;
+    r.x = (int)__builtin_amdgcn_perm(o0, e0, 0x05010400u);
+    r.y = (int)__builtin_amdgcn_perm(o0, e0, 0x07030602u);
+    r.z = (int)__builtin_amdgcn_perm(o1, e1, 0x05010400u);
+    r.w = (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u);
+    return r;
+}
 
 // Epilogue operands of the cursor's tile into LDS area le: wave w loads row
 // scales 64w..64w+63, column scales / fp32 bias 64w..64w+63 and (waves 0-1)

@@ -3,7 +3,8 @@
 // record of stamps per workgroup, each point in the shader clock (s_memtime,
 // cycles) and the kernel's start and end also in the 100 MHz real-time
 // clock.  Measurement tooling for bench.py (--config c1_up_t272_tiles /
-// c1_down_t272_tiles); the product library does not contain it.
+// c1_down_t272_tiles / c2_t272_tiles); the product library does not contain
+// it.
 //
 // The per-workgroup record (64 words):
 //   [0]           kernel start, shader clock
@@ -77,6 +78,48 @@ int phi_probe_t272_trace(void* stream, const int8_t* A, const int8_t* B, const f
                                           (hipStream_t)stream);
     if (e != hipSuccess) return (int)e;
     return (int)phi_dev_t272trace::launch_i8_gemm_t272((hipStream_t)stream, p, cus);
+}
+
+// The traced W4A8 form (i8_gemm_t272w4_kernel): A K-tiled, B the packed codes
+// [N, ldb] with the prepared table lut [N, K / group, 16], per-row scales sB,
+// bf16 bias and output.
+int phi_probe_t272w4_trace(void* stream, const int8_t* A, const uint8_t* codes, long long ldb, const int8_t* lut,
+                           int group, const float* sA, const float* sB, const void* bias, void* C, int M, int N, int K,
+                           unsigned long long* out, long long slots) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return (int)hipErrorInvalidDevice;
+    if (group <= 0 || (group & (group - 1)) != 0 || K % group != 0) return (int)hipErrorInvalidValue;
+    phi_dev_t272trace::GemmParams p{};
+    p.A = A;
+    p.B = (const int8_t*)codes;
+    p.sA = sA;
+    p.sB = sB;
+    p.bias = bias;
+    p.C = C;
+    p.lda = K;
+    p.ldb = ldb;
+    p.ldc = N;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.sb_scalar = 0;
+    p.bias_kind = bias ? phi_dev_t272trace::BIAS_BF16 : phi_dev_t272trace::BIAS_NONE;
+    p.c_kind = phi_dev_t272trace::C_BF16;
+    p.group_m = 4;
+    p.kt = 1;
+    p.lut = lut;
+    p.lut_groups = K / group;
+    int gs = 0;
+    while ((1 << gs) < group) gs++;
+    p.group_shift = gs;
+    if (M <= 0 || N <= 0 || !phi_dev_t272trace::t272w4_ok(p)) return (int)hipErrorInvalidValue;
+    const long long tiles = phi_dev_t272trace::t272_tile_count(M, N);
+    if ((tiles < cus ? tiles : cus) * 64 > slots) return (int)hipErrorInvalidValue;
+    hipError_t e = hipMemcpyToSymbolAsync(HIP_SYMBOL(phi_t272_out), &out, sizeof(out), 0, hipMemcpyHostToDevice,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) return (int)e;
+    return (int)phi_dev_t272trace::launch_i8_gemm_t272w4((hipStream_t)stream, p, cus);
 }
 
 }  // extern "C"

@@ -129,3 +129,58 @@ def test_config1_down_rows_against_oracle(dev, orc):
     assert np.array_equal(acc[ri].cpu().numpy(), acco)
     got = u16(y[ri])
     assert np.array_equal(got, yo), f"{(got != yo).sum()} bf16 mismatches"
+
+
+# ---------------------------------------------------------------- W4A8
+W4_SHAPES = [
+    (64, 256, 1024, 128),     # one partial tile row, N past one tile
+    (300, 520, 3072, 128),    # ragged in both
+    (130, 128, 2048, 256),    # N below one tile
+    (1, 200, 1024, 64),       # one row, group = one K-step
+    (777, 1032, 2048, 1024),  # group = half of K
+    (4352, 9216, 1024, 128),  # config 2's tile grid, three tiles a workgroup
+]
+
+
+@pytest.mark.parametrize("M,N,K,group", W4_SHAPES)
+@pytest.mark.parametrize("with_ws", [False, True])
+def test_w4_in_lds_equals_expand_then_w8a8(dev, monkeypatch, M, N, K, group, with_ws):
+    """asym_w4a8 on the 272 x 192 pipeline (codes and tables DMA'd, expanded
+    in LDS; PHI_W4_T272=1 takes it also when a workspace is given) against
+    expand-then-W8A8, bit for bit."""
+    codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=M + N + K)
+    cd, rd, sd, kd = codes.to(dev), s_rel.to(dev), sch.to(dev), corr.to(dev)
+    x = synth.activations(M, K, seed=M, device=dev)
+    q, s = Q.w4a8_expand(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    lut, s2 = Q.w4a8_prepare(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    ws = Q.w4a8_workspace(M, N, K, group, dev) if with_ws else None
+    monkeypatch.setenv("PHI_W4_T272", "1")
+    y = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
+    monkeypatch.delenv("PHI_W4_T272")
+    y_ref = Q.q8_linear(x, q, s)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("out", ["bf16", "f32", "i32"])
+@pytest.mark.parametrize("bias_kind", ["none", "f32", "bf16"])
+def test_w4_in_lds_outputs_and_padded_code_rows(dev, monkeypatch, out, bias_kind):
+    """Every output kind and bias, with code rows padded past K / 2 bytes."""
+    M, N, K, group = 600, 776, 2048, 128
+    codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=17)
+    padded = torch.zeros((N, K // 2 + 48), dtype=torch.uint8)
+    padded[:, :K // 2] = codes
+    cd = padded.to(dev)[:, :K // 2]
+    rd, sd, kd = s_rel.to(dev), sch.to(dev), corr.to(dev)
+    x = synth.activations(M, K, seed=5, device=dev)
+    q, s = Q.w4a8_expand(codes.to(dev), rd, Q.F16, sd, k=K, group=group, correction=kd)
+    lut, s2 = Q.w4a8_prepare(codes.to(dev), rd, Q.F16, sd, k=K, group=group, correction=kd)
+    bias = {"none": None, "f32": torch.randn(N, device=dev) * 0.02,
+            "bf16": synth.bias(N, seed=6, device=dev)}[bias_kind]
+    monkeypatch.setenv("PHI_W4_T272", "1")
+    y = Q.w4a8_linear(x, cd, lut, s2, group=group, bias=bias, out_dtype=ODT[out])
+    monkeypatch.delenv("PHI_W4_T272")
+    xq, xs = Q.quant_rotate(x)
+    y_ref = Q.i8_gemm(xq, q, xs, s, bias, out_dtype=ODT[out])
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(y), _bits(y_ref))
