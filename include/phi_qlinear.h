@@ -311,10 +311,12 @@ phi_status phi_hip_w4a8_prepare(phi_stream_t stream, const phi_w4a8_weight* w, i
  *   workspace: optional, phi_hip_w4a8_workspace_bytes() bytes (16-byte
  *     aligned).  Given it, a call with many rows expands the codes once into
  *     it (int8 [N, K]) and runs the W8A8 GEMM; without it, or for few rows,
- *     the GEMM expands the codes in registers tile by tile.  Same bits either way.
- *     The expand-once path (K <= 16384) keeps the expanded weight and the
- *     activation codes in the K-tiled layout (phi_hip_pack_k_tiled), so q8
- *     then holds the activation codes K-tiled; s8 is the same on every path.
+ *     the GEMM expands the codes tile by tile: for K % 1024 == 0 (K <= 16384)
+ *     in LDS, once per workgroup, on the 272 x 192 pipeline, otherwise in
+ *     registers.  Same bits on every path.
+ *     The expand-once path and the LDS path (K <= 16384) keep the activation
+ *     codes in the K-tiled layout (phi_hip_pack_k_tiled), so q8 then holds
+ *     them K-tiled; s8 is the same on every path.
  */
 phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx,
                                int64_t M, int64_t K, const uint8_t* codes,
