@@ -638,11 +638,13 @@ struct ColOps {
 
 // Block row R (0 .. 8) of the wave's epilogue: tile block row 8 WM + R; the
 // shared one (R = 8 for wm = 0, R = 0 for wm = 1) holds wave column blocks
-// 3 WM .. 3 WM + 2.  Convert, write the wave's staging rows, read them back as
-// 16-byte pieces (piece x: row x % 16, piece x / 16 of the row) and store.
+// 3 WM .. 3 WM + 2.  fp32 / int32: convert three blocks (192 bytes a row),
+// write the wave's staging rows, read them back as 16-byte pieces (piece x:
+// row x / 12, piece x % 12 of the row) and store.
 template <int WM, int CK, int R>
 __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
                                         const int8_t* e, const __amdgpu_buffer_rsrc_t& rs, int pitch, int colw) {
+    static_assert(CK != C_BF16, "bf16 takes the pipelined rows");
     constexpr bool shared = WM == 0 ? R == 8 : R == 0;
     constexpr int g = 8 * WM + R;          // block row in the tile
     constexpr int c0 = shared ? 3 * WM : 0;  // first wave column block
@@ -657,51 +659,117 @@ __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmPa
         if constexpr (shared) blk = acc.s[c];
         else blk = acc.f[fr < 0 ? 0 : fr][c];
         asm volatile("" : "+v"(blk));
-        if constexpr (CK == C_BF16) {
-            float v[4];
+        u32x4 o;
+        if constexpr (CK == C_F32) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]);
-            *(u32x2*)(lc + lr * SP + stage_slot(lr, 2 * c + (lg >> 1)) * 16 + (lg & 1) * 8) =
-                u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+            for (int q = 0; q < 4; q++)
+                o[q] = __float_as_uint(fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]));
         } else {
-            u32x4 o;
-            if constexpr (CK == C_F32) {
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    o[q] = __float_as_uint(fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]));
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; q++) o[q] = (unsigned)blk[q];
-            }
-            // fp32 / int32: three blocks (192 bytes a row) a pass.
-            *(u32x4*)(lc + lr * SP + stage_slot(lr, 4 * (c % 3) + lg) * 16) = o;
-            if (c % 3 == 2) {
-                const int cg = c - 2;
-#pragma unroll
-                for (int t = 0; t < 3; t++) {
-                    const int x = w.lane + 64 * t, rr = x / 12, ch = x - 12 * rr;
-                    const u32x4 v = *(const u32x4*)(lc + rr * SP + stage_slot(rr, ch) * 16);
-                    const int col = colw + 16 * (c0 + cg) + 4 * ch;
-                    const int off = col < p.N ? (16 * g + rr) * pitch + col * 4 : kDropOffset;
-                    __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
-                }
-            }
+            for (int q = 0; q < 4; q++) o[q] = (unsigned)blk[q];
         }
-    }
-    if constexpr (CK == C_BF16) {
-        // 16 rows x 2 nb pieces in row order (piece x: row x / (2 nb), piece
-        // x % (2 nb) of the row): three stores a lane for a full row, two
-        // (the second half empty) for the shared one.
+        *(u32x4*)(lc + lr * SP + stage_slot(lr, 4 * (c % 3) + lg) * 16) = o;
+        if (c % 3 == 2) {
+            const int cg = c - 2;
 #pragma unroll
-        for (int t = 0; t < (shared ? 2 : 3); t++) {
-            const int x = w.lane + 64 * t, rr = x / (2 * nb), ch = x - 2 * nb * rr;
-            const u32x4 v = *(const u32x4*)(lc + (rr & 15) * SP + stage_slot(rr & 15, ch) * 16);
-            const int col = colw + 16 * c0 + 8 * ch;
-            const int off = col < p.N && rr < 16 ? (16 * g + rr) * pitch + col * 2 : kDropOffset;
-            __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
+            for (int t = 0; t < 3; t++) {
+                const int x = w.lane + 64 * t, rr = x / 12, ch = x - 12 * rr;
+                const u32x4 v = *(const u32x4*)(lc + rr * SP + stage_slot(rr, ch) * 16);
+                const int col = colw + 16 * (c0 + cg) + 4 * ch;
+                const int off = col < p.N ? (16 * g + rr) * pitch + col * 4 : kDropOffset;
+                __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// bf16, software-pipelined: block row R's read-back waits in registers while
+// row R + 1 converts, and is stored after that conversion, so the LDS latency
+// of the read-back (and of the row scales, all read at the start) hides
+// behind VALU work instead of stalling each row.  The LDS runs a wave's
+// operations in order, so row R + 1's staging writes cannot overtake row R's
+// read-back of the same slots.
+struct Pend {
+    u32x4 v[3];
+    int off[3];
+};
+constexpr int EG = 2;  // blocks converted together (measured: 2, 3, 4 and 6 alike within 4%)
+
+template <int WM, int R>
+__device__ __forceinline__ void epi_row_bf16(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
+                                             float sa, Pend& pend, const __amdgpu_buffer_rsrc_t& rs, int pitch,
+                                             int colw) {
+    constexpr bool shared = WM == 0 ? R == 8 : R == 0;
+    constexpr int g = 8 * WM + R;
+    constexpr int c0 = shared ? 3 * WM : 0;
+    constexpr int nb = shared ? 3 : 6;
+    constexpr int fr = WM == 0 ? R : R - 1;
+    // the previous row's store count: the shared row issues two
+    constexpr int prev = R == 0 ? 0 : ((WM == 0 ? R - 1 == 8 : R - 1 == 0) ? 2 : 3);
+    const int lr = w.lane & 15, lg = w.lane >> 4;
+    int8_t* lc = w.lc;
+    // EG blocks at a time: 4 EG independent conversions a step (one block's
+    // four chains alone leave the VALU waiting on its own results: 7.3k
+    // clocks an epilogue against 6.7k at c1 up).
+#pragma unroll
+    for (int c = 0; c < nb; c += EG) {
+        const int nc = c + EG <= nb ? EG : nb - c;
+        v4i blk[EG];
+#pragma unroll
+        for (int j = 0; j < EG; j++) {
+            if (j < nc) {
+                if constexpr (shared) blk[j] = acc.s[c + j];
+                else blk[j] = acc.f[fr < 0 ? 0 : fr][c + j];
+                asm volatile("" : "+v"(blk[j]));
+            }
+        }
+        float v[EG][4];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int j = 0; j < EG; j++)
+                if (j < nc) v[j][q] = (float)blk[j][q] * sa;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int j = 0; j < EG; j++)
+                if (j < nc) v[j][q] = fmaf(v[j][q], co.sb[c0 + c + j][q], co.bz[c0 + c + j][q]);
+#pragma unroll
+        for (int j = 0; j < EG; j++)
+            if (j < nc)
+                *(u32x2*)(lc + lr * SP + stage_slot(lr, 2 * (c + j) + (lg >> 1)) * 16 + (lg & 1) * 8) =
+                    u32x2{f32x2_to_bf16x2(v[j][0], v[j][1]), f32x2_to_bf16x2(v[j][2], v[j][3])};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < prev; t++) __builtin_amdgcn_raw_buffer_store_b128(pend.v[t], rs, pend.off[t], 0, kStoreNT);
+    __builtin_amdgcn_sched_barrier(0);
+    // 16 rows x 2 nb pieces in row order (piece x: row x / (2 nb), piece
+    // x % (2 nb) of the row): three stores a lane for a full row, two (the
+    // second half empty) for the shared one.
+#pragma unroll
+    for (int t = 0; t < (shared ? 2 : 3); t++) {
+        const int x = w.lane + 64 * t, rr = x / (2 * nb), ch = x - 2 * nb * rr;
+        pend.v[t] = *(const u32x4*)(lc + (rr & 15) * SP + stage_slot(rr & 15, ch) * 16);
+        const int col = colw + 16 * c0 + 8 * ch;
+        pend.off[t] = col < p.N && rr < 16 ? (16 * g + rr) * pitch + col * 2 : kDropOffset;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int WM, int R = 0>
+__device__ __forceinline__ void epi_rows_bf16(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
+                                              const float (&sa)[9], Pend& pend, const __amdgpu_buffer_rsrc_t& rs,
+                                              int pitch, int colw) {
+    if constexpr (R < 9) {
+        epi_row_bf16<WM, R>(acc, co, p, w, sa[R], pend, rs, pitch, colw);
+        epi_rows_bf16<WM, R + 1>(acc, co, p, w, sa, pend, rs, pitch, colw);
+    } else {
+        constexpr int last = WM == 0 ? 2 : 3;  // row 8 is the shared one for wm = 0
+#pragma unroll
+        for (int t = 0; t < last; t++) __builtin_amdgcn_raw_buffer_store_b128(pend.v[t], rs, pend.off[t], 0, kStoreNT);
+    }
 }
 
 template <int WM, int CK, int R = 0>
@@ -743,7 +811,16 @@ __device__ __forceinline__ void epilogue(Acc& acc, const GemmParams& p, int m0, 
             co.sb[c] = sbs ? v4f{s0, s0, s0, s0} : sv;
         }
     }
-    epi_rows<WM, CK>(acc, co, p, w, e, rs, pitch, n0 + 96 * w.wn);
+    if constexpr (CK == C_BF16) {
+        float sa[9];
+        const int lr = w.lane & 15;
+#pragma unroll
+        for (int r = 0; r < 9; r++) sa[r] = *(const float*)(e + E_SA + (16 * (8 * WM + r) + lr) * 4);
+        Pend pend;
+        epi_rows_bf16<WM>(acc, co, p, w, sa, pend, rs, pitch, n0 + 96 * w.wn);
+    } else {
+        epi_rows<WM, CK>(acc, co, p, w, e, rs, pitch, n0 + 96 * w.wn);
+    }
 }
 
 template <int WM>
