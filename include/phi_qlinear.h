@@ -241,15 +241,26 @@ int64_t phi_hip_big_tile_rows(int64_t M, int64_t N);
  *             -1 leaves it to the library's cost model (phi_hip_big_tile_rows)
  *   group_m   tile rows per group of the XCD-aware tile order, 1..16; 0: 4
  *   split     1: the two tile sizes as two launches; 0: one launch
+ *   tile      PHI_PLAN_TILE_SQUARE: the 256 x 256 / 128 x 128 plan above;
+ *             PHI_PLAN_TILE_272: 272 x 192 tiles (K-tiled operands with
+ *             K % 512 == 0 only; big_rows and split do not apply, group_m
+ *             does); PHI_PLAN_TILE_AUTO (0): the library's cost model picks
+ *   reserved  0
  * Every plan gives the same bits; only the time differs.  The table is
  * process-wide and thread-safe; the host layer's GemmTuneStore sweeps,
  * persists and loads it.  _set with plan NULL removes the shape's entry;
- * _get returns the plan a launch of that shape runs (tuned = 1 when it comes
- * from the table). */
+ * _get returns the plan a launch of that shape runs, the tile shape resolved
+ * (tuned = 1 when it comes from the table).  PHI_GEMM_T272=0 / 1 in the
+ * environment overrides the tile shape (an A/B switch). */
+#define PHI_PLAN_TILE_AUTO 0
+#define PHI_PLAN_TILE_SQUARE 1
+#define PHI_PLAN_TILE_272 2
 typedef struct phi_gemm_plan {
     int64_t big_rows;
     int32_t group_m;
     int32_t split;
+    int32_t tile;
+    int32_t reserved;
 } phi_gemm_plan;
 phi_status phi_hip_gemm_plan_set(int64_t M, int64_t N, int64_t K, int k_tiled, const phi_gemm_plan* plan);
 phi_status phi_hip_gemm_plan_get(int64_t M, int64_t N, int64_t K, int k_tiled, phi_gemm_plan* plan, int* tuned);

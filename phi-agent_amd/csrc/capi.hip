@@ -234,13 +234,15 @@ double square_plan_cost(int64_t M, int64_t N, int G) {
 // the outputs' ratio, 52224 / 65536.
 constexpr double kT272Round = 52224.0 / 65536.0;
 
-// Whether the 272 x 192 kernel serves p (K-tiled operands only): when its
-// whole rounds cost less than the square plan's.  PHI_GEMM_T272=0 / 1 turns
-// it off / forces it where it applies (an A/B switch).
-bool use_t272(const phi_dev::GemmParams& p, int G) {
+// Whether the 272 x 192 kernel serves p (K-tiled operands only): as the tuned
+// plan's tile field says, else when its whole rounds cost less than the square
+// plan's.  PHI_GEMM_T272=0 / 1 turns it off / forces it where it applies (an
+// A/B switch, above the table).
+bool use_t272(const phi_dev::GemmParams& p, int G, int tile) {
     if (!phi_dev::t272_ok(p)) return false;
     const int e = phi_dev::env_switch("PHI_GEMM_T272", -1, 0, 1);
     if (e >= 0) return e == 1;
+    if (tile != PHI_PLAN_TILE_AUTO) return tile == PHI_PLAN_TILE_272;
     const double t = kT272Round * (double)((phi_dev::t272_tile_count(p.M, p.N) + G - 1) / G);
     return t < square_plan_cost(p.M, p.N, G) - 1e-9;
 }
@@ -252,17 +254,18 @@ bool use_t272(const phi_dev::GemmParams& p, int G) {
 hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p0, GemmKernel gk, bool w4, int c_dtype,
                                int64_t ldc) {
     const int G = num_cus();
-    if (gk == GK_PERSIST && !w4 && p0.kt && use_t272(p0, G)) return phi_dev::launch_i8_gemm_t272(stream, p0, G);
-    // int8 B runs on the four-stage pipeline; PHI_GEMM_PIPE=0 selects the
-    // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
-    // runs on the two-stage kernel.
-    const char* pe = getenv("PHI_GEMM_PIPE");
-    const bool pipe = p0.kt || (!w4 && !(pe && pe[0] == '0'));  // K-tiled operands: the pipeline only
     const int64_t M = p0.M;
     phi_gemm_plan plan{};
     const bool tuned = gk == GK_PERSIST && !w4 && tuned_plan(M, p0.N, p0.K, p0.kt, &plan);
     phi_dev::GemmParams p = p0;
     if (tuned && plan.group_m > 0) p.group_m = plan.group_m;
+    if (gk == GK_PERSIST && !w4 && p0.kt && use_t272(p0, G, tuned ? plan.tile : PHI_PLAN_TILE_AUTO))
+        return phi_dev::launch_i8_gemm_t272(stream, p, G);
+    // int8 B runs on the four-stage pipeline; PHI_GEMM_PIPE=0 selects the
+    // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
+    // runs on the two-stage kernel.
+    const char* pe = getenv("PHI_GEMM_PIPE");
+    const bool pipe = p0.kt || (!w4 && !(pe && pe[0] == '0'));  // K-tiled operands: the pipeline only
     const int64_t rows = gk == GK_PERSIST ? (tuned && plan.big_rows >= 0 ? plan.big_rows : big_tile_rows(M, p.N, G))
                          : gk == GK_PERSIST256 ? M
                                                : 0;
@@ -570,6 +573,12 @@ phi_status phi_hip_gemm_plan_set(int64_t M, int64_t N, int64_t K, int k_tiled, c
         if (plan->group_m < 0 || plan->group_m > 16)
             return fail(PHI_ERR_ARG, "%s: group_m=%d is not 0 (the default) or 1..16", who, (int)plan->group_m);
         if (plan->split != 0 && plan->split != 1) return fail(PHI_ERR_ARG, "%s: split must be 0 or 1", who);
+        if (plan->tile < PHI_PLAN_TILE_AUTO || plan->tile > PHI_PLAN_TILE_272)
+            return fail(PHI_ERR_ARG, "%s: tile=%d is not 0 (the cost model), 1 (square) or 2 (272 x 192)", who,
+                        (int)plan->tile);
+        if (plan->tile == PHI_PLAN_TILE_272 && (!k_tiled || K % 512 != 0))
+            return fail(PHI_ERR_ARG, "%s: tile=2 (272 x 192) needs K-tiled operands and K %% 512 == 0 (K=%lld)", who,
+                        (long long)K);
         g_plans[key] = *plan;
     }
     g_plan_count.store((int64_t)g_plans.size(), std::memory_order_release);
@@ -580,11 +589,26 @@ phi_status phi_hip_gemm_plan_get(int64_t M, int64_t N, int64_t K, int k_tiled, p
     static const char* who = "gemm_plan_get";
     if (M <= 0 || N <= 0 || K <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
     if (!plan) return fail(PHI_ERR_ARG, "%s: null plan", who);
-    phi_gemm_plan p{-1, 0, 0};
+    phi_gemm_plan p{-1, 0, 0, PHI_PLAN_TILE_AUTO, 0};
     const bool t = tuned_plan(M, N, K, k_tiled, &p);
     if (tuned) *tuned = t ? 1 : 0;
-    if (p.big_rows < 0) p.big_rows = big_tile_rows(M, N, num_cus());
+    const int G = num_cus();
+    if (p.big_rows < 0) p.big_rows = big_tile_rows(M, N, G);
     if (p.group_m == 0) p.group_m = 4;
+    // The tile shape a launch with bf16 output (ldc = N) resolves to.
+    bool t272 = false;
+    if (M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX) {
+        phi_dev::GemmParams q{};
+        q.M = (int)M;
+        q.N = (int)N;
+        q.K = (int)K;
+        q.ldc = N;
+        q.c_kind = phi_dev::C_BF16;
+        q.kt = k_tiled ? 1 : 0;
+        t272 = use_t272(q, G, p.tile);
+    }
+    p.tile = t272 ? PHI_PLAN_TILE_272 : PHI_PLAN_TILE_SQUARE;
+    p.reserved = 0;
     *plan = p;
     return ok();
 }

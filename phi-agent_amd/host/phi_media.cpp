@@ -1340,6 +1340,7 @@ bool GemmTuneStore::load(const std::string& path) {
         e.big_rows = (i64)num("big_rows", -1);
         e.group_m = (int)num("group_m", 0);
         e.split = num("split", 0) != 0;
+        e.tile = (int)num("tile", PHI_PLAN_TILE_AUTO);
         e.measured_us = num("us", 0);
         e.tops = num("tops", 0);
         if (e.M <= 0 || e.N <= 0 || e.K <= 0) return false;
@@ -1359,9 +1360,9 @@ bool GemmTuneStore::save(const std::string& path) const {
         const GemmTuneEntry& e = items_[i];
         ok = ok && fprintf(f,
                            "%s\n  {\"M\": %lld, \"N\": %lld, \"K\": %lld, \"k_tiled\": %d, \"big_rows\": %lld, "
-                           "\"group_m\": %d, \"split\": %d, \"us\": %.3f, \"tops\": %.1f}",
+                           "\"group_m\": %d, \"split\": %d, \"tile\": %d, \"us\": %.3f, \"tops\": %.1f}",
                            i ? "," : "", (long long)e.M, (long long)e.N, (long long)e.K, e.k_tiled ? 1 : 0,
-                           (long long)e.big_rows, e.group_m, e.split ? 1 : 0, e.measured_us, e.tops) > 0;
+                           (long long)e.big_rows, e.group_m, e.split ? 1 : 0, e.tile, e.measured_us, e.tops) > 0;
     }
     ok = ok && fprintf(f, "\n]}\n") > 0;
     ok = (fclose(f) == 0) && ok;
@@ -1385,7 +1386,7 @@ const GemmTuneEntry* GemmTuneStore::get(i64 M, i64 N, i64 K, bool k_tiled) const
 
 void GemmTuneStore::apply() const {
     for (const GemmTuneEntry& e : items_) {
-        const phi_gemm_plan p{e.big_rows, e.group_m, e.split ? 1 : 0};
+        const phi_gemm_plan p{e.big_rows, e.group_m, e.split ? 1 : 0, e.tile, 0};
         if (phi_hip_gemm_plan_set(e.M, e.N, e.K, e.k_tiled ? 1 : 0, &p) != PHI_OK)
             throw MediaError(std::string("gemm tuning table: ") + phi_hip_last_error());
     }
@@ -1484,9 +1485,10 @@ GemmTuneResult autotune_int8_gemm(ComputeContext& ctx, i64 M, i64 N, i64 K, int 
         std::vector<uint16_t> ref((size_t)(M * N)), got((size_t)(M * N));
         ctx.download(buf.b, ref.data(), cb, o_c);
 
-        // Candidates: the cost model's 256-row count and its neighbours, all
-        // rows, group heights 2, 4, 8, and one or two launches where both
-        // tile sizes run.
+        // Candidates: the square plan at the cost model's 256-row count and
+        // its neighbours, all rows, group heights 2, 4, 8, and one or two
+        // launches where both tile sizes run; on K-tiled operands with
+        // K % 512 == 0, also 272 x 192 tiles at each group height.
         phi_gemm_plan def{};
         ctx.check(phi_hip_gemm_plan_get(M, N, K, kt, &def, nullptr), "gemm_plan_get");
         std::vector<i64> rows_opts{def.big_rows};
@@ -1504,34 +1506,37 @@ GemmTuneResult autotune_int8_gemm(ComputeContext& ctx, i64 M, i64 N, i64 K, int 
                 (void)hipEventDestroy(b);
             }
         } events{e0, e1};
-        double best_us = 1e300;
+        std::vector<phi_gemm_plan> cands;
         for (const i64 big : rows_opts)
             for (const int gm : {2, 4, 8})
-                for (const int split : {0, 1}) {
-                    if (split && !(big > 0 && big < M)) continue;
-                    const phi_gemm_plan p{big, gm, split};
-                    ctx.check(phi_hip_gemm_plan_set(M, N, K, kt, &p), "gemm_plan_set");
-                    gemm(false);  // untimed
-                    if (hipEventRecord(e0, ctx.stream()) != hipSuccess) throw MediaError("autotune: event record");
-                    for (int i = 0; i < iters; i++) gemm(false);
-                    if (hipEventRecord(e1, ctx.stream()) != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
-                        throw MediaError("autotune: event wait");
-                    float ms = 0.0f;
-                    (void)hipEventElapsedTime(&ms, e0, e1);
-                    GemmTuneEntry e;
-                    e.M = M, e.N = N, e.K = K, e.k_tiled = k_tiled;
-                    e.big_rows = big, e.group_m = gm, e.split = split != 0;
-                    e.measured_us = (double)ms * 1e3 / iters;
-                    e.tops = 2.0 * (double)M * (double)N * (double)K / (e.measured_us * 1e-6) / 1e12;
-                    ctx.download(buf.b, got.data(), cb, o_c);
-                    const bool exact = memcmp(got.data(), ref.data(), (size_t)cb) == 0;
-                    if (exact) r.exact_matches++;
-                    r.tried.push_back(e);
-                    if (exact && e.measured_us < best_us) {
-                        best_us = e.measured_us;
-                        r.best = e;
-                    }
-                }
+                for (const int split : {0, 1})
+                    if (!split || (big > 0 && big < M)) cands.push_back({big, gm, split, PHI_PLAN_TILE_SQUARE, 0});
+        if (kt && K % 512 == 0)
+            for (const int gm : {2, 4, 8}) cands.push_back({def.big_rows, gm, 0, PHI_PLAN_TILE_272, 0});
+        double best_us = 1e300;
+        for (const phi_gemm_plan& p : cands) {
+            ctx.check(phi_hip_gemm_plan_set(M, N, K, kt, &p), "gemm_plan_set");
+            gemm(false);  // untimed
+            if (hipEventRecord(e0, ctx.stream()) != hipSuccess) throw MediaError("autotune: event record");
+            for (int i = 0; i < iters; i++) gemm(false);
+            if (hipEventRecord(e1, ctx.stream()) != hipSuccess || hipEventSynchronize(e1) != hipSuccess)
+                throw MediaError("autotune: event wait");
+            float ms = 0.0f;
+            (void)hipEventElapsedTime(&ms, e0, e1);
+            GemmTuneEntry e;
+            e.M = M, e.N = N, e.K = K, e.k_tiled = k_tiled;
+            e.big_rows = p.big_rows, e.group_m = p.group_m, e.split = p.split != 0, e.tile = p.tile;
+            e.measured_us = (double)ms * 1e3 / iters;
+            e.tops = 2.0 * (double)M * (double)N * (double)K / (e.measured_us * 1e-6) / 1e12;
+            ctx.download(buf.b, got.data(), cb, o_c);
+            const bool exact = memcmp(got.data(), ref.data(), (size_t)cb) == 0;
+            if (exact) r.exact_matches++;
+            r.tried.push_back(e);
+            if (exact && e.measured_us < best_us) {
+                best_us = e.measured_us;
+                r.best = e;
+            }
+        }
         if (best_us == 1e300) throw MediaError("autotune: no candidate reproduced the default plan's output");
         r.ok = r.default_exact;
         if (!r.default_exact) r.error = "autotune: the default plan's accumulators differ from the host integer GEMM";

@@ -460,7 +460,8 @@ LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::string& base, con
 //
 // One plan per (M, N, K, operand layout) for the persistent int8 GEMM:
 // big_rows (rows run as 256 x 256 tiles), group_m (tile rows per group of the
-// XCD-aware tile order) and split (the two tile sizes as two launches).  Every
+// XCD-aware tile order), split (the two tile sizes as two launches) and tile
+// (the square plan or 272 x 192 tiles, K-tiled operands only).  Every
 // plan gives the same bits, so a sweep is free to pick the fastest; it checks
 // that anyway.  The store persists as JSON and apply() hands its plans to the
 // library, whose every launch of such a shape then runs the stored plan.
@@ -470,6 +471,7 @@ struct GemmTuneEntry {
     i64 big_rows = -1;  // -1: the library's cost model
     int group_m = 0;    // 0: 4
     bool split = false;
+    int tile = 0;       // PHI_PLAN_TILE_*: 0 the cost model, 1 square, 2 272 x 192
     double measured_us = 0.0;
     double tops = 0.0;
 };

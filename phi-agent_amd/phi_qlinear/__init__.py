@@ -53,9 +53,14 @@ class W4a8Weight(ctypes.Structure):
                 ("k", ctypes.c_int64), ("group", ctypes.c_int64), ("layout", ctypes.c_int)]
 
 
+PLAN_TILE_AUTO, PLAN_TILE_SQUARE, PLAN_TILE_272 = 0, 1, 2
+
+
 class GemmPlan(ctypes.Structure):
-    """phi_gemm_plan: big_rows (-1: the cost model), group_m (0: 4), split."""
-    _fields_ = [("big_rows", ctypes.c_int64), ("group_m", ctypes.c_int32), ("split", ctypes.c_int32)]
+    """phi_gemm_plan: big_rows (-1: the cost model), group_m (0: 4), split,
+    tile (PLAN_TILE_AUTO / _SQUARE / _272), reserved (0)."""
+    _fields_ = [("big_rows", ctypes.c_int64), ("group_m", ctypes.c_int32), ("split", ctypes.c_int32),
+                ("tile", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class GemvItem(ctypes.Structure):
@@ -519,18 +524,20 @@ def dequant_fp4_rows(codes: torch.Tensor, k: int, block_scale: torch.Tensor | No
 
 
 def gemm_plan_set(M: int, N: int, K: int, *, k_tiled: bool = False, big_rows: int = -1, group_m: int = 0,
-                  split: bool = False, remove: bool = False) -> None:
+                  split: bool = False, tile: int = PLAN_TILE_AUTO, remove: bool = False) -> None:
     """phi_hip_gemm_plan_set: the tuning table's plan for one GEMM shape
     (remove=True drops the entry)."""
-    plan = None if remove else ctypes.byref(GemmPlan(big_rows, group_m, 1 if split else 0))
+    plan = None if remove else ctypes.byref(GemmPlan(big_rows, group_m, 1 if split else 0, tile, 0))
     _check(load().phi_hip_gemm_plan_set(M, N, K, 1 if k_tiled else 0, plan))
 
 
 def gemm_plan_get(M: int, N: int, K: int, *, k_tiled: bool = False) -> dict:
-    """The plan a GEMM of this shape runs: {big_rows, group_m, split, tuned}."""
+    """The plan a GEMM of this shape runs: {big_rows, group_m, split, tile,
+    tuned}, the tile shape resolved (PLAN_TILE_SQUARE or PLAN_TILE_272)."""
     plan, tuned = GemmPlan(), ctypes.c_int(0)
     _check(load().phi_hip_gemm_plan_get(M, N, K, 1 if k_tiled else 0, ctypes.byref(plan), ctypes.byref(tuned)))
-    return {"big_rows": plan.big_rows, "group_m": plan.group_m, "split": bool(plan.split), "tuned": bool(tuned.value)}
+    return {"big_rows": plan.big_rows, "group_m": plan.group_m, "split": bool(plan.split), "tile": plan.tile,
+            "tuned": bool(tuned.value)}
 
 
 def gemm_plan_clear() -> None:

@@ -160,11 +160,14 @@ static int tune(char** argv) {
     int tuned = 0;
     if (phi_hip_gemm_plan_get(M, N, K, kt ? 1 : 0, &p, &tuned) != PHI_OK) throw MediaError(phi_hip_last_error());
     printf("{\"ok\": true, \"default_exact\": %s, \"exact\": %d, \"tried\": %zu, \"best_us\": %.3f, "
-           "\"best\": [%lld, %d, %d], \"applied\": [%lld, %d, %d], \"tuned\": %d, \"entries\": %zu, \"us\": [",
+           "\"best\": [%lld, %d, %d, %d], \"applied\": [%lld, %d, %d, %d], \"tuned\": %d, \"entries\": %zu, "
+           "\"us\": [",
            r.default_exact ? "true" : "false", r.exact_matches, r.tried.size(), r.best.measured_us,
-           (long long)r.best.big_rows, r.best.group_m, r.best.split ? 1 : 0, (long long)p.big_rows, (int)p.group_m,
-           (int)p.split, tuned, back.size());
+           (long long)r.best.big_rows, r.best.group_m, r.best.split ? 1 : 0, r.best.tile, (long long)p.big_rows,
+           (int)p.group_m, (int)p.split, (int)p.tile, tuned, back.size());
     for (size_t i = 0; i < r.tried.size(); i++) printf("%s%.3f", i ? ", " : "", r.tried[i].measured_us);
+    printf("], \"tiles\": [");
+    for (size_t i = 0; i < r.tried.size(); i++) printf("%s%d", i ? ", " : "", r.tried[i].tile);
     printf("]}\n");
     return 0;
 }

@@ -322,15 +322,27 @@ def test_gemm_plan_table(lib):
     Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, big_rows=4096, group_m=8, split=True)
     Q.gemm_plan_set(4352, 12288, 3072, k_tiled=False, big_rows=4352, group_m=2)
     assert Q.gemm_plan_count() == 2
+    # The tile shape comes back resolved: with no device the cost model counts
+    # 256 CUs, where 272 x 192 tiles fill config 1's rounds (K-tiled only).
     assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True) == {"big_rows": 4096, "group_m": 8, "split": True,
-                                                                "tuned": True}
-    assert Q.gemm_plan_get(4352, 12288, 3072) == {"big_rows": 4352, "group_m": 2, "split": False, "tuned": True}
-    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, big_rows=3840, group_m=4)
-    assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True)["big_rows"] == 3840 and Q.gemm_plan_count() == 2
+                                                                "tile": Q.PLAN_TILE_272, "tuned": True}
+    assert Q.gemm_plan_get(4352, 12288, 3072) == {"big_rows": 4352, "group_m": 2, "split": False,
+                                                  "tile": Q.PLAN_TILE_SQUARE, "tuned": True}
+    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, big_rows=3840, group_m=4, tile=Q.PLAN_TILE_SQUARE)
+    now = Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True)
+    assert now["big_rows"] == 3840 and now["tile"] == Q.PLAN_TILE_SQUARE and Q.gemm_plan_count() == 2
+    Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, group_m=2, tile=Q.PLAN_TILE_272)
+    assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True)["tile"] == Q.PLAN_TILE_272
     for bad, msg in ((dict(big_rows=100), "big_rows=100"), (dict(big_rows=5000), "big_rows=5000"),
-                     (dict(big_rows=-2), "big_rows=-2"), (dict(group_m=17), "group_m=17")):
+                     (dict(big_rows=-2), "big_rows=-2"), (dict(group_m=17), "group_m=17"),
+                     (dict(tile=3), "tile=3"), (dict(tile=-1), "tile=-1"),
+                     (dict(tile=Q.PLAN_TILE_272), "needs K-tiled operands")):
         with pytest.raises(Q.QLinearError, match=msg):
             Q.gemm_plan_set(4352, 12288, 3072, **bad)
+    with pytest.raises(Q.QLinearError, match="K % 512 == 0"):
+        Q.gemm_plan_set(4352, 12288, 3328, k_tiled=True, tile=Q.PLAN_TILE_272)
+    # Unresolvable by 272 x 192 tiles (K % 512 != 0): the square plan.
+    assert Q.gemm_plan_get(4352, 12288, 3328, k_tiled=True)["tile"] == Q.PLAN_TILE_SQUARE
     with pytest.raises(Q.QLinearError, match="empty problem"):
         Q.gemm_plan_set(0, 1, 1)
     Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, remove=True)

@@ -41,14 +41,20 @@ def test_tuned_plans_give_the_same_bits(dev, kt):
     try:
         assert not Q.gemm_plan_get(M, N, K, k_tiled=kt)["tuned"]
         want = run()
-        for plan in (dict(big_rows=2304, group_m=2), dict(big_rows=2048, group_m=8, split=True),
-                     dict(big_rows=0, group_m=4), dict(big_rows=1792, group_m=1), dict(big_rows=-1, group_m=16)):
+        plans = [dict(big_rows=2304, group_m=2), dict(big_rows=2048, group_m=8, split=True),
+                 dict(big_rows=0, group_m=4), dict(big_rows=1792, group_m=1), dict(big_rows=-1, group_m=16),
+                 dict(big_rows=1792, group_m=4, tile=Q.PLAN_TILE_SQUARE)]
+        if kt:
+            plans += [dict(big_rows=-1, group_m=g, tile=Q.PLAN_TILE_272) for g in (1, 4, 8)]
+        for plan in plans:
             Q.gemm_plan_set(M, N, K, k_tiled=kt, **plan)
             got = run()
             torch.cuda.synchronize()
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), plan
             now = Q.gemm_plan_get(M, N, K, k_tiled=kt)
             assert now["tuned"] and now["group_m"] == plan["group_m"]
+            if plan.get("tile", Q.PLAN_TILE_AUTO) != Q.PLAN_TILE_AUTO:
+                assert now["tile"] == plan["tile"]
             if plan["big_rows"] >= 0:
                 assert now["big_rows"] == plan["big_rows"]
             else:
@@ -70,4 +76,11 @@ def test_autotune_sweep_round_trip(dev, tmp_path, kt, M, N, K):
     saved = json.loads(path.read_text())
     (e,) = saved["plans"]
     assert (e["M"], e["N"], e["K"], e["k_tiled"]) == (M, N, K, kt)
-    assert [e["big_rows"], e["group_m"], e["split"]] == r["best"]
+    assert [e["big_rows"], e["group_m"], e["split"], e["tile"]] == r["best"]
+    # 272 x 192 candidates where they apply (K-tiled, K % 512 == 0), one a group height
+    assert r["tiles"].count(Q.PLAN_TILE_272) == (3 if kt and K % 512 == 0 else 0)
+    assert len(r["tiles"]) == r["tried"]
+    if kt and K % 512 == 0:
+        assert r["best"][3] in (Q.PLAN_TILE_SQUARE, Q.PLAN_TILE_272)
+    else:
+        assert r["best"][3] == Q.PLAN_TILE_SQUARE
