@@ -143,6 +143,15 @@ def cpu_baseline(cfg) -> dict | None:
     return out
 
 
+def settle(seconds=1.0):
+    """An idle pause with the device drained, so the next burst of launches
+    meets the board's clocks as the first one did."""
+    import torch
+
+    torch.cuda.synchronize()
+    time.sleep(seconds)
+
+
 def bench_w8a8(cfg, steps, warmup, layout="kt", weights="uniform"):
     """One step: rotate + quantise the activations, then the GEMM with the
     dequant + bias epilogue to bf16.  layout "kt": the weight is packed into
@@ -206,10 +215,16 @@ def bench_w8a8(cfg, steps, warmup, layout="kt", weights="uniform"):
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
-    # The roofline region, right after: the same steps with an event pair
-    # around each GEMM launch, on the launch stream.  It runs later in the
-    # clock transient than the timed region, so its GEMM time is, if
-    # anything, pessimistic.
+    # The roofline region: the same steps with an event pair around each GEMM
+    # launch, on the launch stream, under the timed region's conditions.  The
+    # board lowers its clock some launches into a burst and recovers only
+    # after hundreds, so a region run straight after the timed one would sit
+    # deeper in that dip than the launches it describes.  An idle second (the
+    # clocks are back at idle levels within 0.4 s) and the same warm-up come
+    # first, so the GEMM is timed at the same point of a burst.
+    settle()
+    for _ in range(warmup):
+        linear()
     mids = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     for i in range(steps):
@@ -225,8 +240,11 @@ def bench_w8a8(cfg, steps, warmup, layout="kt", weights="uniform"):
              "fused_linear_tops": ops / (ms * 1e-3) / 1e12}
     if layout == "kt":
         # The drop-in's own path (linear_gemm without K-tiled weights): the
-        # row-major linear, `steps` of them timed like the headline region,
-        # after the other two regions.
+        # row-major linear, timed like the headline region (idle second,
+        # warm-up, then `steps` of them).
+        settle()
+        for _ in range(warmup):
+            Q.q8_linear(x, W, sW, b, q8=q8, s8=s8, C=y)
         start.record()
         for _ in range(steps):
             Q.q8_linear(x, W, sW, b, q8=q8, s8=s8, C=y)
