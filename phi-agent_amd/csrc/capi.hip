@@ -230,9 +230,15 @@ double square_plan_cost(int64_t M, int64_t N, int G) {
     return (double)((big + G - 1) / G) + kSmallRound * (double)((small + G - 1) / G);
 }
 
-// A round of 272 x 192 tiles against a round of 256 x 256 ones at the same K:
-// the outputs' ratio, 52224 / 65536.
-constexpr double kT272Round = 52224.0 / 65536.0;
+// A round of 272 x 192 tiles against a round of 256 x 256 ones at the same K,
+// measured.  In cycles it is the outputs' ratio, 52224 / 65536 = 0.80 (the
+// traced builds: 905 against 1117 clocks a K-step, similar epilogues), but
+// the 272 x 192 kernel's 16x16x64 MFMAs draw less power than the square
+// kernel's 32x32x32 ones on random data, and the board runs it at a higher
+// clock: config 3 attention took 635.0 us in 13 rounds against 671.9 us in
+// 10 square ones (0.73 a round), its MLP 1657.8 us in 35 against 1773.1 us in
+// 27 (0.72).
+constexpr double kT272Round = 0.73;
 
 // Whether the 272 x 192 kernel serves p (K-tiled operands only): as the tuned
 // plan's tile field says, else when its whole rounds cost less than the square

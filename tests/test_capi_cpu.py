@@ -343,6 +343,13 @@ def test_gemm_plan_table(lib):
         Q.gemm_plan_set(4352, 12288, 3328, k_tiled=True, tile=Q.PLAN_TILE_272)
     # Unresolvable by 272 x 192 tiles (K % 512 != 0): the square plan.
     assert Q.gemm_plan_get(4352, 12288, 3328, k_tiled=True)["tile"] == Q.PLAN_TILE_SQUARE
+    # The cost model (256 CUs): 272 x 192 tiles at the DiT shapes, config 3's
+    # included (13 and 35 rounds against 10 and 27 square ones); config 0's
+    # 256 rows keep the square plan's 128 x 128 tiles, as row-major operands do.
+    for M, N, K in ((4352, 3072, 12288), (4352, 9216, 3072), (32760, 5120, 5120), (32760, 13824, 5120)):
+        assert Q.gemm_plan_get(M, N, K, k_tiled=True)["tile"] == Q.PLAN_TILE_272, (M, N, K)
+        assert Q.gemm_plan_get(M, N, K)["tile"] == Q.PLAN_TILE_SQUARE, (M, N, K)
+    assert Q.gemm_plan_get(256, 3072, 3072, k_tiled=True)["tile"] == Q.PLAN_TILE_SQUARE
     with pytest.raises(Q.QLinearError, match="empty problem"):
         Q.gemm_plan_set(0, 1, 1)
     Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, remove=True)

@@ -59,6 +59,49 @@ def test_config3_fused_linear(dev, orc, N):
     assert np.array_equal(u16(y[ri]), yo)
 
 
+def _k_tiled_rows(qk, rows, M, K):
+    """Rows of a K-tiled int8 matrix (M rows, K columns) as a dense array: the
+    byte position of (r, k) as the layout defines it."""
+    r, k = rows[:, None], np.arange(K)[None, :]
+    s, rr = r // 256, r % 256
+    h = np.minimum(256, M - 256 * s)
+    pos = 256 * K * s + h * 64 * (k // 64) + 64 * rr + 16 * (((k // 16) % 4) ^ ((rr // 4) % 4)) + k % 16
+    return qk.cpu().numpy()[pos]
+
+
+@pytest.mark.parametrize("N", [5120, 13824])
+def test_config3_fused_linear_k_tiled(dev, orc, N):
+    """Config 3's linears on K-tiled operands, the path the plan sends to
+    272 x 192 tiles (13 and 35 rounds): rows from every 256-row strip against
+    oracle.q8_linear (codes, scales, accumulators, bf16 outputs)."""
+    M, K = 32760, 5120
+    print(f"config 3 K-tiled fused linear M={M} K={K} N={N}", flush=True)
+    assert Q.gemm_plan_get(M, N, K, k_tiled=True)["tile"] == Q.PLAN_TILE_272
+    x = synth.activations(M, K, seed=0, device=dev)
+    W = synth.int8_weight(N, K, seed=1, device=dev)
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev)
+    Wk = Q.pack_k_tiled(W)
+    qk = torch.empty((M * K,), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = Q.q8_linear_kt(x, Wk, N, sW, b, q8=qk, s8=s8)
+    acc = Q.i8_gemm_kt(qk, Wk, M, N, K, None, None, out_dtype=torch.int32)
+    torch.cuda.synchronize()
+    # a row of every fourth 256-row strip at a varying offset, both sides of
+    # the first tile-row boundary, and the last (partial) tile row's first and
+    # last rows
+    rows = np.array([256 * s + (37 * s) % 256 for s in range(0, (M + 255) // 256, 4)] +
+                    [271, 272, 120 * 272, M - 1])
+    rows = np.unique(rows[rows < M])
+    q_rows = _k_tiled_rows(qk, rows, M, K)
+    ri = torch.from_numpy(rows).to(dev)
+    yo, qo, so, acco = orc.q8_linear(u16(x[ri]), W.cpu().numpy(), sW.cpu().numpy(), u16(b))
+    assert np.array_equal(q_rows, qo), f"{(q_rows != qo).sum()} code mismatches"
+    assert np.array_equal(s8[ri].cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert np.array_equal(acc[ri].cpu().numpy(), acco)
+    assert np.array_equal(u16(y[ri]), yo)
+
+
 def test_config1_up_benched_linear(dev, orc):
     """The call the headline bench times, on its own inputs: phi_hip_q8_linear_kt
     with the bf16 bias at M=4352, K=3072, N=12288 (weight packed K-tiled once).
@@ -82,12 +125,7 @@ def test_config1_up_benched_linear(dev, orc):
     strips = np.arange(0, M, 256)
     rows = np.unique(np.concatenate([strips, strips + 255, np.arange(0, M, 61), [M - 1]]))
     assert len(np.unique(rows // 256)) == 17
-    # the K-tiled byte position of (r, k), as the layout defines it
-    r, k = rows[:, None], np.arange(K)[None, :]
-    s, rr = r // 256, r % 256
-    h = np.minimum(256, M - 256 * s)
-    pos = 256 * K * s + h * 64 * (k // 64) + 64 * rr + 16 * (((k // 16) % 4) ^ ((rr // 4) % 4)) + k % 16
-    q_rows = qk.cpu().numpy()[pos]
+    q_rows = _k_tiled_rows(qk, rows, M, K)
     ri = torch.from_numpy(rows).to(dev)
     yo, qo, so, acco = orc.q8_linear(u16(x[ri]), W.cpu().numpy(), sW.cpu().numpy(), u16(b))
     assert np.array_equal(q_rows, qo), f"{(q_rows != qo).sum()} code mismatches"

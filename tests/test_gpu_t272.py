@@ -76,10 +76,12 @@ def test_epilogue_operands(dev, monkeypatch, bias_kind, scalar_sb):
     assert torch.equal(_bits(got), _bits(want))
 
 
-@pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4352, 3072, 12288), (4352, 9216, 3072)])
+@pytest.mark.parametrize("M,N,K", [(4352, 12288, 3072), (4352, 3072, 12288), (4352, 9216, 3072),
+                                   (32760, 5120, 5120), (32760, 13824, 5120)])
 def test_chosen_plan_matches_square_plan(dev, monkeypatch, M, N, K):
-    """At the DiT shapes the plan takes 272 x 192 tiles by itself; the result
-    equals the square plan's."""
+    """At the DiT shapes the plan takes 272 x 192 tiles by itself (config 3's
+    with a partial last round); the result equals the square plan's."""
+    assert Q.gemm_plan_get(M, N, K, k_tiled=True)["tile"] == Q.PLAN_TILE_272
     A, B, sA, sB = _operands(dev, M, N, K, seed=7)
     sB = synth.weight_scale(0.002, device=dev)
     bias = synth.bias(N, seed=5, device=dev)
