@@ -242,9 +242,9 @@ int64_t phi_hip_big_tile_rows(int64_t M, int64_t N);
  *   group_m   tile rows per group of the XCD-aware tile order, 1..16; 0: 4
  *   split     1: the two tile sizes as two launches; 0: one launch
  *   tile      PHI_PLAN_TILE_SQUARE: the 256 x 256 / 128 x 128 plan above;
- *             PHI_PLAN_TILE_272: 272 x 192 tiles (K-tiled operands with
- *             K % 512 == 0 only; big_rows and split do not apply, group_m
- *             does); PHI_PLAN_TILE_AUTO (0): the library's cost model picks
+ *             PHI_PLAN_TILE_272: 272 x 192 tiles (K % 512 == 0 only; big_rows
+ *             and split do not apply, group_m does); PHI_PLAN_TILE_AUTO (0):
+ *             the library's cost model picks
  *   reserved  0
  * Every plan gives the same bits; only the time differs.  The table is
  * process-wide and thread-safe; the host layer's GemmTuneStore sweeps,

@@ -237,19 +237,22 @@ double square_plan_cost(int64_t M, int64_t N, int G) {
 // kernel's 32x32x32 ones on random data, and the board runs it at a higher
 // clock: config 3 attention took 635.0 us in 13 rounds against 671.9 us in
 // 10 square ones (0.73 a round), its MLP 1657.8 us in 35 against 1773.1 us in
-// 27 (0.72).
-constexpr double kT272Round = 0.73;
+// 27 (0.72).  On row-major operands each DMA lane fetches 16 bytes of its own
+// row, half a cache line a K-step, and that advantage is gone: 0.81 a round
+// at config 1 up, 0.80 at config 3 attention (762.6 us in 13 rounds against
+// 734.6 in 10), 0.90 at config 1 down's single round.
+constexpr double kT272Round = 0.73, kT272RoundRowMajor = 0.80;
 
-// Whether the 272 x 192 kernel serves p (K-tiled operands only): as the tuned
-// plan's tile field says, else when its whole rounds cost less than the square
-// plan's.  PHI_GEMM_T272=0 / 1 turns it off / forces it where it applies (an
-// A/B switch, above the table).
+// Whether the 272 x 192 kernel serves p: as the tuned plan's tile field says,
+// else when its rounds cost less than the square plan's.  PHI_GEMM_T272=0 / 1
+// turns it off / forces it where it applies (an A/B switch, above the table).
 bool use_t272(const phi_dev::GemmParams& p, int G, int tile) {
     if (!phi_dev::t272_ok(p)) return false;
     const int e = phi_dev::env_switch("PHI_GEMM_T272", -1, 0, 1);
     if (e >= 0) return e == 1;
     if (tile != PHI_PLAN_TILE_AUTO) return tile == PHI_PLAN_TILE_272;
-    const double t = kT272Round * (double)((phi_dev::t272_tile_count(p.M, p.N) + G - 1) / G);
+    const double t = (p.kt ? kT272Round : kT272RoundRowMajor) *
+                     (double)((phi_dev::t272_tile_count(p.M, p.N) + G - 1) / G);
     return t < square_plan_cost(p.M, p.N, G) - 1e-9;
 }
 
@@ -265,7 +268,7 @@ hipError_t launch_persist_plan(hipStream_t stream, const phi_dev::GemmParams& p0
     const bool tuned = gk == GK_PERSIST && !w4 && tuned_plan(M, p0.N, p0.K, p0.kt, &plan);
     phi_dev::GemmParams p = p0;
     if (tuned && plan.group_m > 0) p.group_m = plan.group_m;
-    if (gk == GK_PERSIST && !w4 && p0.kt && use_t272(p0, G, tuned ? plan.tile : PHI_PLAN_TILE_AUTO))
+    if (gk == GK_PERSIST && !w4 && use_t272(p0, G, tuned ? plan.tile : PHI_PLAN_TILE_AUTO))
         return phi_dev::launch_i8_gemm_t272(stream, p, G);
     // int8 B runs on the four-stage pipeline; PHI_GEMM_PIPE=0 selects the
     // two-stage kernel (an A/B switch).  W4 B (codes expanded in registers)
@@ -582,9 +585,8 @@ phi_status phi_hip_gemm_plan_set(int64_t M, int64_t N, int64_t K, int k_tiled, c
         if (plan->tile < PHI_PLAN_TILE_AUTO || plan->tile > PHI_PLAN_TILE_272)
             return fail(PHI_ERR_ARG, "%s: tile=%d is not 0 (the cost model), 1 (square) or 2 (272 x 192)", who,
                         (int)plan->tile);
-        if (plan->tile == PHI_PLAN_TILE_272 && (!k_tiled || K % 512 != 0))
-            return fail(PHI_ERR_ARG, "%s: tile=2 (272 x 192) needs K-tiled operands and K %% 512 == 0 (K=%lld)", who,
-                        (long long)K);
+        if (plan->tile == PHI_PLAN_TILE_272 && K % 512 != 0)
+            return fail(PHI_ERR_ARG, "%s: tile=2 (272 x 192) needs K %% 512 == 0 (K=%lld)", who, (long long)K);
         g_plans[key] = *plan;
     }
     g_plan_count.store((int64_t)g_plans.size(), std::memory_order_release);
@@ -608,6 +610,8 @@ phi_status phi_hip_gemm_plan_get(int64_t M, int64_t N, int64_t K, int k_tiled, p
         q.M = (int)M;
         q.N = (int)N;
         q.K = (int)K;
+        q.lda = K;
+        q.ldb = K;
         q.ldc = N;
         q.c_kind = phi_dev::C_BF16;
         q.kt = k_tiled ? 1 : 0;

@@ -160,20 +160,39 @@ __device__ __forceinline__ void piece_at(int r, int rows, int K, int& off, int& 
     st = in ? h * PK : 0;
 }
 
+// Row-major operand (row pitch ld bytes): the DMA lane writing byte q of the
+// LDS piece at row r fetches row r + q / 64 at the chunk its slot holds, K-step
+// 0, and steps 64 bytes a K-step.  A row past the operand points at its end
+// with no step: the range check returns zeros (such rows only feed outputs
+// the epilogue drops).
+__device__ __forceinline__ void piece_rm(int r, int q, int rows, int ld, int& off, int& st) {
+    const int rr = q >> 6, c = ((q >> 4) & 3) ^ ((rr >> 1) & 3), row = r + rr;
+    const bool in = row < rows;
+    off = in ? row * ld + 16 * c + (q & 15) : rows * ld;
+    st = in ? PK : 0;
+}
+
+// The cursor of the piece at row r for the DMA lane writing its byte q.
+__device__ __forceinline__ void piece_lane(const GemmParams& p, bool a, int r, int q, int& off, int& st) {
+    const int rows = a ? p.M : p.N;
+    if (p.kt) {
+        piece_at(r, rows, p.K, off, st);
+        off += dma_src(q);
+    } else {
+        piece_rm(r, q, rows, (int)(a ? p.lda : p.ldb), off, st);
+    }
+}
+
 // Cursors onto the tile at (m0, n0), K-step 0; valid = false: onto nothing.
 __device__ __forceinline__ void cursor_to(Tw& w, const GemmParams& p, int m0, int n0, bool valid) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        piece_at(valid ? m0 + 16 * (w.wave + 4 * j) : p.M, p.M, p.K, w.offA[j], w.stA[j]);
-        w.offA[j] += dma_src(w.lane * 16);
-    }
-    piece_at(valid ? m0 + 256 : p.M, p.M, p.K, w.offA[4], w.stA[4]);
-    w.offA[4] += dma_src(256 * w.wave + w.lane * 4);  // this wave's quarter of the 17th piece
+    for (int j = 0; j < 4; j++)
+        piece_lane(p, true, valid ? m0 + 16 * (w.wave + 4 * j) : p.M, w.lane * 16, w.offA[j], w.stA[j]);
+    // this wave's quarter of the 17th piece
+    piece_lane(p, true, valid ? m0 + 256 : p.M, 256 * w.wave + w.lane * 4, w.offA[4], w.stA[4]);
 #pragma unroll
-    for (int j = 0; j < NBL; j++) {
-        piece_at(valid ? n0 + 16 * (w.wave + 4 * j) : p.N, p.N, p.K, w.offB[j], w.stB[j]);
-        w.offB[j] += dma_src(w.lane * 16);
-    }
+    for (int j = 0; j < NBL; j++)
+        piece_lane(p, false, valid ? n0 + 16 * (w.wave + 4 * j) : p.N, w.lane * 16, w.offB[j], w.stB[j]);
 #pragma unroll
     for (int j = 0; j < NA; j++) asm volatile("" : "+v"(w.offA[j]), "+v"(w.stA[j]));
 #pragma unroll
@@ -867,8 +886,8 @@ __device__ __forceinline__ void t272_tiles(const GemmParams& p, int8_t* lds, int
     w.lds = opaque_lds(lds);
     w.le = eall;
     w.lc = cbuf + wave * SBYTES;
-    w.rA = whole_rsrc(p.A, p.M * p.K);
-    w.rB = whole_rsrc(p.B, p.N * p.K);
+    w.rA = whole_rsrc(p.A, p.M * (int)p.lda);
+    w.rB = whole_rsrc(p.B, p.N * (int)p.ldb);
     // Prologue: the epilogue operands and K-steps 0-3 of the first tile, then
     // NST stores that land nowhere, standing where a previous tile's epilogue
     // stores stand, so every tile's first waits count alike.
@@ -1121,8 +1140,13 @@ int t272_tile_count(int64_t M, int64_t N) { return (int)(((M + TM - 1) / TM) * (
 
 bool t272_ok(const GemmParams& p) {
     const int64_t esz = p.c_kind == C_BF16 ? 2 : 4;
-    return p.kt && !p.gate && p.K % 512 == 0 && (int64_t)p.M * p.K < ((int64_t)1 << 31) - (1 << 20) &&
-           (int64_t)p.N * p.K < ((int64_t)1 << 31) - (1 << 20) && (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) &&
+    // Row-major operands: 16-byte lanes, and every source offset (rows x
+    // pitch) within 32 bits.  K-tiled ones are packed with pitch K.
+    const int64_t la = p.kt ? p.K : p.lda, lb = p.kt ? p.K : p.ldb;
+    const bool rm_ok = p.kt || (p.lda >= p.K && p.ldb >= p.K && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
+                                ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0);
+    return rm_ok && !p.gate && p.K % 512 == 0 && (int64_t)p.M * la < ((int64_t)1 << 31) - (1 << 20) &&
+           (int64_t)p.N * lb < ((int64_t)1 << 31) - (1 << 20) && (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) &&
            p.N % (16 / esz) == 0;
 }
 

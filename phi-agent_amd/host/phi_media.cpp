@@ -1487,8 +1487,8 @@ GemmTuneResult autotune_int8_gemm(ComputeContext& ctx, i64 M, i64 N, i64 K, int 
 
         // Candidates: the square plan at the cost model's 256-row count and
         // its neighbours, all rows, group heights 2, 4, 8, and one or two
-        // launches where both tile sizes run; on K-tiled operands with
-        // K % 512 == 0, also 272 x 192 tiles at each group height.
+        // launches where both tile sizes run; with K % 512 == 0, also 272 x
+        // 192 tiles at each group height.
         phi_gemm_plan def{};
         ctx.check(phi_hip_gemm_plan_get(M, N, K, kt, &def, nullptr), "gemm_plan_get");
         std::vector<i64> rows_opts{def.big_rows};
@@ -1511,7 +1511,7 @@ GemmTuneResult autotune_int8_gemm(ComputeContext& ctx, i64 M, i64 N, i64 K, int 
             for (const int gm : {2, 4, 8})
                 for (const int split : {0, 1})
                     if (!split || (big > 0 && big < M)) cands.push_back({big, gm, split, PHI_PLAN_TILE_SQUARE, 0});
-        if (kt && K % 512 == 0)
+        if (K % 512 == 0)
             for (const int gm : {2, 4, 8}) cands.push_back({def.big_rows, gm, 0, PHI_PLAN_TILE_272, 0});
         double best_us = 1e300;
         for (const phi_gemm_plan& p : cands) {

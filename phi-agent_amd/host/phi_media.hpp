@@ -461,7 +461,7 @@ LoraTail load_lora_tail(GpuCtx& g, GpuArena& arena, const std::string& base, con
 // One plan per (M, N, K, operand layout) for the persistent int8 GEMM:
 // big_rows (rows run as 256 x 256 tiles), group_m (tile rows per group of the
 // XCD-aware tile order), split (the two tile sizes as two launches) and tile
-// (the square plan or 272 x 192 tiles, K-tiled operands only).  Every
+// (the square plan or 272 x 192 tiles, K % 512 == 0).  Every
 // plan gives the same bits, so a sweep is free to pick the fastest; it checks
 // that anyway.  The store persists as JSON and apply() hands its plans to the
 // library, whose every launch of such a shape then runs the stored plan.

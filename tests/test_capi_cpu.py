@@ -327,7 +327,7 @@ def test_gemm_plan_table(lib):
     assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True) == {"big_rows": 4096, "group_m": 8, "split": True,
                                                                 "tile": Q.PLAN_TILE_272, "tuned": True}
     assert Q.gemm_plan_get(4352, 12288, 3072) == {"big_rows": 4352, "group_m": 2, "split": False,
-                                                  "tile": Q.PLAN_TILE_SQUARE, "tuned": True}
+                                                  "tile": Q.PLAN_TILE_272, "tuned": True}
     Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, big_rows=3840, group_m=4, tile=Q.PLAN_TILE_SQUARE)
     now = Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True)
     assert now["big_rows"] == 3840 and now["tile"] == Q.PLAN_TILE_SQUARE and Q.gemm_plan_count() == 2
@@ -335,21 +335,26 @@ def test_gemm_plan_table(lib):
     assert Q.gemm_plan_get(4352, 12288, 3072, k_tiled=True)["tile"] == Q.PLAN_TILE_272
     for bad, msg in ((dict(big_rows=100), "big_rows=100"), (dict(big_rows=5000), "big_rows=5000"),
                      (dict(big_rows=-2), "big_rows=-2"), (dict(group_m=17), "group_m=17"),
-                     (dict(tile=3), "tile=3"), (dict(tile=-1), "tile=-1"),
-                     (dict(tile=Q.PLAN_TILE_272), "needs K-tiled operands")):
+                     (dict(tile=3), "tile=3"), (dict(tile=-1), "tile=-1")):
         with pytest.raises(Q.QLinearError, match=msg):
             Q.gemm_plan_set(4352, 12288, 3072, **bad)
-    with pytest.raises(Q.QLinearError, match="K % 512 == 0"):
-        Q.gemm_plan_set(4352, 12288, 3328, k_tiled=True, tile=Q.PLAN_TILE_272)
+    for kt in (True, False):
+        with pytest.raises(Q.QLinearError, match="K % 512 == 0"):
+            Q.gemm_plan_set(4352, 12288, 3328, k_tiled=kt, tile=Q.PLAN_TILE_272)
     # Unresolvable by 272 x 192 tiles (K % 512 != 0): the square plan.
     assert Q.gemm_plan_get(4352, 12288, 3328, k_tiled=True)["tile"] == Q.PLAN_TILE_SQUARE
-    # The cost model (256 CUs): 272 x 192 tiles at the DiT shapes, config 3's
-    # included (13 and 35 rounds against 10 and 27 square ones); config 0's
-    # 256 rows keep the square plan's 128 x 128 tiles, as row-major operands do.
+    # The cost model (256 CUs): K-tiled, 272 x 192 tiles at the DiT shapes,
+    # config 3's included (13 and 35 rounds against 10 and 27 square ones);
+    # row-major, at config 1's whole rounds but not at config 3's; config 0's
+    # 256 rows keep the square plan's 128 x 128 tiles.
     for M, N, K in ((4352, 3072, 12288), (4352, 9216, 3072), (32760, 5120, 5120), (32760, 13824, 5120)):
         assert Q.gemm_plan_get(M, N, K, k_tiled=True)["tile"] == Q.PLAN_TILE_272, (M, N, K)
+    for M, N, K in ((4352, 3072, 12288), (4352, 12288, 3072)):
+        assert Q.gemm_plan_get(M, N, K)["tile"] == Q.PLAN_TILE_272, (M, N, K)
+    for M, N, K in ((32760, 5120, 5120), (32760, 13824, 5120)):
         assert Q.gemm_plan_get(M, N, K)["tile"] == Q.PLAN_TILE_SQUARE, (M, N, K)
-    assert Q.gemm_plan_get(256, 3072, 3072, k_tiled=True)["tile"] == Q.PLAN_TILE_SQUARE
+    for kt in (True, False):
+        assert Q.gemm_plan_get(256, 3072, 3072, k_tiled=kt)["tile"] == Q.PLAN_TILE_SQUARE
     with pytest.raises(Q.QLinearError, match="empty problem"):
         Q.gemm_plan_set(0, 1, 1)
     Q.gemm_plan_set(4352, 12288, 3072, k_tiled=True, remove=True)

@@ -1,17 +1,18 @@
 """GPU parity of the 272 x 192 persistent GEMM (i8_gemm_t272.hip).
 
-The kernel serves K-tiled problems whose rounds it fills better than the
-square plan (config 1 up and down, config 2's shape).  Its outputs must equal
-the row-major path's bit for bit (that path is held bit-exact against the
-oracle by the other GPU tests), and at config 1 down the oracle itself checks
-sampled rows of every tile row:
+The kernel serves problems whose rounds it costs less than the square plan
+(configs 1, 2 and 3), on K-tiled or row-major operands.  Its outputs must
+equal the square plan's bit for bit (PHI_GEMM_T272=0; that plan is held
+bit-exact against the oracle by the other GPU tests), and at config 1 down
+the oracle itself checks sampled rows of every tile row:
 * forced on (PHI_GEMM_T272=1) over ragged shapes: M and N not multiples of
   the tile, partial 256-row strips of the K-tiled layout, fewer tiles than
   CUs, several tiles a workgroup, K from 512 up;
+* the same on row-major operands, with packed and with pitched rows;
 * every output kind (bf16, fp32, int32), per-column or scalar column scales,
   no / fp32 / bf16 bias;
-* the shapes the plan picks it for by itself, against the square plan
-  (PHI_GEMM_T272=0) in the same process.
+* the shapes the plan picks it for by itself, against the square plan in the
+  same process.
 """
 import numpy as np
 import pytest
@@ -53,9 +54,44 @@ SHAPES = [
 def test_forced_matches_row_major(dev, monkeypatch, M, N, K, out):
     A, B, sA, sB = _operands(dev, M, N, K, seed=M + N)
     bias = synth.bias(N, seed=3, device=dev)
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
     want = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=ODT[out])
     monkeypatch.setenv("PHI_GEMM_T272", "1")
     got = Q.i8_gemm_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, sA, sB, bias, out_dtype=ODT[out])
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("out", ["bf16", "f32", "i32"])
+def test_forced_row_major_operands(dev, monkeypatch, M, N, K, out):
+    """Row-major A and B: each DMA lane fetches its row's chunk directly; rows
+    past the operand read zeros."""
+    A, B, sA, sB = _operands(dev, M, N, K, seed=M + 2 * N)
+    bias = synth.bias(N, seed=8, device=dev)
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
+    want = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=ODT[out])
+    monkeypatch.setenv("PHI_GEMM_T272", "1")
+    got = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=ODT[out])
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(want))
+
+
+@pytest.mark.parametrize("M,N,K,pa,pb", [(300, 200, 512, 32, 16), (1000, 4000, 1024, 512, 1536),
+                                         (4352, 3072, 512, 16, 64)])
+def test_forced_row_major_pitched(dev, monkeypatch, M, N, K, pa, pb):
+    """Row-major operands whose rows are K + pa and K + pb bytes apart (views
+    into wider buffers, the padding filled with other codes)."""
+    Aw = synth.int8_weight(M, K + pa, seed=41, device=dev)
+    Bw = synth.int8_weight(N, K + pb, seed=42, device=dev)
+    A, B = Aw[:, :K], Bw[:, :K]
+    sA = torch.rand(M, device=dev) * 0.01 + 1e-3
+    sB = torch.rand(N, device=dev) * 0.01 + 1e-3
+    bias = synth.bias(N, seed=9, device=dev)
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
+    want = Q.i8_gemm(A.contiguous(), B.contiguous(), sA, sB, bias, out_dtype=torch.bfloat16)
+    monkeypatch.setenv("PHI_GEMM_T272", "1")
+    got = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     assert torch.equal(_bits(got), _bits(want))
 
@@ -69,6 +105,7 @@ def test_epilogue_operands(dev, monkeypatch, bias_kind, scalar_sb):
         sB = synth.weight_scale(0.002, device=dev)
     bias = {"none": None, "f32": torch.randn(N, device=dev) * 0.02,
             "bf16": synth.bias(N, seed=4, device=dev)}[bias_kind]
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
     want = Q.i8_gemm(A, B, sA, sB, bias, out_dtype=torch.bfloat16)
     monkeypatch.setenv("PHI_GEMM_T272", "1")
     got = Q.i8_gemm_kt(Q.pack_k_tiled(A), Q.pack_k_tiled(B), M, N, K, sA, sB, bias, out_dtype=torch.bfloat16)
@@ -159,6 +196,7 @@ def test_w4_in_lds_equals_expand_then_w8a8(dev, monkeypatch, M, N, K, group, wit
     monkeypatch.setenv("PHI_W4_T272", "1")
     y = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
     monkeypatch.delenv("PHI_W4_T272")
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
     y_ref = Q.q8_linear(x, q, s)
     torch.cuda.synchronize()
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
@@ -182,6 +220,7 @@ def test_w4_in_lds_outputs_and_padded_code_rows(dev, monkeypatch, out, bias_kind
     monkeypatch.setenv("PHI_W4_T272", "1")
     y = Q.w4a8_linear(x, cd, lut, s2, group=group, bias=bias, out_dtype=ODT[out])
     monkeypatch.delenv("PHI_W4_T272")
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
     xq, xs = Q.quant_rotate(x)
     y_ref = Q.i8_gemm(xq, q, xs, s, bias, out_dtype=ODT[out])
     torch.cuda.synchronize()

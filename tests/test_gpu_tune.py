@@ -44,8 +44,7 @@ def test_tuned_plans_give_the_same_bits(dev, kt):
         plans = [dict(big_rows=2304, group_m=2), dict(big_rows=2048, group_m=8, split=True),
                  dict(big_rows=0, group_m=4), dict(big_rows=1792, group_m=1), dict(big_rows=-1, group_m=16),
                  dict(big_rows=1792, group_m=4, tile=Q.PLAN_TILE_SQUARE)]
-        if kt:
-            plans += [dict(big_rows=-1, group_m=g, tile=Q.PLAN_TILE_272) for g in (1, 4, 8)]
+        plans += [dict(big_rows=-1, group_m=g, tile=Q.PLAN_TILE_272) for g in (1, 4, 8)]
         for plan in plans:
             Q.gemm_plan_set(M, N, K, k_tiled=kt, **plan)
             got = run()
@@ -77,10 +76,10 @@ def test_autotune_sweep_round_trip(dev, tmp_path, kt, M, N, K):
     (e,) = saved["plans"]
     assert (e["M"], e["N"], e["K"], e["k_tiled"]) == (M, N, K, kt)
     assert [e["big_rows"], e["group_m"], e["split"], e["tile"]] == r["best"]
-    # 272 x 192 candidates where they apply (K-tiled, K % 512 == 0), one a group height
-    assert r["tiles"].count(Q.PLAN_TILE_272) == (3 if kt and K % 512 == 0 else 0)
+    # 272 x 192 candidates where they apply (K % 512 == 0), one a group height
+    assert r["tiles"].count(Q.PLAN_TILE_272) == (3 if K % 512 == 0 else 0)
     assert len(r["tiles"]) == r["tried"]
-    if kt and K % 512 == 0:
+    if K % 512 == 0:
         assert r["best"][3] in (Q.PLAN_TILE_SQUARE, Q.PLAN_TILE_272)
     else:
         assert r["best"][3] == Q.PLAN_TILE_SQUARE
