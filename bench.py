@@ -70,6 +70,9 @@ CONFIGS = {
     "c1_up_t272_tiles": dict(kind="t272trace", M=4352, K=3072, N=12288),
     "c1_down_t272_tiles": dict(kind="t272trace", M=4352, K=12288, N=3072),
     "c2_t272_tiles": dict(kind="t272trace", M=4352, K=3072, N=9216, group=128),
+    # the same kernel on row-major operands (the drop-in's default layout)
+    "c1_up_t272_tiles_row": dict(kind="t272trace", M=4352, K=3072, N=12288, layout="row"),
+    "c1_down_t272_tiles_row": dict(kind="t272trace", M=4352, K=12288, N=3072, layout="row"),
     "c1_down_vendor": dict(kind="vendor", M=4352, K=12288, N=3072),
     # A reference point for the prologue: torch's bf16 -> int8 conversion of
     # the same activation tensor moves the prologue's bytes (2K in, K out a row).
@@ -662,12 +665,13 @@ def bench_t272trace(cfg, steps, warmup):
 
     lib = ctypes.CDLL(os.path.join(PKG, "lib", "libphi_probe.so"))
     P, I = ctypes.c_void_p, ctypes.c_int
-    lib.phi_probe_t272_trace.argtypes = [P, P, P, P, P, P, P, I, I, I, P, ctypes.c_longlong]
+    lib.phi_probe_t272_trace.argtypes = [P, P, P, P, P, P, P, I, I, I, P, ctypes.c_longlong, I]
     lib.phi_probe_t272w4_trace.argtypes = [P, P, P, ctypes.c_longlong, P, I, P, P, P, P, I, I, I, P,
                                            ctypes.c_longlong]
     dev = torch.device("cuda:0")
     M, K, N = cfg["M"], cfg["K"], cfg["N"]
     group = cfg.get("group")  # W4A8: the codes expanded in LDS (i8_gemm_t272w4_kernel)
+    kt = cfg.get("layout", "kt") == "kt"  # row: the activations and the weight row-major
     x = synth.activations(M, K, seed=0, device=dev)
     b = synth.bias(N, seed=2, device=dev)
     if group:
@@ -676,7 +680,7 @@ def bench_t272trace(cfg, steps, warmup):
     else:
         W = synth.int8_weight(N, K, seed=1, device=dev)
         sW = synth.weight_scale(0.002, device=dev)
-        Wk = Q.pack_k_tiled(W)
+        Wk = Q.pack_k_tiled(W) if kt else W
     q8 = torch.empty((M * K,), dtype=torch.int8, device=dev)
     s8 = torch.empty((M,), dtype=torch.float32, device=dev)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
@@ -685,14 +689,17 @@ def bench_t272trace(cfg, steps, warmup):
     stream = torch.cuda.current_stream().cuda_stream
 
     def step():
-        Q.quant_rotate_kt(x, q=q8, s=s8)
+        if kt:
+            Q.quant_rotate_kt(x, q=q8, s=s8)
+        else:
+            Q.quant_rotate(x, q=q8.view(M, K), s=s8)
         if group:
             rc = lib.phi_probe_t272w4_trace(stream, q8.data_ptr(), codes.data_ptr(), codes.stride(0),
                                             lut.data_ptr(), group, s8.data_ptr(), sW.data_ptr(), b.data_ptr(),
                                             y.data_ptr(), M, N, K, rec.data_ptr(), slots)
         else:
             rc = lib.phi_probe_t272_trace(stream, q8.data_ptr(), Wk.data_ptr(), s8.data_ptr(), sW.data_ptr(),
-                                          b.data_ptr(), y.data_ptr(), M, N, K, rec.data_ptr(), slots)
+                                          b.data_ptr(), y.data_ptr(), M, N, K, rec.data_ptr(), slots, 1 if kt else 0)
         if rc != 0:
             raise RuntimeError(f"phi_probe_t272_trace failed ({rc})")
 

@@ -45,11 +45,13 @@ __device__ unsigned long long* phi_t272_out;
 
 extern "C" {
 
-// The traced GEMM on K-tiled operands: bf16 C [M, N] = fma((float)(A . B^T) *
-// sA, sB[0], bf16 bias), one record of 64 words per workgroup into out
-// (slots words).  0 on success, else the HIP error code.
+// The traced GEMM: bf16 C [M, N] = fma((float)(A . B^T) * sA, sB[0], bf16
+// bias) on K-tiled operands (kt = 1) or row-major ones of pitch K (kt = 0),
+// one record of 64 words per workgroup into out (slots words).  0 on success,
+// else the HIP error code.
 int phi_probe_t272_trace(void* stream, const int8_t* A, const int8_t* B, const float* sA, const float* sB,
-                         const void* bias, void* C, int M, int N, int K, unsigned long long* out, long long slots) {
+                         const void* bias, void* C, int M, int N, int K, unsigned long long* out, long long slots,
+                         int kt) {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return (int)hipErrorInvalidDevice;
@@ -70,7 +72,7 @@ int phi_probe_t272_trace(void* stream, const int8_t* A, const int8_t* B, const f
     p.bias_kind = bias ? phi_dev_t272trace::BIAS_BF16 : phi_dev_t272trace::BIAS_NONE;
     p.c_kind = phi_dev_t272trace::C_BF16;
     p.group_m = 4;
-    p.kt = 1;
+    p.kt = kt ? 1 : 0;
     if (M <= 0 || N <= 0 || !phi_dev_t272trace::t272_ok(p)) return (int)hipErrorInvalidValue;
     const long long tiles = phi_dev_t272trace::t272_tile_count(M, N);
     if ((tiles < cus ? tiles : cus) * 64 > slots) return (int)hipErrorInvalidValue;
