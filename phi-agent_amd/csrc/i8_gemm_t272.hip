@@ -520,14 +520,17 @@ struct W4u {
     u32x2 code;
     u32x4 tab;
     uint32_t m, ev, od;
+    u32x2 lo;  // code word 0's 8 output bytes, written with word 1's as one 16-byte chunk
 };
 
 // Piece P (0 .. 10) of expansion unit U (thread t: row t / 4 + 64 U, columns
 // 16 (t % 4) ..).  0: the reads.  Then for each code word h (8 codes): the
 // even columns' lookup (mask, then the v_perm pair and select: lut4b split in
 // two), the odd columns' (the same on the high nibbles), and the interleave
-// of the two into 8 output bytes, written into int8 area bo.  No MFMA slot
-// carries more than five VALU instructions, and a unit keeps nine registers.
+// of the two into 8 output bytes; word 1's piece writes both words' bytes
+// into int8 area bo as one 16-byte chunk (two 8-byte writes a word took 63
+// clocks more a K-step, 1623 against 1560).  No MFMA slot carries more than
+// five VALU instructions, and a unit keeps eleven registers.
 // This thread's byte offsets of unit 0 in a code stage, a table stage and an
 // int8 B area (row t / 4, 16-byte chunk t % 4); unit u adds 64 u rows, an
 // immediate offset.
@@ -570,7 +573,8 @@ __device__ __forceinline__ void w4_piece(W4u& u, int U, const W4o& lo4, const in
             // ev holds columns 0, 2, 4, 6 and od columns 1, 3, 5, 7: interleave.
             const u32x2 o = {__builtin_amdgcn_perm(u.od, u.ev, 0x05010400u),
                              __builtin_amdgcn_perm(u.od, u.ev, 0x07030602u)};
-            *(u32x2*)(bo + lo4.b + 64 * 64 * U + 8 * h) = o;
+            if constexpr (h == 0) u.lo = o;
+            else *(u32x4*)(bo + lo4.b + 64 * 64 * U) = u32x4{u.lo[0], u.lo[1], o[0], o[1]};
         }
     }
 }
