@@ -49,6 +49,13 @@
 // operands); after the last tile they point past the operands, whose range
 // check returns zeros without touching memory.
 //
+// K direction.  A workgroup's odd tiles walk K downward.  With the tile
+// order's groups of four tile rows, the 32 workgroups of an XCD keep the
+// same eight B strips in every round at config 1 up, and the K-steps a round
+// read last are the ones the XCD's L2 still holds when the next round
+// starts: the L2 misses fall from 259 to 219 MB a call there.  The int32
+// sums do not depend on the order.
+//
 // The epilogue converts one block row (16 rows x 96 or 48 columns) at a
 // time, stages it in the wave's LDS area and stores whole 16-byte pieces.
 #include "device_common.hpp"
@@ -184,7 +191,9 @@ __device__ __forceinline__ void piece_lane(const GemmParams& p, bool a, int r, i
 }
 
 // Cursors onto the tile at (m0, n0), K-step 0; valid = false: onto nothing.
-__device__ __forceinline__ void cursor_to(Tw& w, const GemmParams& p, int m0, int n0, bool valid) {
+// rev: the tile walks K downward, from its last K-step (the cursors start
+// there and step back); the int32 sums are the same in either order.
+__device__ __forceinline__ void cursor_to(Tw& w, const GemmParams& p, int m0, int n0, bool valid, bool rev) {
 #pragma unroll
     for (int j = 0; j < 4; j++)
         piece_lane(p, true, valid ? m0 + 16 * (w.wave + 4 * j) : p.M, w.lane * 16, w.offA[j], w.stA[j]);
@@ -193,6 +202,19 @@ __device__ __forceinline__ void cursor_to(Tw& w, const GemmParams& p, int m0, in
 #pragma unroll
     for (int j = 0; j < NBL; j++)
         piece_lane(p, false, valid ? n0 + 16 * (w.wave + 4 * j) : p.N, w.lane * 16, w.offB[j], w.stB[j]);
+    if (rev) {
+        const int last = p.K / PK - 1;
+#pragma unroll
+        for (int j = 0; j < NA; j++) {
+            w.offA[j] += last * w.stA[j];
+            w.stA[j] = -w.stA[j];
+        }
+#pragma unroll
+        for (int j = 0; j < NBL; j++) {
+            w.offB[j] += last * w.stB[j];
+            w.stB[j] = -w.stB[j];
+        }
+    }
 #pragma unroll
     for (int j = 0; j < NA; j++) asm volatile("" : "+v"(w.offA[j]), "+v"(w.stA[j]));
 #pragma unroll
@@ -358,7 +380,7 @@ __device__ __forceinline__ void mma1(const Frag& f, Acc& acc) {
 
 struct NextTile {
     int m0, n0;
-    bool valid;
+    bool valid, rev;  // rev: its K-loop walks K downward
 };
 
 // The K-step's instruction order, fixed: MFMA q, then the fragment read and
@@ -400,7 +422,7 @@ __device__ __forceinline__ void kslots(const Frag& f, Frag& g, Acc& acc, Tw& w, 
 template <int WM, int S, int VWT, bool Z, bool SW>
 __device__ __forceinline__ void kstep(const Frag& f, Frag& g, Acc& acc, Tw& w, const GemmParams& p,
                                       const NextTile& nt, int8_t* ln) {
-    if constexpr (SW) cursor_to(w, p, nt.m0, nt.n0, nt.valid);
+    if constexpr (SW) cursor_to(w, p, nt.m0, nt.n0, nt.valid, nt.rev);
     wait_vm_lgkm0<VWT>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
@@ -633,7 +655,7 @@ __device__ __forceinline__ void kslots4(const Frag& f, Frag& g, Acc& acc, Tw& w,
 template <int WM, int S, int VWT, bool Z, bool SWA, bool SWC>
 __device__ __forceinline__ void kstep4(const Frag& f, Frag& g, Acc& acc, Tw& w, W4c& c, const W4o& lo4,
                                        const GemmParams& p, const NextTile& nt, int8_t* ln) {
-    if constexpr (SWA) cursor_to(w, p, nt.m0, nt.n0, nt.valid);
+    if constexpr (SWA) cursor_to(w, p, nt.m0, nt.n0, nt.valid, false);
     if constexpr (SWC) w4_cursor_to(c, w, p, nt.n0, nt.valid);
     wait_vm_lgkm0<VWT>();
     __builtin_amdgcn_s_barrier();
@@ -847,8 +869,8 @@ __device__ __forceinline__ void epilogue(Acc& acc, const GemmParams& p, int m0, 
 }
 
 template <int WM>
-__device__ __forceinline__ NextTile next_tile(const Shape& s, int t, bool valid) {
-    NextTile nt{0, 0, valid};
+__device__ __forceinline__ NextTile next_tile(const Shape& s, int t, bool valid, bool rev) {
+    NextTile nt{0, 0, valid, rev};
     if (valid) {
         int tm, tn;
         tile_mn(s, t, tm, tn);
@@ -895,8 +917,8 @@ __device__ __forceinline__ void t272_tiles(const GemmParams& p, int8_t* lds, int
     // Prologue: the epilogue operands and K-steps 0-3 of the first tile, then
     // NST stores that land nowhere, standing where a previous tile's epilogue
     // stores stand, so every tile's first waits count alike.
-    const NextTile first = next_tile<WM>(s, r0, true);
-    cursor_to(w, p, first.m0, first.n0, true);
+    const NextTile first = next_tile<WM>(s, r0, true, false);
+    cursor_to(w, p, first.m0, first.n0, true, false);
     issue_epi(w, p, w.le);
     load_step<0>(w);
     load_step<1>(w);
@@ -919,7 +941,11 @@ __device__ __forceinline__ void t272_tiles(const GemmParams& p, int8_t* lds, int
         const int t = r0 + i * s.G;
         int8_t* le = w.le + (i & 1) * EB;
         int8_t* ln = w.le + ((i + 1) & 1) * EB;
-        const NextTile nt = next_tile<WM>(s, t + s.G, i + 1 < ntile);
+        // Odd tiles walk K downward: a workgroup's tiles in consecutive
+        // rounds share their B strips (the XCD's tile order keeps its column
+        // strips), and the K-steps a round read last are the ones its L2
+        // still holds when the next round starts.
+        const NextTile nt = next_tile<WM>(s, t + s.G, i + 1 < ntile, ((i + 1) & 1) != 0);
         PHI_T272_STAMP(i, 0);
         kstep<WM, 0, VWR, true, false>(f, g, acc, w, p, nt, ln);
         kstep<WM, 1, VWR, false, false>(g, f, acc, w, p, nt, ln);
@@ -989,8 +1015,8 @@ __device__ __forceinline__ void t272w4_tiles(const GemmParams& p, int8_t* lds, i
     // and tables of K-step 4 into the stage K-step 0's codes left, and NST
     // stores that land nowhere, standing where a previous tile's epilogue
     // stores stand.  From there every K-step's wait counts as in the loop.
-    const NextTile first = next_tile<WM>(s, r0, true);
-    cursor_to(w, p, first.m0, first.n0, true);
+    const NextTile first = next_tile<WM>(s, r0, true, false);
+    cursor_to(w, p, first.m0, first.n0, true, false);
     w4_cursor_to(c, w, p, first.n0, true);
     const W4o lo4 = w4_lane_offsets(w);
     issue_epi(w, p, w.le);
@@ -1083,7 +1109,7 @@ __device__ __forceinline__ void t272w4_tiles(const GemmParams& p, int8_t* lds, i
         const int t = r0 + i * s.G;
         int8_t* le = w.le + (i & 1) * EB;
         int8_t* ln = w.le + ((i + 1) & 1) * EB;
-        const NextTile nt = next_tile<WM>(s, t + s.G, i + 1 < ntile);
+        const NextTile nt = next_tile<WM>(s, t + s.G, i + 1 < ntile, false);
         PHI_T272_STAMP(i, 0);
         kstep4<WM, 0, VWR, true, false, false>(f, g, acc, w, c, lo4, p, nt, ln);
         kstep4<WM, 1, VWR, false, false, false>(g, f, acc, w, c, lo4, p, nt, ln);
