@@ -7,7 +7,8 @@ bit-exact against the oracle by the other GPU tests), and at config 1 down
 the oracle itself checks sampled rows of every tile row:
 * forced on (PHI_GEMM_T272=1) over ragged shapes: M and N not multiples of
   the tile, partial 256-row strips of the K-tiled layout, fewer tiles than
-  CUs, several tiles a workgroup, K from 512 up;
+  CUs, several tiles a workgroup (a workgroup's odd tiles walk K downward),
+  K from 512 up;
 * the same on row-major operands, with packed and with pitched rows;
 * every output kind (bf16, fp32, int32), per-column or scalar column scales,
   no / fp32 / bf16 bias;
@@ -43,7 +44,8 @@ SHAPES = [
     (300, 200, 512),      # ragged in both, four tiles
     (100, 8, 1024),       # a partial tile, N = one 16-byte piece
     (4352, 3072, 512),    # config 1 down's tile grid at small K
-    (1000, 4000, 1024),   # several tiles a workgroup, partial strips
+    (1000, 4000, 1024),   # partial strips
+    (2000, 30000, 512),   # ragged, about five tiles a workgroup (odd ones walk K downward)
     (4352, 12288, 512),   # config 1 up's grid, four tiles a workgroup
     (555, 9216, 3072),
 ]
