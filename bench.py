@@ -256,6 +256,21 @@ def bench_w8a8(cfg, steps, warmup, layout="kt", weights="uniform"):
         row_ms = start.elapsed_time(end) / steps
         extra["row_major_linear_us"] = row_ms * 1e3
         extra["row_major_linear_tops"] = ops / (row_ms * 1e-3) / 1e12
+        # What linear_gemm runs for a row-major weight: the same linear with
+        # the activation scratch K-tiled where the 272 x 192 plan takes it
+        # (phi_hip_q8_linear_kq), timed the same way.
+        qk2 = torch.empty((M, K), dtype=torch.int8, device=dev)
+        settle()
+        for _ in range(warmup):
+            Q.q8_linear_kq(x, W, sW, b, q8=qk2, s8=s8, C=y)
+        start.record()
+        for _ in range(steps):
+            Q.q8_linear_kq(x, W, sW, b, q8=qk2, s8=s8, C=y)
+        end.record()
+        torch.cuda.synchronize()
+        dl_ms = start.elapsed_time(end) / steps
+        extra["drop_in_linear_us"] = dl_ms * 1e3
+        extra["drop_in_linear_tops"] = ops / (dl_ms * 1e-3) / 1e12
     return {
         "value": ops / (ms * 1e-3) / 1e12, "ms": ms, "gemm_ms": gemm_ms, "prologue_ms": pro_ms,
         "roofline": {"bound": "mfma", "achieved": ops / (gemm_ms * 1e-3) / 1e12,

@@ -275,6 +275,18 @@ phi_status phi_hip_q8_linear_kt(phi_stream_t stream, const void* x, int x_dtype,
                                 const int8_t* W, const float* sW, int sw_scalar, const void* bias, int bias_dtype,
                                 int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8, int round_mode);
 
+/* linear_gemm's int8 branch (core/models/model_common.cpp:1384-1411) for a
+ * row-major weight, as phi_hip_q8_linear (same arguments, same C and s8, bit
+ * for bit), with the activation scratch q8 written K-tiled where the
+ * 272 x 192 plan takes the problem (K % 256 == 0, K <= 16384, 16-byte
+ * aligned q8, W rows and C rows): the GEMM then reads A in K-tiled pieces
+ * and only the weight's rows are gathered.  Elsewhere it is phi_hip_q8_linear
+ * and q8 is row-major.  q8 is scratch either way: callers must not read it. */
+phi_status phi_hip_q8_linear_kq(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                                const int8_t* W, int64_t ldw, const float* sW, int sw_scalar, const void* bias,
+                                int bias_dtype, int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8,
+                                int round_mode, void* workspace, size_t ws_bytes);
+
 /* A grouped low-bit weight as the checkpoint stores it
  * (W4a8ExpandArgs, core/kernels/w4a8_expand.hpp:86-117). */
 typedef struct phi_w4a8_weight {

@@ -242,6 +242,9 @@ double square_plan_cost(int64_t M, int64_t N, int G) {
 // at config 1 up, 0.80 at config 3 attention (762.6 us in 13 rounds against
 // 734.6 in 10), 0.90 at config 1 down's single round.
 constexpr double kT272Round = 0.73, kT272RoundRowMajor = 0.80;
+// K-tiled activations against a row-major weight (b_rm): only B's 192 rows a
+// K-step are gathered row by row.
+constexpr double kT272RoundMixed = 0.76;
 
 // Whether the 272 x 192 kernel serves p: as the tuned plan's tile field says,
 // else when its rounds cost less than the square plan's.  PHI_GEMM_T272=0 / 1
@@ -251,7 +254,7 @@ bool use_t272(const phi_dev::GemmParams& p, int G, int tile) {
     const int e = phi_dev::env_switch("PHI_GEMM_T272", -1, 0, 1);
     if (e >= 0) return e == 1;
     if (tile != PHI_PLAN_TILE_AUTO) return tile == PHI_PLAN_TILE_272;
-    const double t = (p.kt ? kT272Round : kT272RoundRowMajor) *
+    const double t = (p.kt ? (p.b_rm ? kT272RoundMixed : kT272Round) : kT272RoundRowMajor) *
                      (double)((phi_dev::t272_tile_count(p.M, p.N) + G - 1) / G);
     return t < square_plan_cost(p.M, p.N, G) - 1e-9;
 }
@@ -717,6 +720,55 @@ phi_status phi_hip_q8_linear_kt(phi_stream_t stream, const void* x, int x_dtype,
     st = phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode);
     if (st != PHI_OK) return st;
     return i8_gemm_kt_impl(who, stream, q8, W, s8, sW, sw_scalar, bias, bias_dtype, C, c_dtype, ldc, M, N, K);
+}
+
+// phi_hip_q8_linear with the activation scratch written K-tiled while the
+// weight stays row-major: the 272 x 192 kernel reads A in K-tiled pieces and
+// gathers B's rows.  Where that plan does not apply or does not pay (its
+// rounds against the square plan's), the call is phi_hip_q8_linear itself.
+phi_status phi_hip_q8_linear_kq(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                                const int8_t* W, int64_t ldw, const float* sW, int sw_scalar, const void* bias,
+                                int bias_dtype, int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8, float* s8,
+                                int round_mode, void* workspace, size_t ws_bytes) {
+    static const char* who = "linear_gemm";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!q8 || !s8) return fail(PHI_ERR_ARG, "linear_gemm: the int8 path needs activation scratch");
+    if (M <= 0) return fail(PHI_ERR_SHAPE, "%s: empty problem", who);
+    phi_status st = check_gemm(who, q8, K, W, ldw, M, N, K, s8, sW, C, c_dtype, ldc, false);
+    if (st != PHI_OK) return st;
+    const int bk = bias_kind_of(bias, bias_dtype, &st);
+    if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    bool mixed = K % 256 == 0 && K <= 16384 && aligned(q8, 16) && persist_ok(C, c_dtype, N, K, K, ldw, ldc) &&
+                 !(bias && !aligned(bias, bk == phi_dev::BIAS_BF16 ? 2 : 4)) && !getenv("PHI_GEMM_KERNEL");
+    phi_dev::GemmParams p{};
+    if (mixed) {
+        p.A = q8;
+        p.B = W;
+        p.sA = s8;
+        p.sB = sW;
+        p.bias = bias;
+        p.C = C;
+        p.lda = K;
+        p.ldb = ldw;
+        p.ldc = ldc;
+        p.M = (int)M;
+        p.N = (int)N;
+        p.K = (int)K;
+        p.sb_scalar = sw_scalar ? 1 : 0;
+        p.bias_kind = bk;
+        p.c_kind = c_kind_of(c_dtype);
+        p.group_m = 4;
+        p.kt = 1;
+        p.b_rm = 1;
+        set_vec_flags(p, c_dtype, ldc);
+        mixed = use_t272(p, num_cus(), PHI_PLAN_TILE_AUTO);
+    }
+    if (!mixed)
+        return phi_hip_q8_linear(stream, x, x_dtype, ldx, M, K, W, ldw, sW, sw_scalar, bias, bias_dtype, N, C, c_dtype,
+                                 ldc, q8, s8, round_mode, workspace, ws_bytes);
+    st = phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode);
+    if (st != PHI_OK) return st;
+    return check_hip(phi_dev::launch_i8_gemm_t272((hipStream_t)stream, p, num_cus()), who);
 }
 
 static phi_status check_w4a8(const char* who, const phi_w4a8_weight* w, bool lut) {

@@ -38,6 +38,9 @@ struct GemmParams {
     // Persistent pipeline: A and B in the K-tiled layout (k_tiled_offset) instead
     // of row-major; lda / ldb are then K.
     int kt;
+    // With kt, the 272 x 192 kernel only: B stays row-major (pitch ldb) while
+    // A is K-tiled.  No other kernel reads it; it must be 0 for them.
+    int b_rm;
 };
 
 // The K-tiled operand layout: rows in strips of 256 (the last strip may be
@@ -72,8 +75,9 @@ hipError_t launch_i8_gemm_persist_mixed(hipStream_t stream, const GemmParams& pb
 hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_cus, int wave_tile);
 hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus);
 // Persistent kernel on 272 x 192 tiles (i8_gemm_t272.hip): K-tiled operands,
-// or row-major ones at 16-byte pitches and addresses; K % 512 == 0, no gate,
-// rows x pitch below 2^31 for both operands (t272_ok).
+// row-major ones at 16-byte pitches and addresses, or (b_rm) A K-tiled and B
+// row-major; K % 512 == 0, no gate, rows x pitch below 2^31 for both
+// operands (t272_ok).
 bool t272_ok(const GemmParams& p);
 int t272_tile_count(int64_t M, int64_t N);
 hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_cus);

@@ -182,7 +182,7 @@ __device__ __forceinline__ void piece_rm(int r, int q, int rows, int ld, int& of
 // The cursor of the piece at row r for the DMA lane writing its byte q.
 __device__ __forceinline__ void piece_lane(const GemmParams& p, bool a, int r, int q, int& off, int& st) {
     const int rows = a ? p.M : p.N;
-    if (p.kt) {
+    if (p.kt && (a || !p.b_rm)) {
         piece_at(r, rows, p.K, off, st);
         off += dma_src(q);
     } else {
@@ -1171,11 +1171,14 @@ int t272_tile_count(int64_t M, int64_t N) { return (int)(((M + TM - 1) / TM) * (
 bool t272_ok(const GemmParams& p) {
     const int64_t esz = p.c_kind == C_BF16 ? 2 : 4;
     // Row-major operands: 16-byte lanes, and every source offset (rows x
-    // pitch) within 32 bits.  K-tiled ones are packed with pitch K.
-    const int64_t la = p.kt ? p.K : p.lda, lb = p.kt ? p.K : p.ldb;
-    const bool rm_ok = p.kt || (p.lda >= p.K && p.ldb >= p.K && p.lda % 16 == 0 && p.ldb % 16 == 0 &&
-                                ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0);
-    return rm_ok && !p.gate && p.K % 512 == 0 && (int64_t)p.M * la < ((int64_t)1 << 31) - (1 << 20) &&
+    // pitch) within 32 bits.  K-tiled ones are packed with pitch K.  b_rm:
+    // A K-tiled, B row-major.
+    const bool kta = p.kt != 0, ktb = p.kt && !p.b_rm;
+    const int64_t la = kta ? p.K : p.lda, lb = ktb ? p.K : p.ldb;
+    const bool a_ok = kta || (p.lda >= p.K && p.lda % 16 == 0 && ((uintptr_t)p.A & 15) == 0);
+    const bool b_ok = ktb || (p.ldb >= p.K && p.ldb % 16 == 0 && ((uintptr_t)p.B & 15) == 0);
+    return a_ok && b_ok && (!p.b_rm || p.kt) && !p.gate && p.K % 512 == 0 &&
+           (int64_t)p.M * la < ((int64_t)1 << 31) - (1 << 20) &&
            (int64_t)p.N * lb < ((int64_t)1 << 31) - (1 << 20) && (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) &&
            p.N % (16 / esz) == 0;
 }

@@ -1579,46 +1579,31 @@ void linear_gemm(GpuCtx& g, const QuantLinear& w, const GpuAlloc& x, i64 m, i64 
     if (!w.w || !w.scale) throw MediaError("linear_gemm: the int8 weight is empty");
     if (!q8 || !s8) throw MediaError("linear_gemm: the int8 path needs activation scratch");
     if (!g.ctx) throw MediaError("linear_gemm: no compute context");
+    const void* xp = cat(x.res, x.off);
+    const float* sw = (const float*)cat(w.scale.res, w.scale.off);
+    int8_t* qp = (int8_t*)at(q8.res, q8.off);
+    float* sp = (float*)at(s8.res, s8.off);
     if (w.k_tiled) {
         // The prologue writes q8 K-tiled and the GEMM reads both operands that
-        // way: the same fp32 output as the row-major pair below.
+        // way: the same fp32 output as the row-major weight's path below.
         if (x.bytes < (u64)m * (u64)k * 4 || out.bytes < (u64)m * (u64)w.n * 4 || q8.bytes < (u64)m * (u64)k ||
             s8.bytes < (u64)m * 4)
             throw MediaError("linear_gemm: a buffer is smaller than the [" + std::to_string(m) + ", " +
                              std::to_string(k) + "] x [" + std::to_string(w.n) + "] linear needs");
-        g.ctx->check(phi_hip_q8_linear_kt(g.ctx->stream(), cat(x.res, x.off), PHI_F32, k, m, k,
-                                          (const int8_t*)cat(w.w.res, w.w.off), (const float*)cat(w.scale.res, w.scale.off),
-                                          0, nullptr, PHI_F32, w.n, at(out.res, out.off), PHI_F32, w.n,
-                                          (int8_t*)at(q8.res, q8.off), (float*)at(s8.res, s8.off), PHI_ROUND_HALF_AWAY),
+        g.ctx->check(phi_hip_q8_linear_kt(g.ctx->stream(), xp, PHI_F32, k, m, k, (const int8_t*)cat(w.w.res, w.w.off),
+                                          sw, 0, nullptr, PHI_F32, w.n, at(out.res, out.off), PHI_F32, w.n, qp, sp,
+                                          PHI_ROUND_HALF_AWAY),
                      "linear_gemm");
         return;
     }
-    QuantConvrotArgs qa;
-    qa.x = x.res;
-    qa.x_offset = x.off;
-    qa.q = q8.res;
-    qa.q_offset = q8.off;
-    qa.s = s8.res;
-    qa.s_offset = s8.off;
-    qa.rows = m;
-    qa.K = k;
-    dispatch_quant_convrot(*g.ctx, qa);
-
-    Int8GemmArgs ga;
-    ga.a = q8.res;
-    ga.a_offset = q8.off;
-    ga.b = w.w.res;
-    ga.b_offset = w.w.off;
-    ga.sa = s8.res;
-    ga.sa_offset = s8.off;
-    ga.sb = w.scale.res;
-    ga.sb_offset = w.scale.off;
-    ga.c = out.res;
-    ga.c_offset = out.off;
-    ga.M = m;
-    ga.N = w.n;
-    ga.K = k;
-    dispatch_int8_gemm(*g.ctx, ga);
+    // A row-major weight: the reference's rotate+quantise (dispatch_quant_convrot)
+    // then int8 GEMM (dispatch_int8_gemm), fused in one call that writes the
+    // scratch q8 K-tiled where the 272 x 192 plan takes the shape; the output
+    // is the same, bit for bit.
+    g.ctx->check(phi_hip_q8_linear_kq(g.ctx->stream(), xp, PHI_F32, k, m, k, (const int8_t*)cat(w.w.res, w.w.off), k,
+                                      sw, 0, nullptr, PHI_F32, w.n, at(out.res, out.off), PHI_F32, w.n, qp, sp,
+                                      PHI_ROUND_HALF_AWAY, nullptr, 0),
+                 "linear_gemm");
 }
 
 }  // namespace phi::media

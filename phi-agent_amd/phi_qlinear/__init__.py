@@ -76,7 +76,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_silu_gate", "phi_hip_i4_gemm", "phi_hip_i4_workspace_bytes", "phi_hip_lora_tail",
            "phi_hip_lora_down", "phi_hip_lora_rank_add", "phi_hip_dequant_rows", "phi_hip_convrot_rows",
            "phi_hip_lora_fold", "phi_hip_q8_linear_noalloc", "phi_hip_noalloc_scratch_bytes",
-           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows",
+           "phi_hip_pack_k_tiled", "phi_hip_i8_gemm_kt", "phi_hip_q8_linear_kt", "phi_hip_q8_linear_kq",
+           "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows",
            "phi_hip_quant_rotate_mod_kt", "phi_hip_quant_rotate_act_kt", "phi_hip_i8_gemm_residual_kt",
            "phi_hip_dequant_fp4_rows", "phi_hip_gemm_plan_set", "phi_hip_gemm_plan_get", "phi_hip_gemm_plan_count",
            "phi_hip_gemm_plan_clear"]
@@ -142,6 +143,8 @@ def load() -> ctypes.CDLL:
     L.phi_hip_big_tile_rows.restype = I64
     L.phi_hip_i8_gemm_kt.argtypes = [P, P, P, P, P, I, P, I, P, I, I64, I64, I64, I64]
     L.phi_hip_q8_linear_kt.argtypes = [P, P, I, I64, I64, I64, P, P, I, P, I, I64, P, I, I64, P, P, I]
+    L.phi_hip_q8_linear_kq.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, P, P,
+                                       I, P, SZ]
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:
@@ -289,6 +292,32 @@ def q8_linear(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
                                     _ptr(bias), _dt(bias) if bias is not None else F32, N,
                                     _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8), round_mode,
                                     wp, wn))
+    return C
+
+
+def q8_linear_kq(x: torch.Tensor, W: torch.Tensor, sW: torch.Tensor,
+                 bias: torch.Tensor | None = None, *, out_dtype=torch.bfloat16,
+                 q8: torch.Tensor | None = None, s8: torch.Tensor | None = None,
+                 C: torch.Tensor | None = None, round_mode: int = ROUND_HALF_AWAY,
+                 workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """q8_linear on a row-major weight with the activation scratch q8 written
+    K-tiled where the 272 x 192 plan takes the problem (phi_hip_q8_linear_kq):
+    C and s8 are q8_linear's, bit for bit; q8 is scratch."""
+    _require_device(x, W, sW, bias, q8, s8, C)
+    M, K = x.shape
+    N = W.shape[0]
+    if q8 is None:
+        q8 = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if s8 is None:
+        s8 = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    wp, wn = _ws(workspace)
+    _check(load().phi_hip_q8_linear_kq(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(W),
+                                       W.stride(0), _ptr(sW), 1 if sW.numel() == 1 else 0,
+                                       _ptr(bias), _dt(bias) if bias is not None else F32, N,
+                                       _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8), round_mode,
+                                       wp, wn))
     return C
 
 

@@ -1,6 +1,7 @@
 """GPU parity of the K-tiled operand path (phi_hip_pack_k_tiled,
 phi_hip_quant_rotate_kt / _mod_kt / _act_kt, phi_hip_i8_gemm_kt,
-phi_hip_i8_gemm_residual_kt, phi_hip_q8_linear_kt).
+phi_hip_i8_gemm_residual_kt, phi_hip_q8_linear_kt, and phi_hip_q8_linear_kq: K-tiled
+activations against a row-major weight).
 
 The K-tiled layout is a re-arrangement of the same bytes, so the bar is
 identity with the row-major path, which the other GPU tests hold bit-exact
@@ -112,6 +113,55 @@ def test_q8_linear_kt_matches_q8_linear(dev, M, K, N):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert torch.equal(sk, s8)
     assert torch.equal(qk, Q.pack_k_tiled(q8))
+
+
+def _kq_against_q8_linear(dev, M, K, N, *, ldw=None, out=torch.bfloat16, bias=True, seed=0):
+    """q8_linear_kq against q8_linear on the same inputs: C and s8 bit for
+    bit; q8 holds the row-major codes, K-tiled (the mixed plan) or as they are
+    (where the call falls back to q8_linear).  Returns which layout q8 took."""
+    x = synth.activations(M, K, seed=M + seed, device=dev)
+    Ww = synth.int8_weight(N, ldw or K, seed=3 + seed, device=dev)
+    W = Ww[:, :K]
+    sW = synth.weight_scale(0.002, device=dev)
+    b = synth.bias(N, seed=2, device=dev) if bias else None
+    q8 = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s8 = torch.empty((M,), dtype=torch.float32, device=dev)
+    want = Q.q8_linear(x, W.contiguous(), sW, b, q8=q8, s8=s8, out_dtype=out)
+    qk = torch.empty((M, K), dtype=torch.int8, device=dev)
+    sk = torch.empty((M,), dtype=torch.float32, device=dev)
+    got = Q.q8_linear_kq(x, W, sW, b, q8=qk, s8=sk, out_dtype=out)
+    torch.cuda.synchronize()
+    bits = torch.int16 if out == torch.bfloat16 else torch.int32
+    assert torch.equal(got.view(bits), want.view(bits))
+    assert torch.equal(sk, s8)
+    if torch.equal(qk, q8):
+        return "row-major"
+    assert torch.equal(qk.view(-1), Q.pack_k_tiled(q8).view(-1))
+    return "k-tiled"
+
+
+@pytest.mark.parametrize("M,K,N", [(4352, 3072, 12288), (4352, 12288, 3072), (4352, 3072, 9216)])
+def test_q8_linear_kq_at_dit_shapes(dev, M, K, N):
+    """The drop-in's row-major weight at the DiT shapes: the mixed plan (A
+    K-tiled, B gathered row by row on the 272 x 192 kernel) takes them."""
+    assert _kq_against_q8_linear(dev, M, K, N) == "k-tiled"
+
+
+@pytest.mark.parametrize("M,K,N,ldw", [(300, 512, 200, 512), (1000, 1024, 4000, 1040), (2000, 512, 30000, 512),
+                                       (555, 3072, 9216, 3088), (100, 1024, 8, 1024)])
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
+def test_q8_linear_kq_forced_mixed(dev, monkeypatch, M, K, N, ldw, out):
+    """The mixed plan forced (PHI_GEMM_T272=1) over ragged shapes, weights
+    with a row pitch above K, several tiles a workgroup."""
+    monkeypatch.setenv("PHI_GEMM_T272", "1")
+    assert _kq_against_q8_linear(dev, M, K, N, ldw=ldw, out=out, seed=ldw) == "k-tiled"
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 3072, 3072), (77, 768, 300), (64, 256, 512)])
+def test_q8_linear_kq_falls_back(dev, M, K, N):
+    """Shapes the mixed plan does not take (too few tiles to pay, K not a
+    multiple of 512) run q8_linear itself."""
+    assert _kq_against_q8_linear(dev, M, K, N, bias=False) == "row-major"
 
 
 @pytest.mark.parametrize("M,K", [(1, 256), (77, 3072), (300, 1024), (4352, 3072)])
