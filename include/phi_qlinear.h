@@ -496,7 +496,8 @@ phi_status phi_hip_lora_fold(phi_stream_t stream, float* w, int64_t ldw, int64_t
  * phi_hip_q8_linear without caller scratch, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  Same arguments, arithmetic
- * and bits as phi_hip_q8_linear; its q8 [M, K] / s8 [M] activation scratch is
+ * and bits as phi_hip_q8_linear (it runs phi_hip_q8_linear_kq); its q8
+ * (M x K bytes) / s8 [M] activation scratch is
  * a static device array of PHI_NOALLOC_SCRATCH_BYTES per GPU (held from the
  * library's load until the process ends), so M * K (rounded up to 256) + 4 M
  * must fit in it: larger calls return PHI_ERR_WORKSPACE.  Allocates nothing.

@@ -1,7 +1,8 @@
 // The W8A8 linear for callers that cannot allocate (code under HIP graph
 // capture, tight serving loops, harnesses that forbid hipMalloc): the
-// activation scratch of phi_hip_q8_linear (q8 [M, K] int8 and s8 [M] fp32)
-// lives in a file-scope device array instead of caller buffers.
+// activation scratch of phi_hip_q8_linear / phi_hip_q8_linear_kq (q8, M x K
+// int8 codes, and s8 [M] fp32) lives in a file-scope device array instead of
+// caller buffers.
 //
 // `scratch` is a static device variable: every GPU the library runs on holds
 // its own copy (kScratchBytes) from the code object's load until the process
@@ -103,8 +104,10 @@ phi_status phi_hip_q8_linear_noalloc(phi_stream_t stream, const void* x, int x_d
     if (!base)
         return phi_capi::fail(PHI_ERR_HIP, "%s: the static scratch of device %d cannot be addressed (%s)", who, dev,
                               hipGetErrorString(e));
-    return phi_hip_q8_linear(stream, x, x_dtype, ldx, M, K, W, ldw, sW, sw_scalar, bias, bias_dtype, N, C, c_dtype,
-                             ldc, (int8_t*)base, (float*)(base + s_off), round_mode, nullptr, 0);
+    // phi_hip_q8_linear_kq: the same C as phi_hip_q8_linear, with the codes
+    // written K-tiled where the 272 x 192 plan takes the shape.
+    return phi_hip_q8_linear_kq(stream, x, x_dtype, ldx, M, K, W, ldw, sW, sw_scalar, bias, bias_dtype, N, C,
+                                c_dtype, ldc, (int8_t*)base, (float*)(base + s_off), round_mode, nullptr, 0);
 }
 
 }  // extern "C"
