@@ -76,8 +76,8 @@ hipError_t launch_i8_gemm_pipe(hipStream_t stream, const GemmParams& p, int num_
 hipError_t launch_i8_gemm_pipe_mixed(hipStream_t stream, const GemmParams& pb, const GemmParams& ps, int num_cus);
 // Persistent kernel on 272 x 192 tiles (i8_gemm_t272.hip): K-tiled operands,
 // row-major ones at 16-byte pitches and addresses, or (b_rm) A K-tiled and B
-// row-major; K % 512 == 0, no gate, rows x pitch below 2^31 for both
-// operands (t272_ok).
+// row-major; K % 512 == 0, a gate only with fp32 output, rows x pitch below
+// 2^31 for both operands (t272_ok).
 bool t272_ok(const GemmParams& p);
 int t272_tile_count(int64_t M, int64_t N);
 hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_cus);

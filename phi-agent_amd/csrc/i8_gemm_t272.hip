@@ -2,7 +2,8 @@
 // operands, four-stage 64-deep K ring):
 //
 //   acc[m,n] = sum_k A[m,k] * B[n,k]                  (exact int32)
-//   C[m,n]   = fma((float)acc * sA[m], sB[n], bias[n])  -> bf16 (RNE) / fp32 / raw int32
+//   C[m,n]   = fma((float)acc * sA[m], sB[n], bias[n])  -> bf16 (RNE) / fp32 / raw int32,
+//              or fp32 into a gated residual: C = fma(that, gate[n], C)
 //
 // The product and epilogue are those of the reference's int8_gemm_tc
 // (core/kernels/int8_gemm.cpp:466-621, epilogue :588-620) and host gemm_int8
@@ -77,6 +78,12 @@ namespace {
 
 using namespace persist;
 
+// Output kinds: CKind's C_F32 / C_BF16 / C_I32, and the fp32 output into a
+// gated residual stream, updated in place: C = fma(linear, gate[n], C), the
+// reference's AddMul `a + b * c` (core/kernels/ops.cpp:80, after the
+// projection at core/models/av_dit.cpp:1389) as NVRTC's --fmad=true
+// contracts it.
+constexpr int C_F32G = 3;
 constexpr int TM = 272, TN = 192;      // output tile
 constexpr int PK = 64, NSTG = 4;       // K bytes per stage, stages
 constexpr int BOFF = TM * PK;          // B's offset within a stage
@@ -688,8 +695,10 @@ struct ColOps {
 // row x / 12, piece x % 12 of the row) and store.
 template <int WM, int CK, int R>
 __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
-                                        const int8_t* e, const __amdgpu_buffer_rsrc_t& rs, int pitch, int colw) {
+                                        const int8_t* e, const __amdgpu_buffer_rsrc_t& rs,
+                                        const __amdgpu_buffer_rsrc_t& rg, int pitch, int colw) {
     static_assert(CK != C_BF16, "bf16 takes the pipelined rows");
+    constexpr bool gated = CK == C_F32G;
     constexpr bool shared = WM == 0 ? R == 8 : R == 0;
     constexpr int g = 8 * WM + R;          // block row in the tile
     constexpr int c0 = shared ? 3 * WM : 0;  // first wave column block
@@ -698,14 +707,29 @@ __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmPa
     const int lr = w.lane & 15, lg = w.lane >> 4;
     int8_t* lc = w.lc;
     const float sa = CK != C_I32 ? *(const float*)(e + E_SA + (16 * g + lr) * 4) : 0.0f;
+    // Gated: the residual pieces and the gate columns a group of three blocks
+    // stores, fetched before its conversion so their latency overlaps it.
+    u32x4 res[3], gts[3];
 #pragma unroll
     for (int c = 0; c < nb; c++) {
+        if constexpr (gated) {
+            if (c % 3 == 0) {
+#pragma unroll
+                for (int t = 0; t < 3; t++) {
+                    const int x = w.lane + 64 * t, rr = x / 12, ch = x - 12 * rr;
+                    const int col = colw + 16 * (c0 + c) + 4 * ch;
+                    res[t] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rs, col < p.N ? (16 * g + rr) * pitch + col * 4 : kDropOffset, 0, 0);
+                    gts[t] = __builtin_amdgcn_raw_buffer_load_b128(rg, col * 4, 0, 0);
+                }
+            }
+        }
         v4i blk;
         if constexpr (shared) blk = acc.s[c];
         else blk = acc.f[fr < 0 ? 0 : fr][c];
         asm volatile("" : "+v"(blk));
         u32x4 o;
-        if constexpr (CK == C_F32) {
+        if constexpr (CK == C_F32 || gated) {
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 o[q] = __float_as_uint(fmaf((float)blk[q] * sa, co.sb[c0 + c][q], co.bz[c0 + c][q]));
@@ -719,7 +743,13 @@ __device__ __forceinline__ void epi_row(Acc& acc, const ColOps& co, const GemmPa
 #pragma unroll
             for (int t = 0; t < 3; t++) {
                 const int x = w.lane + 64 * t, rr = x / 12, ch = x - 12 * rr;
-                const u32x4 v = *(const u32x4*)(lc + rr * SP + stage_slot(rr, ch) * 16);
+                u32x4 v = *(const u32x4*)(lc + rr * SP + stage_slot(rr, ch) * 16);
+                if constexpr (gated) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        v[q] = __float_as_uint(
+                            fmaf(__uint_as_float(v[q]), __uint_as_float(gts[t][q]), __uint_as_float(res[t][q])));
+                }
                 const int col = colw + 16 * (c0 + cg) + 4 * ch;
                 const int off = col < p.N ? (16 * g + rr) * pitch + col * 4 : kDropOffset;
                 __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kStoreNT);
@@ -819,10 +849,11 @@ __device__ __forceinline__ void epi_rows_bf16(Acc& acc, const ColOps& co, const 
 
 template <int WM, int CK, int R = 0>
 __device__ __forceinline__ void epi_rows(Acc& acc, const ColOps& co, const GemmParams& p, const Tw& w,
-                                         const int8_t* e, const __amdgpu_buffer_rsrc_t& rs, int pitch, int colw) {
+                                         const int8_t* e, const __amdgpu_buffer_rsrc_t& rs,
+                                         const __amdgpu_buffer_rsrc_t& rg, int pitch, int colw) {
     if constexpr (R < 9) {
-        epi_row<WM, CK, R>(acc, co, p, w, e, rs, pitch, colw);
-        epi_rows<WM, CK, R + 1>(acc, co, p, w, e, rs, pitch, colw);
+        epi_row<WM, CK, R>(acc, co, p, w, e, rs, rg, pitch, colw);
+        epi_rows<WM, CK, R + 1>(acc, co, p, w, e, rs, rg, pitch, colw);
     }
 }
 
@@ -864,7 +895,10 @@ __device__ __forceinline__ void epilogue(Acc& acc, const GemmParams& p, int m0, 
         Pend pend;
         epi_rows_bf16<WM>(acc, co, p, w, sa, pend, rs, pitch, n0 + 96 * w.wn);
     } else {
-        epi_rows<WM, CK>(acc, co, p, w, e, rs, pitch, n0 + 96 * w.wn);
+        // The gate's columns (fp32 [N]); beyond N its loads read zeros.
+        const __amdgpu_buffer_rsrc_t rg = whole_rsrc(CK == C_F32G ? (const void*)p.gate : (const void*)p.C,
+                                                     CK == C_F32G ? p.N * 4 : 0);
+        epi_rows<WM, CK>(acc, co, p, w, e, rs, rg, pitch, n0 + 96 * w.wn);
     }
 }
 
@@ -1177,7 +1211,7 @@ bool t272_ok(const GemmParams& p) {
     const int64_t la = kta ? p.K : p.lda, lb = ktb ? p.K : p.ldb;
     const bool a_ok = kta || (p.lda >= p.K && p.lda % 16 == 0 && ((uintptr_t)p.A & 15) == 0);
     const bool b_ok = ktb || (p.ldb >= p.K && p.ldb % 16 == 0 && ((uintptr_t)p.B & 15) == 0);
-    return a_ok && b_ok && (!p.b_rm || p.kt) && !p.gate && p.K % 512 == 0 &&
+    return a_ok && b_ok && (!p.b_rm || p.kt) && (!p.gate || p.c_kind == C_F32) && p.K % 512 == 0 &&
            (int64_t)p.M * la < ((int64_t)1 << 31) - (1 << 20) &&
            (int64_t)p.N * lb < ((int64_t)1 << 31) - (1 << 20) && (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) &&
            p.N % (16 / esz) == 0;
@@ -1209,6 +1243,7 @@ hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_
     const int tiles = t272_tile_count(p.M, p.N);
     const dim3 g3(tiles < num_cus ? tiles : num_cus), b3(256);
     if (p.c_kind == C_BF16) hipLaunchKernelGGL((i8_gemm_t272_kernel<C_BF16>), g3, b3, 0, stream, p);
+    else if (p.c_kind == C_F32 && p.gate) hipLaunchKernelGGL((i8_gemm_t272_kernel<C_F32G>), g3, b3, 0, stream, p);
     else if (p.c_kind == C_F32) hipLaunchKernelGGL((i8_gemm_t272_kernel<C_F32>), g3, b3, 0, stream, p);
     else hipLaunchKernelGGL((i8_gemm_t272_kernel<C_I32>), g3, b3, 0, stream, p);
     return hipGetLastError();

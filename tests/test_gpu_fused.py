@@ -52,7 +52,7 @@ def test_quant_rotate_mod_zero_modulation_is_plain(dev):
     assert torch.equal(q0, q1) and torch.equal(s0.view(torch.int32), s1.view(torch.int32))
 
 
-@pytest.mark.parametrize("kernel", ["auto", "persist256", "persist128", "auto:2stage"])
+@pytest.mark.parametrize("kernel", ["auto", "persist256", "persist128", "auto:2stage", "auto:t272"])
 @pytest.mark.parametrize("bias_kind", [None, "f32", "bf16"])
 @pytest.mark.parametrize("M,N,K", [(64, 256, 512), (300, 1000, 1024), (4352, 3072, 512),
                                    (777, 520, 768), (300, 1000, 256)])
@@ -66,6 +66,12 @@ def test_gemm_residual_matches_epilogue_then_addmul(dev, orc, monkeypatch, kerne
         monkeypatch.setenv("PHI_GEMM_PIPE", "0")
     else:
         monkeypatch.delenv("PHI_GEMM_PIPE", raising=False)
+    # t272: the 272 x 192 kernel's gated fp32 epilogue wherever it applies
+    # (K % 512 == 0); the other shapes keep the square plan.
+    if variant == "t272":
+        monkeypatch.setenv("PHI_GEMM_T272", "1")
+    else:
+        monkeypatch.delenv("PHI_GEMM_T272", raising=False)
     g = torch.Generator().manual_seed(M * 7 + N)
     A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
     B = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
@@ -89,8 +95,11 @@ def test_gemm_residual_matches_epilogue_then_addmul(dev, orc, monkeypatch, kerne
     assert np.array_equal(H.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
-def test_gemm_residual_strided_stream(dev, orc):
-    """A residual stream with a padded row pitch: the pad stays untouched."""
+@pytest.mark.parametrize("t272", ["0", "1"])
+def test_gemm_residual_strided_stream(dev, orc, monkeypatch, t272):
+    """A residual stream with a padded row pitch: the pad stays untouched
+    (on the square plan and on the 272 x 192 kernel)."""
+    monkeypatch.setenv("PHI_GEMM_T272", t272)
     M, N, K = 300, 264, 512
     g = torch.Generator().manual_seed(3)
     A = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
