@@ -371,6 +371,26 @@ phi_status phi_hip_i8_gemv_batched(phi_stream_t stream, const int8_t* q8, const 
                                    int n_items, int bias_dtype, int c_dtype, void* workspace,
                                    size_t ws_bytes);
 
+/* The W4A8 weight packed for the in-LDS expansion (no counterpart in the
+ * reference, whose loaders expand W4A8 to int8 at load time,
+ * core/models/model_common.cpp:589-748): once per weight, codes (the nibble
+ * layout, 16-byte aligned rows) and the table phi_hip_w4a8_prepare wrote are
+ * laid out in bands of 192 rows, one contiguous block per band and K-step
+ * (codes) or group (tables), so that the GEMM's loads read whole blocks
+ * instead of gathering 32 code rows each.  phi_hip_w4a8_banded_bytes gives
+ * the buffer's size (0 for a shape it cannot hold).
+ * phi_hip_w4a8_linear_banded is phi_hip_w4a8_linear on it, with no
+ * workspace: the same C and s8 bit for bit; q8 (M x K bytes) is written
+ * K-tiled.  Needs K % 1024 == 0, K <= 16384, group a power of two >= 64, and
+ * the phi_hip_q8_linear_kt rules for q8 and C. */
+size_t phi_hip_w4a8_banded_bytes(int64_t rows, int64_t k, int64_t group);
+phi_status phi_hip_w4a8_pack_banded(phi_stream_t stream, const uint8_t* codes, int64_t codes_row_bytes,
+                                    const int8_t* lut, int64_t rows, int64_t k, int64_t group, void* banded);
+phi_status phi_hip_w4a8_linear_banded(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M,
+                                      int64_t K, const void* banded, int64_t group, const float* s_w, const void* bias,
+                                      int bias_dtype, int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8,
+                                      float* s8, int round_mode);
+
 /* Workspace with which phi_hip_w4a8_linear expands the codes once per call
  * (N*K bytes; 0 when the shape keeps the in-register expansion).  No reference
  * counterpart: the reference expands at load time (dispatch_w4a8_expand). */

@@ -956,6 +956,80 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     return check_hip(phi_dev::launch_w4a8_gemm((hipStream_t)stream, p, gemm_cfg_for(M, N)), who);
 }
 
+size_t phi_hip_w4a8_banded_bytes(int64_t rows, int64_t k, int64_t group) {
+    if (rows <= 0 || rows > INT32_MAX || k <= 0 || k > INT32_MAX) return 0;
+    return (size_t)phi_dev::w4_banded_bytes(rows, k, group);
+}
+
+phi_status phi_hip_w4a8_pack_banded(phi_stream_t stream, const uint8_t* codes, int64_t codes_row_bytes,
+                                    const int8_t* lut, int64_t rows, int64_t k, int64_t group, void* banded) {
+    static const char* who = "w4a8_pack_banded";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!codes || !lut || !banded) return fail(PHI_ERR_ARG, "%s: null operand", who);
+    if (rows <= 0 || k <= 0 || rows > INT32_MAX || k > INT32_MAX) return fail(PHI_ERR_SHAPE, "%s: empty or oversized weight", who);
+    if (k % 64 != 0 || group <= 0 || k % group != 0)
+        return fail(PHI_ERR_SHAPE, "%s: K=%lld must be a multiple of 64 and of group=%lld", who, (long long)k, (long long)group);
+    if (codes_row_bytes < k / 2) return fail(PHI_ERR_SHAPE, "%s: a %lld-column nibble row needs %lld bytes", who, (long long)k, (long long)(k / 2));
+    if (!aligned(codes, 16) || codes_row_bytes % 16 != 0 || !aligned(lut, 16) || !aligned(banded, 16))
+        return fail(PHI_ERR_ALIGN, "%s: codes rows, lut and the packed buffer must be 16-byte aligned", who);
+    if (phi_hip_w4a8_banded_bytes(rows, k, group) == 0 ||
+        phi_hip_w4a8_banded_bytes(rows, k, group) >= ((size_t)1 << 31))
+        return fail(PHI_ERR_SHAPE, "%s: the packed weight must stay below 2 GiB", who);
+    return check_hip(phi_dev::launch_w4_pack_banded((hipStream_t)stream, codes, codes_row_bytes, lut, (int)rows, (int)k,
+                                                    (int)(k / group), (uint8_t*)banded),
+                     who);
+}
+
+phi_status phi_hip_w4a8_linear_banded(phi_stream_t stream, const void* x, int x_dtype, int64_t ldx, int64_t M,
+                                      int64_t K, const void* banded, int64_t group, const float* s_w, const void* bias,
+                                      int bias_dtype, int64_t N, void* C, int c_dtype, int64_t ldc, int8_t* q8,
+                                      float* s8, int round_mode) {
+    static const char* who = "w4a8_linear_banded";
+    if (g_lost) return fail(PHI_ERR_DEVICE_LOST, "%s: device was lost earlier", who);
+    if (!q8 || !s8) return fail(PHI_ERR_ARG, "%s: the int8 path needs activation scratch", who);
+    if (!banded || !s_w) return fail(PHI_ERR_ARG, "%s: missing packed weight or row scales", who);
+    phi_status st = check_gemm(who, q8, K, banded, K / 2, M, N, K, s8, s_w, C, c_dtype, ldc, true);
+    if (st != PHI_OK) return st;
+    if (group <= 0 || group % 64 != 0 || K % group != 0 || (group & (group - 1)) != 0)
+        return fail(PHI_ERR_SHAPE, "%s: group=%lld must be a power of two, a multiple of 64 and divide K", who, (long long)group);
+    if (K % 1024 != 0 || K > 16384)
+        return fail(PHI_ERR_UNSUPPORTED, "%s: needs K %% 1024 == 0 and K <= 16384 (K=%lld)", who, (long long)K);
+    if (!aligned(q8, 16) || !aligned(banded, 16))
+        return fail(PHI_ERR_ALIGN, "%s: q8 and the packed weight must be 16-byte aligned", who);
+    if (!persist_ok(C, c_dtype, N, K, K, K, ldc))
+        return fail(PHI_ERR_UNSUPPORTED, "%s: needs whole 16-byte output pieces on 16-byte aligned C rows", who);
+    const int bk = bias_kind_of(bias, bias_dtype, &st);
+    if (st != PHI_OK) return fail(st, "%s: bias dtype must be f32 or bf16", who);
+    phi_dev::GemmParams q{};
+    q.A = q8;
+    q.B = (const int8_t*)banded;
+    q.sA = s8;
+    q.sB = s_w;
+    q.bias = bias;
+    q.C = C;
+    q.lda = K;
+    q.ldb = K / 2;
+    q.ldc = ldc;
+    q.M = (int)M;
+    q.N = (int)N;
+    q.K = (int)K;
+    q.bias_kind = bk;
+    q.c_kind = c_kind_of(c_dtype);
+    q.group_m = 4;
+    q.lut_groups = K / group;
+    q.lut = (const int8_t*)banded + (((N + 191) / 192) * (K / 64) * (192 * 32));
+    int gs = 0;
+    while ((1ll << gs) < group) gs++;
+    q.group_shift = gs;
+    q.kt = 1;
+    q.w4_banded = 1;
+    set_vec_flags(q, c_dtype, ldc);
+    if (!phi_dev::t272w4_ok(q)) return fail(PHI_ERR_UNSUPPORTED, "%s: shape outside the in-LDS kernel's limits", who);
+    st = phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode);
+    if (st != PHI_OK) return st;
+    return check_hip(phi_dev::launch_i8_gemm_t272w4((hipStream_t)stream, q, num_cus()), who);
+}
+
 size_t phi_hip_w4a8_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group) {
     // The expand-then-W8A8 path pays off once enough rows share each weight.
     if (M < kW4ExpandMinRows || N <= 0 || K <= 0 || K % 256 != 0 || group <= 0 || group % 128 != 0) return 0;

@@ -41,6 +41,10 @@ struct GemmParams {
     // With kt, the 272 x 192 kernel only: B stays row-major (pitch ldb) while
     // A is K-tiled.  No other kernel reads it; it must be 0 for them.
     int b_rm;
+    // The in-LDS W4 kernel only: B and lut point into one band-packed buffer
+    // (w4_banded_bytes, the codes region then the tables region) instead of
+    // the checkpoint's code rows and the [N, K / group, 16] table.
+    int w4_banded;
 };
 
 // The K-tiled operand layout: rows in strips of 256 (the last strip may be
@@ -84,6 +88,14 @@ hipError_t launch_i8_gemm_t272(hipStream_t stream, const GemmParams& p, int num_
 // The same tiles with B as W4 codes (p.B [N, ldb], p.lut, p.group_shift)
 // expanded in LDS; K-tiled A, K % 1024 == 0 (t272w4_ok).
 bool t272w4_ok(const GemmParams& p);
+// Bytes of the band-packed W4 operand of an N x K weight (0 for a shape it
+// cannot hold): bands of 192 rows, a 6144-byte code block a band and K-step,
+// then a 3072-byte table block a band and group.
+int64_t w4_banded_bytes(int64_t N, int64_t K, int64_t group);
+// Packs codes [N, crb] (nibbles) and the prepared table lut [N, K / group, 16]
+// into that layout (16-byte aligned sources, crb % 16 == 0).
+hipError_t launch_w4_pack_banded(hipStream_t stream, const uint8_t* codes, int64_t crb, const int8_t* lut, int N,
+                                 int K, int groups, uint8_t* out);
 hipError_t launch_i8_gemm_t272w4(hipStream_t stream, const GemmParams& p, int num_cus);
 // The W4 operand of p (codes, lut, group_shift, N, K) expanded to int8 [N, K] in out,
 // row-major or (kt, K % 64 == 0) in the K-tiled layout.

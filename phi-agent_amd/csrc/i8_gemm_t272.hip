@@ -479,19 +479,56 @@ constexpr int NC = 3, NTB = 3, NLD4 = NA + NC + NTB;  // loads a wave issues per
 constexpr int VW4 = 2 * NLD4;
 
 // The code and table cursors: this lane's source byte of each of the wave's
-// code and table pieces at K-step 0 (codes advance 32 bytes a K-step, tables
-// 16 bytes a group, both through the scalar offset), and the cursors' K-step.
+// code and table pieces at K-step 0, the cursors' K-step, and the strides of
+// the scalar offset: codes advance cstep bytes a K-step (32 on the
+// checkpoint's rows, 6144 in the band layout), tables lstep bytes a group (16
+// or 3072).
 struct W4c {
     __amdgpu_buffer_rsrc_t rC, rL;
     int offC[NC], offL[NTB];
-    int kc;
+    int kc, cstep, lstep;
 };
+
+// The band layout (p.w4_banded, phi_hip_w4a8_pack_banded): B rows in bands of
+// TN = 192; band b's 32 code bytes of every row for K-step s are one block of
+// 6144 bytes at (b KT + s) 6144, row r at 32 r; after all code blocks, band
+// b's tables of group g are one block of 3072 bytes at (b G + g) 3072, row r
+// at 16 r.  Rows past N are zero.  A block is a stage's code or table area
+// byte for byte, so every DMA a wave issues reads contiguous bytes; on the
+// checkpoint's rows each one gathers 32 rows 3 KB apart (at config 2 that
+// costs about 22 us of a 151 us step, measured with contiguous sources).
+__device__ __forceinline__ int64_t w4_banded_code_bytes(int N, int K) {
+    return (int64_t)((N + TN - 1) / TN) * (K / PK) * (TN * 32);
+}
 
 // Code and table cursors onto the tile with B rows n0 .., K-step 0; valid =
 // false: onto nothing (every source past the resources).
 __device__ __forceinline__ void w4_cursor_to(W4c& c, const Tw& w, const GemmParams& p, int n0, bool valid) {
+    c.kc = 0;
+    if (p.w4_banded) {
+        const int KT = p.K / PK, G = (int)p.lut_groups, bands = (p.N + TN - 1) / TN;
+        const int b = valid ? n0 / TN : bands;  // past the last band: past both resources
+        const int cb = b * KT * (TN * 32), lb = b * G * (TN * 16);
+        c.offC[0] = cb + 1024 * w.wave + 16 * w.lane;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int qi = 2 * w.wave + i;
+            c.offC[1 + i] = cb + 4096 + 1024 * (qi >> 2) + 256 * (qi & 3) + 4 * w.lane;
+        }
+#pragma unroll
+        for (int i = 0; i < NTB; i++) c.offL[i] = lb + 256 * (3 * w.wave + i) + 4 * w.lane;
+        c.cstep = TN * 32;
+        c.lstep = TN * 16;
+#pragma unroll
+        for (int i = 0; i < NC; i++) asm volatile("" : "+v"(c.offC[i]));
+#pragma unroll
+        for (int i = 0; i < NTB; i++) asm volatile("" : "+v"(c.offL[i]));
+        return;
+    }
     const int N = p.N, ldb = (int)p.ldb, g16 = (int)p.lut_groups * 16;
     const int base = valid ? n0 : N;
+    c.cstep = 32;
+    c.lstep = 16;
     {
         const int n = base + 32 * w.wave + (w.lane >> 1);  // whole piece w: rows 32 w .., 16 bytes a lane
         c.offC[0] = n < N ? n * ldb + 16 * (w.lane & 1) : N * ldb;
@@ -511,7 +548,6 @@ __device__ __forceinline__ void w4_cursor_to(W4c& c, const Tw& w, const GemmPara
     for (int i = 0; i < NC; i++) asm volatile("" : "+v"(c.offC[i]));
 #pragma unroll
     for (int i = 0; i < NTB; i++) asm volatile("" : "+v"(c.offL[i]));
-    c.kc = 0;
 }
 
 // W4 stage bases (opaque, computed in the K-step like the int8 ones).
@@ -531,14 +567,14 @@ template <int CS, int J>
 __device__ __forceinline__ void w4_load1(const W4c& c, const Tw& w, const GemmParams& p) {
     if constexpr (J == 0) {
         int8_t* d = opaque_lds(w.lds + W4_C + CS * W4_CS + 1024 * w.wave);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rC, (lptr_t)d, 16, c.offC[0], 32 * c.kc, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rC, (lptr_t)d, 16, c.offC[0], c.cstep * c.kc, 0, 0);
     } else if constexpr (J < 3) {
         const int qi = 2 * w.wave + (J - 1);
         int8_t* d = opaque_lds(w.lds + W4_C + CS * W4_CS + 4096 + 1024 * (qi >> 2) + 256 * (qi & 3));
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rC, (lptr_t)d, 4, c.offC[J], 32 * c.kc, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rC, (lptr_t)d, 4, c.offC[J], c.cstep * c.kc, 0, 0);
     } else {
         int8_t* d = opaque_lds(w.lds + W4_L + CS * W4_LS + 256 * (3 * w.wave + (J - 3)));
-        const int goff = ((c.kc * PK) >> p.group_shift) * 16;
+        const int goff = ((c.kc * PK) >> p.group_shift) * c.lstep;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(c.rL, (lptr_t)d, 4, c.offL[J - 3], goff, 0, 0);
     }
 }
@@ -1041,8 +1077,14 @@ __device__ __forceinline__ void t272w4_tiles(const GemmParams& p, int8_t* lds, i
     w.le = eall;
     w.lc = cbuf + wave * SBYTES;
     w.rA = whole_rsrc(p.A, p.M * p.K);
-    c.rC = whole_rsrc(p.B, p.N * (int)p.ldb);
-    c.rL = whole_rsrc(p.lut, p.N * (int)p.lut_groups * 16);
+    if (p.w4_banded) {
+        const int64_t cb = w4_banded_code_bytes(p.N, p.K);
+        c.rC = whole_rsrc(p.B, (int)cb);
+        c.rL = whole_rsrc(p.lut, (int)((p.N + TN - 1) / TN * p.lut_groups * (TN * 16)));
+    } else {
+        c.rC = whole_rsrc(p.B, p.N * (int)p.ldb);
+        c.rL = whole_rsrc(p.lut, p.N * (int)p.lut_groups * 16);
+    }
     // Prologue: the epilogue operands; codes and tables of K-steps 0-3 and A
     // of K-steps 0-3 (in the order the K-steps would issue them); the
     // expansion of K-steps 0 and 1 once their codes have landed; then codes
@@ -1219,13 +1261,25 @@ bool t272_ok(const GemmParams& p) {
 
 bool t272w4_ok(const GemmParams& p) {
     const int64_t esz = p.c_kind == C_BF16 ? 2 : 4;
+    // The band layout: both regions' offsets within 31 bits, the tables
+    // 16-byte aligned.  The checkpoint's rows: 16-byte code rows.
+    const int64_t bands = (p.N + TN - 1) / TN;
+    const bool src_ok = p.w4_banded ? bands * (p.K / 2) * TN + bands * p.lut_groups * TN * 16 < ((int64_t)1 << 31) &&
+                                          ((uintptr_t)p.lut & 15) == 0
+                                    : p.ldb >= p.K / 2 && p.ldb % 16 == 0 &&
+                                          ((int64_t)p.N + 512) * p.ldb < ((int64_t)1 << 31) &&
+                                          ((int64_t)p.N + 512) * p.lut_groups * 16 < ((int64_t)1 << 31);
     return p.kt && !p.gate && !p.w4_signed && p.lut && p.K % 1024 == 0 && p.group_shift >= 6 &&
            p.group_shift < 31 && (1ll << p.group_shift) <= p.K && p.lut_groups == (p.K >> p.group_shift) &&
-           p.ldb >= p.K / 2 && p.ldb % 16 == 0 && ((uintptr_t)p.B & 15) == 0 &&
+           src_ok && ((uintptr_t)p.B & 15) == 0 &&
            (int64_t)p.M * p.K < ((int64_t)1 << 31) - (1 << 20) &&
-           ((int64_t)p.N + 512) * p.ldb < ((int64_t)1 << 31) &&
-           ((int64_t)p.N + 512) * p.lut_groups * 16 < ((int64_t)1 << 31) &&
            (int64_t)TM * p.ldc * esz < ((int64_t)1 << 31) && p.N % (16 / esz) == 0;
+}
+
+int64_t w4_banded_bytes(int64_t N, int64_t K, int64_t group) {
+    if (N <= 0 || K <= 0 || K % PK != 0 || group <= 0 || K % group != 0) return 0;
+    const int64_t bands = (N + TN - 1) / TN;
+    return bands * (K / PK) * (TN * 32) + bands * (K / group) * (TN * 16);
 }
 
 hipError_t launch_i8_gemm_t272w4(hipStream_t stream, const GemmParams& p, int num_cus) {

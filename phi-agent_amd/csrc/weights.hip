@@ -19,6 +19,10 @@
 //                 core/models/lora.cpp:182-201)
 //   pack_k_tiled  an int8 row-major weight into the K-tiled operand layout of
 //                 the persistent pipeline (k_tiled_offset); a pure re-layout
+//   pack_banded   a W4 weight's codes and prepared tables into the band layout
+//                 the 272 x 192 kernel's in-LDS expansion reads (bands of 192
+//                 rows, one contiguous block a band and K-step or group); a
+//                 pure re-layout
 //
 // The rotate + quantise that turns the result into int8 is quant_rotate, the
 // same kernel the activations take: the reference's weight and activation
@@ -150,6 +154,32 @@ __global__ __launch_bounds__(256) void pack_k_tiled_kernel(const int8_t* __restr
     }
 }
 
+// One 16-byte chunk of the band-packed W4 operand a thread (w4_banded_bytes):
+// the code blocks (band b, K-step s: rows 192 b .. + 191, 32 bytes each),
+// then the table blocks (band b, group g: 16 bytes a row); rows past N zero.
+__global__ __launch_bounds__(256) void pack_banded_kernel(const uint8_t* __restrict__ codes, int64_t crb,
+                                                          const int8_t* __restrict__ lut, int N, int K, int groups,
+                                                          uint8_t* __restrict__ out, int64_t code_bytes,
+                                                          int64_t total) {
+    constexpr int TB = 192;
+    const int KT = K / 64;
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16; i < total; i += (int64_t)gridDim.x * 256 * 16) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (i < code_bytes) {
+            const int64_t blk = i / (TB * 32);
+            const int within = (int)(i - blk * (TB * 32)), b = (int)(blk / KT), st = (int)(blk - (int64_t)b * KT);
+            const int64_t n = (int64_t)b * TB + within / 32;
+            if (n < N) v = *(const uint4*)(codes + n * crb + st * 32 + (within & 31));
+        } else {
+            const int64_t t = i - code_bytes, blk = t / (TB * 16);
+            const int within = (int)(t - blk * (TB * 16)), b = (int)(blk / groups), g = (int)(blk - (int64_t)b * groups);
+            const int64_t n = (int64_t)b * TB + within / 16;
+            if (n < N) v = *(const uint4*)(lut + (n * groups + g) * 16);
+        }
+        *(uint4*)(out + i) = v;
+    }
+}
+
 static unsigned grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return (unsigned)(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -178,6 +208,15 @@ hipError_t launch_lora_fold(hipStream_t stream, float* w, int64_t ldw, int64_t r
                             const float* B, int64_t rank, float scale) {
     hipLaunchKernelGGL(lora_fold_kernel, dim3(grid_for(rows * k)), dim3(256), 0, stream, w, ldw, rows, k, A, B, rank,
                        scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_w4_pack_banded(hipStream_t stream, const uint8_t* codes, int64_t crb, const int8_t* lut, int N,
+                                 int K, int groups, uint8_t* out) {
+    const int64_t bands = (N + 191) / 192, code_bytes = bands * (K / 64) * (192 * 32);
+    const int64_t total = code_bytes + bands * groups * (192 * 16);
+    hipLaunchKernelGGL(pack_banded_kernel, dim3(grid_for(total / 16)), dim3(256), 0, stream, codes, crb, lut, N, K,
+                       groups, out, code_bytes, total);
     return hipGetLastError();
 }
 

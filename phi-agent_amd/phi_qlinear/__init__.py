@@ -80,7 +80,8 @@ EXPORTS = ["phi_hip_last_error", "phi_hip_abi_version", "phi_hip_quant_rotate", 
            "phi_hip_quant_rotate_kt", "phi_hip_big_tile_rows",
            "phi_hip_quant_rotate_mod_kt", "phi_hip_quant_rotate_act_kt", "phi_hip_i8_gemm_residual_kt",
            "phi_hip_dequant_fp4_rows", "phi_hip_gemm_plan_set", "phi_hip_gemm_plan_get", "phi_hip_gemm_plan_count",
-           "phi_hip_gemm_plan_clear"]
+           "phi_hip_gemm_plan_clear", "phi_hip_w4a8_banded_bytes", "phi_hip_w4a8_pack_banded",
+           "phi_hip_w4a8_linear_banded"]
 
 _lib = None
 
@@ -145,6 +146,10 @@ def load() -> ctypes.CDLL:
     L.phi_hip_q8_linear_kt.argtypes = [P, P, I, I64, I64, I64, P, P, I, P, I, I64, P, I, I64, P, P, I]
     L.phi_hip_q8_linear_kq.argtypes = [P, P, I, I64, I64, I64, P, I64, P, I, P, I, I64, P, I, I64, P, P,
                                        I, P, SZ]
+    L.phi_hip_w4a8_banded_bytes.argtypes = [I64, I64, I64]
+    L.phi_hip_w4a8_banded_bytes.restype = SZ
+    L.phi_hip_w4a8_pack_banded.argtypes = [P, P, I64, P, I64, I64, I64, P]
+    L.phi_hip_w4a8_linear_banded.argtypes = [P, P, I, I64, I64, I64, P, I64, P, P, I, I64, P, I, I64, P, P, I]
     for name in EXPORTS:
         f = getattr(L, name)
         if f.restype is None:
@@ -398,6 +403,40 @@ def w4a8_linear(x, codes, lut, s_w, *, group, bias=None, out_dtype=torch.bfloat1
                                       _ptr(bias), _dt(bias) if bias is not None else F32, N,
                                       _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8),
                                       round_mode, *_ws(workspace)))
+    return C
+
+
+def w4a8_pack_banded(codes: torch.Tensor, lut: torch.Tensor, *, k: int, group: int,
+                     stream=None) -> torch.Tensor:
+    """The W4A8 weight (codes [N, >= k/2] nibbles, lut from w4a8_prepare)
+    packed in bands of 192 rows for the in-LDS expansion
+    (phi_hip_w4a8_pack_banded): a uint8 buffer of phi_hip_w4a8_banded_bytes."""
+    _require_device(codes, lut)
+    N = codes.shape[0]
+    n = load().phi_hip_w4a8_banded_bytes(N, k, group)
+    if not n:
+        raise ValueError(f"no band layout for a {N} x {k} weight with group {group}")
+    out = torch.empty(n, dtype=torch.uint8, device=codes.device)
+    _check(load().phi_hip_w4a8_pack_banded(_stream(stream), _ptr(codes), codes.stride(0), _ptr(lut), N, k, group,
+                                           _ptr(out)))
+    return out
+
+
+def w4a8_linear_banded(x, banded, s_w, *, N: int, group: int, bias=None, out_dtype=torch.bfloat16, q8=None,
+                       s8=None, C=None, round_mode=ROUND_HALF_AWAY, stream=None):
+    """w4a8_linear on a band-packed weight (phi_hip_w4a8_linear_banded): the
+    codes expanded in LDS, no workspace; q8 (M * K bytes) is written K-tiled."""
+    _require_device(x, banded, s_w, bias, q8, s8, C)
+    M, K = x.shape
+    if q8 is None:
+        q8 = torch.empty((M * K,), dtype=torch.int8, device=x.device)
+    if s8 is None:
+        s8 = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if C is None:
+        C = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    _check(load().phi_hip_w4a8_linear_banded(_stream(stream), _ptr(x), _dt(x), x.stride(0), M, K, _ptr(banded),
+                                             group, _ptr(s_w), _ptr(bias), _dt(bias) if bias is not None else F32,
+                                             N, _ptr(C), _dt(C), C.stride(0), _ptr(q8), _ptr(s8), round_mode))
     return C
 
 

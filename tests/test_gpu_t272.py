@@ -204,6 +204,44 @@ def test_w4_in_lds_equals_expand_then_w8a8(dev, monkeypatch, M, N, K, group, wit
     assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("N,K,group,pad", [(200, 1024, 128, 0), (384, 2048, 64, 16), (5, 1024, 1024, 32)])
+def test_w4_pack_banded_is_the_documented_layout(dev, N, K, group, pad):
+    """phi_hip_w4a8_pack_banded against the layout written out with numpy:
+    code blocks (band, K-step) of 192 rows x 32 bytes, then table blocks
+    (band, group) of 192 rows x 16 bytes, rows past N zero."""
+    g = torch.Generator().manual_seed(N + K)
+    codes = torch.randint(0, 256, (N, K // 2 + pad), generator=g, dtype=torch.uint8)
+    lut = torch.randint(-127, 128, (N, K // group, 16), generator=g, dtype=torch.int8)
+    got = Q.w4a8_pack_banded(codes.to(dev), lut.to(dev), k=K, group=group).cpu().numpy()
+    bands, KT, G = (N + 191) // 192, K // 64, K // group
+    c = np.zeros((bands * 192, K // 2), np.uint8)
+    c[:N] = codes.numpy()[:, :K // 2]
+    t = np.zeros((bands * 192, G, 16), np.int8)
+    t[:N] = lut.numpy()
+    want_c = c.reshape(bands, 192, KT, 32).transpose(0, 2, 1, 3).reshape(-1)
+    want_t = t.reshape(bands, 192, G, 16).transpose(0, 2, 1, 3).reshape(-1).view(np.uint8)
+    assert got.size == Q.load().phi_hip_w4a8_banded_bytes(N, K, group)
+    assert np.array_equal(got, np.concatenate([want_c, want_t]))
+
+
+@pytest.mark.parametrize("M,N,K,group", W4_SHAPES + [(4352, 9216, 3072, 128)])
+def test_w4_banded_equals_expand_then_w8a8(dev, monkeypatch, M, N, K, group):
+    """The band-packed weight on the in-LDS kernel against expand-then-W8A8,
+    bit for bit (config 2's shape included)."""
+    codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=M + 2 * N + K)
+    cd, rd, sd, kd = codes.to(dev), s_rel.to(dev), sch.to(dev), corr.to(dev)
+    x = synth.activations(M, K, seed=M + 1, device=dev)
+    b = synth.bias(N, seed=4, device=dev)
+    q, s = Q.w4a8_expand(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    lut, s2 = Q.w4a8_prepare(cd, rd, Q.F16, sd, k=K, group=group, correction=kd)
+    banded = Q.w4a8_pack_banded(cd, lut, k=K, group=group)
+    y = Q.w4a8_linear_banded(x, banded, s2, N=N, group=group, bias=b)
+    monkeypatch.setenv("PHI_GEMM_T272", "0")
+    y_ref = Q.q8_linear(x, q, s, b)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("out", ["bf16", "f32", "i32"])
 @pytest.mark.parametrize("bias_kind", ["none", "f32", "bf16"])
 def test_w4_in_lds_outputs_and_padded_code_rows(dev, monkeypatch, out, bias_kind):
