@@ -355,6 +355,18 @@ __device__ __forceinline__ void mfma_first(v4i& acc, const v4i& b, const v4i& a)
 // accumulators: 18, more than the four-pass instruction's requirement.
 __device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory"); }
 
+// Block of the wave's full block rows that MFMA q of a K-step updates.  The
+// rows run in alternating column order, and the half row sits at the end
+// (WM 0) or the start (WM 1) in the order that joins it: every change of
+// A fragment keeps the B fragment of the MFMA before it, so the operands
+// that switch from one MFMA to the next are fewer (the MFMA array's draw,
+// and with it the board clock, follows how many operand bits toggle).
+template <int WM, int Q>
+struct Blk {
+    static constexpr int q = WM == 0 ? Q : Q - 3, r = q / 6;
+    static constexpr int c = ((r + WM) & 1) ? 5 - q % 6 : q % 6;
+};
+
 template <int WM, int Q, bool Z>
 __device__ __forceinline__ void mma1t(const Frag& f, Acc& acc) {
     if constexpr (WM == 0 && Q >= 48) {
@@ -365,7 +377,7 @@ __device__ __forceinline__ void mma1t(const Frag& f, Acc& acc) {
         if constexpr (Z) mfma_first(acc.s[Q], f.b[3 + Q], f.a[0]);
         else mfma_tied(acc.s[Q], f.b[3 + Q], f.a[0]);
     } else {
-        constexpr int q = WM == 0 ? Q : Q - 3, r = q / 6, c = q % 6;
+        constexpr int r = Blk<WM, Q>::r, c = Blk<WM, Q>::c;
         if constexpr (Z) mfma_first(acc.f[r][c], f.b[c], f.a[r + WM]);
         else mfma_tied(acc.f[r][c], f.b[c], f.a[r + WM]);
     }
@@ -379,7 +391,7 @@ __device__ __forceinline__ void mma1(const Frag& f, Acc& acc) {
     } else if constexpr (WM == 1 && Q < 3) {
         acc.s[Q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[3 + Q], f.a[0], Z ? v4i{} : acc.s[Q], 0, 0, 0);
     } else {
-        constexpr int q = WM == 0 ? Q : Q - 3, r = q / 6, c = q % 6;
+        constexpr int r = Blk<WM, Q>::r, c = Blk<WM, Q>::c;
         acc.f[r][c] =
             __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[c], f.a[r + WM], Z ? v4i{} : acc.f[r][c], 0, 0, 0);
     }
@@ -909,18 +921,27 @@ __device__ __forceinline__ void epilogue(Acc& acc, const GemmParams& p, int m0, 
     const __amdgpu_buffer_rsrc_t rs = whole_rsrc((int8_t*)p.C + (int64_t)m0 * pitch, min(TM, p.M - m0) * pitch);
     ColOps co;
     if constexpr (CK != C_I32) {
-        const bool bf = p.bias_kind == BIAS_BF16, sbs = p.sb_scalar != 0;
+        // The formats are wave-uniform: a scalar branch runs one form (the
+        // bias as bf16 pairs or fp32 words, the column scale as one scalar or
+        // a row of columns), without converting and selecting both.
         const int lg = w.lane >> 4;
+        if (p.bias_kind == BIAS_BF16) {
 #pragma unroll
-        for (int c = 0; c < 6; c++) {
-            const int col = 96 * w.wn + 16 * c + 4 * lg;
-            const v4f fz = *(const v4f*)(e + E_BZ + col * 4);
-            const u32x2 hz = *(const u32x2*)(e + E_BZ + col * 2);
-            const v4f hb = {bf16_to_f32(hz[0] & 0xffffu), bf16_to_f32(hz[0] >> 16), bf16_to_f32(hz[1] & 0xffffu),
-                            bf16_to_f32(hz[1] >> 16)};
-            co.bz[c] = bf ? hb : fz;
-            const v4f sv = *(const v4f*)(e + E_SB + col * 4);
-            co.sb[c] = sbs ? v4f{s0, s0, s0, s0} : sv;
+            for (int c = 0; c < 6; c++) {
+                const u32x2 hz = *(const u32x2*)(e + E_BZ + (96 * w.wn + 16 * c + 4 * lg) * 2);
+                co.bz[c] = v4f{__uint_as_float(hz[0] << 16), __uint_as_float(hz[0] & 0xffff0000u),
+                               __uint_as_float(hz[1] << 16), __uint_as_float(hz[1] & 0xffff0000u)};
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 6; c++) co.bz[c] = *(const v4f*)(e + E_BZ + (96 * w.wn + 16 * c + 4 * lg) * 4);
+        }
+        if (p.sb_scalar) {
+#pragma unroll
+            for (int c = 0; c < 6; c++) co.sb[c] = v4f{s0, s0, s0, s0};
+        } else {
+#pragma unroll
+            for (int c = 0; c < 6; c++) co.sb[c] = *(const v4f*)(e + E_SB + (96 * w.wn + 16 * c + 4 * lg) * 4);
         }
     }
     if constexpr (CK == C_BF16) {
