@@ -466,8 +466,7 @@ def bench_w4a4(cfg, steps, warmup):
                          "unit": "TFLOP/s", "frac": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
                          "traffic": None},
             "extra": {"in_register_us": ms_reg * 1e3,
-                      "expand_once_us": None if ms_ws is None else ms_ws * 1e3,
-                      "in_lds_banded_us": None if ms_band is None else ms_band * 1e3}}
+                      "expand_once_us": None if ms_ws is None else ms_ws * 1e3}}
 
 
 def bench_lora(cfg, steps, warmup):
