@@ -289,6 +289,9 @@ __global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restr
             acc[i][j] = v;
         }
     }
+    // R % 4 == 0 with 16-byte aligned h and B: a lane's four ranks of a row
+    // are one 16-byte load (r < R then covers r + 3).
+    const bool r4 = (R & 3) == 0 && ((uintptr_t)h & 15) == 0 && ((uintptr_t)B & 15) == 0;
     for (int r0 = 0; r0 < R; r0 += RA_BR) {
         // 128 rows x 32 ranks of h and of B: lane t loads 4 consecutive ranks of
         // rows t/8 + 32 s and stores them rank-major.
@@ -296,6 +299,14 @@ __global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restr
         for (int s = 0; s < 4; s++) {
             const int row = (tid >> 3) + 32 * s, rr = (tid & 7) * 4, r = r0 + rr;
             const int m = m0 + row, n = n0 + row;
+            if (r4) {
+                const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const float4 hv = (m < M && r < R) ? *(const float4*)&h[(int64_t)m * R + r] : z;
+                const float4 bv = (n < N && r < R) ? *(const float4*)&B[(int64_t)n * R + r] : z;
+                sh[rr][row] = hv.x, sh[rr + 1][row] = hv.y, sh[rr + 2][row] = hv.z, sh[rr + 3][row] = hv.w;
+                sb[rr][row] = bv.x, sb[rr + 1][row] = bv.y, sb[rr + 2][row] = bv.z, sb[rr + 3][row] = bv.w;
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 sh[rr + i][row] = (m < M && r + i < R) ? h[(int64_t)m * R + r + i] : 0.0f;
