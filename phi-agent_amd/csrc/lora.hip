@@ -240,9 +240,12 @@ __device__ __forceinline__ void rank_step(const float* __restrict__ hr, const fl
 }
 
 // VEC: C's rows are 16-byte (fp32) or 8-byte (bf16) aligned and N % 4 == 0,
-// so each lane moves its four adjacent columns as one access.
+// so each lane moves its four adjacent columns as one access.  Four waves a
+// SIMD (at most 128 VGPRs; the LDS holds four blocks a CU): against three at
+// the 134 the compiler picks unasked, 123.1 -> 110.9 us at 4352 x 12288 x 64,
+// with 32 bytes of spill a lane outside the rank loop.
 template <bool CB, bool VEC>
-__global__ __launch_bounds__(256) void lora_rank_add_kernel(const float* __restrict__ h, const float* __restrict__ B,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void lora_rank_add_kernel(const float* __restrict__ h, const float* __restrict__ B,
                                                             void* __restrict__ C, int64_t ldc, int M, int N, int R) {
     __shared__ __align__(16) float sh[RA_BR][RA_P];
     __shared__ __align__(16) float sb[RA_BR][RA_P];
