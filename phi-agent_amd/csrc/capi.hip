@@ -903,9 +903,6 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
                         aligned(codes, 16) && codes_row_bytes % 16 == 0 && persist_ok(C, c_dtype, N, K, K, K, ldc);
     const char* ekt = getenv("PHI_GEMM_KT");
     const bool kt = expand && K <= 16384 && aligned(q8, 16) && !(ekt && ekt[0] == '0');
-    st = kt ? phi_hip_quant_rotate_kt(stream, x, x_dtype, M, K, ldx, q8, s8, 127.0f, round_mode)
-            : phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
-    if (st != PHI_OK) return st;
     phi_dev::GemmParams p{};
     p.A = q8;
     p.B = (const int8_t*)codes;
@@ -928,9 +925,31 @@ phi_status phi_hip_w4a8_linear(phi_stream_t stream, const void* x, int x_dtype, 
     int sh = 0;
     while ((1ll << sh) < group) sh++;
     p.group_shift = sh;
+    // With K-tiled activations the expansion runs as extra blocks of the
+    // prologue's launch, beside the rotation (PHI_W4_FUSE=0: two launches).
+    const bool fuse = kt && phi_dev::w4_expand_ok(p, (const int8_t*)workspace, true) &&
+                      phi_dev::env_switch("PHI_W4_FUSE", 1, 0, 1);
+    phi_dev::QrPre pre{};
+    if (fuse) {
+        pre.ex.on = 1;
+        pre.ex.codes = codes;
+        pre.ex.ldb = codes_row_bytes;
+        pre.ex.lut = lut;
+        pre.ex.lut_groups = p.lut_groups;
+        pre.ex.group_shift = p.group_shift;
+        pre.ex.kt = 1;
+        pre.ex.N = N;
+        pre.ex.K = K;
+        pre.ex.out = (int8_t*)workspace;
+    }
+    st = kt ? quant_rotate_kt_impl("quant_convrot_kt", stream, x, x_dtype, M, K, ldx, pre, q8, s8, 127.0f, round_mode)
+            : phi_hip_quant_rotate(stream, x, x_dtype, M, K, ldx, q8, K, s8, 127.0f, round_mode, 1);
+    if (st != PHI_OK) return st;
     if (expand) {
-        st = check_hip(phi_dev::launch_w4_lut_expand((hipStream_t)stream, p, (int8_t*)workspace, kt), who);
-        if (st != PHI_OK) return st;
+        if (!fuse) {
+            st = check_hip(phi_dev::launch_w4_lut_expand((hipStream_t)stream, p, (int8_t*)workspace, kt), who);
+            if (st != PHI_OK) return st;
+        }
         phi_dev::GemmParams g = p;
         g.B = (const int8_t*)workspace;
         g.ldb = K;

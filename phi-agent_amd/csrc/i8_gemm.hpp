@@ -62,6 +62,9 @@ __host__ __device__ __forceinline__ int64_t k_tiled_offset(int64_t r, int64_t c,
 
 hipError_t launch_i8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_w4a8_gemm(hipStream_t stream, const GemmParams& p, int cfg);
+// Whether p's W4 operand (codes p.B, pitch p.ldb, tables p.lut) can be expanded
+// into out (K-tiled with kt) by w4_lut_expand_kernel or a prologue's W4Expand.
+bool w4_expand_ok(const GemmParams& p, const int8_t* out, bool kt);
 // Any K > 0, operands at any byte offset and pitch (the K tail zero-filled).
 hipError_t launch_i8_gemm_any(hipStream_t stream, const GemmParams& p, int cfg);
 hipError_t launch_i8_gemm_256(hipStream_t stream, const GemmParams& p);
@@ -103,11 +106,29 @@ hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t*
 
 // Element-wise operation applied to every input element before the rotation.
 enum QrPreOp { QR_PLAIN = 0, QR_MOD = 1, QR_GELU = 2, QR_SILU_GATE = 3 };
+// A 4-bit weight's expansion to int8 (w4_lut_expand_kernel's work) run as
+// extra blocks of a plain prologue launch (the tiles kernel), so the
+// memory-bound expansion overlaps the VALU-bound rotation.  `on` set by the
+// caller after w4_expand_ok(); `blocks` and `nq` set by the launcher.
+struct W4Expand {
+    int on = 0;
+    const uint8_t* codes = nullptr;
+    int64_t ldb = 0;
+    const int8_t* lut = nullptr;
+    int64_t lut_groups = 0;
+    int group_shift = 0, w4_signed = 0, kt = 0;
+    int64_t N = 0, K = 0;
+    int8_t* out = nullptr;
+    int blocks = 0;  // expansion blocks in the launch
+    int nq = 0;      // prologue blocks in the launch
+};
+
 struct QrPre {
     int op;             // QrPreOp
     const float* sc;    // QR_MOD: v = fma(v, 1 + sc[k], sh[k]); either may be NULL (0)
     const float* sh;
     int64_t off2;       // QR_SILU_GATE: v = silu(x[k]) * x[k + off2] (elements)
+    W4Expand ex{};      // QR_PLAIN through the tiles kernel only
 };
 // q_kt: q is written in the K-tiled layout of `rows` rows (ldq unused; K <= 16384).
 hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, int64_t rows,

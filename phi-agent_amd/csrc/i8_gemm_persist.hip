@@ -435,10 +435,13 @@ __global__ __launch_bounds__(256) void w4_lut_expand_kernel(const uint8_t* __res
     *(v4i*)o1 = expand16b(c[2], c[3], t);
 }
 
+bool w4_expand_ok(const GemmParams& p, const int8_t* out, bool kt) {
+    return !(p.K % 32 != 0 || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 || ((uintptr_t)out & 15) != 0 ||
+             (!p.w4_signed && (p.group_shift < 5 || !p.lut)) || (kt && p.K % 64 != 0));
+}
+
 hipError_t launch_w4_lut_expand(hipStream_t stream, const GemmParams& p, int8_t* out, bool kt) {
-    if (p.K % 32 != 0 || p.ldb % 16 != 0 || ((uintptr_t)p.B & 15) != 0 || ((uintptr_t)out & 15) != 0 ||
-        (!p.w4_signed && (p.group_shift < 5 || !p.lut)) || (kt && p.K % 64 != 0))
-        return hipErrorInvalidValue;
+    if (!w4_expand_ok(p, out, kt)) return hipErrorInvalidValue;
     const int64_t threads = (int64_t)p.N * (p.K / 32);
     hipLaunchKernelGGL(w4_lut_expand_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
                        (const uint8_t*)p.B, p.ldb, p.lut, p.lut_groups, p.group_shift, p.w4_signed, (int64_t)p.N,

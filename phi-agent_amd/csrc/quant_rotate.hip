@@ -32,6 +32,7 @@
 
 #include "device_common.hpp"
 #include "i8_gemm.hpp"
+#include "persist_common.hpp"
 #include "qt_scale.hpp"
 
 namespace phi_dev {
@@ -579,6 +580,25 @@ __device__ __forceinline__ void qt_row(const uint32_t (&raw)[R][qt_ns<OP>][qt_nw
     }
 }
 
+// One block's share of a W4Expand job: item i (idx * threads + thread)
+// turns 32 consecutive codes of one weight row into 32 int8, as
+// w4_lut_expand_kernel's thread i does.
+__device__ __forceinline__ void w4_expand_part(const W4Expand& ex, int idx) {
+    const int nt = blockDim.x * blockDim.y;
+    const int64_t per_row = ex.K / 32;
+    const int64_t i = (int64_t)idx * nt + threadIdx.y * blockDim.x + threadIdx.x;
+    if (i >= ex.N * per_row) return;
+    const int64_t row = i / per_row, c32 = i - row * per_row;
+    using persist::u32x4;
+    const u32x4 c = *(const u32x4*)(ex.codes + row * ex.ldb + c32 * 16);
+    const u32x4 t = ex.w4_signed ? persist::signed_nibble_table()
+                                 : *(const u32x4*)(ex.lut + (row * ex.lut_groups + ((c32 * 32) >> ex.group_shift)) * 16);
+    int8_t* o0 = ex.out + (ex.kt ? k_tiled_offset(row, c32 * 32, ex.K, ex.N) : row * ex.K + c32 * 32);
+    int8_t* o1 = ex.out + (ex.kt ? k_tiled_offset(row, c32 * 32 + 16, ex.K, ex.N) : row * ex.K + c32 * 32 + 16);
+    *(v4i*)o0 = persist::expand16b(c[0], c[1], t);
+    *(v4i*)o1 = persist::expand16b(c[2], c[3], t);
+}
+
 template <bool BF16_IN, bool HALF_EVEN, int R, int OP>
 __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restrict__ x, int64_t ldx, int rows,
                                                            int G, int8_t* __restrict__ q, int64_t ldq,
@@ -596,9 +616,31 @@ __global__ __launch_bounds__(1024) void quant_rotate_tiles(const void* __restric
     // lines of the K-tiled codes (two rows a line) are written through one
     // L2.  The last partial set of runs keeps its order.
     int blk = blockIdx.x;
+    unsigned nblk = gridDim.x;
+    if (OP == QR_PLAIN && pre_op.ex.blocks) {
+        // Beside a W4Expand job: groups of 16 blocks, 8 of the prologue then 8
+        // of the expansion (each kind on all 8 XCDs), while both last; then
+        // the rest of the longer one.
+        const int nq = pre_op.ex.nq, ne = pre_op.ex.blocks, full = min(nq, ne) / 8;
+        int kind, idx;
+        if (blk < 16 * full) {
+            kind = (blk >> 3) & 1;
+            idx = 8 * (blk >> 4) + (blk & 7);
+        } else {
+            const int rest = blk - 16 * full, qrem = nq - 8 * full;
+            kind = rest >= qrem;
+            idx = 8 * full + (kind ? rest - qrem : rest);
+        }
+        if (kind) {
+            w4_expand_part(pre_op.ex, idx);
+            return;
+        }
+        blk = idx;
+        nblk = (unsigned)nq;
+    }
     {
         const int span = 8 << lg_run;
-        if (blk < (int)(gridDim.x & ~(unsigned)(span - 1))) {
+        if (blk < (int)(nblk & ~(unsigned)(span - 1))) {
             const int c = blk & (span - 1);
             blk += ((c & 7) << lg_run) + (c >> 3) - c;
         }
@@ -659,13 +701,22 @@ static hipError_t launch_tiles_r(hipStream_t stream, const void* x, int64_t rows
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
+    dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block((unsigned)(64 * wpr), (unsigned)rpb);
+    QrPre p2 = pre;
+    if (OP == QR_PLAIN && pre.ex.on) {
+        const int64_t items = pre.ex.N * (pre.ex.K / 32), nt = 64 * wpr * rpb;
+        p2.ex.nq = (int)grid.x;
+        p2.ex.blocks = (int)((items + nt - 1) / nt);
+        grid.x += (unsigned)p2.ex.blocks;
+    } else {
+        p2.ex.blocks = 0;
+    }
     // Runs of 8 blocks a XCD: config 1's prologue 11.0 -> 10.4 us, config 1
     // down's 32.3 -> 29.0 us (K-tiled codes; runs of 2 and 4 measured too).
     // A/B switch: log2 of the run length, 0..4 (the kernel shifts by it)
     const int lg_run = env_switch("PHI_QR_RUN", 3, 0, 4);
     hipLaunchKernelGGL((quant_rotate_tiles<BF16_IN, HALF_EVEN, R, OP>), grid, block, lds, stream, x, ldx, (int)rows,
-                       G, q, ldq, s, qmax, 1.0f / qmax, rotate, pre, qkt, lg_run);
+                       G, q, ldq, s, qmax, 1.0f / qmax, rotate, p2, qkt, lg_run);
     return hipGetLastError();
 }
 

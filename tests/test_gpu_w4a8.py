@@ -141,8 +141,9 @@ def test_in_register_linear_equals_expand_then_w8a8(dev, monkeypatch, kernel, wi
 @pytest.mark.parametrize("M,N,K,group", [(600, 520, 3072, 128), (777, 1032, 768, 128), (4352, 2304, 512, 256),
                                          (640, 264, 1280, 128)])
 def test_expand_once_row_major_switch(dev, monkeypatch, M, N, K, group):
-    """The expand-once path (512 rows and more) with its operands row-major (PHI_GEMM_KT=0)
-    gives the bits of its K-tiled default and of expand-then-W8A8."""
+    """The expand-once path (512 rows and more) with its operands row-major (PHI_GEMM_KT=0),
+    and K-tiled with the expansion in its own launch (PHI_W4_FUSE=0) instead of beside the
+    prologue, gives the bits of its K-tiled default and of expand-then-W8A8."""
     codes, s_rel, sch, corr = synth.w4a8_weight(N, K, group, seed=M + N + 1)
     cd, rd, sd, kd = codes.to(dev), s_rel.to(dev), sch.to(dev), corr.to(dev)
     x = synth.activations(M, K, seed=M + 1, device=dev)
@@ -154,10 +155,15 @@ def test_expand_once_row_major_switch(dev, monkeypatch, M, N, K, group):
     monkeypatch.setenv("PHI_GEMM_KT", "0")
     y_row = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
     monkeypatch.delenv("PHI_GEMM_KT")
+    ws.fill_(0)
+    monkeypatch.setenv("PHI_W4_FUSE", "0")
+    y_sep = Q.w4a8_linear(x, cd, lut, s2, group=group, workspace=ws)
+    monkeypatch.delenv("PHI_W4_FUSE")
     y_ref = Q.q8_linear(x, q, s)
     torch.cuda.synchronize()
     assert torch.equal(y_kt.view(torch.int16), y_ref.view(torch.int16))
     assert torch.equal(y_row.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(y_sep.view(torch.int16), y_ref.view(torch.int16))
 
 
 @pytest.mark.slow
