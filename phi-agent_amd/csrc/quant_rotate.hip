@@ -757,6 +757,8 @@ hipError_t launch_quant_rotate(hipStream_t stream, const void* x, bool bf16_in, 
     const int G = (int)(K / 256);
     if (rows == 0) return hipSuccess;
     if (qkt && G > 64) return hipErrorInvalidValue;  // the row kernel writes row-major q only
+    // A W4Expand job rides only on the plain tiles kernel.
+    if (pre.ex.on && (G > 64 || pre.op != QR_PLAIN)) return hipErrorInvalidValue;
     if (G <= 64) {
         if (bf16_in)
             return half_even ? launch_tiles<true, true>(stream, x, rows, G, ldx, q, ldq, s, qmax, rotate, pre, qkt)
